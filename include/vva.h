@@ -1,0 +1,205 @@
+/*
+ * vva.h — C ABI of the MI355X (gfx950) Qwen2 self-attention path.
+ *
+ * Scope: NeoX RoPE, KV-cache append, causal grouped-query attention for
+ * prefill and single-token decode — the attention section of
+ * vibevoice.cpp's Qwen2 layer builders (src/qwen2.cpp:101-185 classic,
+ * src/qwen2.cpp:278-347 resident).  Everything else in the layer
+ * (projections, norms, FFN) stays in the caller.
+ *
+ * Conventions (mirroring include/vibevoice.h:23-33 and src/vibevoice_capi.cpp):
+ *   - every entry point returns vva_status: 0 = OK, negative = error, with
+ *     the same numbering as vv_status; nothing aborts, nothing throws;
+ *   - all tensor arguments are device pointers described by vva_tensor, a
+ *     ggml-shaped view (ne[] element counts fastest-first, nb[] byte strides),
+ *     so a ggml custom op can forward ggml_tensor fields unchanged;
+ *   - a vva_context owns (or borrows) exactly one HIP stream; every call on a
+ *     context is enqueued on that stream in call order, so a KV append issued
+ *     before an attention call is always visible to it.  A context is not
+ *     re-entrant: callers serialize, as vv_capi does with its global mutex
+ *     (src/vibevoice_capi.cpp:29).
+ *   - no HIP/CUDA types appear here; the stream is passed as void*.
+ */
+#ifndef VVA_H
+#define VVA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VVA_API __attribute__((visibility("default")))
+
+/* Status codes: numbering follows vv_status (include/vibevoice.h:23-33). */
+typedef enum {
+    VVA_OK                  =  0,
+    VVA_ERR_GENERIC         = -1,
+    VVA_ERR_INVALID_ARG     = -2,
+    VVA_ERR_OUT_OF_MEMORY   = -5,
+    VVA_ERR_NOT_IMPLEMENTED = -6,
+    VVA_ERR_DEVICE          = -9
+} vva_status;
+
+/* Element types: numbering is ggml's enum ggml_type, so t->type of a
+ * ggml_tensor can be passed straight through. */
+typedef enum {
+    VVA_TYPE_F32  = 0,
+    VVA_TYPE_F16  = 1,
+    VVA_TYPE_Q8_0 = 8,   /* GGUF block: { fp16 d; int8 qs[32]; } = 34 bytes */
+    VVA_TYPE_I32  = 26,
+    VVA_TYPE_BF16 = 30
+} vva_type;
+
+/* RoPE mode: ggml's GGML_ROPE_TYPE_NEOX (src/rope.hpp:14). */
+#define VVA_ROPE_TYPE_NEOX 2
+
+/* Largest number of sequences one call may touch (CFG uses 2). */
+#define VVA_MAX_BATCH 16
+
+/* ggml-shaped strided view of a device tensor.
+ * ne[0] is the fastest dimension; nb[i] is the byte stride of dimension i.
+ * For VVA_TYPE_Q8_0, ne[0] counts elements (a multiple of 32) and nb[0] is
+ * the block size (34). */
+typedef struct {
+    void*    data;
+    int32_t  type;
+    int64_t  ne[4];
+    size_t   nb[4];
+} vva_tensor;
+
+typedef struct vva_context vva_context;
+typedef struct vva_kv      vva_kv;
+
+/* ---------------------------------------------------------------- context */
+
+/* Create a context on HIP device `device`.  `stream` is a hipStream_t to
+ * borrow (not destroyed by vva_destroy) or NULL to create an owned one.
+ * Replaces vv::backend() / init (src/backend.cpp:64-133). */
+VVA_API vva_status  vva_create(int device, void* stream, vva_context** out);
+VVA_API void        vva_destroy(vva_context* ctx);
+/* Rebind the context to another borrowed stream (NULL = the owned one). */
+VVA_API vva_status  vva_set_stream(vva_context* ctx, void* stream);
+/* Block until all work enqueued on the context's stream is done. */
+VVA_API vva_status  vva_synchronize(vva_context* ctx);
+/* Last error message recorded on this context ("" if none).  With ctx NULL
+ * returns the message of the last failed vva_create. */
+VVA_API const char* vva_last_error(const vva_context* ctx);
+/* Library version string. */
+VVA_API const char* vva_version(void);
+
+/* ------------------------------------------------------------- KV cache */
+
+/* Resident KV cache: one K and one V tensor per (layer, sequence), each
+ * ggml-shaped ne = [head_dim, n_kv_heads, max_seq, 1] (memory [s][h][d]),
+ * exactly the layout of ResidentKV (src/qwen2.cpp:218-220) but in any of
+ * F32 / F16 / BF16 / Q8_0 and for n_seq independent sequences (the CFG
+ * positive and negative streams, src/vibevoice_tts.cpp:727-730). */
+typedef struct {
+    int32_t n_layers;
+    int32_t n_kv_heads;
+    int32_t head_dim;
+    int32_t max_seq;
+    int32_t n_seq;
+    int32_t type;       /* vva_type of the cache rows */
+} vva_kv_desc;
+
+/* Allocate (hipMalloc, one slab) and zero a cache.
+ * Replaces ResidentKV::init (src/qwen2.cpp:207-229). */
+VVA_API vva_status vva_kv_create(vva_context* ctx, const vva_kv_desc* desc, vva_kv** out);
+/* Replaces ResidentKV::free (src/qwen2.cpp:231-244). */
+VVA_API void       vva_kv_free(vva_kv* kv);
+/* Number of valid rows of sequence `seq` — ResidentKV::past_len
+ * (src/qwen2.hpp:83), owned and advanced by the caller
+ * (src/qwen2.hpp:116-121, src/vibevoice_asr.cpp:641). */
+VVA_API vva_status vva_kv_get_len(const vva_kv* kv, int seq, int32_t* len);
+VVA_API vva_status vva_kv_set_len(vva_kv* kv, int seq, int32_t len);
+/* ggml-shaped views of the resident K and V tensors of (layer, seq):
+ * ne = [head_dim, n_kv_heads, max_seq, 1].  Equivalent of kvs.k[layer] /
+ * kvs.v[layer] (src/qwen2.cpp:293-294).  Either output may be NULL. */
+VVA_API vva_status vva_kv_view(const vva_kv* kv, int layer, int seq,
+                               vva_tensor* k, vva_tensor* v);
+/* Copy host F32 rows [len][n_kv_heads][head_dim] of K and V into rows
+ * [start, start+len) of (layer, seq), converting to the cache type.  Used for
+ * the pre-baked voice-prompt KV (src/vibevoice_tts.cpp:735-749, layout
+ * scripts/convert_voice_to_gguf.py:115-128).  Synchronous. */
+VVA_API vva_status vva_kv_upload(vva_context* ctx, vva_kv* kv, int layer, int seq,
+                                 int32_t start, int32_t len,
+                                 const float* k_host, const float* v_host);
+
+/* ------------------------------------------------------------------ ops */
+
+/* NeoX RoPE, ggml_rope_ext(ctx, x, pos, NULL, n_dims, GGML_ROPE_TYPE_NEOX,
+ * 0, freq_base, 1, 0, 1, 0, 0) (src/qwen2.cpp:282-287):
+ *   x, dst: ne = [head_dim, n_heads, T, B], F32 / F16 / BF16 (may alias);
+ *   pos:    I32, ne = [T] or [T, B] (per-sequence positions).
+ * Requires n_dims == head_dim, head_dim even. */
+VVA_API vva_status vva_rope_ext(vva_context* ctx, const vva_tensor* x, const vva_tensor* pos,
+                                int n_dims, int mode, float freq_base, const vva_tensor* dst);
+
+/* Fused RoPE + KV append — the RoPE of Q and K plus the two ggml_cpy's into
+ * the resident views at past_len (src/qwen2.cpp:282-306):
+ *   q: ne = [d, Hq,  T, B]   k, v: ne = [d, Hkv, T, B]   (F32 / F16 / BF16)
+ *   pos: I32 ne = [T] or [T, B]
+ *   seq_ids: host array [B] mapping batch b to a cache sequence (NULL = b)
+ *   q_out: ne = [d, Hq, T, B] in F32 / F16 / BF16 (may alias q when the
+ *          types match); receives RoPE(q).
+ * Writes RoPE(k) and v into rows [len(seq_b), len(seq_b)+T) of (layer,
+ * seq_b), converted to the cache type (Q8_0: one block per 32 values, scale
+ * amax/127, codes round(x*127/amax)).  Does NOT advance len (the caller does,
+ * after attention, like kv.past_len at src/vibevoice_asr.cpp:641). */
+VVA_API vva_status vva_rope_append(vva_context* ctx, vva_kv* kv, int layer,
+                                   const vva_tensor* q, const vva_tensor* k, const vva_tensor* v,
+                                   const vva_tensor* pos, const int32_t* seq_ids,
+                                   float freq_base, const vva_tensor* q_out);
+
+/* Attention over the resident window — the FA branch
+ * ggml_flash_attn_ext(q_p, k_full, v_full, mask, scale, 0, 0) with
+ * set_prec(F32) and cont_2d (src/qwen2.cpp:312-335):
+ *   q:    ne = [d, Hq, T, B] (F32 / F16 / BF16), already RoPE'd;
+ *   seq_ids: host [B] (NULL = b);  each sequence sees L_b = len(seq_b) + T
+ *         keys (the T new rows were appended by vva_rope_append);
+ *   mask: NULL for implicit causal masking (key j visible to query row i
+ *         iff j <= len(seq_b) + i), or F16 ne = [>=L_b, T, 1, 1 or B] with
+ *         0 / -inf entries as built at src/vibevoice_asr.cpp:616-627;
+ *   out:  F32 ne = [d, Hq, T, B], the FA output layout (src/qwen2.cpp:156-159).
+ * Q is rounded to the dot type of K as ggml's CPU FA does (F16 -> f16,
+ * BF16 -> bf16, Q8_0 -> Q8_0 blocks, F32 -> f32).  T == 1 runs the split-K
+ * decode kernel; larger T runs the MFMA prefill kernel (F16 / BF16 caches)
+ * or the VALU kernel (F32 / Q8_0 caches). */
+VVA_API vva_status vva_attn(vva_context* ctx, const vva_kv* kv, int layer,
+                            const vva_tensor* q, const int32_t* seq_ids,
+                            const vva_tensor* mask, float scale, const vva_tensor* out);
+
+/* ggml_flash_attn_ext on arbitrary strided device tensors (ggml.h semantics):
+ *   q: ne = [d, T, Hq, B] (F32 / F16 / BF16)  — the permuted q_p of
+ *      src/qwen2.cpp:320;
+ *   k, v: ne = [d, L, Hkv, B] (F32 / F16 / BF16 / Q8_0), any strides;
+ *   mask: NULL (no masking, as in ggml) or F16 ne = [>=L, T, 1, 1 or B];
+ *   dst: F32 ne = [d, Hq, T, B] (contiguous rows of d).
+ * max_bias and logit_softcap must be 0 (the reference passes 0, 0 at
+ * src/qwen2.cpp:332-333); anything else returns VVA_ERR_NOT_IMPLEMENTED. */
+VVA_API vva_status vva_flash_attn_ext(vva_context* ctx, const vva_tensor* q, const vva_tensor* k,
+                                      const vva_tensor* v, const vva_tensor* mask, float scale,
+                                      float max_bias, float logit_softcap, const vva_tensor* dst);
+
+/* Capability probe — analogue of backend_supports_flash_attn()
+ * (src/backend.cpp:157-196).  Returns 1 if vva_attn / vva_flash_attn_ext can
+ * run this combination on the context's device, 0 otherwise. */
+VVA_API int vva_supports(const vva_context* ctx, int head_dim, int n_q_heads, int n_kv_heads,
+                         int q_type, int kv_type);
+
+/* ------------------------------------------------------------ debugging */
+
+/* Kernel path selection for tests: 0 = automatic (default), 1 = force the
+ * VALU row kernel for every attention call.  Per context. */
+VVA_API vva_status vva_set_attn_path(vva_context* ctx, int path);
+/* Number of key splits used by the last decode call (0 if none). */
+VVA_API int        vva_last_decode_splits(const vva_context* ctx);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VVA_H */

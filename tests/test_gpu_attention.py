@@ -1,0 +1,173 @@
+"""GPU parity of attention through the C ABI against the oracle.
+
+The oracle runs on the exact bytes the GPU holds (cache rows downloaded
+from the device) with Q rounded to K's dot type as ggml's CPU flash
+attention does.  Tolerances (stated per test): 1e-4 max-abs for the F32
+path, 2e-3 max-abs / 1e-3 mean-abs for F16 / BF16 / Q8_0 caches.  Each case
+also reports the distance to the ggml-order oracle mode (per-key online
+softmax, F16 running sum for F16 V).
+"""
+import os
+
+import numpy as np
+import pytest
+
+import vva
+import vvo
+from gpu_util import as_f32, assert_close, err_stats, fill_cache, oracle_attn, to_gpu
+
+pytestmark = pytest.mark.gpu
+
+TOL = {vva.F32: (1e-4, 1e-4), vva.F16: (2e-3, 1e-3), vva.BF16: (2e-3, 1e-3), vva.Q8_0: (2e-3, 1e-3)}
+
+
+def run_attn(ctx, torch, kv, layer, T, B, Hq, q_type, seed, seqs=None, mask=None):
+    rng = np.random.default_rng(seed)
+    d = kv.head_dim
+    q = to_gpu(torch, rng.standard_normal((B, T, Hq, d)), q_type)
+    out = torch.full((B, T, Hq, d), float("nan"), dtype=torch.float32, device="cuda")
+    mask_t = None
+    if mask is not None:
+        mask_t = torch.from_numpy(mask.view(np.float16)).to("cuda")
+    ctx.attn(kv, layer, q, out, d ** -0.5, seq_ids=seqs, mask=mask_t)
+    torch.cuda.synchronize()
+    return as_f32(torch, q), as_f32(torch, out)
+
+
+DECODE = [
+    # d, Hq, Hkv, type, lens (per seq, incl. the new token), q_type
+    (64, 14, 2, vva.F16, [1025, 1025], vva.F32),          # TTS CFG decode, 0.5B
+    (64, 14, 2, vva.F16, [1224, 990], vva.F32),           # ragged CFG streams
+    (128, 28, 4, vva.Q8_0, [4097, 3000], vva.F32),        # 7B Q8_0 decode
+    (128, 28, 4, vva.Q8_0, [1], vva.F32),                 # first token
+    (128, 12, 2, vva.BF16, [2049], vva.BF16),             # 1.5B
+    (128, 28, 4, vva.F16, [17, 300], vva.F16),
+    (64, 14, 2, vva.Q8_0, [777], vva.F32),
+    (128, 28, 4, vva.F32, [513], vva.F32),                # F32 cache: VALU path
+]
+
+
+@pytest.mark.parametrize("d,Hq,Hkv,t,lens,q_type", DECODE)
+def test_decode_matches_oracle(ctx, torch_gpu, d, Hq, Hkv, t, lens, q_type):
+    torch = torch_gpu
+    B = len(lens)
+    print(f"decode d={d} Hq={Hq} Hkv={Hkv} type={t} lens={lens}", flush=True)
+    kv = vva.KVCache(ctx, 1, Hkv, d, max(lens) + 4, B, t)
+    fill_cache(kv, lens, seed=d + t + sum(lens))
+    for s, n in enumerate(lens):
+        kv.set_len(s, n - 1)                               # the last row is "the new token"
+    q, out = run_attn(ctx, torch, kv, 0, 1, B, Hq, q_type, seed=7)
+    ref = oracle_attn(q, kv, 0, range(B), lens, 1, d ** -0.5)
+    mx, mn = assert_close(out, ref, *TOL[t], what="decode vs exact")
+    gg = oracle_attn(q, kv, 0, range(B), lens, 1, d ** -0.5, mode=vvo.GGML)
+    gmx, gmn = err_stats(out, gg)
+    print(f"  vs exact max {mx:.2e} mean {mn:.2e}; vs ggml-order max {gmx:.2e} mean {gmn:.2e}; "
+          f"splits {ctx.last_decode_splits()}")
+    assert gmx <= TOL[t][0] and gmn <= TOL[t][1]
+    kv.free()
+
+
+def test_decode_split_count_does_not_change_result(ctx, torch_gpu):
+    torch = torch_gpu
+    lens = [5000, 4321]
+    kv = vva.KVCache(ctx, 1, 4, 128, 5008, 2, vva.Q8_0)
+    fill_cache(kv, lens, seed=3)
+    for s, n in enumerate(lens):
+        kv.set_len(s, n - 1)
+    outs = []
+    for wgs in ("2", "16", "512", "4096"):
+        os.environ["VVA_DECODE_WGS"] = wgs
+        try:
+            _, out = run_attn(ctx, torch, kv, 0, 1, 2, 28, vva.F32, seed=9)
+        finally:
+            del os.environ["VVA_DECODE_WGS"]
+        outs.append((ctx.last_decode_splits(), out))
+    assert len({s for s, _ in outs}) == 4, [s for s, _ in outs]
+    for s, o in outs[1:]:
+        assert np.abs(o - outs[0][1]).max() < 1e-5, s
+    kv.free()
+
+
+def test_decode_explicit_mask(ctx, torch_gpu):
+    torch = torch_gpu
+    L = 700
+    kv = vva.KVCache(ctx, 1, 2, 64, L, 1, vva.F16)
+    fill_cache(kv, [L], seed=4)
+    kv.set_len(0, L - 1)
+    m = np.zeros((1, 1, L), np.float32)
+    m[0, 0, 100:300] = -np.inf                             # a hole in the window
+    mbits = vvo.f16_bits(m)
+    q, out = run_attn(ctx, torch, kv, 0, 1, 1, 14, vva.F32, seed=5, mask=mbits)
+    ref = oracle_attn(q, kv, 0, [0], [L], 1, 64 ** -0.5, mask=mbits)
+    assert_close(out, ref, *TOL[vva.F16], what="masked decode")
+    kv.free()
+
+
+ROWS = [
+    # d, Hq, Hkv, type, T, past  — VALU row kernel cases
+    (64, 14, 2, vva.F32, 256, 0),        # 0.5B prefill (fp32 eager-equivalent)
+    (128, 28, 4, vva.Q8_0, 64, 500),     # chunk into a Q8_0 cache
+    (128, 12, 2, vva.F32, 33, 7),
+]
+
+
+@pytest.mark.parametrize("d,Hq,Hkv,t,T,past", ROWS)
+def test_row_kernel_prefill_matches_oracle(ctx, torch_gpu, d, Hq, Hkv, t, T, past):
+    torch = torch_gpu
+    print(f"rows d={d} Hq={Hq} Hkv={Hkv} type={t} T={T} past={past}", flush=True)
+    L = past + T
+    kv = vva.KVCache(ctx, 1, Hkv, d, L, 1, t)
+    fill_cache(kv, [L], seed=11, scale=1.0 if t != vva.F32 else 0.125)
+    kv.set_len(0, past)
+    q, out = run_attn(ctx, torch, kv, 0, T, 1, Hq, vva.F32, seed=12)
+    ref = oracle_attn(q, kv, 0, [0], [L], T, d ** -0.5)
+    assert_close(out, ref, *TOL[t], what="row kernel")
+    kv.free()
+
+
+def test_forced_row_path_matches_decode(ctx, torch_gpu):
+    torch = torch_gpu
+    lens = [2000]
+    kv = vva.KVCache(ctx, 1, 4, 128, 2000, 1, vva.F16)
+    fill_cache(kv, lens, seed=21)
+    kv.set_len(0, 1999)
+    _, a = run_attn(ctx, torch, kv, 0, 1, 1, 28, vva.F32, seed=22)
+    ctx.set_attn_path(1)
+    try:
+        _, b = run_attn(ctx, torch, kv, 0, 1, 1, 28, vva.F32, seed=22)
+    finally:
+        ctx.set_attn_path(0)
+    assert np.abs(a - b).max() < 1e-5
+    kv.free()
+
+
+def test_flash_attn_ext_strided_head_major_kv(ctx, torch_gpu):
+    """ggml_flash_attn_ext on tensors laid out [B][Hkv][L][d] (not the cache layout), no mask."""
+    torch = torch_gpu
+    rng = np.random.default_rng(31)
+    B, Hq, Hkv, L, T, d = 2, 12, 2, 300, 1, 128
+    q = to_gpu(torch, rng.standard_normal((B, Hq, T, d)), vva.F32)
+    k = to_gpu(torch, rng.standard_normal((B, Hkv, L, d)), vva.F16)
+    v = to_gpu(torch, rng.standard_normal((B, Hkv, L, d)), vva.F16)
+    out = torch.empty((B, T, Hq, d), dtype=torch.float32, device="cuda")
+    ctx.flash_attn_ext(q, k, v, out, d ** -0.5)
+    torch.cuda.synchronize()
+    q32 = as_f32(torch, q).transpose(0, 2, 1, 3)                  # [B, T, Hq, d]
+    kc = [vvo.from_f32(as_f32(torch, k)[b].transpose(1, 0, 2), vvo.F16) for b in range(B)]
+    vc = [vvo.from_f32(as_f32(torch, v)[b].transpose(1, 0, 2), vvo.F16) for b in range(B)]
+    ref = vvo.attn(q32, kc, vc, 1, 1, [L] * B, n_kv_heads=Hkv, scale=d ** -0.5, mask_mode=vvo.MASK_NONE)
+    assert_close(as_f32(torch, out), ref, *TOL[vva.F16], what="flash_attn_ext strided")
+
+
+def test_unsupported_options_are_rejected(ctx, torch_gpu):
+    torch = torch_gpu
+    q = torch.zeros((1, 4, 1, 64), device="cuda")
+    k = torch.zeros((1, 2, 8, 64), device="cuda", dtype=torch.float16)
+    out = torch.zeros((1, 1, 4, 64), device="cuda")
+    with pytest.raises(vva.VvaError) as e:
+        ctx.lib_check = None
+        st = ctx.lib.vva_flash_attn_ext(ctx.h, vva.ctypes.byref(vva.view(q)), vva.ctypes.byref(vva.view(k)),
+                                        vva.ctypes.byref(vva.view(k)), None, 0.125, 1.0, 0.0,
+                                        vva.ctypes.byref(vva.view(out)))
+        ctx.check(st)
+    assert e.value.status == vva.ERR_NOT_IMPLEMENTED

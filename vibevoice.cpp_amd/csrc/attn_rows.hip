@@ -1,0 +1,165 @@
+// attn_rows.hip — VALU attention, one wavefront per query row.
+//
+// Covers every combination the MFMA prefill and split-K decode kernels do
+// not: F32 caches (the eager mul_mat -> soft_max_ext -> mul_mat branch,
+// src/qwen2.cpp:337-343, computed in fp32 throughout), Q8_0 caches with more
+// than one new token, and explicit masks of any shape.  Semantics follow
+// ggml's flash_attn_ext (src/qwen2.cpp:332-334): Q rounded to K's dot type
+// (F16 -> f16, BF16 -> bf16, Q8_0 -> Q8_0 blocks with integer dots), scores
+// scaled then masked, fp32 online softmax, fp32 V accumulation, rows with no
+// visible key produce 0.
+//
+// Mapping: lane l owns dims l, l+64, ... (DPL = d/64 rounded up per lane);
+// each key's dot is a 64-lane butterfly sum.  Keys are taken four at a time
+// so four butterflies are in flight.  Latency-oriented: it serves the small
+// shapes (0.5B prefill of 256 tokens, chunk tails) rather than the roofline
+// configurations.
+#include "vva_internal.hpp"
+
+namespace vva {
+
+namespace {
+
+constexpr int kRowsPerBlock = 4;   // one row per wave
+
+template <int DPL>
+__global__ void __launch_bounds__(256) attn_rows_kernel(AttnArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    if (row >= a.B * a.T * a.Hq) return;        // whole wave leaves together
+    const int h = row % a.Hq;
+    const int bt = row / a.Hq;
+    const int t = bt % a.T;
+    const int b = bt / a.T;
+    const int kvh = h / (a.Hq / a.Hkv);
+    const int d = a.d;
+
+    // ---- query, rounded to K's dot type
+    const int64_t qes = type_elem_bytes(a.q_type);
+    const char* qrow = a.q + b * a.q_nb_b + t * a.q_nb_t + h * a.q_nb_h;
+    float q[DPL];
+    float qs[DPL];          // Q8_0: per-lane block scale of q
+#pragma unroll
+    for (int r = 0; r < DPL; ++r) {
+        const int i = lane + 64 * r;
+        q[r] = i < d ? load_elem(qrow + i * qes, a.q_type) : 0.0f;
+        qs[r] = 0.0f;
+    }
+    const bool k_q8 = a.k_type == VVA_TYPE_Q8_0;
+    if (k_q8) {
+#pragma unroll
+        for (int r = 0; r < DPL; ++r) {
+            // lanes 0-31 / 32-63 hold blocks 2r / 2r+1 of the row
+            float am = fabsf(q[r]);
+#pragma unroll
+            for (int m = 16; m >= 1; m >>= 1) am = fmaxf(am, __shfl_xor(am, m, 32));
+            const float dq = am / 127.0f;
+            const float id = dq != 0.0f ? 1.0f / dq : 0.0f;
+            q[r] = roundf(q[r] * id);              // integer code, exact in f32
+            qs[r] = f16_to_f32(f32_to_f16(dq));
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < DPL; ++r) q[r] = round_to_type(q[r], a.k_type);
+    }
+
+    // ---- visible window
+    const int L = a.L[b];
+    int jend = L;
+    if (a.mask_mode == kMaskCausal) jend = min(L, a.past[b] + t + 1);
+    const char* kbase = a.k[b] + kvh * a.k_nb_head;
+    const char* vbase = a.v[b] + kvh * a.v_nb_head;
+    const char* mrow = a.mask ? a.mask + b * a.mask_nb_b + t * a.mask_nb_row : nullptr;
+    const int64_t kes = type_elem_bytes(a.k_type), ves = type_elem_bytes(a.v_type);
+
+    float M = -INFINITY, S = 0.0f;
+    float acc[DPL];
+#pragma unroll
+    for (int r = 0; r < DPL; ++r) acc[r] = 0.0f;
+
+    for (int j0 = 0; j0 < jend; j0 += 4) {
+        float part[4];
+        float mv[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int j = j0 + u;
+            part[u] = 0.0f;
+            mv[u] = -INFINITY;
+            if (j < jend) {
+                mv[u] = (a.mask_mode == kMaskExplicit)
+                            ? f16_to_f32(*(const uint16_t*)(mrow + 2 * (int64_t)j)) : 0.0f;
+                const char* kr = kbase + (int64_t)j * a.k_nb_tok;
+#pragma unroll
+                for (int r = 0; r < DPL; ++r) {
+                    const int i = lane + 64 * r;
+                    if (i < d) {
+                        if (k_q8) {
+                            const char* blk = kr + (i / kQK8) * kQ8Bytes;
+                            const float dk = f16_to_f32(*(const uint16_t*)blk);
+                            const float ck = (float)(int8_t)blk[2 + (i & (kQK8 - 1))];
+                            part[u] = fmaf(q[r] * ck, dk * qs[r], part[u]);
+                        } else {
+                            part[u] = fmaf(q[r], load_elem(kr + i * kes, a.k_type), part[u]);
+                        }
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) part[u] += __shfl_xor(part[u], m, 64);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if (mv[u] == -INFINITY) continue;         // masked / past the window
+            const int j = j0 + u;
+            const float s = part[u] * a.scale + mv[u];
+            float ms = 1.0f, vs = 1.0f;
+            if (s > M) { ms = __expf(M - s); M = s; }   // exp(-inf) = 0 on the first key
+            else       { vs = __expf(s - M); }
+            const char* vr = vbase + (int64_t)j * a.v_nb_tok;
+#pragma unroll
+            for (int r = 0; r < DPL; ++r) {
+                const int i = lane + 64 * r;
+                float vv = 0.0f;
+                if (i < d) {
+                    if (a.v_type == VVA_TYPE_Q8_0) {
+                        const char* blk = vr + (i / kQK8) * kQ8Bytes;
+                        vv = (float)(int8_t)blk[2 + (i & (kQK8 - 1))] * f16_to_f32(*(const uint16_t*)blk);
+                    } else {
+                        vv = load_elem(vr + i * ves, a.v_type);
+                    }
+                }
+                acc[r] = fmaf(vv, vs, acc[r] * ms);
+            }
+            S = S * ms + vs;
+        }
+    }
+    const float inv = S == 0.0f ? 0.0f : 1.0f / S;
+    float* orow = (float*)((char*)a.out + b * a.o_nb_b + t * a.o_nb_t + h * a.o_nb_h);
+#pragma unroll
+    for (int r = 0; r < DPL; ++r) {
+        const int i = lane + 64 * r;
+        if (i < d) orow[i] = acc[r] * inv;
+    }
+}
+
+}  // namespace
+
+hipError_t launch_attn_rows(const AttnArgs& a, hipStream_t s) {
+    const int64_t rows = (int64_t)a.B * a.T * a.Hq;
+    if (rows == 0) return hipSuccess;
+    dim3 grid((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock));
+    const int dpl = (a.d + 63) / 64;
+    switch (dpl) {
+        case 1: hipLaunchKernelGGL(attn_rows_kernel<1>, grid, dim3(256), 0, s, a); break;
+        case 2: hipLaunchKernelGGL(attn_rows_kernel<2>, grid, dim3(256), 0, s, a); break;
+        case 3: hipLaunchKernelGGL(attn_rows_kernel<3>, grid, dim3(256), 0, s, a); break;
+        case 4: hipLaunchKernelGGL(attn_rows_kernel<4>, grid, dim3(256), 0, s, a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace vva

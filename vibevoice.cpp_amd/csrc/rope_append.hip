@@ -1,0 +1,116 @@
+// rope_append.hip — fused NeoX RoPE of Q and K plus the KV-cache append.
+//
+// Replaces, in one launch, the four ggml ops the reference builds per layer
+// (src/qwen2.cpp:282-306): ggml_rope_ext on q, ggml_rope_ext on k (NeoX,
+// src/rope.hpp:14-15), and the two ggml_cpy's of k and v into the resident
+// cache views at row past_len.  The cache may be F32 / F16 / BF16 / Q8_0; the
+// rotated Q is written in the attention's input type.
+//
+// Launch: one workgroup per (token t, batch b), 256 threads.  Threads
+// 0..d/2-1 first build the angle table of the token in LDS with the fp32
+// recurrence ggml's CPU rope cache uses (theta_0 = pos, theta_{i+1} =
+// theta_i * base^(-2/d)); then every thread takes rotation pairs
+// (x[i], x[i+d/2]) of the Hq q heads, the Hkv k heads and the Hkv v heads
+// ("slots").  With d/2 a multiple of 32, each aligned group of 32 threads
+// holds exactly two Q8_0 blocks of one head (elements i and i + d/2), so the
+// block amax is a 32-lane butterfly and the codes are written without LDS.
+//
+// Memory: HBM-bound elementwise pass; per token it reads Hq+2*Hkv source rows
+// and writes Hq rows of Q plus one K and one V cache row.
+#include "vva_internal.hpp"
+
+namespace vva {
+
+namespace {
+
+__device__ __forceinline__ void store_q8_pair(char* row, int i, int P, float y0, float y1) {
+    // elements i (block i/32) and i + P (block (i+P)/32); the 32 lanes of
+    // this aligned group cover both blocks completely
+    float a0 = fabsf(y0), a1 = fabsf(y1);
+#pragma unroll
+    for (int m = 16; m >= 1; m >>= 1) {
+        a0 = fmaxf(a0, __shfl_xor(a0, m, 32));
+        a1 = fmaxf(a1, __shfl_xor(a1, m, 32));
+    }
+    const float d0 = a0 / 127.0f, d1 = a1 / 127.0f;
+    const float id0 = d0 != 0.0f ? 1.0f / d0 : 0.0f;
+    const float id1 = d1 != 0.0f ? 1.0f / d1 : 0.0f;
+    const int j0 = i, j1 = i + P;
+    char* b0 = row + (j0 / kQK8) * kQ8Bytes;
+    char* b1 = row + (j1 / kQK8) * kQ8Bytes;
+    if ((j0 & (kQK8 - 1)) == 0) {
+        *(uint16_t*)b0 = f32_to_f16(d0);
+        *(uint16_t*)b1 = f32_to_f16(d1);
+    }
+    b0[2 + (j0 & (kQK8 - 1))] = (char)(int8_t)roundf(y0 * id0);
+    b1[2 + (j1 & (kQK8 - 1))] = (char)(int8_t)roundf(y1 * id1);
+}
+
+__global__ void __launch_bounds__(256) rope_append_kernel(RopeAppendArgs a) {
+    const int t = blockIdx.x, b = blockIdx.y;
+    const int P = a.d >> 1;
+    __shared__ float cs[128], sn[128];
+    const float p = (float)a.pos[b * a.pos_stride_b + t];
+    for (int i = threadIdx.x; i < P; i += blockDim.x) {
+        float th = p;
+        for (int k = 0; k < i; ++k) th *= a.theta_scale;
+        cs[i] = cosf(th);
+        sn[i] = sinf(th);
+    }
+    __syncthreads();
+
+    const int nq = a.do_q ? a.Hq : 0;
+    const int nslots = nq + (a.do_kv ? 2 * a.Hkv : 0);
+    const int total = nslots * P;
+    for (int w = threadIdx.x; w < total; w += blockDim.x) {
+        const int slot = w / P;
+        const int i = w - slot * P;
+        const float c = cs[i], s = sn[i];
+        if (slot < nq) {
+            const int64_t es = type_elem_bytes(a.q_type);
+            const char* src = a.q + b * a.q_nb_b + t * a.q_nb_t + slot * a.q_nb_h;
+            const float x0 = load_elem(src + i * es, a.q_type);
+            const float x1 = load_elem(src + (i + P) * es, a.q_type);
+            const float y0 = fmaf(x0, c, -(x1 * s));
+            const float y1 = fmaf(x0, s, x1 * c);
+            const int64_t eo = type_elem_bytes(a.q_out_type);
+            char* dst = a.q_out + b * a.qo_nb_b + t * a.qo_nb_t + slot * a.qo_nb_h;
+            store_elem(dst + i * eo, a.q_out_type, y0);
+            store_elem(dst + (i + P) * eo, a.q_out_type, y1);
+        } else {
+            const int hs = slot - nq;
+            const bool is_k = hs < a.Hkv;
+            const int h = is_k ? hs : hs - a.Hkv;
+            const int typ = is_k ? a.k_type : a.v_type;
+            const int64_t es = type_elem_bytes(typ);
+            const char* src = is_k ? a.k + b * a.k_nb_b + t * a.k_nb_t + h * a.k_nb_h
+                                   : a.v + b * a.v_nb_b + t * a.v_nb_t + h * a.v_nb_h;
+            const float x0 = load_elem(src + i * es, typ);
+            const float x1 = load_elem(src + (i + P) * es, typ);
+            float y0 = x0, y1 = x1;
+            if (is_k) {
+                y0 = fmaf(x0, c, -(x1 * s));
+                y1 = fmaf(x0, s, x1 * c);
+            }
+            char* row = (is_k ? a.k_dst[b] : a.v_dst[b]) + t * a.cache_row_bytes + h * a.cache_head_bytes;
+            if (a.cache_type == VVA_TYPE_Q8_0) {
+                store_q8_pair(row, i, P, y0, y1);
+            } else {
+                const int64_t ec = type_elem_bytes(a.cache_type);
+                store_elem(row + i * ec, a.cache_type, y0);
+                store_elem(row + (i + P) * ec, a.cache_type, y1);
+            }
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_rope_append(const RopeAppendArgs& a, hipStream_t s) {
+    if (a.T <= 0 || a.B <= 0) return hipSuccess;
+    dim3 grid(a.T, a.B);
+    hipLaunchKernelGGL(rope_append_kernel, grid, dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace vva

@@ -1,0 +1,573 @@
+// vva.cpp — host side of the C ABI declared in include/vva.h.
+//
+// Owns the context (device + one stream), the resident KV cache slab, input
+// validation and kernel dispatch.  Error conventions follow vibevoice.cpp's
+// public API (include/vibevoice.h:23-33): every call returns a status, the
+// message is kept per context, nothing aborts.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "vva_internal.hpp"
+
+using namespace vva;
+
+struct vva_context {
+    int device = 0;
+    hipStream_t stream = nullptr;        // active stream
+    hipStream_t own_stream = nullptr;    // created by us (destroyed in vva_destroy)
+    std::string err;
+    int n_cu = 256;
+    int attn_path = 0;
+    int last_splits = 0;
+    float* ws = nullptr;                 // decode split partials
+    size_t ws_bytes = 0;
+};
+
+struct vva_kv {
+    vva_context* ctx = nullptr;
+    vva_kv_desc desc{};
+    char* base = nullptr;
+    size_t tensor_bytes = 0;             // one K or V tensor of one (layer, seq)
+    int64_t row_bytes = 0;               // one token row: [Hkv][d]
+    int64_t head_bytes = 0;              // one head row: [d]
+    std::vector<int32_t> len;
+};
+
+namespace {
+
+thread_local std::string g_create_err;
+
+struct DeviceGuard {
+    int prev = -1;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        if (prev != dev) (void)hipSetDevice(dev);
+    }
+    ~DeviceGuard() {
+        int cur = -1;
+        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+    }
+};
+
+vva_status fail(vva_context* ctx, vva_status st, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    if (ctx) ctx->err = buf;
+    else g_create_err = buf;
+    return st;
+}
+
+vva_status hip_fail(vva_context* ctx, hipError_t e, const char* what) {
+    return fail(ctx, e == hipErrorOutOfMemory ? VVA_ERR_OUT_OF_MEMORY : VVA_ERR_DEVICE,
+                "%s: %s", what, hipGetErrorString(e));
+}
+
+bool float_type(int t) { return t == VVA_TYPE_F32 || t == VVA_TYPE_F16 || t == VVA_TYPE_BF16; }
+bool cache_type(int t) { return float_type(t) || t == VVA_TYPE_Q8_0; }
+
+// head_dim constraints shared by every kernel: multiple of 32 (Q8_0 blocks),
+// even halves for NeoX pairs, at most 256 (LDS angle table).
+bool head_dim_ok(int d, int type) {
+    if (d <= 0 || d > 256 || d % 32) return false;
+    if (type == VVA_TYPE_Q8_0 && d % 64) return false;   // two whole blocks per rotation pair group
+    return true;
+}
+
+char* kv_tensor(const vva_kv* kv, int layer, int seq, int which) {
+    const size_t idx = ((size_t)layer * kv->desc.n_seq + seq) * 2 + which;
+    return kv->base + idx * kv->tensor_bytes;
+}
+
+vva_status check_tensor(vva_context* ctx, const vva_tensor* t, const char* name) {
+    if (!t || !t->data) return fail(ctx, VVA_ERR_INVALID_ARG, "%s: null tensor", name);
+    for (int i = 0; i < 4; ++i)
+        if (t->ne[i] < 1) return fail(ctx, VVA_ERR_INVALID_ARG, "%s: ne[%d] = %lld", name, i, (long long)t->ne[i]);
+    return VVA_OK;
+}
+
+vva_status ensure_ws(vva_context* ctx, size_t bytes) {
+    if (bytes <= ctx->ws_bytes) return VVA_OK;
+    if (ctx->ws) {
+        (void)hipStreamSynchronize(ctx->stream);
+        (void)hipFree(ctx->ws);
+        ctx->ws = nullptr;
+        ctx->ws_bytes = 0;
+    }
+    size_t sz = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
+    hipError_t e = hipMalloc(&ctx->ws, sz);
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipMalloc(decode workspace)");
+    ctx->ws_bytes = sz;
+    return VVA_OK;
+}
+
+// Shared by vva_attn and vva_flash_attn_ext once AttnArgs is filled.
+vva_status run_attention(vva_context* ctx, AttnArgs& a) {
+    hipError_t e;
+    ctx->last_splits = 0;
+    if (ctx->attn_path != 1 && a.T == 1 && decode_supported(a)) {
+        const int nw = decode_waves(a);
+        const int R = nw / a.Hkv;
+        const int unit = decode_tokens_per_iter(a) * R;
+        int Lmax = 1;
+        for (int b = 0; b < a.B; ++b) Lmax = a.L[b] > Lmax ? a.L[b] : Lmax;
+        int target = 2 * ctx->n_cu / a.B;
+        if (const char* env = std::getenv("VVA_DECODE_WGS")) target = std::atoi(env) / a.B;
+        if (target < 1) target = 1;
+        int split_len = (Lmax + target - 1) / target;
+        int min_len = 2 * unit;
+        if (const char* env = std::getenv("VVA_DECODE_MIN_SPLIT")) min_len = std::atoi(env);
+        if (split_len < min_len) split_len = min_len;
+        split_len = (split_len + unit - 1) / unit * unit;
+        const int n_splits = (Lmax + split_len - 1) / split_len;
+        if (n_splits > 1) {
+            vva_status st = ensure_ws(ctx, (size_t)n_splits * a.B * a.Hq * (a.d + 2) * sizeof(float));
+            if (st != VVA_OK) return st;
+        }
+        e = launch_decode(a, ctx->ws, n_splits, split_len, ctx->stream);
+        if (e != hipSuccess) return hip_fail(ctx, e, "decode launch");
+        ctx->last_splits = n_splits;
+        return VVA_OK;
+    }
+    if (ctx->attn_path != 1 && a.T > 1 && prefill_supported(a)) {
+        e = launch_prefill(a, ctx->stream);
+        if (e != hipSuccess) return hip_fail(ctx, e, "prefill launch");
+        return VVA_OK;
+    }
+    e = launch_attn_rows(a, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "attention launch");
+    return VVA_OK;
+}
+
+vva_status fill_mask(vva_context* ctx, AttnArgs& a, const vva_tensor* mask, int T, int B, int Lmax) {
+    if (!mask) return VVA_OK;
+    vva_status st = check_tensor(ctx, mask, "mask");
+    if (st != VVA_OK) return st;
+    if (mask->type != VVA_TYPE_F16) return fail(ctx, VVA_ERR_INVALID_ARG, "mask must be F16");
+    if (mask->nb[0] != 2) return fail(ctx, VVA_ERR_INVALID_ARG, "mask rows must be contiguous");
+    if (mask->ne[0] < Lmax || mask->ne[1] < T)
+        return fail(ctx, VVA_ERR_INVALID_ARG, "mask ne=[%lld,%lld] smaller than [L=%d,T=%d]",
+                    (long long)mask->ne[0], (long long)mask->ne[1], Lmax, T);
+    if (mask->ne[2] != 1) return fail(ctx, VVA_ERR_NOT_IMPLEMENTED, "per-head masks are not supported");
+    if (mask->ne[3] != 1 && mask->ne[3] != B)
+        return fail(ctx, VVA_ERR_INVALID_ARG, "mask ne[3] must be 1 or B");
+    a.mask = (const char*)mask->data;
+    a.mask_nb_row = (int64_t)mask->nb[1];
+    a.mask_nb_b = mask->ne[3] == 1 ? 0 : (int64_t)mask->nb[3];
+    a.mask_mode = kMaskExplicit;
+    return VVA_OK;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ context
+
+extern "C" vva_status vva_create(int device, void* stream, vva_context** out) {
+    if (!out) return fail(nullptr, VVA_ERR_INVALID_ARG, "out is null");
+    *out = nullptr;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n == 0) return fail(nullptr, VVA_ERR_DEVICE, "no HIP device available");
+    if (device < 0 || device >= n) return fail(nullptr, VVA_ERR_INVALID_ARG, "device %d out of range", device);
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess) return fail(nullptr, VVA_ERR_DEVICE, "hipGetDeviceProperties failed");
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(nullptr, VVA_ERR_NOT_IMPLEMENTED, "kernels are built for gfx950, device is %s", prop.gcnArchName);
+    DeviceGuard g(device);
+    auto* ctx = new vva_context();
+    ctx->device = device;
+    ctx->n_cu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+    if (stream) {
+        ctx->stream = (hipStream_t)stream;
+    } else {
+        e = hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking);
+        if (e != hipSuccess) { delete ctx; return fail(nullptr, VVA_ERR_DEVICE, "hipStreamCreate failed"); }
+        ctx->stream = ctx->own_stream;
+    }
+    *out = ctx;
+    return VVA_OK;
+}
+
+extern "C" void vva_destroy(vva_context* ctx) {
+    if (!ctx) return;
+    DeviceGuard g(ctx->device);
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->ws) (void)hipFree(ctx->ws);
+    if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
+    delete ctx;
+}
+
+extern "C" vva_status vva_set_stream(vva_context* ctx, void* stream) {
+    if (!ctx) return VVA_ERR_INVALID_ARG;
+    DeviceGuard g(ctx->device);
+    if (!stream && !ctx->own_stream) {
+        hipError_t e = hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking);
+        if (e != hipSuccess) return hip_fail(ctx, e, "hipStreamCreate");
+    }
+    ctx->stream = stream ? (hipStream_t)stream : ctx->own_stream;
+    return VVA_OK;
+}
+
+extern "C" vva_status vva_synchronize(vva_context* ctx) {
+    if (!ctx) return VVA_ERR_INVALID_ARG;
+    DeviceGuard g(ctx->device);
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    return e == hipSuccess ? VVA_OK : hip_fail(ctx, e, "hipStreamSynchronize");
+}
+
+extern "C" const char* vva_last_error(const vva_context* ctx) {
+    return ctx ? ctx->err.c_str() : g_create_err.c_str();
+}
+
+extern "C" const char* vva_version(void) { return "vva 0.1.0 (gfx950)"; }
+
+extern "C" vva_status vva_set_attn_path(vva_context* ctx, int path) {
+    if (!ctx || path < 0 || path > 1) return VVA_ERR_INVALID_ARG;
+    ctx->attn_path = path;
+    return VVA_OK;
+}
+
+extern "C" int vva_last_decode_splits(const vva_context* ctx) { return ctx ? ctx->last_splits : 0; }
+
+// ----------------------------------------------------------------- KV cache
+
+extern "C" vva_status vva_kv_create(vva_context* ctx, const vva_kv_desc* d, vva_kv** out) {
+    if (!ctx) return VVA_ERR_INVALID_ARG;
+    if (!d || !out) return fail(ctx, VVA_ERR_INVALID_ARG, "kv_create: null argument");
+    *out = nullptr;
+    if (d->n_layers < 1 || d->n_kv_heads < 1 || d->max_seq < 1 || d->n_seq < 1 || d->n_seq > 1024)
+        return fail(ctx, VVA_ERR_INVALID_ARG, "kv_create: bad sizes");
+    if (!cache_type(d->type)) return fail(ctx, VVA_ERR_INVALID_ARG, "kv_create: unsupported type %d", d->type);
+    if (!head_dim_ok(d->head_dim, d->type))
+        return fail(ctx, VVA_ERR_NOT_IMPLEMENTED, "kv_create: head_dim %d unsupported for type %d", d->head_dim, d->type);
+    DeviceGuard g(ctx->device);
+    auto* kv = new vva_kv();
+    kv->ctx = ctx;
+    kv->desc = *d;
+    kv->head_bytes = type_row_bytes(d->type, d->head_dim);
+    kv->row_bytes = kv->head_bytes * d->n_kv_heads;
+    kv->tensor_bytes = ((size_t)kv->row_bytes * d->max_seq + 255) / 256 * 256;
+    const size_t total = kv->tensor_bytes * 2 * (size_t)d->n_layers * d->n_seq;
+    hipError_t e = hipMalloc(&kv->base, total);
+    if (e != hipSuccess) { delete kv; return hip_fail(ctx, e, "kv_create: hipMalloc"); }
+    e = hipMemsetAsync(kv->base, 0, total, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) { (void)hipFree(kv->base); delete kv; return hip_fail(ctx, e, "kv_create: memset"); }
+    kv->len.assign(d->n_seq, 0);
+    *out = kv;
+    return VVA_OK;
+}
+
+extern "C" void vva_kv_free(vva_kv* kv) {
+    if (!kv) return;
+    DeviceGuard g(kv->ctx->device);
+    (void)hipStreamSynchronize(kv->ctx->stream);
+    (void)hipFree(kv->base);
+    delete kv;
+}
+
+extern "C" vva_status vva_kv_get_len(const vva_kv* kv, int seq, int32_t* len) {
+    if (!kv || !len || seq < 0 || seq >= kv->desc.n_seq) return VVA_ERR_INVALID_ARG;
+    *len = kv->len[seq];
+    return VVA_OK;
+}
+
+extern "C" vva_status vva_kv_set_len(vva_kv* kv, int seq, int32_t len) {
+    if (!kv || seq < 0 || seq >= kv->desc.n_seq || len < 0 || len > kv->desc.max_seq) return VVA_ERR_INVALID_ARG;
+    kv->len[seq] = len;
+    return VVA_OK;
+}
+
+extern "C" vva_status vva_kv_view(const vva_kv* kv, int layer, int seq, vva_tensor* k, vva_tensor* v) {
+    if (!kv || layer < 0 || layer >= kv->desc.n_layers || seq < 0 || seq >= kv->desc.n_seq)
+        return VVA_ERR_INVALID_ARG;
+    for (int which = 0; which < 2; ++which) {
+        vva_tensor* t = which == 0 ? k : v;
+        if (!t) continue;
+        t->data = kv_tensor(kv, layer, seq, which);
+        t->type = kv->desc.type;
+        t->ne[0] = kv->desc.head_dim;
+        t->ne[1] = kv->desc.n_kv_heads;
+        t->ne[2] = kv->desc.max_seq;
+        t->ne[3] = 1;
+        t->nb[0] = (size_t)type_elem_bytes(kv->desc.type);
+        t->nb[1] = (size_t)kv->head_bytes;
+        t->nb[2] = (size_t)kv->row_bytes;
+        t->nb[3] = (size_t)kv->row_bytes * kv->desc.max_seq;
+    }
+    return VVA_OK;
+}
+
+extern "C" vva_status vva_kv_upload(vva_context* ctx, vva_kv* kv, int layer, int seq, int32_t start,
+                                    int32_t len, const float* k_host, const float* v_host) {
+    if (!ctx) return VVA_ERR_INVALID_ARG;
+    if (!kv || layer < 0 || layer >= kv->desc.n_layers || seq < 0 || seq >= kv->desc.n_seq)
+        return fail(ctx, VVA_ERR_INVALID_ARG, "kv_upload: bad cache / layer / seq");
+    if (start < 0 || len < 0 || (int64_t)start + len > kv->desc.max_seq)
+        return fail(ctx, VVA_ERR_INVALID_ARG, "kv_upload: rows [%d,%d) outside max_seq %d", start, start + len,
+                    kv->desc.max_seq);
+    if (len == 0) return VVA_OK;
+    if (!k_host || !v_host) return fail(ctx, VVA_ERR_INVALID_ARG, "kv_upload: null host rows");
+    DeviceGuard g(ctx->device);
+    // Stage the F32 rows on the device and convert with the append kernel
+    // (no rotation: positions are irrelevant for V, and K rows of a voice
+    // prompt are stored post-RoPE, scripts/convert_voice_to_gguf.py:115-128).
+    const int d = kv->desc.head_dim, H = kv->desc.n_kv_heads;
+    const size_t n = (size_t)len * H * d;
+    float* dev = nullptr;
+    hipError_t e = hipMalloc(&dev, 2 * n * sizeof(float));
+    if (e != hipSuccess) return hip_fail(ctx, e, "kv_upload: hipMalloc");
+    e = hipMemcpyAsync(dev, k_host, n * sizeof(float), hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(dev + n, v_host, n * sizeof(float), hipMemcpyHostToDevice, ctx->stream);
+    int32_t* zero_pos = nullptr;
+    if (e == hipSuccess) e = hipMalloc(&zero_pos, sizeof(int32_t) * len);
+    if (e == hipSuccess) e = hipMemsetAsync(zero_pos, 0, sizeof(int32_t) * len, ctx->stream);
+    if (e == hipSuccess) {
+        RopeAppendArgs a{};
+        a.k = (const char*)dev;
+        a.v = (const char*)(dev + n);
+        a.k_type = a.v_type = VVA_TYPE_F32;
+        a.k_nb_h = a.v_nb_h = (int64_t)d * 4;
+        a.k_nb_t = a.v_nb_t = (int64_t)H * d * 4;
+        a.k_nb_b = a.v_nb_b = 0;
+        a.pos = zero_pos;              // position 0: the rotation is the identity
+        a.pos_stride_b = 0;
+        a.k_dst[0] = kv_tensor(kv, layer, seq, 0) + (int64_t)start * kv->row_bytes;
+        a.v_dst[0] = kv_tensor(kv, layer, seq, 1) + (int64_t)start * kv->row_bytes;
+        a.cache_row_bytes = kv->row_bytes;
+        a.cache_head_bytes = kv->head_bytes;
+        a.cache_type = kv->desc.type;
+        a.d = d; a.Hq = 0; a.Hkv = H; a.T = len; a.B = 1;
+        a.do_q = 0; a.do_kv = 1;
+        a.theta_scale = 1.0f;
+        e = launch_rope_append(a, ctx->stream);
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    (void)hipFree(dev);
+    if (zero_pos) (void)hipFree(zero_pos);
+    return e == hipSuccess ? VVA_OK : hip_fail(ctx, e, "kv_upload");
+}
+
+// ---------------------------------------------------------------------- ops
+
+namespace {
+
+// Validates x/dst for RoPE: ne = [d, H, T, B], float types, contiguous rows.
+vva_status check_rows(vva_context* ctx, const vva_tensor* t, const char* name, int64_t d, int64_t H,
+                      int64_t T, int64_t B) {
+    vva_status st = check_tensor(ctx, t, name);
+    if (st != VVA_OK) return st;
+    if (!float_type(t->type)) return fail(ctx, VVA_ERR_INVALID_ARG, "%s: type %d not F32/F16/BF16", name, t->type);
+    if ((int64_t)t->nb[0] != type_elem_bytes(t->type))
+        return fail(ctx, VVA_ERR_INVALID_ARG, "%s: rows must be contiguous (nb[0])", name);
+    if (t->ne[0] != d || (H > 0 && t->ne[1] != H) || t->ne[2] != T || t->ne[3] != B)
+        return fail(ctx, VVA_ERR_INVALID_ARG, "%s: ne=[%lld,%lld,%lld,%lld] expected [%lld,%lld,%lld,%lld]", name,
+                    (long long)t->ne[0], (long long)t->ne[1], (long long)t->ne[2], (long long)t->ne[3],
+                    (long long)d, (long long)H, (long long)T, (long long)B);
+    return VVA_OK;
+}
+
+vva_status check_pos(vva_context* ctx, const vva_tensor* pos, int64_t T, int64_t B, int64_t* stride_b) {
+    vva_status st = check_tensor(ctx, pos, "pos");
+    if (st != VVA_OK) return st;
+    if (pos->type != VVA_TYPE_I32 || pos->nb[0] != 4) return fail(ctx, VVA_ERR_INVALID_ARG, "pos must be contiguous I32");
+    if (pos->ne[0] != T) return fail(ctx, VVA_ERR_INVALID_ARG, "pos ne[0]=%lld != T=%lld", (long long)pos->ne[0], (long long)T);
+    if (pos->ne[1] != 1 && pos->ne[1] != B) return fail(ctx, VVA_ERR_INVALID_ARG, "pos ne[1] must be 1 or B");
+    if (pos->nb[1] % 4) return fail(ctx, VVA_ERR_INVALID_ARG, "pos nb[1] misaligned");
+    *stride_b = (pos->ne[1] == 1) ? 0 : (int64_t)(pos->nb[1] / 4);
+    return VVA_OK;
+}
+
+}  // namespace
+
+extern "C" vva_status vva_rope_ext(vva_context* ctx, const vva_tensor* x, const vva_tensor* pos, int n_dims,
+                                   int mode, float freq_base, const vva_tensor* dst) {
+    if (!ctx) return VVA_ERR_INVALID_ARG;
+    if (mode != VVA_ROPE_TYPE_NEOX) return fail(ctx, VVA_ERR_NOT_IMPLEMENTED, "rope: only NEOX mode");
+    vva_status st = check_tensor(ctx, x, "x");
+    if (st != VVA_OK) return st;
+    const int64_t d = x->ne[0], H = x->ne[1], T = x->ne[2], B = x->ne[3];
+    if (n_dims != d) return fail(ctx, VVA_ERR_NOT_IMPLEMENTED, "rope: n_dims must equal ne[0]");
+    if (!head_dim_ok((int)d, VVA_TYPE_F32)) return fail(ctx, VVA_ERR_NOT_IMPLEMENTED, "rope: head dim %lld", (long long)d);
+    if (B > VVA_MAX_BATCH) return fail(ctx, VVA_ERR_INVALID_ARG, "rope: B > %d", VVA_MAX_BATCH);
+    if ((st = check_rows(ctx, x, "x", d, H, T, B)) != VVA_OK) return st;
+    if ((st = check_rows(ctx, dst, "dst", d, H, T, B)) != VVA_OK) return st;
+    int64_t ps = 0;
+    if ((st = check_pos(ctx, pos, T, B, &ps)) != VVA_OK) return st;
+    DeviceGuard g(ctx->device);
+    RopeAppendArgs a{};
+    a.q = (const char*)x->data; a.q_type = x->type;
+    a.q_nb_h = x->nb[1]; a.q_nb_t = x->nb[2]; a.q_nb_b = x->nb[3];
+    a.q_out = (char*)dst->data; a.q_out_type = dst->type;
+    a.qo_nb_h = dst->nb[1]; a.qo_nb_t = dst->nb[2]; a.qo_nb_b = dst->nb[3];
+    a.pos = (const int32_t*)pos->data; a.pos_stride_b = ps;
+    a.d = (int)d; a.Hq = (int)H; a.Hkv = 0; a.T = (int)T; a.B = (int)B;
+    a.do_q = 1; a.do_kv = 0;
+    a.theta_scale = powf(freq_base, -2.0f / (float)n_dims);
+    hipError_t e = launch_rope_append(a, ctx->stream);
+    return e == hipSuccess ? VVA_OK : hip_fail(ctx, e, "rope launch");
+}
+
+extern "C" vva_status vva_rope_append(vva_context* ctx, vva_kv* kv, int layer, const vva_tensor* q,
+                                      const vva_tensor* k, const vva_tensor* v, const vva_tensor* pos,
+                                      const int32_t* seq_ids, float freq_base, const vva_tensor* q_out) {
+    if (!ctx) return VVA_ERR_INVALID_ARG;
+    if (!kv || kv->ctx == nullptr) return fail(ctx, VVA_ERR_INVALID_ARG, "rope_append: null cache");
+    if (layer < 0 || layer >= kv->desc.n_layers) return fail(ctx, VVA_ERR_INVALID_ARG, "rope_append: layer %d", layer);
+    vva_status st = check_tensor(ctx, q, "q");
+    if (st != VVA_OK) return st;
+    const int64_t d = kv->desc.head_dim, Hkv = kv->desc.n_kv_heads;
+    const int64_t Hq = q->ne[1], T = q->ne[2], B = q->ne[3];
+    if (Hq % Hkv) return fail(ctx, VVA_ERR_INVALID_ARG, "rope_append: Hq %% Hkv != 0");
+    if (B > VVA_MAX_BATCH) return fail(ctx, VVA_ERR_INVALID_ARG, "rope_append: B > %d", VVA_MAX_BATCH);
+    if ((st = check_rows(ctx, q, "q", d, Hq, T, B)) != VVA_OK) return st;
+    if ((st = check_rows(ctx, k, "k", d, Hkv, T, B)) != VVA_OK) return st;
+    if ((st = check_rows(ctx, v, "v", d, Hkv, T, B)) != VVA_OK) return st;
+    if ((st = check_rows(ctx, q_out, "q_out", d, Hq, T, B)) != VVA_OK) return st;
+    int64_t ps = 0;
+    if ((st = check_pos(ctx, pos, T, B, &ps)) != VVA_OK) return st;
+    RopeAppendArgs a{};
+    for (int b = 0; b < B; ++b) {
+        const int seq = seq_ids ? seq_ids[b] : b;
+        if (seq < 0 || seq >= kv->desc.n_seq) return fail(ctx, VVA_ERR_INVALID_ARG, "rope_append: seq %d", seq);
+        for (int b2 = 0; b2 < b; ++b2)
+            if ((seq_ids ? seq_ids[b2] : b2) == seq)
+                return fail(ctx, VVA_ERR_INVALID_ARG, "rope_append: sequence %d appears twice", seq);
+        const int64_t past = kv->len[seq];
+        if (past + T > kv->desc.max_seq)
+            return fail(ctx, VVA_ERR_INVALID_ARG, "rope_append: seq %d: %lld + %lld rows exceed max_seq %d", seq,
+                        (long long)past, (long long)T, kv->desc.max_seq);
+        a.k_dst[b] = kv_tensor(kv, layer, seq, 0) + past * kv->row_bytes;
+        a.v_dst[b] = kv_tensor(kv, layer, seq, 1) + past * kv->row_bytes;
+    }
+    DeviceGuard g(ctx->device);
+    a.q = (const char*)q->data; a.q_type = q->type;
+    a.q_nb_h = q->nb[1]; a.q_nb_t = q->nb[2]; a.q_nb_b = q->nb[3];
+    a.k = (const char*)k->data; a.k_type = k->type;
+    a.k_nb_h = k->nb[1]; a.k_nb_t = k->nb[2]; a.k_nb_b = k->nb[3];
+    a.v = (const char*)v->data; a.v_type = v->type;
+    a.v_nb_h = v->nb[1]; a.v_nb_t = v->nb[2]; a.v_nb_b = v->nb[3];
+    a.q_out = (char*)q_out->data; a.q_out_type = q_out->type;
+    a.qo_nb_h = q_out->nb[1]; a.qo_nb_t = q_out->nb[2]; a.qo_nb_b = q_out->nb[3];
+    a.pos = (const int32_t*)pos->data; a.pos_stride_b = ps;
+    a.cache_row_bytes = kv->row_bytes;
+    a.cache_head_bytes = kv->head_bytes;
+    a.cache_type = kv->desc.type;
+    a.d = (int)d; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.T = (int)T; a.B = (int)B;
+    a.do_q = 1; a.do_kv = 1;
+    a.theta_scale = powf(freq_base, -2.0f / (float)d);
+    hipError_t e = launch_rope_append(a, ctx->stream);
+    return e == hipSuccess ? VVA_OK : hip_fail(ctx, e, "rope_append launch");
+}
+
+extern "C" vva_status vva_attn(vva_context* ctx, const vva_kv* kv, int layer, const vva_tensor* q,
+                               const int32_t* seq_ids, const vva_tensor* mask, float scale, const vva_tensor* out) {
+    if (!ctx) return VVA_ERR_INVALID_ARG;
+    if (!kv) return fail(ctx, VVA_ERR_INVALID_ARG, "attn: null cache");
+    if (layer < 0 || layer >= kv->desc.n_layers) return fail(ctx, VVA_ERR_INVALID_ARG, "attn: layer %d", layer);
+    vva_status st = check_tensor(ctx, q, "q");
+    if (st != VVA_OK) return st;
+    const int64_t d = kv->desc.head_dim, Hkv = kv->desc.n_kv_heads;
+    const int64_t Hq = q->ne[1], T = q->ne[2], B = q->ne[3];
+    if (Hq % Hkv) return fail(ctx, VVA_ERR_INVALID_ARG, "attn: Hq %% Hkv != 0");
+    if (B > VVA_MAX_BATCH) return fail(ctx, VVA_ERR_INVALID_ARG, "attn: B > %d", VVA_MAX_BATCH);
+    if ((st = check_rows(ctx, q, "q", d, Hq, T, B)) != VVA_OK) return st;
+    if ((st = check_rows(ctx, out, "out", d, Hq, T, B)) != VVA_OK) return st;
+    if (out->type != VVA_TYPE_F32) return fail(ctx, VVA_ERR_INVALID_ARG, "attn: out must be F32");
+    AttnArgs a{};
+    int Lmax = 0;
+    for (int b = 0; b < B; ++b) {
+        const int seq = seq_ids ? seq_ids[b] : b;
+        if (seq < 0 || seq >= kv->desc.n_seq) return fail(ctx, VVA_ERR_INVALID_ARG, "attn: seq %d", seq);
+        const int64_t past = kv->len[seq];
+        if (past + T > kv->desc.max_seq)
+            return fail(ctx, VVA_ERR_INVALID_ARG, "attn: seq %d window %lld exceeds max_seq", seq, (long long)(past + T));
+        a.k[b] = kv_tensor(kv, layer, seq, 0);
+        a.v[b] = kv_tensor(kv, layer, seq, 1);
+        a.L[b] = (int)(past + T);
+        a.past[b] = (int)past;
+        Lmax = a.L[b] > Lmax ? a.L[b] : Lmax;
+    }
+    a.q = (const char*)q->data; a.q_type = q->type;
+    a.q_nb_h = q->nb[1]; a.q_nb_t = q->nb[2]; a.q_nb_b = q->nb[3];
+    a.k_nb_tok = a.v_nb_tok = kv->row_bytes;
+    a.k_nb_head = a.v_nb_head = kv->head_bytes;
+    a.k_type = a.v_type = kv->desc.type;
+    a.mask_mode = kMaskCausal;
+    if ((st = fill_mask(ctx, a, mask, (int)T, (int)B, Lmax)) != VVA_OK) return st;
+    a.scale = scale;
+    a.out = (float*)out->data;
+    a.o_nb_h = out->nb[1]; a.o_nb_t = out->nb[2]; a.o_nb_b = out->nb[3];
+    a.d = (int)d; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.T = (int)T; a.B = (int)B;
+    DeviceGuard g(ctx->device);
+    return run_attention(ctx, a);
+}
+
+extern "C" vva_status vva_flash_attn_ext(vva_context* ctx, const vva_tensor* q, const vva_tensor* k,
+                                         const vva_tensor* v, const vva_tensor* mask, float scale, float max_bias,
+                                         float logit_softcap, const vva_tensor* dst) {
+    if (!ctx) return VVA_ERR_INVALID_ARG;
+    if (max_bias != 0.0f || logit_softcap != 0.0f)
+        return fail(ctx, VVA_ERR_NOT_IMPLEMENTED, "flash_attn_ext: max_bias / logit_softcap must be 0");
+    vva_status st;
+    if ((st = check_tensor(ctx, q, "q")) != VVA_OK) return st;
+    if ((st = check_tensor(ctx, k, "k")) != VVA_OK) return st;
+    if ((st = check_tensor(ctx, v, "v")) != VVA_OK) return st;
+    if ((st = check_tensor(ctx, dst, "dst")) != VVA_OK) return st;
+    const int64_t d = q->ne[0], T = q->ne[1], Hq = q->ne[2], B = q->ne[3];
+    const int64_t L = k->ne[1], Hkv = k->ne[2];
+    if (!float_type(q->type) || (int64_t)q->nb[0] != type_elem_bytes(q->type))
+        return fail(ctx, VVA_ERR_INVALID_ARG, "q: F32/F16/BF16 with contiguous rows");
+    if (!cache_type(k->type) || !cache_type(v->type)) return fail(ctx, VVA_ERR_INVALID_ARG, "k/v: unsupported type");
+    if (!head_dim_ok((int)d, k->type) || !head_dim_ok((int)d, v->type))
+        return fail(ctx, VVA_ERR_NOT_IMPLEMENTED, "head dim %lld unsupported", (long long)d);
+    if (k->ne[0] != d || v->ne[0] != d || v->ne[1] != L || v->ne[2] != Hkv)
+        return fail(ctx, VVA_ERR_INVALID_ARG, "k/v shapes do not match q");
+    if ((int64_t)k->nb[0] != type_elem_bytes(k->type) || (int64_t)v->nb[0] != type_elem_bytes(v->type))
+        return fail(ctx, VVA_ERR_INVALID_ARG, "k/v rows must be contiguous");
+    if (Hq % Hkv) return fail(ctx, VVA_ERR_INVALID_ARG, "Hq %% Hkv != 0");
+    if ((k->ne[3] != 1 && k->ne[3] != B) || (v->ne[3] != 1 && v->ne[3] != B))
+        return fail(ctx, VVA_ERR_INVALID_ARG, "k/v ne[3] must be 1 or B");
+    if (B > VVA_MAX_BATCH) return fail(ctx, VVA_ERR_INVALID_ARG, "B > %d", VVA_MAX_BATCH);
+    if (dst->type != VVA_TYPE_F32 || dst->nb[0] != 4 || dst->ne[0] != d || dst->ne[1] != Hq || dst->ne[2] != T ||
+        dst->ne[3] != B)
+        return fail(ctx, VVA_ERR_INVALID_ARG, "dst must be F32 ne=[d,Hq,T,B]");
+    AttnArgs a{};
+    for (int b = 0; b < B; ++b) {
+        a.k[b] = (const char*)k->data + (k->ne[3] == 1 ? 0 : b * (int64_t)k->nb[3]);
+        a.v[b] = (const char*)v->data + (v->ne[3] == 1 ? 0 : b * (int64_t)v->nb[3]);
+        a.L[b] = (int)L;
+        a.past[b] = (int)(L - T);
+    }
+    a.q = (const char*)q->data; a.q_type = q->type;
+    a.q_nb_t = q->nb[1]; a.q_nb_h = q->nb[2]; a.q_nb_b = q->nb[3];
+    a.k_nb_tok = k->nb[1]; a.k_nb_head = k->nb[2];
+    a.v_nb_tok = v->nb[1]; a.v_nb_head = v->nb[2];
+    a.k_type = k->type; a.v_type = v->type;
+    a.mask_mode = kMaskNone;
+    if ((st = fill_mask(ctx, a, mask, (int)T, (int)B, (int)L)) != VVA_OK) return st;
+    a.scale = scale;
+    a.out = (float*)dst->data;
+    a.o_nb_h = dst->nb[1]; a.o_nb_t = dst->nb[2]; a.o_nb_b = dst->nb[3];
+    a.d = (int)d; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.T = (int)T; a.B = (int)B;
+    DeviceGuard g(ctx->device);
+    return run_attention(ctx, a);
+}
+
+extern "C" int vva_supports(const vva_context* ctx, int head_dim, int n_q_heads, int n_kv_heads, int q_type,
+                            int kv_type) {
+    if (!ctx) return 0;
+    if (n_kv_heads < 1 || n_q_heads < 1 || n_q_heads % n_kv_heads) return 0;
+    if (!float_type(q_type) || !cache_type(kv_type)) return 0;
+    return head_dim_ok(head_dim, kv_type) ? 1 : 0;
+}
