@@ -1,0 +1,274 @@
+#!/usr/bin/env python3
+"""Benchmark of the Qwen2 attention path on one MI355X.
+
+Workloads (synthetic, seeded):
+  prefill  Qwen2.5-7B attention (28 q heads / 4 kv heads, head_dim 128),
+           causal prefill of 32768 tokens through all 28 layers: per layer the
+           fused RoPE + KV append (bf16 Q/K/V in, F16 cache, theta 1e6) and the
+           MFMA flash prefill.  One step = 28 layers.
+           Throughput = 4 * Hq * d * sum_i (i + 1) FLOP per layer.
+  decode   ASR transcript decode with CFG-style batch 2: 7B heads, one new
+           token per step per stream, Q8_0 caches pre-filled to 32768
+           positions, 28 layers (each with its own 2 x 71 MB of cache, 2 GB in
+           all, so the 256 MB MALL cannot hold it).  One step = 28 layers of
+           RoPE + append + split-K decode.
+           Attention bytes per layer-step = K/V cache rows read (2 streams x L
+           x Hkv x 2 x 136 B) + f32 Q read + f32 O write; the whole-step rate
+           also counts the RoPE + append traffic.
+
+Prints one JSON line: `value` is the prefill throughput (TFLOP/s), `decode`
+holds the decode throughput (GB/s); each carries a roofline entry measured
+with HIP events around every attention launch on the library's stream.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "vibevoice.cpp_amd"))
+sys.path.insert(0, os.path.join(REPO, "oracle"))
+
+PEAK_F16_TFLOPS = 2500.0     # MI355X dense fp16/bf16 MFMA
+PEAK_HBM_GBS = 8000.0        # MI355X HBM3E
+
+D, HQ, HKV, LAYERS = 128, 28, 4, 28
+T_PREFILL = 32768
+L_DECODE = 32768
+B_DECODE = 2
+THETA = 1.0e6
+
+
+def prefill_flops_per_layer(T: int, past: int = 0) -> float:
+    # 2 * d for QK^T and 2 * d for PV per visible (query, key) pair
+    return 4.0 * HQ * D * (T * past + T * (T + 1) / 2)
+
+
+def decode_attn_bytes(lens) -> float:
+    """Attention launch: K and V cache rows of every stream + f32 Q read + f32 O write."""
+    q8_row = (D // 32) * 34
+    return sum(L * HKV * 2 * q8_row for L in lens) + 2 * len(lens) * HQ * D * 4
+
+
+def decode_append_bytes(B: int) -> float:
+    """RoPE + append launch: f32 q, k, v read, f32 rotated q written, Q8_0 K and V rows written."""
+    return B * ((HQ + 2 * HKV) * D * 4 + HQ * D * 4 + 2 * HKV * (D // 32) * 34)
+
+
+def run_prefill(torch, vva, ctx, steps: int, warmup: int):
+    rng = torch.Generator(device="cuda").manual_seed(1234)
+    q = torch.randn((1, T_PREFILL, HQ, D), generator=rng, device="cuda").to(torch.bfloat16)
+    k = torch.randn((1, T_PREFILL, HKV, D), generator=rng, device="cuda").to(torch.bfloat16)
+    v = torch.randn((1, T_PREFILL, HKV, D), generator=rng, device="cuda").to(torch.bfloat16)
+    pos = torch.arange(T_PREFILL, dtype=torch.int32, device="cuda")
+    qr = torch.empty((1, T_PREFILL, HQ, D), dtype=torch.float16, device="cuda")
+    out = torch.empty((1, T_PREFILL, HQ, D), dtype=torch.float32, device="cuda")
+    kv = vva.KVCache(ctx, LAYERS, HKV, D, T_PREFILL, 1, vva.F16)
+    scale = D ** -0.5
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(LAYERS * steps)]
+
+    def step(events=None):
+        kv.set_len(0, 0)
+        for layer in range(LAYERS):
+            ctx.rope_append(kv, layer, q, k, v, pos, qr, freq_base=THETA)
+            if events is not None:
+                events[layer][0].record()
+            ctx.attn(kv, layer, qr, out, scale)
+            if events is not None:
+                events[layer][1].record()
+        kv.set_len(0, T_PREFILL)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(steps):
+        step(ev[s * LAYERS:(s + 1) * LAYERS])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    attn_ms = float(np.mean([a.elapsed_time(b) for a, b in ev]))
+    flops_layer = prefill_flops_per_layer(T_PREFILL)
+    res = {
+        "ms_per_step": wall * 1e3 / steps,
+        "tflops": flops_layer * LAYERS * steps / wall / 1e12,
+        "attn_ms": attn_ms,
+        "attn_tflops": flops_layer / (attn_ms * 1e-3) / 1e12,
+        "flops_per_layer": flops_layer,
+    }
+    return res, kv, qr, out
+
+
+def run_decode(torch, vva, ctx, steps: int, warmup: int):
+    rng = torch.Generator(device="cuda").manual_seed(4321)
+    kv = vva.KVCache(ctx, LAYERS, HKV, D, L_DECODE + steps + warmup + 8, B_DECODE, vva.Q8_0)
+    # fill every layer's caches by appending 32768 random rows (RoPE'd K, raw V)
+    chunk = 8192
+    for layer in range(LAYERS):
+        for c0 in range(0, L_DECODE, chunk):
+            for s in range(B_DECODE):
+                kv.set_len(s, c0)
+            kk = torch.randn((B_DECODE, chunk, HKV, D), generator=rng, device="cuda")
+            vv = torch.randn((B_DECODE, chunk, HKV, D), generator=rng, device="cuda")
+            qq = torch.empty((B_DECODE, chunk, 1 * HKV, D), device="cuda")
+            pos = torch.arange(c0, c0 + chunk, dtype=torch.int32, device="cuda")
+            ctx.rope_append(kv, layer, qq, kk, vv, pos, qq, freq_base=THETA)
+    torch.cuda.synchronize()
+    for s in range(B_DECODE):
+        kv.set_len(s, L_DECODE)
+    q = torch.randn((B_DECODE, 1, HQ, D), generator=rng, device="cuda")
+    k = torch.randn((B_DECODE, 1, HKV, D), generator=rng, device="cuda")
+    v = torch.randn((B_DECODE, 1, HKV, D), generator=rng, device="cuda")
+    qr = torch.empty_like(q)
+    out = torch.empty((B_DECODE, 1, HQ, D), dtype=torch.float32, device="cuda")
+    scale = D ** -0.5
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(LAYERS * steps)]
+    lens_timed = []
+
+    def step(events=None):
+        cur = kv.get_len(0)
+        pos = torch.full((B_DECODE, 1), cur, dtype=torch.int32, device="cuda")
+        for layer in range(LAYERS):
+            ctx.rope_append(kv, layer, q, k, v, pos, qr, freq_base=THETA)
+            if events is not None:
+                events[layer][0].record()
+            ctx.attn(kv, layer, qr, out, scale)
+            if events is not None:
+                events[layer][1].record()
+        for s in range(B_DECODE):
+            kv.set_len(s, cur + 1)
+        return cur + 1
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(steps):
+        lens_timed.append(step(ev[s * LAYERS:(s + 1) * LAYERS]))
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    attn_us = float(np.mean([a.elapsed_time(b) for a, b in ev])) * 1e3
+    bytes_total = sum(decode_attn_bytes([L] * B_DECODE) + decode_append_bytes(B_DECODE)
+                      for L in lens_timed) * LAYERS
+    mean_L = float(np.mean(lens_timed))
+    bytes_layer = decode_attn_bytes([mean_L] * B_DECODE)
+    kv_bytes_layer = B_DECODE * mean_L * HKV * 2 * (D // 32) * 34
+    res = {
+        "ms_per_step": wall * 1e3 / steps,
+        "gbs": bytes_total / wall / 1e9,
+        "attn_us": attn_us,
+        "attn_gbs": bytes_layer / (attn_us * 1e-6) / 1e9,
+        "bytes_per_layer": bytes_layer,
+        "kv_bytes_per_layer": kv_bytes_layer,
+        "splits": ctx.last_decode_splits(),
+        "mean_L": mean_L,
+    }
+    return res, kv
+
+
+def cpu_baseline_prefill(torch, vva, vvo, kv, qr):
+    """Oracle (ggml-order mode, all host cores) on layer 0: 256 query rows spread over [0, 32k)."""
+    rows = np.linspace(0, T_PREFILL - 1, 256).astype(np.int32)
+    kraw, vraw = kv.download(0, 0, T_PREFILL)
+    q32 = qr.float().cpu().numpy()
+    t0 = time.perf_counter()
+    vvo.attn(q32, [kraw.reshape(-1)], [vraw.reshape(-1)], vvo.F16, vvo.F16, [T_PREFILL], n_kv_heads=HKV,
+             scale=D ** -0.5, mode=vvo.GGML, rows=rows)
+    dt = time.perf_counter() - t0
+    flops = float(sum(4.0 * HQ * D * (int(r) + 1) for r in rows))
+    return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": vvo.n_cores(), "kind": "port",
+            "sample": f"1 layer, 256 query rows spread over [0,{T_PREFILL}) x {HQ} heads, "
+                      f"ggml-order oracle (F16 K/V), {dt:.1f} s"}
+
+
+def cpu_baseline_decode(torch, vva, vvo, kv):
+    """Oracle (ggml-order mode, Q8_0 integer dots) on 2 layers x 1 decode step of both streams."""
+    rng = np.random.default_rng(9)
+    L = kv.get_len(0)
+    caches = [kv.download(layer, s, L) for layer in range(2) for s in range(B_DECODE)]
+    q = rng.standard_normal((B_DECODE, 1, HQ, D)).astype(np.float32)
+    t0 = time.perf_counter()
+    for layer in range(2):
+        ks = [caches[layer * B_DECODE + s][0].reshape(-1) for s in range(B_DECODE)]
+        vs = [caches[layer * B_DECODE + s][1].reshape(-1) for s in range(B_DECODE)]
+        vvo.attn(q, ks, vs, vvo.Q8_0, vvo.Q8_0, [L] * B_DECODE, n_kv_heads=HKV, scale=D ** -0.5,
+                 mode=vvo.GGML)
+    dt = time.perf_counter() - t0
+    nbytes = 2 * decode_attn_bytes([L] * B_DECODE)
+    return {"value": nbytes / dt / 1e9, "unit": "GB/s", "cores": vvo.n_cores(), "kind": "port",
+            "sample": f"2 layers x 1 step, B=2, L={L}, Q8_0 cache, ggml-order oracle, {dt:.2f} s"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3, help="timed prefill steps (28 layers each)")
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--decode-steps", type=int, default=512)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--only", choices=["prefill", "decode", "both"], default="both")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the attention path has no multi-GPU mode in this build "
+              "(heads or CFG streams would shard with no exchange); run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+    import vva
+    import vvo
+
+    torch.cuda.set_device(0)
+    ctx = vva.Context(0)
+    line = {
+        "metric": "prefill attn TFLOP/s (% MFMA peak); decode attn HBM GB/s (% peak), 1 GPU",
+        "value": None, "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": None, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16", "data": "synthetic",
+        "config": {"workload": "Qwen2.5-7B-shaped causal prefill, 32768 tokens, 28 layers, 28q/4kv d=128, "
+                               "bf16 Q/K/V in, F16 KV cache, RoPE theta 1e6",
+                   "global_batch": 1, "seq_len": T_PREFILL, "layers": LAYERS},
+    }
+    if args.only in ("prefill", "both"):
+        pre, kv, qr, _ = run_prefill(torch, vva, ctx, args.steps, args.warmup)
+        line["value"] = round(pre["tflops"], 2)
+        line["ms_per_step"] = round(pre["ms_per_step"], 3)
+        line["roofline"] = {"bound": "mfma", "achieved": round(pre["attn_tflops"], 2), "peak": PEAK_F16_TFLOPS,
+                            "unit": "TFLOP/s", "frac": round(pre["attn_tflops"] / PEAK_F16_TFLOPS, 4),
+                            "traffic": None, "kernel": "prefill_kernel<128,F16>",
+                            "avg_launch_ms": round(pre["attn_ms"], 4),
+                            "flop_per_launch": pre["flops_per_layer"]}
+        if not args.no_cpu:
+            line["cpu_baseline"] = cpu_baseline_prefill(torch, vva, vvo, kv, qr)
+        kv.free()
+        torch.cuda.empty_cache()
+    if args.only in ("decode", "both"):
+        dec, kvd = run_decode(torch, vva, ctx, args.decode_steps, max(1, args.warmup))
+        line["decode"] = {
+            "workload": "Qwen2.5-7B-shaped CFG decode, batch 2, Q8_0 KV cache 32768 positions, 28 layers",
+            "value": round(dec["gbs"], 1), "unit": "GB/s", "steps": args.decode_steps,
+            "ms_per_step": round(dec["ms_per_step"], 4), "dtype": "q8_0/f32",
+            "roofline": {"bound": "hbm", "achieved": round(dec["attn_gbs"], 1), "peak": PEAK_HBM_GBS,
+                         "unit": "GB/s", "frac": round(dec["attn_gbs"] / PEAK_HBM_GBS, 4), "traffic": None,
+                         "kernel": "decode_kernel<128,7,Q8_0> + decode_merge_kernel<128>",
+                         "avg_launch_us": round(dec["attn_us"], 3), "bytes_per_launch": dec["bytes_per_layer"],
+                         "splits": dec["splits"]},
+        }
+        if not args.no_cpu:
+            line["decode"]["cpu_baseline"] = cpu_baseline_decode(torch, vva, vvo, kvd)
+        kvd.free()
+        if line["value"] is None:
+            line["metric"] = "decode attn HBM GB/s (% peak), 1 GPU"
+            line["value"], line["unit"] = line["decode"]["value"], "GB/s"
+            line["ms_per_step"] = line["decode"]["ms_per_step"]
+            line["roofline"] = line["decode"]["roofline"]
+    ctx.close()
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

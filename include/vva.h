@@ -78,6 +78,8 @@ typedef struct vva_kv      vva_kv;
  * borrow (not destroyed by vva_destroy) or NULL to create an owned one.
  * Replaces vv::backend() / init (src/backend.cpp:64-133). */
 VVA_API vva_status  vva_create(int device, void* stream, vva_context** out);
+/* Destroys the context and every cache created on it that is still alive
+ * (their handles become invalid). */
 VVA_API void        vva_destroy(vva_context* ctx);
 /* Rebind the context to another borrowed stream (NULL = the owned one). */
 VVA_API vva_status  vva_set_stream(vva_context* ctx, void* stream);

@@ -75,7 +75,7 @@ def test_decode_split_count_does_not_change_result(ctx, torch_gpu):
     for s, n in enumerate(lens):
         kv.set_len(s, n - 1)
     outs = []
-    for wgs in ("2", "16", "512", "4096"):
+    for wgs in ("2", "16", "100", "512"):
         os.environ["VVA_DECODE_WGS"] = wgs
         try:
             _, out = run_attn(ctx, torch, kv, 0, 1, 2, 28, vva.F32, seed=9)
@@ -165,7 +165,6 @@ def test_unsupported_options_are_rejected(ctx, torch_gpu):
     k = torch.zeros((1, 2, 8, 64), device="cuda", dtype=torch.float16)
     out = torch.zeros((1, 1, 4, 64), device="cuda")
     with pytest.raises(vva.VvaError) as e:
-        ctx.lib_check = None
         st = ctx.lib.vva_flash_attn_ext(ctx.h, vva.ctypes.byref(vva.view(q)), vva.ctypes.byref(vva.view(k)),
                                         vva.ctypes.byref(vva.view(k)), None, 0.125, 1.0, 0.0,
                                         vva.ctypes.byref(vva.view(out)))

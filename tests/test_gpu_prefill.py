@@ -1,0 +1,157 @@
+"""GPU parity of the MFMA flash prefill through the C ABI.
+
+Cases cover the three prefill shapes of the reference (0.5B / 1.5B / 7B
+Qwen2.5 heads), single-shot and chunked (past > 0, the ASR 512-token chunk
+loop, src/vibevoice_asr.cpp:542-652), ragged CFG batches, explicit masks and
+the ggml-shaped vva_flash_attn_ext entry.  Tolerance 2e-3 max-abs / 1e-3
+mean-abs against the oracle on the device's own cache bytes.  The chunked
+replay mirrors tests/test_qwen2_resident.cpp paths B-D (single shot, two
+chunks, four uneven chunks).  At the full 32768-token 7B shape the oracle
+checks a deterministic row subset plus the first and last 128 rows.
+"""
+import numpy as np
+import pytest
+
+import vva
+import vvo
+from gpu_util import as_f32, assert_close, err_stats, fill_cache, oracle_attn, to_gpu
+
+pytestmark = pytest.mark.gpu
+TOL = (2e-3, 1e-3)
+
+CASES = [
+    # d, Hq, Hkv, type, T, past, q_type, B
+    (128, 12, 2, vva.F16, 512, 0, vva.BF16, 1),     # 1.5B voice-cloning prefill shape
+    (128, 12, 2, vva.BF16, 512, 0, vva.BF16, 1),
+    (128, 28, 4, vva.F16, 300, 0, vva.F16, 1),      # 7B, tail tile
+    (128, 28, 4, vva.F16, 512, 1536, vva.F16, 1),   # ASR chunk 4 of a 512-chunk prefill
+    (128, 28, 4, vva.BF16, 77, 3000, vva.F32, 1),
+    (64, 14, 2, vva.F16, 256, 0, vva.F32, 1),       # 0.5B
+    (64, 14, 2, vva.F16, 5, 1030, vva.F32, 2),      # TTS text window on both CFG streams
+    (128, 28, 4, vva.F16, 2, 0, vva.F32, 1),
+]
+
+
+@pytest.mark.parametrize("d,Hq,Hkv,t,T,past,q_type,B", CASES)
+def test_prefill_matches_oracle(ctx, torch_gpu, d, Hq, Hkv, t, T, past, q_type, B):
+    torch = torch_gpu
+    print(f"prefill d={d} Hq={Hq} Hkv={Hkv} type={t} T={T} past={past} B={B}", flush=True)
+    pasts = [past + 17 * b for b in range(B)]
+    L = [p + T for p in pasts]
+    kv = vva.KVCache(ctx, 1, Hkv, d, max(L), B, t)
+    fill_cache(kv, L, seed=T + past + d)
+    for b in range(B):
+        kv.set_len(b, pasts[b])
+    rng = np.random.default_rng(T)
+    q = to_gpu(torch, rng.standard_normal((B, T, Hq, d)), q_type)
+    out = torch.full((B, T, Hq, d), float("nan"), dtype=torch.float32, device="cuda")
+    ctx.attn(kv, 0, q, out, d ** -0.5)
+    torch.cuda.synchronize()
+    q32, o = as_f32(torch, q), as_f32(torch, out)
+    ref = oracle_attn(q32, kv, 0, range(B), L, T, d ** -0.5)
+    mx, mn = assert_close(o, ref, *TOL, what="prefill vs exact")
+    gg = oracle_attn(q32, kv, 0, range(B), L, T, d ** -0.5, mode=vvo.GGML)
+    gmx, gmn = err_stats(o, gg)
+    print(f"  vs exact max {mx:.2e} mean {mn:.2e}; vs ggml-order max {gmx:.2e} mean {gmn:.2e}")
+    kv.free()
+
+
+def test_prefill_explicit_mask_and_no_mask(ctx, torch_gpu):
+    torch = torch_gpu
+    d, Hq, Hkv, T, past = 128, 28, 4, 96, 40
+    L = past + T
+    kv = vva.KVCache(ctx, 1, Hkv, d, L, 1, vva.F16)
+    fill_cache(kv, [L], seed=5)
+    kv.set_len(0, past)
+    rng = np.random.default_rng(6)
+    m = np.where(np.arange(L)[None, :] > past + np.arange(T)[:, None], -np.inf, 0.0).astype(np.float32)
+    m[:, 10:30] = -np.inf                              # a block of keys nobody sees
+    m[7, :] = -np.inf                                  # a row with no visible key -> 0
+    mbits = vvo.f16_bits(m)[None]
+    q = to_gpu(torch, rng.standard_normal((1, T, Hq, d)), vva.F16)
+    out = torch.empty((1, T, Hq, d), dtype=torch.float32, device="cuda")
+    ctx.attn(kv, 0, q, out, d ** -0.5, mask=torch.from_numpy(mbits.view(np.float16)).cuda())
+    torch.cuda.synchronize()
+    o = as_f32(torch, out)
+    ref = oracle_attn(as_f32(torch, q), kv, 0, [0], [L], T, d ** -0.5, mask=mbits)
+    assert_close(o, ref, *TOL, what="explicit mask")
+    assert not o[0, 7].any()
+    # ggml_flash_attn_ext without a mask: every key visible
+    kview, vview = kv.views(0, 0)
+    for t_ in (kview, vview):
+        t_.ne[1], t_.ne[2] = t_.ne[2], t_.ne[1]        # ne = [d, L, Hkv, 1] (permuted view)
+        t_.nb[1], t_.nb[2] = t_.nb[2], t_.nb[1]
+        t_.ne[1] = L
+    qp = q.permute(0, 2, 1, 3)                          # ne = [d, T, Hq, 1]
+    ctx.flash_attn_ext(qp, None, None, out, d ** -0.5, k_view=kview, v_view=vview)
+    torch.cuda.synchronize()
+    kraw, vraw = kv.download(0, 0, L)
+    ref = vvo.attn(as_f32(torch, q), [kraw.reshape(-1)], [vraw.reshape(-1)], 1, 1, [L], n_kv_heads=Hkv,
+                   scale=d ** -0.5, mask_mode=vvo.MASK_NONE)
+    assert_close(as_f32(torch, out), ref, *TOL, what="no mask")
+    kv.free()
+
+
+def _resident_replay(ctx, torch, bounds, t, seed=1):
+    """RoPE + append + attention of N tokens in the given chunks, one layer."""
+    d, Hq, Hkv = 128, 28, 4
+    N = bounds[-1]
+    rng = np.random.default_rng(seed)
+    q = to_gpu(torch, rng.standard_normal((1, N, Hq, d)), vva.BF16)
+    k = to_gpu(torch, rng.standard_normal((1, N, Hkv, d)), vva.BF16)
+    v = to_gpu(torch, rng.standard_normal((1, N, Hkv, d)), vva.BF16)
+    kv = vva.KVCache(ctx, 1, Hkv, d, N, 1, t)
+    out = torch.empty((1, N, Hq, d), dtype=torch.float32, device="cuda")
+    qr = torch.empty((1, N, Hq, d), dtype=torch.float16, device="cuda")
+    for a, b in zip(bounds[:-1], bounds[1:]):
+        pos = torch.arange(a, b, dtype=torch.int32, device="cuda")
+        ctx.rope_append(kv, 0, q[:, a:b], k[:, a:b], v[:, a:b], pos, qr[:, a:b])
+        ctx.attn(kv, 0, qr[:, a:b], out[:, a:b], d ** -0.5)
+        kv.set_len(0, b)
+    torch.cuda.synchronize()
+    res = as_f32(torch, out), kv.download(0, 0, N)
+    kv.free()
+    return res
+
+
+def test_chunked_prefill_equals_single_shot(ctx, torch_gpu):
+    """tests/test_qwen2_resident.cpp paths B (one shot), C (two chunks), D (four uneven)."""
+    torch = torch_gpu
+    N = 700
+    one, cache1 = _resident_replay(ctx, torch, [0, N], vva.F16)
+    two, cache2 = _resident_replay(ctx, torch, [0, N // 2, N], vva.F16)
+    four, cache4 = _resident_replay(ctx, torch, [0, N // 4, N // 2, 3 * N // 4, N], vva.F16)
+    for c in (cache2, cache4):
+        np.testing.assert_array_equal(c[0], cache1[0])
+        np.testing.assert_array_equal(c[1], cache1[1])
+    assert np.abs(two - one).max() < 1e-5
+    assert np.abs(four - one).max() < 1e-5
+
+
+def test_decode_after_prefill_equals_last_prefill_row(ctx, torch_gpu):
+    torch = torch_gpu
+    N = 1000
+    full, _ = _resident_replay(ctx, torch, [0, N], vva.F16, seed=3)
+    step, _ = _resident_replay(ctx, torch, [0, N - 1, N], vva.F16, seed=3)
+    assert np.abs(step[0, N - 1] - full[0, N - 1]).max() < 1e-5
+
+
+def test_full_size_7b_prefill_row_subset(ctx, torch_gpu):
+    """32768-token causal prefill, 28q/4kv, d=128, F16 cache (bf16 inputs)."""
+    torch = torch_gpu
+    d, Hq, Hkv, T = 128, 28, 4, 32768
+    kv = vva.KVCache(ctx, 1, Hkv, d, T, 1, vva.F16)
+    fill_cache(kv, [T], seed=77)
+    kv.set_len(0, 0)
+    rng = np.random.default_rng(78)
+    q = to_gpu(torch, rng.standard_normal((1, T, Hq, d)), vva.BF16)
+    out = torch.empty((1, T, Hq, d), dtype=torch.float32, device="cuda")
+    ctx.attn(kv, 0, q, out, d ** -0.5)
+    torch.cuda.synchronize()
+    o = as_f32(torch, out)
+    assert np.isfinite(o).all()
+    rows = np.unique(np.concatenate([np.arange(128), np.arange(T - 128, T),
+                                     np.linspace(128, T - 129, 64).astype(np.int64)])).astype(np.int32)
+    ref = oracle_attn(as_f32(torch, q), kv, 0, [0], [T], T, d ** -0.5, rows=rows)
+    assert_close(o[0, rows], ref[0, rows], *TOL, what="32k subset")
+    kv.free()

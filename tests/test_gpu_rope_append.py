@@ -62,7 +62,8 @@ def test_rope_append_matches_oracle(ctx, torch_gpu, d, Hq, Hkv, T, B, in_t, cach
         tol = {vva.F32: 2e-6, vva.F16: 2e-3, vva.BF16: 2e-2, vva.Q8_0: 4e-2}[cache_t]
         np.testing.assert_allclose(k_got, k_exp, atol=tol, rtol=0)
         same = np.mean(kraw[past[b]:] == vvo.from_f32(k_ref[b], cache_t).reshape(T, rb))
-        assert same > 0.99, same
+        # F32 rows expose 1-ulp sinf/cosf differences in their low bytes
+        assert same > (0.9 if cache_t == vva.F32 else 0.99), same
         # the other layer is untouched
         k0, v0 = kv.download(0, b, past[b] + T)
         assert not k0.any() and not v0.any()

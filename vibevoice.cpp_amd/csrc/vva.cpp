@@ -11,6 +11,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <set>
 #include <string>
 #include <vector>
 
@@ -28,6 +29,7 @@ struct vva_context {
     int last_splits = 0;
     float* ws = nullptr;                 // decode split partials
     size_t ws_bytes = 0;
+    std::set<vva_kv*> caches;            // released by vva_destroy if still alive
 };
 
 struct vva_kv {
@@ -202,6 +204,11 @@ extern "C" void vva_destroy(vva_context* ctx) {
     if (!ctx) return;
     DeviceGuard g(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    for (vva_kv* kv : ctx->caches) {
+        (void)hipFree(kv->base);
+        delete kv;
+    }
+    ctx->caches.clear();
     if (ctx->ws) (void)hipFree(ctx->ws);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
     delete ctx;
@@ -264,15 +271,18 @@ extern "C" vva_status vva_kv_create(vva_context* ctx, const vva_kv_desc* d, vva_
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     if (e != hipSuccess) { (void)hipFree(kv->base); delete kv; return hip_fail(ctx, e, "kv_create: memset"); }
     kv->len.assign(d->n_seq, 0);
+    ctx->caches.insert(kv);
     *out = kv;
     return VVA_OK;
 }
 
 extern "C" void vva_kv_free(vva_kv* kv) {
     if (!kv) return;
-    DeviceGuard g(kv->ctx->device);
-    (void)hipStreamSynchronize(kv->ctx->stream);
+    vva_context* ctx = kv->ctx;
+    DeviceGuard g(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
     (void)hipFree(kv->base);
+    ctx->caches.erase(kv);
     delete kv;
 }
 

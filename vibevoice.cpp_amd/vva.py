@@ -10,6 +10,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import weakref
 
 F32, F16, Q8_0, I32, BF16 = 0, 1, 8, 26, 30
 ROPE_NEOX = 2
@@ -136,6 +137,7 @@ class Context:
         if st != OK:
             raise VvaError(st, self.lib.vva_last_error(None).decode())
         self.h = h
+        self.caches = weakref.WeakSet()
 
     def check(self, st: int):
         if st != OK:
@@ -143,6 +145,8 @@ class Context:
 
     def close(self):
         if getattr(self, "h", None):
+            for kv in list(self.caches):      # vva_destroy releases them natively
+                kv.h = None
             self.lib.vva_destroy(self.h)
             self.h = None
 
@@ -220,13 +224,14 @@ class KVCache:
         h = ctypes.c_void_p()
         ctx.check(ctx.lib.vva_kv_create(ctx.h, ctypes.byref(d), ctypes.byref(h)))
         self.h = h
+        ctx.caches.add(self)
         self.n_layers, self.n_kv_heads, self.head_dim = n_layers, n_kv_heads, head_dim
         self.max_seq, self.n_seq, self.type = max_seq, n_seq, type_
 
     def free(self):
-        if getattr(self, "h", None):
+        if getattr(self, "h", None) and getattr(self.ctx, "h", None):
             self.ctx.lib.vva_kv_free(self.h)
-            self.h = None
+        self.h = None
 
     def __del__(self):
         try:
