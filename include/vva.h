@@ -74,14 +74,16 @@ typedef struct vva_kv      vva_kv;
 
 /* ---------------------------------------------------------------- context */
 
-/* Create a context on HIP device `device`.  `stream` is a hipStream_t to
- * borrow (not destroyed by vva_destroy) or NULL to create an owned one.
- * Replaces vv::backend() / init (src/backend.cpp:64-133). */
+/* Create a context on HIP device `device`.  `stream` is the hipStream_t all
+ * work is enqueued on (borrowed, never destroyed here); NULL selects the
+ * device's null stream.  Replaces vv::backend() / init
+ * (src/backend.cpp:64-133). */
 VVA_API vva_status  vva_create(int device, void* stream, vva_context** out);
 /* Destroys the context and every cache created on it that is still alive
  * (their handles become invalid). */
 VVA_API void        vva_destroy(vva_context* ctx);
-/* Rebind the context to another borrowed stream (NULL = the owned one). */
+/* Rebind the context to another stream (NULL = the null stream) after
+ * waiting for the work already queued on the current one. */
 VVA_API vva_status  vva_set_stream(vva_context* ctx, void* stream);
 /* Block until all work enqueued on the context's stream is done. */
 VVA_API vva_status  vva_synchronize(vva_context* ctx);

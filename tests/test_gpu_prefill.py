@@ -133,7 +133,9 @@ def test_decode_after_prefill_equals_last_prefill_row(ctx, torch_gpu):
     N = 1000
     full, _ = _resident_replay(ctx, torch, [0, N], vva.F16, seed=3)
     step, _ = _resident_replay(ctx, torch, [0, N - 1, N], vva.F16, seed=3)
-    assert np.abs(step[0, N - 1] - full[0, N - 1]).max() < 1e-5
+    # different kernels (split-K fp32 P vs MFMA f16 P): the FA tolerance of
+    # tests/test_qwen2_resident.cpp:478
+    assert np.abs(step[0, N - 1] - full[0, N - 1]).max() < 1e-3
 
 
 def test_full_size_7b_prefill_row_subset(ctx, torch_gpu):

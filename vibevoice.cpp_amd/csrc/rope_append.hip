@@ -46,7 +46,7 @@ __device__ __forceinline__ void store_q8_pair(char* row, int i, int P, float y0,
     b1[2 + (j1 & (kQK8 - 1))] = (char)(int8_t)roundf(y1 * id1);
 }
 
-__global__ void __launch_bounds__(256) rope_append_kernel(RopeAppendArgs a) {
+__global__ void __launch_bounds__(256) rope_append_kernel(RopeAppendArgs a, int items_per_block) {
     const int t = blockIdx.x, b = blockIdx.y;
     const int P = a.d >> 1;
     __shared__ float cs[128], sn[128];
@@ -61,8 +61,11 @@ __global__ void __launch_bounds__(256) rope_append_kernel(RopeAppendArgs a) {
 
     const int nq = a.do_q ? a.Hq : 0;
     const int nslots = nq + (a.do_kv ? 2 * a.Hkv : 0);
-    const int total = nslots * P;
-    for (int w = threadIdx.x; w < total; w += blockDim.x) {
+    // blockIdx.z takes a multiple-of-256 slice of the token's items, so few-token
+    // calls (decode) still spread over many workgroups
+    const int w_begin = blockIdx.z * items_per_block;
+    const int total = min(nslots * P, w_begin + items_per_block);
+    for (int w = w_begin + threadIdx.x; w < total; w += blockDim.x) {
         const int slot = w / P;
         const int i = w - slot * P;
         const float c = cs[i], s = sn[i];
@@ -108,8 +111,14 @@ __global__ void __launch_bounds__(256) rope_append_kernel(RopeAppendArgs a) {
 
 hipError_t launch_rope_append(const RopeAppendArgs& a, hipStream_t s) {
     if (a.T <= 0 || a.B <= 0) return hipSuccess;
-    dim3 grid(a.T, a.B);
-    hipLaunchKernelGGL(rope_append_kernel, grid, dim3(256), 0, s, a);
+    const int items = ((a.do_q ? a.Hq : 0) + (a.do_kv ? 2 * a.Hkv : 0)) * (a.d / 2);
+    if (items <= 0) return hipSuccess;
+    int split = 1;
+    if ((int64_t)a.T * a.B < 512) split = (items + 255) / 256;       // one item per thread
+    const int per_block = ((items + split - 1) / split + 255) / 256 * 256;
+    split = (items + per_block - 1) / per_block;
+    dim3 grid(a.T, a.B, split);
+    hipLaunchKernelGGL(rope_append_kernel, grid, dim3(256), 0, s, a, per_block);
     return hipGetLastError();
 }
 

@@ -21,13 +21,12 @@ using namespace vva;
 
 struct vva_context {
     int device = 0;
-    hipStream_t stream = nullptr;        // active stream
-    hipStream_t own_stream = nullptr;    // created by us (destroyed in vva_destroy)
+    hipStream_t stream = nullptr;        // borrowed stream; nullptr = the HIP null stream
     std::string err;
     int n_cu = 256;
     int attn_path = 0;
     int last_splits = 0;
-    float* ws = nullptr;                 // decode split partials
+    float* ws = nullptr;                 // decode split partials, after the ticket area
     size_t ws_bytes = 0;
     std::set<vva_kv*> caches;            // released by vva_destroy if still alive
 };
@@ -118,18 +117,20 @@ vva_status run_attention(vva_context* ctx, AttnArgs& a) {
     ctx->last_splits = 0;
     if (ctx->attn_path != 1 && a.T == 1 && decode_supported(a)) {
         const int nw = decode_waves(a);
-        const int R = nw / a.Hkv;
-        const int unit = decode_tokens_per_iter(a) * R;
         int Lmax = 1;
         for (int b = 0; b < a.B; ++b) Lmax = a.L[b] > Lmax ? a.L[b] : Lmax;
-        int target = 2 * ctx->n_cu / a.B;
+        // about one workgroup per CU over (split, sequence); each of the
+        // nw / Hkv waves of a kv head takes at least 32 keys
+        const int R = nw / a.Hkv;
+        int target = ctx->n_cu / a.B;
         if (const char* env = std::getenv("VVA_DECODE_WGS")) target = std::atoi(env) / a.B;
         if (target < 1) target = 1;
-        int split_len = (Lmax + target - 1) / target;
-        int min_len = 2 * unit;
-        if (const char* env = std::getenv("VVA_DECODE_MIN_SPLIT")) min_len = std::atoi(env);
-        if (split_len < min_len) split_len = min_len;
-        split_len = (split_len + unit - 1) / unit * unit;
+        int min_sub = 32;
+        if (const char* env = std::getenv("VVA_DECODE_MIN_SUB")) min_sub = std::atoi(env);
+        if (min_sub < 1) min_sub = 1;
+        int sub_len = (Lmax + target * R - 1) / (target * R);
+        if (sub_len < min_sub) sub_len = min_sub;
+        const int split_len = sub_len * R;
         const int n_splits = (Lmax + split_len - 1) / split_len;
         if (n_splits > 1) {
             vva_status st = ensure_ws(ctx, (size_t)n_splits * a.B * a.Hq * (a.d + 2) * sizeof(float));
@@ -189,13 +190,7 @@ extern "C" vva_status vva_create(int device, void* stream, vva_context** out) {
     auto* ctx = new vva_context();
     ctx->device = device;
     ctx->n_cu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
-    if (stream) {
-        ctx->stream = (hipStream_t)stream;
-    } else {
-        e = hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking);
-        if (e != hipSuccess) { delete ctx; return fail(nullptr, VVA_ERR_DEVICE, "hipStreamCreate failed"); }
-        ctx->stream = ctx->own_stream;
-    }
+    ctx->stream = (hipStream_t)stream;
     *out = ctx;
     return VVA_OK;
 }
@@ -210,18 +205,16 @@ extern "C" void vva_destroy(vva_context* ctx) {
     }
     ctx->caches.clear();
     if (ctx->ws) (void)hipFree(ctx->ws);
-    if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
     delete ctx;
 }
 
 extern "C" vva_status vva_set_stream(vva_context* ctx, void* stream) {
     if (!ctx) return VVA_ERR_INVALID_ARG;
     DeviceGuard g(ctx->device);
-    if (!stream && !ctx->own_stream) {
-        hipError_t e = hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking);
-        if (e != hipSuccess) return hip_fail(ctx, e, "hipStreamCreate");
-    }
-    ctx->stream = stream ? (hipStream_t)stream : ctx->own_stream;
+    // finish work queued on the previous stream before switching
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipStreamSynchronize");
+    ctx->stream = (hipStream_t)stream;
     return VVA_OK;
 }
 

@@ -81,13 +81,12 @@ enum { kMaskNone = 0, kMaskExplicit = 1, kMaskCausal = 2 };
 
 hipError_t launch_rope_append(const RopeAppendArgs& a, hipStream_t s);
 hipError_t launch_attn_rows(const AttnArgs& a, hipStream_t s);
-// Split-K decode (T == 1): writes partials into `ws` (n_splits * B * Hq *
-// (d + 2) floats) then merges into out.  Returns the split count used.
-hipError_t launch_decode(const AttnArgs& a, float* ws, int n_splits, int split_len,
-                         hipStream_t s);
+// Split-K decode (T == 1): workgroups write partials into `ws`
+// (B * Hq * n_splits * (d + 2) floats), a second launch combines them.
+hipError_t launch_decode(const AttnArgs& a, float* ws, int n_splits, int split_len, hipStream_t s);
 bool decode_supported(const AttnArgs& a);
-int decode_waves(const AttnArgs& a);            // waves per workgroup
-int decode_tokens_per_iter(const AttnArgs& a);  // keys per wave iteration
+int decode_waves(const AttnArgs& a);            // waves per workgroup (one key sub-range each)
+int decode_max_splits();
 // MFMA flash prefill (F16 / BF16 caches).
 hipError_t launch_prefill(const AttnArgs& a, hipStream_t s);
 bool prefill_supported(const AttnArgs& a);
