@@ -8,38 +8,51 @@
 // Grid: one workgroup of 8 waves per (key split, sequence).  Wave w takes kv
 // head w % Hkv and the (w / Hkv)-th part of the split, with the g = Hq / Hkv
 // query heads of that kv head (GQA: each K/V byte is read once per group).
-// The waves of a workgroup together read whole cache rows ([Hkv][d] per
-// token), so no cache line is fetched by two CUs.
+// The waves of a workgroup together read whole cache rows, so no cache line
+// is fetched by two CUs.  A wave walks its keys 32 at a time ("an
+// iteration") in two layouts of its 64 lanes:
 //
-// Lane l of a wave owns key l / (d/32) and 32-dim chunk l % (d/32) of each
-// group of 64 / (d/32) keys ("a step").  Per step the lane loads its K and V
-// chunks with wide loads one step ahead of use (two register sets used in
-// turn).  F16 / BF16: 4 x 16 B per chunk.  Q8_0: the 32 codes of the 34-byte
-// block from the 4-byte aligned address at or below them (2 x 16 B + 4 B,
-// aligned by v_alignbyte with a per-lane shift) plus the fp16 scale.
-//   K      dots against Q rounded to K's dot type: v_dot2_f32_f16 /
-//          v_dot2_f32_bf16, or v_dot4_i32_i8 against Q quantized to Q8_0 per
-//          32-dim block (ggml's Q8_0 x Q8_0 dot: integer block sums times
-//          d_k * d_q); DPP completes each score across the key's lanes.
-//   soft-  two steps (32 keys at d = 128) per update; the running max is raised
-//   max    lazily (only when a score exceeds it by 2^8), so the common path
-//          needs no cross-lane max and no rescale.
-//   V      raw V chunks go to the wave's slice of LDS, p * (V block scale) goes
-//          to LDS as f16 pairs of consecutive keys; lane l then owns d/64 dims
-//          and accumulates over key pairs with v_dot2_f32_f16 (codes and f16
-//          values are exact in f16; fp32 accumulation).
-// The waves of one kv head merge through LDS (log-sum-exp).  With one split
-// the output is written directly; otherwise the workgroup writes (m, l,
-// acc[d]) per head and decode_merge_kernel combines the splits (a second
-// launch: kernel boundaries give the cross-XCD visibility that a device-scope
-// fence would buy with an L2 write-back per workgroup).
+//   K phase  lane = (key, chunk of KD dims): KD = 32 for Q8_0 (one block),
+//            16 for F16 / BF16.  Dots against Q rounded to K's dot type:
+//            v_dot4_i32_i8 against Q quantized to Q8_0 per block (ggml's
+//            Q8_0 x Q8_0 dot: integer block sums times d_k * d_q), or
+//            v_dot2_f32_f16 / v_dot2_f32_bf16; DPP completes each score over
+//            the key's lanes.  Online softmax in the exp2 domain with a lazy
+//            running max (raised only when a score exceeds it by 2^8).  Each
+//            lane writes p (times its V block scale for Q8_0) as f16 to LDS.
+//   V phase  lane = (pair of dims, every key pair at d = 128; half of them
+//            at d = 64).  The lane reads its 2 dims of each key straight from
+//            HBM (2 bytes of Q8_0 codes or 4 bytes of F16 / BF16), turns pairs
+//            of consecutive keys into f16 pairs (SDWA byte converts; int8
+//            codes are exact in f16), and accumulates every head with
+//            v_dot2_f32_f16 against the f16 p pairs from LDS (fp32 sums).
+//
+// Loads run one iteration ahead: each step's K chunk and each key's V
+// bytes are re-issued for the next iteration as soon as they are consumed,
+// and the first iteration's loads are issued before Q is converted.  All
+// cache loads are raw buffer loads whose range ends at the wave's last key.
+// At d = 64 the two halves of the key pairs are added with
+// v_permlane32_swap; the waves of one kv head merge through LDS
+// (log-sum-exp).  With one split the output
+// is written directly; otherwise the workgroup writes (m, l, acc[d]) per head
+// and decode_merge_kernel combines the splits in one pass (a second launch:
+// kernel boundaries give the cross-XCD visibility that a device-scope fence
+// would buy with an L2 write-back per workgroup).
 #include "vva_internal.hpp"
 
 namespace vva {
 
 namespace {
 
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4), aligned(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __amdgpu_buffer_rsrc_t BufRsrc;
+
+// Raw buffer descriptor (stride 0, range `bytes`; word 3 = 0x00020000, the
+// gfx9 raw-buffer configuration): loads at offsets past the range return 0.
+__device__ __forceinline__ BufRsrc make_rsrc(const char* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), (short)0, (int)bytes, 0x00020000);
+}
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
 
@@ -93,15 +106,27 @@ __device__ __forceinline__ float max_swap32(float x) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
-// Sum over the LPT lanes of one key (aligned groups of 2 or 4), for N values
-// at once so consecutive DPP steps do not wait on each other.
+__device__ __forceinline__ float add_swap16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float add_swap32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// Sum over the LPT lanes of one key (aligned groups of 2, 4 or 8), for N
+// values at once so consecutive DPP steps do not wait on each other.
 template <int LPT, int N>
 __device__ __forceinline__ void key_sum(float (&x)[N]) {
 #pragma unroll
     for (int i = 0; i < N; ++i) x[i] += dpp<kDppXor1>(x[i]);
-    if constexpr (LPT == 4) {
+    if constexpr (LPT >= 4) {
 #pragma unroll
         for (int i = 0; i < N; ++i) x[i] += dpp<kDppXor2>(x[i]);
+    }
+    if constexpr (LPT == 8) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) x[i] += dpp<kDppHalfMirror>(x[i]);
     }
 }
 // Max over all keys of the wave, for values equal within each LPT group.
@@ -111,8 +136,10 @@ __device__ __forceinline__ void keys_max(float (&x)[N]) {
 #pragma unroll
         for (int i = 0; i < N; ++i) x[i] = fmaxf(x[i], dpp<kDppXor2>(x[i]));
     }
+    if constexpr (LPT <= 4) {
 #pragma unroll
-    for (int i = 0; i < N; ++i) x[i] = fmaxf(x[i], dpp<kDppHalfMirror>(x[i]));
+        for (int i = 0; i < N; ++i) x[i] = fmaxf(x[i], dpp<kDppHalfMirror>(x[i]));
+    }
 #pragma unroll
     for (int i = 0; i < N; ++i) x[i] = fmaxf(x[i], dpp<kDppMirror>(x[i]));
 #pragma unroll
@@ -120,79 +147,81 @@ __device__ __forceinline__ void keys_max(float (&x)[N]) {
 #pragma unroll
     for (int i = 0; i < N; ++i) x[i] = max_swap32(x[i]);
 }
-
-// int8 code -> f16 (exact)
-__device__ __forceinline__ _Float16 code_f16(uint32_t byte) {
-    return (_Float16)(int16_t)(int8_t)(uint8_t)byte;
+// Sum over all 64 lanes (every lane gets the total).
+__device__ __forceinline__ float wave_sum(float x) {
+    x += dpp<kDppXor1>(x);
+    x += dpp<kDppXor2>(x);
+    x += dpp<kDppHalfMirror>(x);
+    x += dpp<kDppMirror>(x);
+    x = add_swap16(x);
+    return add_swap32(x);
 }
 
-// Per-lane 32-dim chunk of a cache row.
-template <int KT> struct Chunk;
-template <> struct Chunk<VVA_TYPE_Q8_0> {
-    static constexpr int W = 9;
-    // Codes of block c start at byte c*34 + 2 of the row: 2 mod 4 for even
-    // c, 0 mod 4 for odd c.  Load 9 dwords from the aligned address at or
-    // below them (odd lanes, which need only 8, re-read an in-block dword as
-    // the 9th so no load leaves the block) plus the fp16 scale.
-    static __device__ __forceinline__ void load(const char* row, int c, uint32_t (&w)[W], float& scale) {
-        const char* blk = row + c * kQ8Bytes;
-        const bool odd = (c & 1) != 0;
-        const char* base = blk + (odd ? 2 : 0);
-        const u32x4 a = *(const u32x4*)base;
-        const u32x4 b = *(const u32x4*)(base + 16);
-        w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
-        w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
-        w[8] = *(const uint32_t*)(base + (odd ? 28 : 32));
-        scale = f16_to_f32(*(const uint16_t*)blk);
+// First dot of a chain: the VOP3P form with an inline 0 accumulator (the
+// accumulate-in-place form would need the zero moved in first).
+__device__ __forceinline__ int sdot4_first(uint32_t a, uint32_t b) {
+    int r;
+    asm("v_dot4_i32_i8 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
+// (int8 byte N of a, int8 byte N of b) -> f16 pair (exact): two SDWA
+// converts, the second writing the high half in place.
+#define VVA_I8_PAIR(N)                                                                          \
+    __device__ __forceinline__ uint32_t i8_pair_b##N(uint16_t a, uint16_t b) {                  \
+        uint32_t r;                                                                             \
+        asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_" #N "\n\t" \
+            "v_cvt_f16_i16_sdwa %0, sext(%2) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_" #N \
+            : "=&v"(r) : "v"(a), "v"(b));                                                       \
+        return r;                                                                               \
     }
-    // byte offset of code 0 within the loaded words
-    static __device__ __forceinline__ int shift(int c) { return (c & 1) ? 0 : 2; }
+VVA_I8_PAIR(0)
+VVA_I8_PAIR(1)
+VVA_I8_PAIR(2)
+VVA_I8_PAIR(3)
+#undef VVA_I8_PAIR
+
+template <int D, int G, int KT>
+struct Cfg {
+    static constexpr bool Q8 = KT == VVA_TYPE_Q8_0;
+    static constexpr int KD = Q8 ? 32 : 16;         // dims per lane, K phase
+    static constexpr int LPT = D / KD;              // lanes per key, K phase
+    static constexpr int TPS = 64 / LPT;            // keys per K step
+    static constexpr int TPI = 32;                  // keys per iteration
+    static constexpr int SPI = TPI / TPS;           // K steps per iteration
+    static constexpr int CW = 8 + (Q8 ? 1 : 0);     // K words per lane per step
+    static constexpr int QW = 8;                    // Q words per head per lane
+    static constexpr int VD = 2;                    // dims per lane, V phase
+    static constexpr int DG = D / VD;               // V dim groups
+    static constexpr int KG = 64 / DG;              // V key groups (1 at d = 128, 2 at d = 64)
+    static constexpr int PPI = TPI / 2 / KG;        // key pairs per lane per iteration
+    static constexpr int NPB = Q8 ? D / 32 : 1;     // p rows per key pair (one per V block)
+    static constexpr int GP = (G + 3) / 4 * 4;      // p row padded for 16-byte reads
 };
-template <> struct Chunk<VVA_TYPE_F16> {
-    static constexpr int W = 16;
-    static __device__ __forceinline__ void load(const char* row, int c, uint32_t (&w)[W], float& scale) {
-        const u32x4* p = (const u32x4*)(row + c * 64);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const u32x4 v = p[k];
-            w[4 * k] = v.x; w[4 * k + 1] = v.y; w[4 * k + 2] = v.z; w[4 * k + 3] = v.w;
-        }
-        scale = 1.0f;
-    }
-    static __device__ __forceinline__ int shift(int) { return 0; }
-};
-template <> struct Chunk<VVA_TYPE_BF16> : Chunk<VVA_TYPE_F16> {};
 
 // D: head dim (64 / 128); G: query heads per kv head; KT: cache type.
 template <int D, int G, int KT>
 __global__ void __launch_bounds__(kWaves * 64)
 decode_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split_len) {
-    constexpr int NW = kWaves;
-    constexpr int LPT = D / 32;                 // lanes per key in the K phase
-    constexpr int TPS = 64 / LPT;               // keys per step
-    constexpr int SPI = D == 128 ? 2 : 1;       // steps per softmax update
-    constexpr int TPI = TPS * SPI;              // keys per iteration
-    constexpr int DV = D / 64;                  // dims per lane in the V phase
-    constexpr int NB = D / 32;                  // 32-dim blocks per row
-    constexpr bool Q8 = KT == VVA_TYPE_Q8_0;
-    constexpr int QW = Q8 ? 8 : 16;             // Q words per head per lane
-    constexpr int CW = Chunk<KT>::W;
-    constexpr int SLOT = CW * 4;                // LDS bytes per staged V chunk
-    constexpr int GP = G == 7 ? 8 : G;          // p row padded for 16-byte reads
+    using C = Cfg<D, G, KT>;
+    constexpr bool Q8 = C::Q8;
+    constexpr int NW = kWaves, LPT = C::LPT, TPS = C::TPS, TPI = C::TPI, SPI = C::SPI;
+    constexpr int CW = C::CW, QW = C::QW, VD = C::VD, DG = C::DG, KG = C::KG, PPI = C::PPI;
+    constexpr int NPB = C::NPB, GP = C::GP;
+    constexpr int QSLOT = QW + 1;
+    static_assert(KG == 1 || KG == 2, "V key groups are combined with v_permlane32_swap");
 
-    constexpr int STAGE_BYTES = NW * TPI * LPT * SLOT;
+    constexpr int QAREA_BYTES = 64 * LPT * QSLOT * 4;                // Hq <= 64
     constexpr int MERGE_BYTES = NW * G * D * 4;
-    constexpr int QAREA_BYTES = 8 * G * NB * (QW + 1) * 4;           // Hkv <= 8
-    constexpr int A1 = STAGE_BYTES > MERGE_BYTES ? STAGE_BYTES : MERGE_BYTES;
-    // one area serves, in turn: Q conversion, V staging, the cross-wave merge
-    __shared__ __attribute__((aligned(16))) char smem[A1 > QAREA_BYTES ? A1 : QAREA_BYTES];
-    // p * (V block scale) as f16 pairs of consecutive keys: [wave][chunk][pair][head]
-    __shared__ __attribute__((aligned(16))) uint32_t pbuf[NW][LPT][TPI / 2][GP];
+    __shared__ __attribute__((aligned(16))) char smem[QAREA_BYTES > MERGE_BYTES ? QAREA_BYTES : MERGE_BYTES];
+    // p (times the V block scale) as f16 pairs of consecutive keys:
+    // [wave][V block][key pair][head]
+    __shared__ __attribute__((aligned(16))) uint32_t pbuf[NW][NPB][TPI / 2][GP];
     __shared__ float mbuf[NW][G];
     __shared__ float lbuf[NW][G];
 
     const int lane = threadIdx.x & 63;
-    const int w = threadIdx.x >> 6;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform
     const int Hkv = a.Hkv;
     const int R = NW / Hkv;                                 // waves per kv head
     const int kvh = w % Hkv, r = w / Hkv;
@@ -201,31 +230,103 @@ decode_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split_len) {
     const int sub_len = split_len / R;
     const int j_begin = min(L, split * split_len + r * sub_len);
     const int j_end = min(L, j_begin + sub_len);
-    const int tl = lane / LPT, c = lane % LPT;
+    const int tl = lane / LPT, c = lane % LPT;              // K-phase key, chunk
+    const int dg = lane % DG, kg = lane / DG;               // V-phase dim group, key group
     const int h0 = kvh * G;
 
-    // ---- Q in K's dot type: one thread per (query head, 32-dim block)
-    // converts it with vector loads (Q8_0: codes + fp16 scale; F16 / BF16:
-    // packed pairs) into LDS; each lane then reads its chunk of its g heads
+    // K and V of this kv head as raw buffers: SGPR descriptor + 32-bit
+    // offsets (row offsets are wave-uniform scalars, lane offsets fixed per
+    // lane).  The range ends with the wave's last key, so loads for keys at
+    // or past j_end return 0 without touching memory: the next iteration's
+    // loads are issued unconditionally (a branch around them would keep two
+    // register sets alive), and the last one's cost no traffic.
+    constexpr int HEAD_BYTES = Q8 ? D / 32 * kQ8Bytes : 2 * D;
+    const uint32_t nbk = (uint32_t)a.k_nb_tok, nbv = (uint32_t)a.v_nb_tok;
+    const BufRsrc krs = make_rsrc(a.k[b] + kvh * a.k_nb_head, j_end > 0 ? (uint32_t)(j_end - 1) * nbk + HEAD_BYTES : 0);
+    const BufRsrc vrs = make_rsrc(a.v[b] + kvh * a.v_nb_head, j_end > 0 ? (uint32_t)(j_end - 1) * nbv + HEAD_BYTES : 0);
+
+    // K-phase lane offsets.  Q8_0: the 32 codes of block c from the 4-byte
+    // aligned address at or below them (2 x 16 B + 4 B; odd blocks, which need
+    // only 8 dwords, re-read an in-block dword as the 9th), plus the K and V
+    // block scales.  F16 / BF16: 2 x 16 B.
+    const uint32_t ko = tl * nbk + (Q8 ? c * kQ8Bytes + ((c & 1) ? 2 : 0) : c * 32);
+    const uint32_t ko9 = ko + ((c & 1) ? 28 : 32);
+    const uint32_t kso = tl * nbk + c * kQ8Bytes;
+    const uint32_t vso = tl * nbv + c * kQ8Bytes;
+    // V-phase lane offset of dims [2dg, 2dg+2): Q8_0 codes 2 (dg mod 16) and
+    // 2 (dg mod 16) + 1 of block dg / 16 (2 bytes); F16 / BF16 4 bytes.
+    const uint32_t vo = 2 * kg * nbv + (Q8 ? (dg * VD) / 32 * kQ8Bytes + 2 + (dg * VD) % 32 : dg * VD * 2);
+
+    // register sets for one iteration: K chunk per step, V dwords per key pair
+    uint32_t kbuf[SPI][CW];
+    float ksc[SPI], vsc[SPI];
+    // V: Q8_0 codes as loaded (2 bytes), F16 / BF16 pairs (4 bytes)
+    typedef std::conditional_t<Q8, uint16_t, uint32_t> vword;
+    vword vbuf[PPI][2];
+    auto issue_k = [&](int i0, int st) {
+        const uint32_t sk = (uint32_t)(i0 + st * TPS) * nbk;
+        const uint32_t sv = (uint32_t)(i0 + st * TPS) * nbv;
+        const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(krs, ko, sk, 0);
+        const u32x4 y = __builtin_amdgcn_raw_buffer_load_b128(krs, ko + 16, sk, 0);
+        kbuf[st][0] = x.x; kbuf[st][1] = x.y; kbuf[st][2] = x.z; kbuf[st][3] = x.w;
+        kbuf[st][4] = y.x; kbuf[st][5] = y.y; kbuf[st][6] = y.z; kbuf[st][7] = y.w;
+        if constexpr (Q8) {
+            kbuf[st][8] = __builtin_amdgcn_raw_buffer_load_b32(krs, ko9, sk, 0);
+            ksc[st] = f16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(krs, kso, sk, 0));
+            vsc[st] = f16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(vrs, vso, sv, 0));
+        }
+    };
+    auto issue_v = [&](int i0, int k) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const uint32_t sv = (uint32_t)(i0 + 2 * KG * k + t) * nbv;
+            if constexpr (Q8)
+                vbuf[k][t] = __builtin_amdgcn_raw_buffer_load_b16(vrs, vo, sv, 0);
+            else
+                vbuf[k][t] = __builtin_amdgcn_raw_buffer_load_b32(vrs, vo, sv, 0);
+        }
+    };
+    // Q, then the first iteration's K and V, go out before Q is converted:
+    // one thread per (query head, KD-dim chunk) loads its chunk (threads past
+    // the last chunk re-load chunk 0 so every load is unconditional)
+    constexpr int KD = C::KD;
+    const int qslot = threadIdx.x < a.Hq * LPT ? (int)threadIdx.x : 0;
+    uint4 qraw[KD / 4];
+    {
+        const int hq = qslot / LPT, ch = qslot % LPT;
+        const char* src = a.q + b * a.q_nb_b + hq * a.q_nb_h + (int64_t)(ch * KD) * type_elem_bytes(a.q_type);
+        if (a.q_type == VVA_TYPE_F32) {
+#pragma unroll
+            for (int k = 0; k < KD / 4; ++k) qraw[k] = ((const uint4*)src)[k];
+        } else {
+#pragma unroll
+            for (int k = 0; k < KD / 8; ++k) qraw[k] = ((const uint4*)src)[k];
+        }
+    }
+#pragma unroll
+    for (int st = 0; st < SPI; ++st) issue_k(j_begin, st);
+#pragma unroll
+    for (int k = 0; k < PPI; ++k) issue_v(j_begin, k);
+
+    // ---- Q in K's dot type (Q8_0: codes + fp16 scale; F16 / BF16: packed
+    // pairs), through LDS; each lane then reads its chunk of its g heads
     uint32_t qw[G][QW];
     float qd[G];
     {
-        constexpr int QSLOT = QW + 1;
         uint32_t* qlds = (uint32_t*)smem;
-        if (threadIdx.x < a.Hq * NB) {
-            const int hq = threadIdx.x / NB, blk = threadIdx.x % NB;
-            const char* src = a.q + b * a.q_nb_b + hq * a.q_nb_h + (int64_t)(blk * 32) * type_elem_bytes(a.q_type);
-            float x[32];
+        if (threadIdx.x < a.Hq * LPT) {
+            float x[KD];
             if (a.q_type == VVA_TYPE_F32) {
 #pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    const float4 v = ((const float4*)src)[k];
-                    x[4 * k] = v.x; x[4 * k + 1] = v.y; x[4 * k + 2] = v.z; x[4 * k + 3] = v.w;
+                for (int k = 0; k < KD / 4; ++k) {
+                    const uint4 v = qraw[k];
+                    x[4 * k] = __uint_as_float(v.x); x[4 * k + 1] = __uint_as_float(v.y);
+                    x[4 * k + 2] = __uint_as_float(v.z); x[4 * k + 3] = __uint_as_float(v.w);
                 }
             } else {
 #pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    const uint4 v = ((const uint4*)src)[k];
+                for (int k = 0; k < KD / 8; ++k) {
+                    const uint4 v = qraw[k];
                     const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
@@ -252,101 +353,69 @@ decode_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split_len) {
                 dst[8] = __float_as_uint(f16_to_f32(f32_to_f16(dq)));
             } else {
 #pragma unroll
-                for (int k = 0; k < 16; ++k) dst[k] = pack2<KT>(x[2 * k], x[2 * k + 1]);
-                dst[16] = __float_as_uint(1.0f);
+                for (int k = 0; k < 8; ++k) dst[k] = pack2<KT>(x[2 * k], x[2 * k + 1]);
+                dst[8] = __float_as_uint(1.0f);
             }
         }
         __syncthreads();
         const float sl2 = a.scale * kLog2e;      // scores come out in the exp2 domain
 #pragma unroll
         for (int hh = 0; hh < G; ++hh) {
-            const uint32_t* srcw = qlds + ((h0 + hh) * NB + c) * QSLOT;
+            const uint32_t* srcw = qlds + ((h0 + hh) * LPT + c) * QSLOT;
 #pragma unroll
             for (int k = 0; k < QW; ++k) qw[hh][k] = srcw[k];
             qd[hh] = __uint_as_float(srcw[QW]) * sl2;
         }
-        __syncthreads();                         // the area becomes V staging
+        __syncthreads();                         // the area is reused by the merge
     }
 
-    const char* kb = a.k[b] + kvh * a.k_nb_head;
-    const char* vb = a.v[b] + kvh * a.v_nb_head;
     const char* mrow = a.mask ? a.mask + b * a.mask_nb_b : nullptr;   // query row 0
-    char* my_stage = smem + w * (TPI * LPT * SLOT);
-    const int ksh = Chunk<KT>::shift(c);
+    const int pblk = Q8 ? (dg * VD) / 32 : 0;                          // V-phase p row
 
-    float m[G], l[G], acc[G][DV];
+    float m[G], l[G], acc[G][VD];
 #pragma unroll
     for (int hh = 0; hh < G; ++hh) {
         m[hh] = -INFINITY;
         l[hh] = 0.0f;
 #pragma unroll
-        for (int e = 0; e < DV; ++e) acc[hh][e] = 0.0f;
+        for (int e = 0; e < VD; ++e) acc[hh][e] = 0.0f;
     }
 
-    // one step ahead: K and V chunks in one of two register sets
-    uint32_t kbuf[2][CW], vbuf[2][CW];
-    float kscale[2], vscale[2];
-    auto issue = [&](int j0, int set) {
-        const int j = min(j0 + tl, L - 1);                // clamped: masked later
-        Chunk<KT>::load(kb + (int64_t)j * a.k_nb_tok, c, kbuf[set], kscale[set]);
-        Chunk<KT>::load(vb + (int64_t)j * a.v_nb_tok, c, vbuf[set], vscale[set]);
-    };
-    if (j_begin < j_end) issue(j_begin, 0);
-
     for (int i0 = j_begin; i0 < j_end; i0 += TPI) {
+        // ---------------- K phase
         float sc[SPI][G];
         float dvs[SPI];
         bool live[SPI];
         float mv[SPI];
 #pragma unroll
         for (int st = 0; st < SPI; ++st) {
-            const int j0 = i0 + st * TPS;
-            const int cur = SPI == 2 ? st : 0;
-            // the second step of an iteration is always loaded (rows clamped to
-            // the window) so staged values stay finite where p = 0; the next
-            // iteration's first step only if it exists
-            const bool more = (st + 1 < SPI) || (i0 + TPI < j_end);
-            if constexpr (SPI == 2) {
-                if (more) issue(j0 + TPS, st ^ 1);
-            } else {
-#pragma unroll
-                for (int k = 0; k < CW; ++k) { kbuf[1][k] = kbuf[0][k]; vbuf[1][k] = vbuf[0][k]; }
-                kscale[1] = kscale[0];
-                vscale[1] = vscale[0];
-                if (more) issue(j0 + TPS, 0);
-            }
-            const int rs = SPI == 2 ? cur : 1;
-            const uint32_t* kc = kbuf[rs];
-            const uint32_t* vc = vbuf[rs];
-            {
-                uint32_t* dst = (uint32_t*)(my_stage + ((st * TPS + tl) * LPT + c) * SLOT);
-#pragma unroll
-                for (int k = 0; k < CW; ++k) dst[k] = vc[k];
-            }
-            dvs[st] = vscale[rs];
-            const int j = j0 + tl;
+            const int j = i0 + st * TPS + tl;
             mv[st] = 0.0f;
             if (a.mask_mode == kMaskExplicit && j < j_end)
                 mv[st] = f16_to_f32(*(const uint16_t*)(mrow + 2 * (int64_t)j)) * kLog2e;
             live[st] = j < j_end && mv[st] != -INFINITY;
+            const uint32_t* kc = kbuf[st];
             if constexpr (Q8) {
+                const int ksh = (c & 1) ? 0 : 2;
                 uint32_t kq[8];
 #pragma unroll
                 for (int k = 0; k < 8; ++k) kq[k] = __builtin_amdgcn_alignbyte(kc[k + 1], kc[k], ksh);
-                const float dk = kscale[rs];
+                const float dk = ksc[st];
+                dvs[st] = vsc[st];
 #pragma unroll
                 for (int hh = 0; hh < G; ++hh) {
-                    int si = 0;
+                    int si = sdot4_first(qw[hh][0], kq[0]);
 #pragma unroll
-                    for (int k = 0; k < 8; ++k) si = __builtin_amdgcn_sdot4((int)qw[hh][k], (int)kq[k], si, false);
+                    for (int k = 1; k < 8; ++k) si = __builtin_amdgcn_sdot4((int)qw[hh][k], (int)kq[k], si, false);
                     sc[st][hh] = (float)si * (dk * qd[hh]);
                 }
             } else {
+                dvs[st] = 1.0f;
 #pragma unroll
                 for (int hh = 0; hh < G; ++hh) {
                     float d0 = 0.0f, d1 = 0.0f;
 #pragma unroll
-                    for (int k = 0; k < 16; k += 2) {
+                    for (int k = 0; k < 8; k += 2) {
                         if constexpr (KT == VVA_TYPE_BF16) {
                             d0 = dot2_bf16(qw[hh][k], kc[k], d0);
                             d1 = dot2_bf16(qw[hh][k + 1], kc[k + 1], d1);
@@ -358,6 +427,7 @@ decode_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split_len) {
                     sc[st][hh] = (d0 + d1) * qd[hh];
                 }
             }
+            issue_k(i0 + TPI, st);
         }
         {
             float* flat = &sc[0][0];
@@ -370,11 +440,15 @@ decode_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split_len) {
 #pragma unroll
                 for (int hh = 0; hh < G; ++hh) sc[st][hh] += mv[st];
         }
+        // keys past the wave's range or masked to -inf: only the last
+        // iteration and explicit masks have any
+        if (i0 + TPI > j_end || a.mask_mode == kMaskExplicit) {
 #pragma unroll
-        for (int st = 0; st < SPI; ++st)
+            for (int st = 0; st < SPI; ++st)
 #pragma unroll
-            for (int hh = 0; hh < G; ++hh) sc[st][hh] = live[st] ? sc[st][hh] : -INFINITY;
-        // ---------------- online softmax, running max raised lazily
+                for (int hh = 0; hh < G; ++hh) sc[st][hh] = live[st] ? sc[st][hh] : -INFINITY;
+        }
+        // online softmax, running max raised lazily
         bool raise = false;
 #pragma unroll
         for (int hh = 0; hh < G; ++hh) {
@@ -398,7 +472,7 @@ decode_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split_len) {
                     const float alpha = __builtin_amdgcn_exp2f(m[hh] - cm[hh]);   // 0 when m = -inf
                     l[hh] *= alpha;
 #pragma unroll
-                    for (int e = 0; e < DV; ++e) acc[hh][e] *= alpha;
+                    for (int e = 0; e < VD; ++e) acc[hh][e] *= alpha;
                     m[hh] = cm[hh];
                 }
             }
@@ -418,91 +492,78 @@ decode_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split_len) {
 #pragma unroll
         for (int st = 0; st < SPI; ++st) {
             const int u = st * TPS + tl;
-            uint16_t* dst = (uint16_t*)&pbuf[w][c][u >> 1][0] + (u & 1);
+            uint16_t* dst = (uint16_t*)&pbuf[w][Q8 ? c : 0][u >> 1][0] + (u & 1);
+            if constexpr (Q8) {
 #pragma unroll
-            for (int hh = 0; hh < G; ++hh) dst[2 * hh] = f32_to_f16(sc[st][hh] * dvs[st]);
+                for (int hh = 0; hh < G; ++hh) dst[2 * hh] = f32_to_f16(sc[st][hh] * dvs[st]);
+            } else {
+                // the LPT lanes of a key hold the same p: lane c writes heads c, c + LPT, ...
+#pragma unroll
+                for (int hh = 0; hh < G; ++hh)
+                    if (hh % LPT == c) dst[2 * hh] = f32_to_f16(sc[st][hh]);
+            }
         }
         wave_lds_sync();
-        // ---------------- V phase: lane owns dims [lane*DV, lane*DV + DV)
-        const int dim0 = lane * DV;
-        const int cc = dim0 / 32, e0 = dim0 % 32;
-        const int voff = Chunk<KT>::shift(cc) + (Q8 ? e0 : 2 * e0);
+        // ---------------- V phase: lane owns dims [2 dg, 2 dg + 2) of its key pairs
 #pragma unroll
-        for (int u = 0; u < TPI; u += 2) {
-            const char* s0 = my_stage + (u * LPT + cc) * SLOT + voff;
-            const char* s1 = s0 + LPT * SLOT;
-            uint32_t x[DV];                   // f16 pairs (key u, key u+1) per owned dim
-            typedef _Float16 hv2 __attribute__((ext_vector_type(2)));
+        for (int k = 0; k < PPI; ++k) {
+            const int pi = kg + KG * k;
+            uint32_t x[VD];           // f16 pairs (key 2 pi, key 2 pi + 1), one per dim
+            const vword wa = vbuf[k][0], wb = vbuf[k][1];
             if constexpr (Q8) {
-                if constexpr (DV == 2) {
-                    const uint32_t w0 = *(const uint16_t*)s0;
-                    const uint32_t w1 = *(const uint16_t*)s1;
-                    hv2 a0 = {code_f16(w0 & 0xff), code_f16(w1 & 0xff)};
-                    hv2 a1 = {code_f16(w0 >> 8), code_f16(w1 >> 8)};
-                    __builtin_memcpy(&x[0], &a0, 4);
-                    __builtin_memcpy(&x[1], &a1, 4);
-                } else {
-                    hv2 a0 = {code_f16((uint8_t)s0[0]), code_f16((uint8_t)s1[0])};
-                    __builtin_memcpy(&x[0], &a0, 4);
-                }
+                x[0] = i8_pair_b0(wa, wb);
+                x[1] = i8_pair_b1(wa, wb);
+            } else if constexpr (KT == VVA_TYPE_F16) {
+                x[0] = __builtin_amdgcn_perm(wb, wa, 0x05040100u);
+                x[1] = __builtin_amdgcn_perm(wb, wa, 0x07060302u);
             } else {
-                if constexpr (DV == 2) {
-                    uint32_t w0 = *(const uint32_t*)s0;
-                    uint32_t w1 = *(const uint32_t*)s1;
-                    if constexpr (KT == VVA_TYPE_BF16) {
-                        w0 = pack2<VVA_TYPE_F16>(bf16_to_f32(w0 & 0xffffu), bf16_to_f32(w0 >> 16));
-                        w1 = pack2<VVA_TYPE_F16>(bf16_to_f32(w1 & 0xffffu), bf16_to_f32(w1 >> 16));
-                    }
-                    x[0] = (w0 & 0xffffu) | (w1 << 16);
-                    x[1] = (w0 >> 16) | (w1 & 0xffff0000u);
-                } else {
-                    uint32_t w0 = *(const uint16_t*)s0;
-                    uint32_t w1 = *(const uint16_t*)s1;
-                    if constexpr (KT == VVA_TYPE_BF16) {
-                        w0 = f32_to_f16(bf16_to_f32(w0));
-                        w1 = f32_to_f16(bf16_to_f32(w1));
-                    }
-                    x[0] = w0 | (w1 << 16);
-                }
+                h2 lo = {(_Float16)__uint_as_float(wa << 16), (_Float16)__uint_as_float(wb << 16)};
+                h2 hi = {(_Float16)__uint_as_float(wa & 0xffff0000u), (_Float16)__uint_as_float(wb & 0xffff0000u)};
+                __builtin_memcpy(&x[0], &lo, 4);
+                __builtin_memcpy(&x[1], &hi, 4);
             }
+            // convert before the next iteration's load of the same key is
+            // issued, so it can land in the register just freed
+            __builtin_amdgcn_sched_barrier(0);
+            issue_v(i0 + TPI, k);
             uint32_t pw[GP];
-            const uint32_t* prow = &pbuf[w][cc][u >> 1][0];
-            if constexpr (GP % 4 == 0) {
+            const uint32_t* prow = &pbuf[w][pblk][pi][0];
 #pragma unroll
-                for (int k = 0; k < GP; k += 4) {
-                    const uint4 q4 = *(const uint4*)(prow + k);
-                    pw[k] = q4.x; pw[k + 1] = q4.y; pw[k + 2] = q4.z; pw[k + 3] = q4.w;
-                }
-            } else {
-#pragma unroll
-                for (int k = 0; k < GP; ++k) pw[k] = prow[k];
+            for (int q = 0; q < GP; q += 4) {
+                const uint4 q4 = *(const uint4*)(prow + q);
+                pw[q] = q4.x; pw[q + 1] = q4.y; pw[q + 2] = q4.z; pw[q + 3] = q4.w;
             }
 #pragma unroll
             for (int hh = 0; hh < G; ++hh)
 #pragma unroll
-                for (int e = 0; e < DV; ++e) acc[hh][e] = dot2_f16(pw[hh], x[e], acc[hh][e]);
+                for (int e = 0; e < VD; ++e) acc[hh][e] = dot2_f16(pw[hh], x[e], acc[hh][e]);
+            // keep each pair's LDS reads next to their use: hoisting them all
+            // would cost a register set per pair
+            __builtin_amdgcn_sched_barrier(0);
         }
         wave_lds_sync();
     }
 
-    // l over the lanes (each key counted by its LPT lanes)
+    // l over the lanes (each key counted by its LPT lanes); acc over the key
+    // groups (lanes dg, dg + DG, ...)
 #pragma unroll
-    for (int hh = 0; hh < G; ++hh) {
+    for (int hh = 0; hh < G; ++hh) l[hh] = wave_sum(l[hh]) * (1.0f / LPT);
+    if constexpr (KG == 2) {
 #pragma unroll
-        for (int msk = 1; msk < 64; msk <<= 1) l[hh] += __shfl_xor(l[hh], msk, 64);
-        l[hh] *= 1.0f / LPT;
+        for (int hh = 0; hh < G; ++hh)
+#pragma unroll
+            for (int e = 0; e < VD; ++e) acc[hh][e] = add_swap32(acc[hh][e]);
     }
 
-    // ---- merge the R waves of each kv head (log-sum-exp) through LDS
+    // ---- merge the R waves of each kv head (log-sum-exp) through LDS; the
+    // key groups hold identical sums, the first writes
     float (*abuf)[G][D] = (float (*)[G][D])smem;
     if (R > 1) {
-        __syncthreads();                    // every wave is done with its V staging
         if (r > 0) {
 #pragma unroll
             for (int hh = 0; hh < G; ++hh) {
                 if (lane == 0) { mbuf[w][hh] = m[hh]; lbuf[w][hh] = l[hh]; }
-#pragma unroll
-                for (int e = 0; e < DV; ++e) abuf[w][hh][lane * DV + e] = acc[hh][e];
+                if (kg == 0) *(float2*)&abuf[w][hh][dg * VD] = make_float2(acc[hh][0], acc[hh][1]);
             }
         }
         __syncthreads();
@@ -516,19 +577,21 @@ decode_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split_len) {
                 const float fa = mn == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m[hh] - mn);
                 const float fb = mn == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mo - mn);
                 l[hh] = l[hh] * fa + lbuf[ow][hh] * fb;
-#pragma unroll
-                for (int e = 0; e < DV; ++e) acc[hh][e] = acc[hh][e] * fa + abuf[ow][hh][lane * DV + e] * fb;
+                const float2 o = *(const float2*)&abuf[ow][hh][dg * VD];
+                acc[hh][0] = acc[hh][0] * fa + o.x * fb;
+                acc[hh][1] = acc[hh][1] * fa + o.y * fb;
                 m[hh] = mn;
             }
         }
     }
+    // the KG copies of each head's row split the stores: group kg writes heads kg, kg + KG, ...
     if (n_splits == 1) {
 #pragma unroll
         for (int hh = 0; hh < G; ++hh) {
+            if (hh % KG != kg) continue;
             const float inv = l[hh] == 0.0f ? 0.0f : 1.0f / l[hh];
             float* orow = (float*)((char*)a.out + b * a.o_nb_b + (h0 + hh) * a.o_nb_h);
-#pragma unroll
-            for (int e = 0; e < DV; ++e) orow[lane * DV + e] = acc[hh][e] * inv;
+            *(float2*)(orow + dg * VD) = make_float2(acc[hh][0] * inv, acc[hh][1] * inv);
         }
         return;
     }
@@ -537,70 +600,85 @@ decode_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split_len) {
     float* wml = ws + (size_t)a.B * a.Hq * n_splits * D;
 #pragma unroll
     for (int hh = 0; hh < G; ++hh) {
+        if (hh % KG != kg) continue;
         const size_t idx = ((size_t)b * a.Hq + (h0 + hh)) * n_splits + split;
-#pragma unroll
-        for (int e = 0; e < DV; ++e) wacc[idx * D + lane * DV + e] = acc[hh][e];
-        if (lane == 0) { wml[idx * 2] = m[hh]; wml[idx * 2 + 1] = l[hh]; }
+        *(float2*)(wacc + idx * D + dg * VD) = make_float2(acc[hh][0], acc[hh][1]);
+        if (dg == 0) *(float2*)(wml + idx * 2) = make_float2(m[hh], l[hh]);
     }
 }
 
-// One workgroup of 1024 threads per (query head, batch): the split maxima go
-// through LDS once, then 1024 / D groups of D threads each keep up to
-// kMergeDepth partial rows in flight (clamped unconditional loads, so they
-// issue together) and their sums meet in LDS.
-constexpr int kMergeThreads = 1024;
+// One workgroup of 256 threads per (query head, sequence): 256 / (D/4)
+// groups of D/4 threads each take every NG-th split, with up to kMergeDepth
+// partial rows (float4 per thread) in flight at once, fold them with a
+// running log-sum-exp, and the groups meet in LDS.  For n_splits <= NG *
+// kMergeDepth (128 at D = 128) every load goes out in one round trip.
+constexpr int kMergeThreads = 256;
 constexpr int kMergeDepth = 16;
 
 template <int D>
 __global__ void __launch_bounds__(kMergeThreads) decode_merge_kernel(AttnArgs a, const float* __restrict__ ws,
                                                                      int n_splits) {
-    constexpr int NG = kMergeThreads / D;
-    __shared__ float wmax[kMergeThreads / 64];
-    __shared__ float num_s[NG][D];
-    __shared__ float den_s[NG];
-    const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
-    const int grp = tid / D, i = tid % D;
-    const float* wacc = ws;
-    const float* wml = ws + (size_t)a.B * a.Hq * n_splits * D;
+    constexpr int TPR = D / 4;                  // threads per partial row
+    constexpr int NG = kMergeThreads / TPR;     // row groups
+    __shared__ float sm[NG], sden[NG];
+    __shared__ float4 snum[NG][TPR];
+    const int h = blockIdx.x, b = blockIdx.y;
+    const int grp = threadIdx.x / TPR, i4 = threadIdx.x % TPR;
     const size_t base = ((size_t)b * a.Hq + h) * n_splits;
-    float M = -INFINITY;
-    for (int s = tid; s < n_splits; s += kMergeThreads) M = fmaxf(M, wml[(base + s) * 2]);
+    const float4* wacc = (const float4*)ws + base * TPR;
+    const float* wml = ws + (size_t)a.B * a.Hq * n_splits * D + base * 2;
+    float M = -INFINITY, den = 0.0f;
+    float4 num = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int s0 = grp; s0 < n_splits; s0 += NG * kMergeDepth) {
+        float4 av[kMergeDepth];
+        float mv[kMergeDepth], lv[kMergeDepth];
 #pragma unroll
-    for (int msk = 32; msk >= 1; msk >>= 1) M = fmaxf(M, __shfl_xor(M, msk, 64));
-    if ((tid & 63) == 0) wmax[tid >> 6] = M;
+        for (int k = 0; k < kMergeDepth; ++k) {
+            const int s = min(s0 + k * NG, n_splits - 1);     // clamped: unconditional loads
+            av[k] = wacc[(size_t)s * TPR + i4];
+            const float2 ml = *(const float2*)(wml + 2 * s);
+            mv[k] = s0 + k * NG < n_splits ? ml.x : -INFINITY;
+            lv[k] = ml.y;
+        }
+        float mn = M;
+#pragma unroll
+        for (int k = 0; k < kMergeDepth; ++k) mn = fmaxf(mn, mv[k]);
+        if (mn == -INFINITY) continue;                        // nothing visible yet
+        const float f0 = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(M - mn);
+        num.x *= f0; num.y *= f0; num.z *= f0; num.w *= f0;
+        den *= f0;
+#pragma unroll
+        for (int k = 0; k < kMergeDepth; ++k) {
+            const float f = __builtin_amdgcn_exp2f(mv[k] - mn);   // 0 for -inf
+            num.x = fmaf(av[k].x, f, num.x);
+            num.y = fmaf(av[k].y, f, num.y);
+            num.z = fmaf(av[k].z, f, num.z);
+            num.w = fmaf(av[k].w, f, num.w);
+            den = fmaf(lv[k], f, den);
+        }
+        M = mn;
+    }
+    if (i4 == 0) { sm[grp] = M; sden[grp] = den; }
+    snum[grp][i4] = num;
     __syncthreads();
-    M = wmax[0];
+    if (grp != 0) return;
+    float MM = -INFINITY;
 #pragma unroll
-    for (int k = 1; k < kMergeThreads / 64; ++k) M = fmaxf(M, wmax[k]);
-    float num = 0.0f, den = 0.0f;
-    if (M != -INFINITY) {
-        for (int s0 = grp; s0 < n_splits; s0 += NG * kMergeDepth) {
-            float av[kMergeDepth], mv[kMergeDepth], lv[kMergeDepth];
+    for (int g = 0; g < NG; ++g) MM = fmaxf(MM, sm[g]);
+    float4 n = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float d = 0.0f;
+    if (MM != -INFINITY) {
 #pragma unroll
-            for (int k = 0; k < kMergeDepth; ++k) {
-                const size_t id = base + min(s0 + k * NG, n_splits - 1);
-                av[k] = wacc[id * D + i];
-                mv[k] = wml[id * 2];
-                lv[k] = wml[id * 2 + 1];
-            }
-#pragma unroll
-            for (int k = 0; k < kMergeDepth; ++k) {
-                const float f = s0 + k * NG < n_splits ? __builtin_amdgcn_exp2f(mv[k] - M) : 0.0f;
-                num = fmaf(av[k], f, num);
-                den = fmaf(lv[k], f, den);
-            }
+        for (int g = 0; g < NG; ++g) {
+            const float f = __builtin_amdgcn_exp2f(sm[g] - MM);      // 0 for -inf
+            const float4 v = snum[g][i4];
+            n.x = fmaf(v.x, f, n.x); n.y = fmaf(v.y, f, n.y); n.z = fmaf(v.z, f, n.z); n.w = fmaf(v.w, f, n.w);
+            d = fmaf(sden[g], f, d);
         }
     }
-    num_s[grp][i] = num;
-    if (i == 0) den_s[grp] = den;
-    __syncthreads();
-    if (grp == 0) {
-        float n = 0.0f, d = 0.0f;
-#pragma unroll
-        for (int k = 0; k < NG; ++k) { n += num_s[k][i]; d += den_s[k]; }
-        float* orow = (float*)((char*)a.out + b * a.o_nb_b + h * a.o_nb_h);
-        orow[i] = d == 0.0f ? 0.0f : n / d;
-    }
+    const float inv = d == 0.0f ? 0.0f : 1.0f / d;
+    float* orow = (float*)((char*)a.out + b * a.o_nb_b + h * a.o_nb_h);
+    *(float4*)(orow + 4 * i4) = make_float4(n.x * inv, n.y * inv, n.z * inv, n.w * inv);
 }
 
 template <int D, int KT>
@@ -631,12 +709,17 @@ bool decode_supported(const AttnArgs& a) {
     if (a.Hq % a.Hkv != 0 || a.Hq / a.Hkv > 8) return false;
     if (kWaves % a.Hkv != 0) return false;
     if (a.mask_mode == kMaskExplicit && (a.mask_nb_b % 2 != 0)) return false;
-    // vector-load alignment of cache rows and Q rows
+    // vector-load alignment of cache rows, Q rows and output rows
     const int64_t need = a.k_type == VVA_TYPE_Q8_0 ? 4 : 16;
     if (a.k_nb_tok % need || a.k_nb_head % need || a.v_nb_tok % need || a.v_nb_head % need) return false;
     for (int b = 0; b < a.B; ++b)
         if (((uintptr_t)a.k[b] % need) || ((uintptr_t)a.v[b] % need)) return false;
+    // 32-bit buffer offsets: rows up to one iteration past the last key
+    for (int b = 0; b < a.B; ++b)
+        if ((int64_t)(a.L[b] + 64) * a.k_nb_tok >= ((int64_t)1 << 31) ||
+            (int64_t)(a.L[b] + 64) * a.v_nb_tok >= ((int64_t)1 << 31)) return false;
     if (((uintptr_t)a.q % 16) || a.q_nb_h % 16 || a.q_nb_b % 16) return false;
+    if (((uintptr_t)a.out % 16) || a.o_nb_h % 16 || a.o_nb_b % 16) return false;
     return true;
 }
 
