@@ -157,3 +157,27 @@ def test_full_size_7b_prefill_row_subset(ctx, torch_gpu):
     ref = oracle_attn(as_f32(torch, q), kv, 0, [0], [T], T, d ** -0.5, rows=rows)
     assert_close(o[0, rows], ref[0, rows], *TOL, what="32k subset")
     kv.free()
+
+
+def test_prefill_score_jump_restarts_key_loop(ctx, torch_gpu):
+    """Scores of later keys exceed the first tile's by far more than 2^15 in
+    the exp2 domain: the kernel's reference max must be raised (key loop
+    restarted) without overflowing the f16 probabilities."""
+    torch = torch_gpu
+    d, Hq, Hkv, T = 128, 28, 4, 400
+    rng = np.random.default_rng(11)
+    k = rng.standard_normal((1, T, Hkv, d)) * 0.05
+    k[:, 150:] *= 160.0                               # logits up to ~x60 larger after key 150
+    v = rng.standard_normal((1, T, Hkv, d))
+    kv = vva.KVCache(ctx, 1, Hkv, d, T, 1, vva.F16)
+    kv.upload(0, 0, 0, k[0].astype(np.float32), v[0].astype(np.float32))
+    kv.set_len(0, 0)
+    q = to_gpu(torch, rng.standard_normal((1, T, Hq, d)), vva.F16)
+    out = torch.full((1, T, Hq, d), float("nan"), dtype=torch.float32, device="cuda")
+    ctx.attn(kv, 0, q, out, d ** -0.5)
+    torch.cuda.synchronize()
+    o = as_f32(torch, out)
+    assert np.isfinite(o).all()
+    ref = oracle_attn(as_f32(torch, q), kv, 0, [0], [T], T, d ** -0.5)
+    assert_close(o, ref, *TOL, what="score jump")
+    kv.free()

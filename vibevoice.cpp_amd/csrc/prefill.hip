@@ -41,12 +41,20 @@ typedef __bf16 b8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLazy = 15.0f;     // running-max slack in log2 units: p <= 2^15 (f16-safe)
 constexpr int kBN = 64;        // keys per tile
 constexpr int kRowsWave = 64;  // query rows per wave
 constexpr int kWaves = 4;
 constexpr int kRowsWG = kRowsWave * kWaves;
+
+// max of x over lanes l and l ^ 32 (v_permlane32_swap exchanges the halves)
+__device__ __forceinline__ float max_swap32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
 
 template <int KT> struct Frag;
 template <> struct Frag<VVA_TYPE_F16> {
@@ -76,7 +84,8 @@ __device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t x) {
     return (uint32_t)f32_to_f16(lo) | ((uint32_t)f32_to_f16(hi) << 16);
 }
 
-template <int D, int KT>
+// EXPL: explicit F16 mask (otherwise implicit causal / length masking only).
+template <int D, int KT, bool EXPL>
 __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a) {
     using F = Frag<KT>;
     using QF = typename F::type;
@@ -102,8 +111,8 @@ __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a) {
     const int R0 = (n_rt - 1 - (int)blockIdx.x) * kRowsWG;    // heaviest tiles first
     const int wr0 = R0 + w * kRowsWave;
     const int L = a.L[b], past = a.past[b];
-    const bool causal = a.mask_mode == kMaskCausal;
-    const bool explicit_mask = a.mask_mode == kMaskExplicit;
+    const bool causal = !EXPL && a.mask_mode == kMaskCausal;
+    constexpr bool explicit_mask = EXPL;
 
     // key range of the workgroup and of this wave
     const int t_hi_wg = min(a.T - 1, (min(R0 + kRowsWG, nrows) - 1) / g);
@@ -216,83 +225,114 @@ __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a) {
         }
     };
 
+    // Per 64-key tile: both 32-key halves of S^T are issued on the MFMA pipe
+    // first, then each half's softmax VALU runs while the MFMAs of the other
+    // half or of the previous P.V product are in flight.
+    //
+    // The reference max m of a row is fixed by the first tile with a visible
+    // key and never moves inside the tile loop, so O stays in MFMA
+    // accumulators with no VALU rescale: p = 2^(x - m) is allowed up to 2^15
+    // (f16).  If a row's score exceeds m + 15 (rare: logits rarely grow by
+    // 2^15 after the first tile), the workgroup restarts its key loop from
+    // tile 0 with the raised m (each restart raises it by more than 15, so
+    // restarts are few).
+    for (;;) {
     if (n_tiles > 0) {
         load_tile(0);
         store_tile(0);
     }
     __syncthreads();
-
+    bool restart = false;
     for (int j = 0; j < n_tiles; ++j) {
         const int stage = j & 1;
         if (j + 1 < n_tiles) load_tile(j + 1);
         const int k0 = j * kBN;
+        bool raise = false;
         if (k0 < kend_w) {
             const char* kb = lds + stage * STAGE;
             const char* vb = kb + KBUF;
-            const bool need_mask = explicit_mask || k0 + kBN > L || (causal && k0 + kBN - 1 > past + t_lo_w);
-            // the 64-key tile is processed as two 32-key halves to bound the
-            // number of live accumulators
+            // the second half is skipped when no row of the wave sees it
+            const bool two = !(causal && k0 + 32 > past + t_hi_w);             // wave-uniform
+            // ---------------- S^T = K Q^T (32 keys x 64 rows per half)
+            f32x16 s[2][2];
 #pragma unroll
             for (int kt = 0; kt < 2; ++kt) {
-                if (causal && k0 + kt * 32 > past + t_hi_w) break;     // wave-uniform
-                // ---------------- S^T = K Q^T (32 keys x 64 rows)
-                f32x16 s[2];
-#pragma unroll
-                for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) s[cb][r] = 0.0f;
 #pragma unroll
                 for (int ds = 0; ds < DS; ++ds) {
                     const QF kf = as_vec<QF>(*(const u32x4*)(kb + (kt * 32 + l32) * KROW + ds * 32 + half * 16));
 #pragma unroll
-                    for (int cb = 0; cb < 2; ++cb) s[cb] = F::mma(kf, qf[cb][ds], s[cb]);
+                    for (int cb = 0; cb < 2; ++cb)
+                        s[kt][cb] = ds == 0 ? F::mma(kf, qf[cb][0], f32x16{}) : F::mma(kf, qf[cb][ds], s[kt][cb]);
                 }
-                // ---------------- online softmax (exp2 domain)
-                h8 pf[2][2];
+                if (!two) break;
+            }
+            // ---------------- masks: raw scores, or scores already in the
+            // exp2 domain (scaled, mask added) when the mask is explicit
+            float mul = sl2;
+            const bool need_mask = EXPL || k0 + kBN > L || (causal && k0 + kBN - 1 > past + t_lo_w);
+            if (need_mask) {
 #pragma unroll
-                for (int cb = 0; cb < 2; ++cb) {
-                    float x[16];
+                for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) x[r] = s[cb][r] * sl2;
-                    if (need_mask) {
+                    for (int cb = 0; cb < 2; ++cb) {
                         const int lim = causal ? min(L - 1, past + tcol[cb]) : L - 1;
-                        const char* mrow =
-                            explicit_mask ? a.mask + b * a.mask_nb_b + tcol[cb] * a.mask_nb_row : nullptr;
 #pragma unroll
                         for (int r = 0; r < 16; ++r) {
                             const int key = k0 + kt * 32 + 8 * (r / 4) + 4 * half + (r % 4);
-                            if (key > lim) x[r] = -INFINITY;
-                            else if (explicit_mask)
-                                x[r] = fmaf(f16_to_f32(*(const uint16_t*)(mrow + 2 * key)), kLog2e, x[r]);
+                            float x = s[kt][cb][r];
+                            if constexpr (EXPL) {
+                                const char* mrow = a.mask + b * a.mask_nb_b + tcol[cb] * a.mask_nb_row;
+                                x = fmaf(x, sl2, f16_to_f32(*(const uint16_t*)(mrow + 2 * min(key, L - 1))) * kLog2e);
+                            }
+                            s[kt][cb][r] = (key > lim || (kt == 1 && !two)) ? -INFINITY : x;
                         }
                     }
-                    float mx = x[0];
+                if constexpr (EXPL) mul = 1.0f;
+            } else if (!two) {
 #pragma unroll
-                    for (int i = 1; i < 16; ++i) mx = fmaxf(mx, x[i]);
-                    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-                    const float mn = fmaxf(m[cb], mx);
-                    const float base = mn == -INFINITY ? 0.0f : mn;
-                    const float alpha = __builtin_amdgcn_exp2f(m[cb] - base);   // m = -inf -> 0
-                    m[cb] = mn;
-                    float ps = 0.0f;
+                for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) s[1][cb][r] = -INFINITY;
+            }
+            // ---------------- row max of the tile against the reference
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) {
+                float mx = fmaxf(s[0][cb][0], s[1][cb][0]);
+#pragma unroll
+                for (int r = 1; r < 16; ++r) mx = fmaxf(fmaxf(mx, s[0][cb][r]), s[1][cb][r]);
+                mx = max_swap32(mx) * mul;
+                if (m[cb] == -INFINITY) m[cb] = mx;        // O and the row sum are still 0
+                if (mx > m[cb] + kLazy) {
+                    raise = true;
+                    m[cb] = mx;                            // the restart uses the raised max
+                }
+            }
+            // a raising wave skips the rest of the tile: the restart discards it
+            if (!__any(raise)) {
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt) {
+                if (kt == 1 && !two) break;
+                // ---------------- p = 2^(x * mul - m) as f16, row sums from the f16 values
+                h8 pf[2][2];
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb) {
+                    const float nb = m[cb] == -INFINITY ? 0.0f : -m[cb];
+                    float ps = lsum[cb];
 #pragma unroll
                     for (int ks = 0; ks < 2; ++ks) {
                         h8 p;
 #pragma unroll
-                        for (int e = 0; e < 8; ++e) {
-                            const _Float16 ph = (_Float16)__builtin_amdgcn_exp2f(x[ks * 8 + e] - base);
-                            p[e] = ph;
-                            ps += (float)ph;
+                        for (int e = 0; e < 8; e += 2) {
+                            const float p0 = __builtin_amdgcn_exp2f(fmaf(s[kt][cb][ks * 8 + e], mul, nb));
+                            const float p1 = __builtin_amdgcn_exp2f(fmaf(s[kt][cb][ks * 8 + e + 1], mul, nb));
+                            h2 pp = {(_Float16)p0, (_Float16)p1};
+                            p[e] = pp.x;
+                            p[e + 1] = pp.y;
+                            ps = __builtin_amdgcn_fdot2(pp, h2{(_Float16)1.0f, (_Float16)1.0f}, ps, false);
                         }
                         pf[cb][ks] = p;
                     }
-                    lsum[cb] = lsum[cb] * alpha + ps;
-                    if (!__all(alpha == 1.0f)) {
-#pragma unroll
-                        for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-                            for (int r = 0; r < 16; ++r) o[dt][cb][r] *= alpha;
-                    }
+                    lsum[cb] = ps;
                 }
                 // ---------------- O^T += V^T P^T (the two 16-key steps of this half)
 #pragma unroll
@@ -310,9 +350,20 @@ __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a) {
                     }
                 }
             }
+            }
         }
         if (j + 1 < n_tiles) store_tile(stage ^ 1);
-        __syncthreads();
+        if (__syncthreads_or(raise)) {                      // workgroup-uniform
+            restart = true;
+            break;
+        }
+    }
+    if (!restart) break;
+    lsum[0] = lsum[1] = 0.0f;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) o[dt][cb] = f32x16{};
     }
 
     // ---- normalize and write (each lane owns one row per column block)
@@ -341,7 +392,10 @@ hipError_t launch_pf(const AttnArgs& a, hipStream_t s) {
     const int g = a.Hq / a.Hkv;
     const int nrows = a.T * g;
     dim3 grid((nrows + kRowsWG - 1) / kRowsWG, a.Hkv, a.B);
-    hipLaunchKernelGGL((prefill_kernel<D, KT>), grid, dim3(256), 0, s, a);
+    if (a.mask_mode == kMaskExplicit)
+        hipLaunchKernelGGL((prefill_kernel<D, KT, true>), grid, dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL((prefill_kernel<D, KT, false>), grid, dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
