@@ -12,24 +12,35 @@
 // workgroup is 4 waves x 64 rows and walks the key tiles (64 keys) its rows
 // can see; row tiles are issued heaviest-first for the causal imbalance.
 //
+// Staging.  K and V tiles go from HBM straight into LDS with buffer loads
+// that write LDS (no registers, no VALU), into a ring of three stages: the
+// loads of tile j + 2 are issued while tile j is computed.  Both tiles are
+// kept row-major ([key][dim], rows padded by 16 bytes against bank
+// conflicts); the V^T operand of the second product is read with
+// ds_read_b64_tr_b16, whose 16-lane transpose hands each lane 4 consecutive
+// keys of one dim.  Keys past L read as 0 through the buffer range check.
+//
 // Per wave and key tile, with v_mfma_f32_32x32x16_{f16,bf16}:
 //   S^T[key][row] = K . Q^T  A = K rows from LDS (16 B per lane), B = Q^T
 //                            held in registers for the whole kernel, so each
 //                            lane owns one query row (column) of S^T and the
 //                            softmax row reductions are in-register plus one
 //                            cross-half exchange;
-//   online softmax           fp32, exp2 domain, causal / length / explicit
-//                            masks applied only on tiles that need them;
-//   O^T[d][row] += V^T . P^T A = V^T from LDS (stored transposed),
-//                            B = P^T converted in place from the S^T
+//   softmax                  fp32, exp2 domain; masks only on the tiles that
+//                            need them (interior tiles run a branch-free path);
+//   O^T[d][row] += V^T . P^T B = P^T converted in place from the S^T
 //                            accumulators: the key order of an MFMA step is
 //                            chosen to be the one the accumulator layout
 //                            already has, so no shuffle is needed.
-// P and V enter the second product as f16 (BF16 V is converted on its way to
-// LDS): an 8-bit-mantissa P would cost up to ~4e-3 on short rows, f16 P stays
-// below 4e-4.  Q is rounded to K's type, as ggml's CPU flash attention does.
-// K/V tiles are double-buffered in LDS: the next tile's global loads are in
-// flight while the current tile is computed.
+// The reference max m of a row is fixed by the first tile (key 0 is visible
+// to every row) and never moves inside the tile loop, so O stays in MFMA
+// accumulators with no rescale: p = 2^(x - m) may grow to 2^15 (f16).  A row
+// whose score exceeds m + 15 (rare: logits rarely grow by 2^15 after the
+// first tile) makes the workgroup restart its key loop with the raised m.
+// P and V enter the second product as f16 (BF16 V is converted after the
+// transposing read): an 8-bit-mantissa P would cost up to ~4e-3 on short
+// rows, f16 P stays below 4e-4.  Q is rounded to K's type, as ggml's CPU
+// flash attention does.
 #include "vva_internal.hpp"
 
 namespace vva {
@@ -37,18 +48,51 @@ namespace vva {
 namespace {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef __bf16 b8 __attribute__((ext_vector_type(8)));
+typedef short s4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) char lds_char;
 
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kLazy = 15.0f;     // running-max slack in log2 units: p <= 2^15 (f16-safe)
-constexpr int kBN = 64;        // keys per tile
-constexpr int kRowsWave = 64;  // query rows per wave
+constexpr float kLazy = 15.0f;     // headroom of p over 2^0 in log2 units: p <= 2^15 (f16-safe)
+constexpr int kBN = 64;            // keys per tile
+constexpr int kRowsWave = 64;      // query rows per wave
 constexpr int kWaves = 4;
 constexpr int kRowsWG = kRowsWave * kWaves;
+constexpr int kStages = 3;
+
+// buffer_load_dwordx4 ... lds: each lane's 16 bytes land at LDS address
+// m0 + 16 * lane.  Issued as inline asm so the compiler does not fence LDS
+// reads on them; completion is waited for explicitly (wait_vmcnt) before the
+// workgroup barrier that publishes a stage.
+__device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t lds_addr, int voffset, int soffset) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :
+                 : "s"(lds_addr), "v"(voffset), "s"(rsrc), "s"(soffset)
+                 : "memory", "m0");
+}
+
+__device__ __forceinline__ i32x4 make_rsrc(const char* base, uint32_t bytes) {
+    const __amdgpu_buffer_rsrc_t r =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), (short)0, (int)bytes, 0x00020000);
+    i32x4 v;
+    __builtin_memcpy(&v, &r, 16);
+    // wave-uniform: keep it in SGPRs for the inline-asm loads
+    return i32x4{__builtin_amdgcn_readfirstlane(v.x), __builtin_amdgcn_readfirstlane(v.y),
+                 __builtin_amdgcn_readfirstlane(v.z), __builtin_amdgcn_readfirstlane(v.w)};
+}
+
+// wait until at most N of this wave's loads are outstanding (and its LDS
+// operations are done), then meet the workgroup at a barrier
+template <int N>
+__device__ __forceinline__ void wait_vm_barrier() {
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(N) : "memory");
+}
 
 // max of x over lanes l and l ^ 32 (v_permlane32_swap exchanges the halves)
 __device__ __forceinline__ float max_swap32(float x) {
@@ -72,6 +116,10 @@ template <> struct Frag<VVA_TYPE_BF16> {
     static __device__ __forceinline__ uint16_t cvt(float x) { return f32_to_bf16(x); }
 };
 
+__device__ __forceinline__ float bits16_to_f32(uint32_t v, int type) {
+    return type == VVA_TYPE_BF16 ? bf16_to_f32((uint16_t)v) : f16_to_f32((uint16_t)v);
+}
+
 template <typename V>
 __device__ __forceinline__ V as_vec(const u32x4& u) {
     V v;
@@ -79,9 +127,31 @@ __device__ __forceinline__ V as_vec(const u32x4& u) {
     return v;
 }
 
-__device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t x) {
-    const float lo = __uint_as_float(x << 16), hi = __uint_as_float(x & 0xffff0000u);
-    return (uint32_t)f32_to_f16(lo) | ((uint32_t)f32_to_f16(hi) << 16);
+// V^T fragment of the second product: dims dt*32 + l%32, keys k0 + (0..3)
+// and k1 + (0..3), from the row-major V tile.  In each 16-lane group, lane i
+// points at row k + i/4, dims d0 + 4 (i%4) .. +3; the transposing read then
+// gives lane i the 4 keys of dim d0 + i.
+template <int KT>
+__device__ __forceinline__ h8 v_frag(const lds_char* vrow0, const lds_char* vrow1) {
+    const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)vrow0);
+    const s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)vrow1);
+    h8 v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const uint16_t x = (uint16_t)lo[e], y = (uint16_t)hi[e];
+        if constexpr (KT == VVA_TYPE_BF16) {
+            // the 16-bit patterns are bf16: widen to f32 and round to f16
+            v[e] = (_Float16)bf16_to_f32(x);
+            v[e + 4] = (_Float16)bf16_to_f32(y);
+        } else {
+            _Float16 fx, fy;
+            __builtin_memcpy(&fx, &x, 2);
+            __builtin_memcpy(&fy, &y, 2);
+            v[e] = fx;
+            v[e + 4] = fy;
+        }
+    }
+    return v;
 }
 
 // EXPL: explicit F16 mask (otherwise implicit causal / length masking only).
@@ -89,21 +159,19 @@ template <int D, int KT, bool EXPL>
 __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a) {
     using F = Frag<KT>;
     using QF = typename F::type;
-    constexpr int DS = D / 16;                 // 16-dim MFMA steps of Q.K
-    constexpr int DT = D / 32;                 // 32-dim output tiles
-    constexpr int KROW = D * 2 + 16;           // LDS bytes per K row (padded)
-    constexpr int VROW = kBN * 2 + 8;          // LDS bytes per V^T row (padded)
-    constexpr int KBUF = kBN * KROW;
-    constexpr int VBUF = D * VROW;
-    constexpr int STAGE = KBUF + VBUF;
-    constexpr int KCH = D / 8;                 // 16-byte chunks per K row
-    constexpr int KLD = kBN * KCH / 256;       // K chunks loaded per thread
-    constexpr int VITEMS = (kBN / 4) * (D / 8);  // (4 keys x 8 dims) items per V tile
+    constexpr int DS = D / 16;                     // 16-dim MFMA steps of Q.K
+    constexpr int DT = D / 32;                     // 32-dim output tiles
+    constexpr int RP = D * 2 + 16;                 // LDS bytes per K / V row (padded)
+    constexpr int RB = kBN * RP;                   // bytes of one tile
+    constexpr int NI = (RB + 4096 - 1) / 4096;     // 1 KB loads per wave per tile and operand
+    constexpr int REG = NI * 4096;                 // LDS bytes per operand and stage
+    constexpr int STAGE = 2 * REG;                 // K then V
 
-    __shared__ __attribute__((aligned(16))) char lds[2 * STAGE];
+    __shared__ __attribute__((aligned(16))) char lds[kStages * STAGE];
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, w = tid >> 6, half = lane >> 5, l32 = lane & 31;
+    const int lane = tid & 63, half = lane >> 5, l32 = lane & 31;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int b = blockIdx.z, kvh = blockIdx.y;
     const int g = a.Hq / a.Hkv;
     const int nrows = a.T * g;
@@ -112,7 +180,6 @@ __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a) {
     const int wr0 = R0 + w * kRowsWave;
     const int L = a.L[b], past = a.past[b];
     const bool causal = !EXPL && a.mask_mode == kMaskCausal;
-    constexpr bool explicit_mask = EXPL;
 
     // key range of the workgroup and of this wave
     const int t_hi_wg = min(a.T - 1, (min(R0 + kRowsWG, nrows) - 1) / g);
@@ -123,37 +190,98 @@ __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a) {
     const int t_hi_w = min(a.T - 1, (min(wr0 + kRowsWave, nrows) - 1) / g);
     const int kend_w = !wave_live ? 0 : (causal ? min(L, past + t_hi_w + 1) : L);
 
-    // ---- this lane's query rows (one per 32-row column block) and Q^T fragments
-    int tcol[2];
-    QF qf[2][DS];
-    {
-        const int64_t es = type_elem_bytes(a.q_type);
+    // ---- tile loads: per lane and 1 KB chunk q = i * 4 + w of a stage, the
+    // byte x = 1024 q + 16 lane of the padded tile is row x / RP, column
+    // x % RP; pad bytes and chunks past the tile load from an offset past the
+    // buffer (0 bytes read, zeros written)
+    const uint32_t nbk = (uint32_t)a.k_nb_tok, nbv = (uint32_t)a.v_nb_tok;
+    const i32x4 krs = make_rsrc(a.k[b] + kvh * a.k_nb_head, (uint32_t)(L - 1) * nbk + 2 * D);
+    const i32x4 vrs = make_rsrc(a.v[b] + kvh * a.v_nb_head, (uint32_t)(L - 1) * nbv + 2 * D);
+    int koff[NI], voff[NI];
 #pragma unroll
-        for (int cb = 0; cb < 2; ++cb) {
-            const int row = wr0 + cb * 32 + l32;
-            const bool ok = row < nrows;
-            const int t = ok ? row / g : 0;
-            const int h = kvh * g + (ok ? row % g : 0);
-            tcol[cb] = ok ? t : a.T - 1;
-            const char* qrow = a.q + b * a.q_nb_b + t * a.q_nb_t + h * a.q_nb_h;
+    for (int i = 0; i < NI; ++i) {
+        const int x = (i * kWaves + w) * 1024 + lane * 16;
+        const int r = x / RP, c = x % RP;
+        const bool ok = r < kBN && c < 2 * D;
+        koff[i] = ok ? (int)(r * nbk) + c : 0x40000000;
+        voff[i] = ok ? (int)(r * nbv) + c : 0x40000000;
+    }
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_char*)lds;
+    auto issue = [&](int j) {
+        const uint32_t st = lds0 + (j % kStages) * STAGE;
+        const int sk = (int)((uint32_t)(j * kBN) * nbk), sv = (int)((uint32_t)(j * kBN) * nbv);
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            dma16(krs, st + (i * kWaves + w) * 1024, koff[i], sk);
+            dma16(vrs, st + REG + (i * kWaves + w) * 1024, voff[i], sv);
+        }
+    };
+    // workgroup OR of `flag` at the barrier that ends tile j: each wave
+    // publishes its own word in a slot that alternates with j (a slot is
+    // rewritten two tiles later, after every wave has read it)
+    __shared__ int any_flag[2][kWaves];
+
+    // ---- this lane's query rows (one per 32-row column block) and Q^T
+    // fragments, rounded to K's type; one loop nest per Q type so the loads
+    // of a nest issue back to back
+    int tcol[2];
+    const char* qrow[2];
+    bool qok[2];
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+        const int row = wr0 + cb * 32 + l32;
+        qok[cb] = row < nrows;
+        const int t = qok[cb] ? row / g : 0;
+        const int h = kvh * g + (qok[cb] ? row % g : 0);
+        tcol[cb] = qok[cb] ? t : a.T - 1;
+        qrow[cb] = a.q + b * a.q_nb_b + t * a.q_nb_t + h * a.q_nb_h;
+    }
+    QF qf[2][DS];
+    u32x4 qraw[2][DS];
+    if (a.q_type == VVA_TYPE_F32) {
+        float4 x[2][DS][2];
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
             for (int ds = 0; ds < DS; ++ds) {
                 const int d0 = ds * 16 + half * 8;
-                u32x4 u = {0u, 0u, 0u, 0u};
-                if (ok) {
-                    if (a.q_type == KT) {
-                        u = *(const u32x4*)(qrow + d0 * 2);
-                    } else {
-                        uint16_t hv[8];
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) hv[e] = F::cvt(load_elem(qrow + (d0 + e) * es, a.q_type));
-                        __builtin_memcpy(&u, hv, 16);
-                    }
-                }
-                qf[cb][ds] = as_vec<QF>(u);
+                x[cb][ds][0] = *(const float4*)(qrow[cb] + d0 * 4);
+                x[cb][ds][1] = *(const float4*)(qrow[cb] + d0 * 4 + 16);
             }
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+            for (int ds = 0; ds < DS; ++ds) {
+                const float4 x0 = x[cb][ds][0], x1 = x[cb][ds][1];
+                qraw[cb][ds] = u32x4{F::cvt(x0.x) | ((uint32_t)F::cvt(x0.y) << 16), F::cvt(x0.z) | ((uint32_t)F::cvt(x0.w) << 16),
+                                     F::cvt(x1.x) | ((uint32_t)F::cvt(x1.y) << 16), F::cvt(x1.z) | ((uint32_t)F::cvt(x1.w) << 16)};
+            }
+    } else {
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+            for (int ds = 0; ds < DS; ++ds) qraw[cb][ds] = *(const u32x4*)(qrow[cb] + (ds * 16 + half * 8) * 2);
+        if (a.q_type != KT) {           // the other 16-bit type
+            const int qt = a.q_type;
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+                for (int ds = 0; ds < DS; ++ds) {
+                    const u32x4 r = qraw[cb][ds];
+                    const uint32_t rw[4] = {r.x, r.y, r.z, r.w};
+                    uint32_t cw[4];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        cw[k] = F::cvt(bits16_to_f32(rw[k] & 0xffffu, qt)) |
+                                ((uint32_t)F::cvt(bits16_to_f32(rw[k] >> 16, qt)) << 16);
+                    qraw[cb][ds] = u32x4{cw[0], cw[1], cw[2], cw[3]};
+                }
         }
     }
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds) qf[cb][ds] = as_vec<QF>(qok[cb] ? qraw[cb][ds] : u32x4{0u, 0u, 0u, 0u});
 
     float m[2] = {-INFINITY, -INFINITY};
     float lsum[2] = {0.0f, 0.0f};
@@ -161,116 +289,96 @@ __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a) {
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-        for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) o[dt][cb][r] = 0.0f;
+        for (int cb = 0; cb < 2; ++cb) o[dt][cb] = f32x16{};
 
     const float sl2 = a.scale * kLog2e;
-    const char* kg = a.k[b] + kvh * a.k_nb_head;
-    const char* vg = a.v[b] + kvh * a.v_nb_head;
+    // per-lane LDS offsets of the operand reads within a stage
+    const int k_rd = l32 * RP + half * 16;                                   // K: key l32, dims 8 half ..
+    const int v_rd = ((lane & 15) >> 2) * RP + (16 * ((lane >> 4) & 1) + 4 * (lane & 3)) * 2;   // V^T, see v_frag
 
-    // ---- tile staging: global -> registers -> LDS
-    u32x4 kst[KLD];
-    u32x4 vst[4];
-    const int v_item = tid;                           // (key group, dim chunk)
-    const bool v_active = v_item < VITEMS;
-    const int v_kg = v_item / (D / 8), v_dc = v_item % (D / 8);
-
-    auto load_tile = [&](int j) {
-        const int k0 = j * kBN;
+    // S^T of one 32-key half of the tile at stage base kb
+    auto s_half = [&](const lds_char* kb, int kt, f32x16 (&s)[2]) {
 #pragma unroll
-        for (int i = 0; i < KLD; ++i) {
-            const int c = tid + i * 256;
-            const int key = min(k0 + c / KCH, L - 1);
-            kst[i] = *(const u32x4*)(kg + (int64_t)key * a.k_nb_tok + (c % KCH) * 16);
-        }
-        if (v_active) {
+        for (int ds = 0; ds < DS; ++ds) {
+            const u32x4 kraw = *(const __attribute__((address_space(3))) u32x4*)(kb + kt * 32 * RP + k_rd + ds * 32);
+            const QF kf = as_vec<QF>(kraw);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int key = min(k0 + v_kg * 4 + i, L - 1);
-                vst[i] = *(const u32x4*)(vg + (int64_t)key * a.v_nb_tok + v_dc * 16);
-            }
+            for (int cb = 0; cb < 2; ++cb) s[cb] = ds == 0 ? F::mma(kf, qf[cb][0], f32x16{}) : F::mma(kf, qf[cb][ds], s[cb]);
         }
     };
-    auto store_tile = [&](int stage) {
-        char* kb = lds + stage * STAGE;
-        char* vb = kb + KBUF;
+    // p = 2^(x * mul - m) as f16 in the order of the second product's k
+    // steps, row sums from the f16 values
+    auto probs = [&](const f32x16 (&s)[2], float mul, h8 (&pf)[2][2]) {
 #pragma unroll
-        for (int i = 0; i < KLD; ++i) {
-            const int c = tid + i * 256;
-            *(u32x4*)(kb + (c / KCH) * KROW + (c % KCH) * 16) = kst[i];
-        }
-        if (v_active) {
-            uint32_t x[4][4];
+        for (int cb = 0; cb < 2; ++cb) {
+            const float nb = m[cb] == -INFINITY ? 0.0f : -m[cb];
+            float ps = lsum[cb];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                u32x4 u = vst[i];
-                if constexpr (KT == VVA_TYPE_BF16) {
-                    u.x = bf16x2_to_f16x2(u.x); u.y = bf16x2_to_f16x2(u.y);
-                    u.z = bf16x2_to_f16x2(u.z); u.w = bf16x2_to_f16x2(u.w);
+            for (int ks = 0; ks < 2; ++ks) {
+                h8 pv;
+#pragma unroll
+                for (int e = 0; e < 8; e += 2) {
+                    const float p0 = __builtin_amdgcn_exp2f(fmaf(s[cb][ks * 8 + e], mul, nb));
+                    const float p1 = __builtin_amdgcn_exp2f(fmaf(s[cb][ks * 8 + e + 1], mul, nb));
+                    h2 pp = {(_Float16)p0, (_Float16)p1};
+                    pv[e] = pp.x;
+                    pv[e + 1] = pp.y;
+                    ps = __builtin_amdgcn_fdot2(pp, h2{(_Float16)1.0f, (_Float16)1.0f}, ps, false);
                 }
-                x[i][0] = u.x; x[i][1] = u.y; x[i][2] = u.z; x[i][3] = u.w;
+                pf[cb][ks] = pv;
             }
-            // dims v_dc*8 + e, keys v_kg*4 + 0..3 -> one 8-byte row segment each
+            lsum[cb] = ps;
+        }
+    };
+    // O^T += V^T P^T for the two 16-key steps of half kt
+    auto pv_half = [&](const lds_char* vb, int kt, const h8 (&pf)[2][2]) {
 #pragma unroll
-            for (int p = 0; p < 4; ++p) {
-                const uint32_t lo01 = (x[0][p] & 0xffffu) | (x[1][p] << 16);
-                const uint32_t lo23 = (x[2][p] & 0xffffu) | (x[3][p] << 16);
-                const uint32_t hi01 = (x[0][p] >> 16) | (x[1][p] & 0xffff0000u);
-                const uint32_t hi23 = (x[2][p] >> 16) | (x[3][p] & 0xffff0000u);
-                const int d = v_dc * 8 + 2 * p;
-                *(u32x2*)(vb + d * VROW + v_kg * 8) = u32x2{lo01, lo23};
-                *(u32x2*)(vb + (d + 1) * VROW + v_kg * 8) = u32x2{hi01, hi23};
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                const int kk = (kt * 2 + ks) * 16;
+                const lds_char* base = vb + v_rd + dt * 64;
+                const h8 vf = v_frag<KT>(base + (kk + 4 * half) * RP, base + (kk + 8 + 4 * half) * RP);
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb)
+                    o[dt][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[cb][ks], o[dt][cb], 0, 0, 0);
             }
+    };
+    // max over the 32 keys of half s of each row, in the exp2 domain
+    auto half_max = [&](const f32x16 (&s)[2], float mul, float (&mx)[2]) {
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+            float x = fmaxf(fmaxf(s[cb][0], s[cb][1]), s[cb][2]);
+#pragma unroll
+            for (int r = 3; r < 15; r += 2) x = fmaxf(fmaxf(x, s[cb][r]), s[cb][r + 1]);
+            mx[cb] = max_swap32(fmaxf(x, s[cb][15])) * mul;
         }
     };
 
-    // Per 64-key tile: both 32-key halves of S^T are issued on the MFMA pipe
-    // first, then each half's softmax VALU runs while the MFMAs of the other
-    // half or of the previous P.V product are in flight.
-    //
-    // The reference max m of a row is fixed by the first tile with a visible
-    // key and never moves inside the tile loop, so O stays in MFMA
-    // accumulators with no VALU rescale: p = 2^(x - m) is allowed up to 2^15
-    // (f16).  If a row's score exceeds m + 15 (rare: logits rarely grow by
-    // 2^15 after the first tile), the workgroup restarts its key loop from
-    // tile 0 with the raised m (each restart raises it by more than 15, so
-    // restarts are few).
     for (;;) {
-    if (n_tiles > 0) {
-        load_tile(0);
-        store_tile(0);
-    }
-    __syncthreads();
-    bool restart = false;
-    for (int j = 0; j < n_tiles; ++j) {
-        const int stage = j & 1;
-        if (j + 1 < n_tiles) load_tile(j + 1);
-        const int k0 = j * kBN;
-        bool raise = false;
-        if (k0 < kend_w) {
-            const char* kb = lds + stage * STAGE;
-            const char* vb = kb + KBUF;
-            // the second half is skipped when no row of the wave sees it
-            const bool two = !(causal && k0 + 32 > past + t_hi_w);             // wave-uniform
-            // ---------------- S^T = K Q^T (32 keys x 64 rows per half)
-            f32x16 s[2][2];
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-                for (int ds = 0; ds < DS; ++ds) {
-                    const QF kf = as_vec<QF>(*(const u32x4*)(kb + (kt * 32 + l32) * KROW + ds * 32 + half * 16));
-#pragma unroll
-                    for (int cb = 0; cb < 2; ++cb)
-                        s[kt][cb] = ds == 0 ? F::mma(kf, qf[cb][0], f32x16{}) : F::mma(kf, qf[cb][ds], s[kt][cb]);
-                }
-                if (!two) break;
-            }
-            // ---------------- masks: raw scores, or scores already in the
-            // exp2 domain (scaled, mask added) when the mask is explicit
-            float mul = sl2;
-            const bool need_mask = EXPL || k0 + kBN > L || (causal && k0 + kBN - 1 > past + t_lo_w);
-            if (need_mask) {
+        if (n_tiles > 0) issue(0);
+        if (n_tiles > 1) issue(1);
+        if (n_tiles > 1) wait_vm_barrier<2 * NI>(); else wait_vm_barrier<0>();
+        bool restart = false;
+        for (int j = 0; j < n_tiles; ++j) {
+            const bool ahead = j + 2 < n_tiles;
+            if (ahead) issue(j + 2);          // into the stage tile j - 1 used (free since the last barrier)
+            const lds_char* kb = (const lds_char*)lds + (j % kStages) * STAGE;
+            const lds_char* vb = kb + REG;
+            const int k0 = j * kBN;
+            bool raise = false;
+            if (k0 < kend_w) {
+                // a half no row of the wave sees is masked out whole
+                const bool two = !(causal && k0 + 32 > past + t_hi_w);             // wave-uniform
+                f32x16 s[2][2];
+                s_half(kb, 0, s[0]);
+                s_half(kb, 1, s[1]);
+                // masks (only on tiles that need them): raw scores, or scores
+                // already in the exp2 domain (scaled, mask added) when the
+                // mask is explicit
+                float mul = sl2;
+                const bool need_mask = EXPL || k0 + kBN > L || (causal && k0 + kBN - 1 > past + t_lo_w);
+                if (need_mask) {
 #pragma unroll
                 for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
@@ -279,7 +387,7 @@ __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a) {
 #pragma unroll
                         for (int r = 0; r < 16; ++r) {
                             const int key = k0 + kt * 32 + 8 * (r / 4) + 4 * half + (r % 4);
-                            float x = s[kt][cb][r];
+                            float x = (kt == 1 && !two) ? 0.0f : s[kt][cb][r];
                             if constexpr (EXPL) {
                                 const char* mrow = a.mask + b * a.mask_nb_b + tcol[cb] * a.mask_nb_row;
                                 x = fmaf(x, sl2, f16_to_f32(*(const uint16_t*)(mrow + 2 * min(key, L - 1))) * kLog2e);
@@ -287,83 +395,64 @@ __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a) {
                             s[kt][cb][r] = (key > lim || (kt == 1 && !two)) ? -INFINITY : x;
                         }
                     }
-                if constexpr (EXPL) mul = 1.0f;
-            } else if (!two) {
-#pragma unroll
-                for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) s[1][cb][r] = -INFINITY;
-            }
-            // ---------------- row max of the tile against the reference
-#pragma unroll
-            for (int cb = 0; cb < 2; ++cb) {
-                float mx = fmaxf(s[0][cb][0], s[1][cb][0]);
-#pragma unroll
-                for (int r = 1; r < 16; ++r) mx = fmaxf(fmaxf(mx, s[0][cb][r]), s[1][cb][r]);
-                mx = max_swap32(mx) * mul;
-                if (m[cb] == -INFINITY) m[cb] = mx;        // O and the row sum are still 0
-                if (mx > m[cb] + kLazy) {
-                    raise = true;
-                    m[cb] = mx;                            // the restart uses the raised max
                 }
-            }
-            // a raising wave skips the rest of the tile: the restart discards it
-            if (!__any(raise)) {
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt) {
-                if (kt == 1 && !two) break;
-                // ---------------- p = 2^(x * mul - m) as f16, row sums from the f16 values
-                h8 pf[2][2];
+                if constexpr (EXPL) mul = 1.0f;
+                // the row max of the whole tile sets m on the first visible
+                // tile; a later tile beyond m + 15 raises it and restarts
+                float mx0[2], mx1[2];
+                half_max(s[0], mul, mx0);
+                half_max(s[1], mul, mx1);
 #pragma unroll
                 for (int cb = 0; cb < 2; ++cb) {
-                    const float nb = m[cb] == -INFINITY ? 0.0f : -m[cb];
-                    float ps = lsum[cb];
-#pragma unroll
-                    for (int ks = 0; ks < 2; ++ks) {
-                        h8 p;
-#pragma unroll
-                        for (int e = 0; e < 8; e += 2) {
-                            const float p0 = __builtin_amdgcn_exp2f(fmaf(s[kt][cb][ks * 8 + e], mul, nb));
-                            const float p1 = __builtin_amdgcn_exp2f(fmaf(s[kt][cb][ks * 8 + e + 1], mul, nb));
-                            h2 pp = {(_Float16)p0, (_Float16)p1};
-                            p[e] = pp.x;
-                            p[e + 1] = pp.y;
-                            ps = __builtin_amdgcn_fdot2(pp, h2{(_Float16)1.0f, (_Float16)1.0f}, ps, false);
-                        }
-                        pf[cb][ks] = p;
-                    }
-                    lsum[cb] = ps;
-                }
-                // ---------------- O^T += V^T P^T (the two 16-key steps of this half)
-#pragma unroll
-                for (int dt = 0; dt < DT; ++dt) {
-                    const char* vrow = vb + (dt * 32 + l32) * VROW;
-#pragma unroll
-                    for (int ks = 0; ks < 2; ++ks) {
-                        const int kk = (kt * 2 + ks) * 16;
-                        const u32x2 lo = *(const u32x2*)(vrow + (kk + 4 * half) * 2);
-                        const u32x2 hi = *(const u32x2*)(vrow + (kk + 8 + 4 * half) * 2);
-                        const h8 vf = as_vec<h8>(u32x4{lo.x, lo.y, hi.x, hi.y});
-#pragma unroll
-                        for (int cb = 0; cb < 2; ++cb)
-                            o[dt][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[cb][ks], o[dt][cb], 0, 0, 0);
+                    const float mx = fmaxf(mx0[cb], mx1[cb]);
+                    if (m[cb] == -INFINITY) m[cb] = mx;        // O and the row sum are still 0
+                    if (mx > m[cb] + kLazy) {
+                        raise = true;
+                        m[cb] = mx;
                     }
                 }
+                if (!__any(raise)) {
+                    h8 pf0[2][2], pf1[2][2];
+                    probs(s[0], mul, pf0);
+                    pv_half(vb, 0, pf0);
+                    probs(s[1], mul, pf1);
+                    pv_half(vb, 1, pf1);
+                    // the P.V MFMAs of half 0 (V^T reads ahead) interleaved
+                    // with the softmax VALU of half 1
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);  // VALU
+                        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);   // DS read
+                    }
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+                        __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);
+                        if (i % 2 == 0) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+                    }
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                }
             }
+            // tile j + 1 must be in LDS (tile j + 2's loads may still fly)
+            const bool wave_raise = __any(raise);
+            if (lane == 0) any_flag[j & 1][w] = wave_raise;
+            if (ahead) wait_vm_barrier<2 * NI>(); else wait_vm_barrier<0>();
+            int any = 0;
+#pragma unroll
+            for (int i = 0; i < kWaves; ++i) any |= any_flag[j & 1][i];
+            if (any) {                                          // workgroup-uniform
+                restart = true;
+                break;
             }
         }
-        if (j + 1 < n_tiles) store_tile(stage ^ 1);
-        if (__syncthreads_or(raise)) {                      // workgroup-uniform
-            restart = true;
-            break;
-        }
-    }
-    if (!restart) break;
-    lsum[0] = lsum[1] = 0.0f;
+        if (!restart) break;
+        wait_vm_barrier<0>();                                   // no load may land in a stage after the restart
+        lsum[0] = lsum[1] = 0.0f;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
+        for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-        for (int cb = 0; cb < 2; ++cb) o[dt][cb] = f32x16{};
+            for (int cb = 0; cb < 2; ++cb) o[dt][cb] = f32x16{};
     }
 
     // ---- normalize and write (each lane owns one row per column block)
@@ -407,15 +496,16 @@ bool prefill_supported(const AttnArgs& a) {
     if (a.k_type != a.v_type) return false;
     if (a.k_type != VVA_TYPE_F16 && a.k_type != VVA_TYPE_BF16) return false;
     if (a.Hq % a.Hkv != 0) return false;
-    // 16-byte vector access to K/V rows and Q rows of the matching type,
-    // 16-byte aligned float4 output rows
+    // 16-byte buffer loads of K/V rows, 32-bit buffer offsets (rows up to L),
+    // 16-byte Q and output rows
     if (a.k_nb_tok % 16 || a.k_nb_head % 16 || a.v_nb_tok % 16 || a.v_nb_head % 16) return false;
     for (int b = 0; b < a.B; ++b) {
         if ((uintptr_t)a.k[b] % 16 || (uintptr_t)a.v[b] % 16) return false;
         if (a.L[b] < 1) return false;
+        if ((int64_t)(a.L[b] + kBN) * a.k_nb_tok >= ((int64_t)1 << 30) ||
+            (int64_t)(a.L[b] + kBN) * a.v_nb_tok >= ((int64_t)1 << 30)) return false;
     }
-    if (a.q_type == a.k_type && (((uintptr_t)a.q % 16) || a.q_nb_t % 16 || a.q_nb_h % 16 || a.q_nb_b % 16))
-        return false;
+    if (((uintptr_t)a.q % 16) || a.q_nb_t % 16 || a.q_nb_h % 16 || a.q_nb_b % 16) return false;
     if (((uintptr_t)a.out % 16) || a.o_nb_t % 16 || a.o_nb_h % 16 || a.o_nb_b % 16) return false;
     if (a.mask_mode == kMaskExplicit && (a.mask_nb_row % 2 || a.mask_nb_b % 2)) return false;
     return true;
