@@ -227,7 +227,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--decode-steps", type=int, default=512)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["prefill", "decode", "both"], default="both")
+    ap.add_argument("--only", choices=["prefill", "decode", "both", "copy"], default="both",
+                    help="copy: a plain 1 GiB device-to-device copy, the reference for FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the attention path has no multi-GPU mode in this build "
@@ -239,6 +240,15 @@ def main() -> int:
     import vvo
 
     torch.cuda.set_device(0)
+    if args.only == "copy":
+        n = 1 << 30
+        src = torch.ones(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_per_launch": n, "launches": 3}), flush=True)
+        return 0
     ctx = vva.Context(0)
     line = {
         "metric": "prefill attn TFLOP/s (% MFMA peak); decode attn HBM GB/s (% peak), 1 GPU",

@@ -65,6 +65,7 @@ constexpr int kRowsWave = 64;      // query rows per wave
 constexpr int kWaves = 4;
 constexpr int kRowsWG = kRowsWave * kWaves;
 constexpr int kStages = 3;
+constexpr int kMaxRestarts = 16;   // bound on key-loop restarts per workgroup
 
 // buffer_load_dwordx4 ... lds: each lane's 16 bytes land at LDS address
 // m0 + 16 * lane.  Issued as inline asm so the compiler does not fence LDS
@@ -154,6 +155,8 @@ __device__ __forceinline__ h8 v_frag(const lds_char* vrow0, const lds_char* vrow
     return v;
 }
 
+__device__ __forceinline__ const lds_char* lds_at(uint32_t addr) { return (const lds_char*)(uintptr_t)addr; }
+
 // EXPL: explicit F16 mask (otherwise implicit causal / length masking only).
 template <int D, int KT, bool EXPL>
 __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a) {
@@ -161,11 +164,17 @@ __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a) {
     using QF = typename F::type;
     constexpr int DS = D / 16;                     // 16-dim MFMA steps of Q.K
     constexpr int DT = D / 32;                     // 32-dim output tiles
-    constexpr int RP = D * 2 + 16;                 // LDS bytes per K / V row (padded)
-    constexpr int RB = kBN * RP;                   // bytes of one tile
-    constexpr int NI = (RB + 4096 - 1) / 4096;     // 1 KB loads per wave per tile and operand
-    constexpr int REG = NI * 4096;                 // LDS bytes per operand and stage
-    constexpr int STAGE = 2 * REG;                 // K then V
+    // Row pitches in LDS.  K is read 16 B per lane, 16 rows per bank pass:
+    // a pitch of 16 mod 256 bytes puts them on distinct banks.  V is read by
+    // the transposing 8-byte load, 4 rows x 64 B per 32 lanes: a pitch of
+    // 64 mod 256 bytes puts the 4 rows on distinct banks.
+    constexpr int KP = D * 2 + 16;
+    constexpr int VP = D * 2 + 64;
+    constexpr int NIK = (kBN * KP + 4095) / 4096;  // 1 KB loads per wave per tile (K)
+    constexpr int NIV = (kBN * VP + 4095) / 4096;  // (V)
+    constexpr int KREG = NIK * 4096;               // LDS bytes per stage (K, then V)
+    constexpr int STAGE = KREG + NIV * 4096;
+    constexpr int NLD = NIK + NIV;                 // loads per wave per tile
 
     __shared__ __attribute__((aligned(16))) char lds[kStages * STAGE];
 
@@ -190,31 +199,34 @@ __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a) {
     const int t_hi_w = min(a.T - 1, (min(wr0 + kRowsWave, nrows) - 1) / g);
     const int kend_w = !wave_live ? 0 : (causal ? min(L, past + t_hi_w + 1) : L);
 
-    // ---- tile loads: per lane and 1 KB chunk q = i * 4 + w of a stage, the
-    // byte x = 1024 q + 16 lane of the padded tile is row x / RP, column
-    // x % RP; pad bytes and chunks past the tile load from an offset past the
-    // buffer (0 bytes read, zeros written)
+    // ---- tile loads: per lane and 1 KB chunk q = i * 4 + w of an operand,
+    // the byte x = 1024 q + 16 lane of the padded tile is row x / pitch,
+    // column x % pitch; pad bytes and chunks past the tile load from an
+    // offset past the buffer (0 bytes read, zeros written)
     const uint32_t nbk = (uint32_t)a.k_nb_tok, nbv = (uint32_t)a.v_nb_tok;
     const i32x4 krs = make_rsrc(a.k[b] + kvh * a.k_nb_head, (uint32_t)(L - 1) * nbk + 2 * D);
     const i32x4 vrs = make_rsrc(a.v[b] + kvh * a.v_nb_head, (uint32_t)(L - 1) * nbv + 2 * D);
-    int koff[NI], voff[NI];
+    int koff[NIK], voff[NIV];
 #pragma unroll
-    for (int i = 0; i < NI; ++i) {
+    for (int i = 0; i < NIK; ++i) {
         const int x = (i * kWaves + w) * 1024 + lane * 16;
-        const int r = x / RP, c = x % RP;
-        const bool ok = r < kBN && c < 2 * D;
-        koff[i] = ok ? (int)(r * nbk) + c : 0x40000000;
-        voff[i] = ok ? (int)(r * nbv) + c : 0x40000000;
+        const int r = x / KP, c = x % KP;
+        koff[i] = r < kBN && c < 2 * D ? (int)(r * nbk) + c : 0x40000000;
+    }
+#pragma unroll
+    for (int i = 0; i < NIV; ++i) {
+        const int x = (i * kWaves + w) * 1024 + lane * 16;
+        const int r = x / VP, c = x % VP;
+        voff[i] = r < kBN && c < 2 * D ? (int)(r * nbv) + c : 0x40000000;
     }
     const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_char*)lds;
     auto issue = [&](int j) {
         const uint32_t st = lds0 + (j % kStages) * STAGE;
         const int sk = (int)((uint32_t)(j * kBN) * nbk), sv = (int)((uint32_t)(j * kBN) * nbv);
 #pragma unroll
-        for (int i = 0; i < NI; ++i) {
-            dma16(krs, st + (i * kWaves + w) * 1024, koff[i], sk);
-            dma16(vrs, st + REG + (i * kWaves + w) * 1024, voff[i], sv);
-        }
+        for (int i = 0; i < NIK; ++i) dma16(krs, st + (i * kWaves + w) * 1024, koff[i], sk);
+#pragma unroll
+        for (int i = 0; i < NIV; ++i) dma16(vrs, st + KREG + (i * kWaves + w) * 1024, voff[i], sv);
     };
     // workgroup OR of `flag` at the barrier that ends tile j: each wave
     // publishes its own word in a slot that alternates with j (a slot is
@@ -293,14 +305,16 @@ __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a) {
 
     const float sl2 = a.scale * kLog2e;
     // per-lane LDS offsets of the operand reads within a stage
-    const int k_rd = l32 * RP + half * 16;                                   // K: key l32, dims 8 half ..
-    const int v_rd = ((lane & 15) >> 2) * RP + (16 * ((lane >> 4) & 1) + 4 * (lane & 3)) * 2;   // V^T, see v_frag
+    const int k_rd = l32 * KP + half * 16;                                   // K: key l32, dims 8 half ..
+    const int v_rd = ((lane & 15) >> 2) * VP + (16 * ((lane >> 4) & 1) + 4 * (lane & 3)) * 2 +
+                     4 * half * VP;                                          // V^T, see v_frag
 
-    // S^T of one 32-key half of the tile at stage base kb
-    auto s_half = [&](const lds_char* kb, int kt, f32x16 (&s)[2]) {
+    // S^T of one 32-key half of the tile; ka = stage K base + k_rd, so
+    // every read is at an immediate offset
+    auto s_half = [&](const lds_char* ka, int kt, f32x16 (&s)[2]) {
 #pragma unroll
         for (int ds = 0; ds < DS; ++ds) {
-            const u32x4 kraw = *(const __attribute__((address_space(3))) u32x4*)(kb + kt * 32 * RP + k_rd + ds * 32);
+            const u32x4 kraw = *(const __attribute__((address_space(3))) u32x4*)(ka + kt * 32 * KP + ds * 32);
             const QF kf = as_vec<QF>(kraw);
 #pragma unroll
             for (int cb = 0; cb < 2; ++cb) s[cb] = ds == 0 ? F::mma(kf, qf[cb][0], f32x16{}) : F::mma(kf, qf[cb][ds], s[cb]);
@@ -330,15 +344,16 @@ __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a) {
             lsum[cb] = ps;
         }
     };
-    // O^T += V^T P^T for the two 16-key steps of half kt
-    auto pv_half = [&](const lds_char* vb, int kt, const h8 (&pf)[2][2]) {
+    // O^T += V^T P^T for the two 16-key steps of half kt; va = stage V base
+    // + v_rd
+    auto pv_half = [&](const lds_char* va, int kt, const h8 (&pf)[2][2]) {
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
                 const int kk = (kt * 2 + ks) * 16;
-                const lds_char* base = vb + v_rd + dt * 64;
-                const h8 vf = v_frag<KT>(base + (kk + 4 * half) * RP, base + (kk + 8 + 4 * half) * RP);
+                const lds_char* base = va + dt * 64;
+                const h8 vf = v_frag<KT>(base + kk * VP, base + (kk + 8) * VP);
 #pragma unroll
                 for (int cb = 0; cb < 2; ++cb)
                     o[dt][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[cb][ks], o[dt][cb], 0, 0, 0);
@@ -354,100 +369,237 @@ __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a) {
             mx[cb] = max_swap32(fmaxf(x, s[cb][15])) * mul;
         }
     };
+    // implicit masks on half kt of the tile at key k0: keys past L, and past
+    // the row's own position when causal
+    auto mask_half = [&](f32x16 (&s)[2], int k0, int kt) {
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+            const int lim = causal ? min(L - 1, past + tcol[cb]) : L - 1;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int key = k0 + kt * 32 + 8 * (r / 4) + 4 * half + (r % 4);
+                s[cb][r] = key > lim ? -INFINITY : s[cb][r];
+            }
+        }
+    };
 
-    for (;;) {
-        if (n_tiles > 0) issue(0);
-        if (n_tiles > 1) issue(1);
-        if (n_tiles > 1) wait_vm_barrier<2 * NI>(); else wait_vm_barrier<0>();
-        bool restart = false;
-        for (int j = 0; j < n_tiles; ++j) {
-            const bool ahead = j + 2 < n_tiles;
-            if (ahead) issue(j + 2);          // into the stage tile j - 1 used (free since the last barrier)
-            const lds_char* kb = (const lds_char*)lds + (j % kStages) * STAGE;
-            const lds_char* vb = kb + REG;
-            const int k0 = j * kBN;
-            bool raise = false;
-            if (k0 < kend_w) {
-                // a half no row of the wave sees is masked out whole
-                const bool two = !(causal && k0 + 32 > past + t_hi_w);             // wave-uniform
-                f32x16 s[2][2];
-                s_half(kb, 0, s[0]);
-                s_half(kb, 1, s[1]);
-                // masks (only on tiles that need them): raw scores, or scores
-                // already in the exp2 domain (scaled, mask added) when the
-                // mask is explicit
-                float mul = sl2;
-                const bool need_mask = EXPL || k0 + kBN > L || (causal && k0 + kBN - 1 > past + t_lo_w);
-                if (need_mask) {
+    // stage bases of tile j, through an empty asm so that each read keeps
+    // one base register and a constant offset
+    auto bases = [&](int j, const lds_char*& ka, const lds_char*& va) {
+        uint32_t kaddr = lds0 + (j % kStages) * STAGE + k_rd;
+        uint32_t vaddr = lds0 + (j % kStages) * STAGE + KREG + v_rd;
+        asm volatile("" : "+v"(kaddr), "+v"(vaddr));
+        ka = lds_at(kaddr);
+        va = lds_at(vaddr);
+    };
+    // operand fragments of half kt, read ahead of their MFMAs into
+    // registers of their own
+    auto load_k = [&](const lds_char* ka, int kt, QF (&kf)[DS]) {
 #pragma unroll
-                for (int kt = 0; kt < 2; ++kt)
+        for (int ds = 0; ds < DS; ++ds) {
+            const u32x4 kraw = *(const __attribute__((address_space(3))) u32x4*)(ka + kt * 32 * KP + ds * 32);
+            kf[ds] = as_vec<QF>(kraw);
+        }
+    };
+    auto mma_k = [&](const QF (&kf)[DS], f32x16 (&s)[2]) {
 #pragma unroll
-                    for (int cb = 0; cb < 2; ++cb) {
-                        const int lim = causal ? min(L - 1, past + tcol[cb]) : L - 1;
+        for (int ds = 0; ds < DS; ++ds)
 #pragma unroll
-                        for (int r = 0; r < 16; ++r) {
-                            const int key = k0 + kt * 32 + 8 * (r / 4) + 4 * half + (r % 4);
-                            float x = (kt == 1 && !two) ? 0.0f : s[kt][cb][r];
-                            if constexpr (EXPL) {
-                                const char* mrow = a.mask + b * a.mask_nb_b + tcol[cb] * a.mask_nb_row;
-                                x = fmaf(x, sl2, f16_to_f32(*(const uint16_t*)(mrow + 2 * min(key, L - 1))) * kLog2e);
-                            }
-                            s[kt][cb][r] = (key > lim || (kt == 1 && !two)) ? -INFINITY : x;
-                        }
-                    }
-                }
-                if constexpr (EXPL) mul = 1.0f;
-                // the row max of the whole tile sets m on the first visible
-                // tile; a later tile beyond m + 15 raises it and restarts
-                float mx0[2], mx1[2];
-                half_max(s[0], mul, mx0);
-                half_max(s[1], mul, mx1);
+            for (int cb = 0; cb < 2; ++cb) s[cb] = ds == 0 ? F::mma(kf[0], qf[cb][0], f32x16{}) : F::mma(kf[ds], qf[cb][ds], s[cb]);
+    };
+    auto load_v = [&](const lds_char* va, int kt, h8 (&vf)[DT][2]) {
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                const int kk = (kt * 2 + ks) * 16;
+                vf[dt][ks] = v_frag<KT>(va + dt * 64 + kk * VP, va + dt * 64 + (kk + 8) * VP);
+            }
+    };
+    auto mma_v = [&](const h8 (&vf)[DT][2], const h8 (&pf)[2][2]) {
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb)
+                    o[dt][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[dt][ks], pf[cb][ks], o[dt][cb], 0, 0, 0);
+    };
+    // a tile every row of the workgroup sees whole: no masks, no branches.
+    // Four phases, each one scheduling region: K reads + S of half 0 | S of
+    // half 1 beside the softmax of half 0 (+ V reads of half 0) | P.V of
+    // half 0 beside the softmax of half 1 (+ V reads of half 1) | P.V of
+    // half 1
+    auto fast_tile = [&](const lds_char* ka, const lds_char* va) {
+        f32x16 s0[2], s1[2];
+        h8 p0[2][2], p1[2][2];
+        QF kf0[DS], kf1[DS];
+        h8 vf0[DT][2], vf1[DT][2];
+        load_k(ka, 0, kf0);
+        load_k(ka, 1, kf1);
+        mma_k(kf0, s0);
+        // S of each half moves to VGPRs in the phase that computes it, so
+        // the next half's MFMAs have accumulators of their own
+        asm volatile("" : "+v"(s0[0]), "+v"(s0[1]));
+        __builtin_amdgcn_sched_barrier(0);
+        load_v(va, 0, vf0);
+        mma_k(kf1, s1);
+        probs(s0, sl2, p0);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);       // VALU
+            if (i < 8) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);   // DS read
+        }
+        asm volatile("" : "+v"(s1[0]), "+v"(s1[1]));
+        __builtin_amdgcn_sched_barrier(0);
+        load_v(va, 1, vf1);
+        mma_v(vf0, p0);
+        probs(s1, sl2, p1);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+            if (i < 8) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        mma_v(vf1, p1);
+    };
+    // a tile with masks: the implicit ones, or the explicit mask (scores
+    // then carried in the exp2 domain, the row max tracked per tile: the
+    // first visible tile sets m, a later one beyond m + 15 raises it)
+    auto slow_tile = [&](const lds_char* ka, const lds_char* va, int k0, int restarts) -> bool {
+        f32x16 s[2][2];
+        s_half(ka, 0, s[0]);
+        s_half(ka, 1, s[1]);
+        float mul = sl2;
+        bool raise = false;
+        if constexpr (EXPL) {
+            mul = 1.0f;
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
                 for (int cb = 0; cb < 2; ++cb) {
-                    const float mx = fmaxf(mx0[cb], mx1[cb]);
-                    if (m[cb] == -INFINITY) m[cb] = mx;        // O and the row sum are still 0
-                    if (mx > m[cb] + kLazy) {
-                        raise = true;
-                        m[cb] = mx;
+                    const char* mrow = a.mask + b * a.mask_nb_b + tcol[cb] * a.mask_nb_row;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int key = k0 + kt * 32 + 8 * (r / 4) + 4 * half + (r % 4);
+                        const float x = fmaf(s[kt][cb][r], sl2,
+                                             f16_to_f32(*(const uint16_t*)(mrow + 2 * min(key, L - 1))) * kLog2e);
+                        s[kt][cb][r] = key > L - 1 ? -INFINITY : x;
                     }
                 }
-                if (!__any(raise)) {
-                    h8 pf0[2][2], pf1[2][2];
-                    probs(s[0], mul, pf0);
-                    pv_half(vb, 0, pf0);
-                    probs(s[1], mul, pf1);
-                    pv_half(vb, 1, pf1);
-                    // the P.V MFMAs of half 0 (V^T reads ahead) interleaved
-                    // with the softmax VALU of half 1
+            float mx0[2], mx1[2];
+            half_max(s[0], 1.0f, mx0);
+            half_max(s[1], 1.0f, mx1);
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        __builtin_amdgcn_sched_group_barrier(0x002, 12, 0);  // VALU
-                        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);   // DS read
-                    }
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) {
-                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
-                        __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);
-                        if (i % 2 == 0) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-                    }
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            for (int cb = 0; cb < 2; ++cb) {
+                const float mx = fmaxf(mx0[cb], mx1[cb]);
+                if (m[cb] == -INFINITY) m[cb] = mx;            // O and the row sum are still 0
+                if (mx > m[cb] + kLazy && restarts < kMaxRestarts) {
+                    raise = true;
+                    m[cb] = mx;
                 }
             }
-            // tile j + 1 must be in LDS (tile j + 2's loads may still fly)
-            const bool wave_raise = __any(raise);
-            if (lane == 0) any_flag[j & 1][w] = wave_raise;
-            if (ahead) wait_vm_barrier<2 * NI>(); else wait_vm_barrier<0>();
+            if (__any(raise)) return true;
+        } else {
+            mask_half(s[0], k0, 0);
+            mask_half(s[1], k0, 1);
+        }
+        h8 pf0[2][2], pf1[2][2];
+        probs(s[0], mul, pf0);
+        pv_half(va, 0, pf0);
+        probs(s[1], mul, pf1);
+        pv_half(va, 1, pf1);
+        return false;
+    };
+    // a p of the last tile overflowed f16 (its score passed m + 16), seen as
+    // an inf or nan row sum
+    auto overflow = [&](int restarts) -> bool {
+        return !EXPL && restarts < kMaxRestarts && (!(lsum[0] <= 3.0e38f) || !(lsum[1] <= 3.0e38f));
+    };
+    // all tiles before j_fast are seen whole by every row of the workgroup
+    const int t_lo_wg = min(a.T - 1, R0 / g);
+    const int j_fast = EXPL ? 0 : min(n_tiles, (causal ? min(L, past + t_lo_wg + 1) : L) / kBN);
+
+    for (int restarts = 0;; ++restarts) {
+        if (n_tiles > 0) issue(0);
+        if (n_tiles > 1) issue(1);
+        if (n_tiles > 1) wait_vm_barrier<NLD>(); else wait_vm_barrier<0>();
+        if (!EXPL && restarts == 0 && n_tiles > 0) {
+            // m from half 0 of tile 0: key 0 is visible to every row
+            const lds_char *ka, *va;
+            bases(0, ka, va);
+            f32x16 s0[2];
+            s_half(ka, 0, s0);
+            mask_half(s0, 0, 0);
+            half_max(s0, sl2, m);
+        }
+        int j = 0;
+        bool restart = false;
+        // end of tile j: publish this wave's restart flag, wait for tile j + 1
+        // (tile j + 2's loads may still fly) and OR the flags
+        auto end_tile = [&](int jj, bool flag) -> bool {
+            if (lane == 0) any_flag[jj & 1][w] = flag;
+            if (jj + 2 < n_tiles) wait_vm_barrier<NLD>(); else wait_vm_barrier<0>();
             int any = 0;
 #pragma unroll
-            for (int i = 0; i < kWaves; ++i) any |= any_flag[j & 1][i];
-            if (any) {                                          // workgroup-uniform
+            for (int i = 0; i < kWaves; ++i) any |= any_flag[jj & 1][i];
+            return any != 0;                                    // workgroup-uniform
+        };
+        // (the loops leave through their conditions only: an exit from the
+        // middle makes the compiler copy O through VGPRs on every tile)
+        int jb = 0;                                             // the tile that asked for the restart
+        for (; j < j_fast && !restart; ++j) {
+            if (j + 2 < n_tiles) issue(j + 2);      // into the stage tile j - 1 used (free since the last barrier)
+            const lds_char *ka, *va;
+            bases(j, ka, va);
+            // O stays in AGPRs across the back-edge (without the hint the
+            // compiler moves part of it through VGPRs on every tile)
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb) asm volatile("" : "+a"(o[dt][cb]));
+            fast_tile(ka, va);
+            if (end_tile(j, __any(overflow(restarts)))) {
                 restart = true;
-                break;
+                jb = j;
+            }
+        }
+        for (; j < n_tiles && !restart; ++j) {
+            if (j + 2 < n_tiles) issue(j + 2);
+            const lds_char *ka, *va;
+            bases(j, ka, va);
+            bool flag = false;
+            if (j * kBN < kend_w) flag = slow_tile(ka, va, j * kBN, restarts) || overflow(restarts);
+            if (end_tile(j, __any(flag))) {
+                restart = true;
+                jb = j;
             }
         }
         if (!restart) break;
+        j = jb;
         wait_vm_barrier<0>();                                   // no load may land in a stage after the restart
+        if (!EXPL && j * kBN < kend_w) {
+            // raise m for the rows whose scores on tile j passed m + 15 (tile j
+            // is still in its stage: tile j + 3 was never issued)
+            const lds_char *ka, *va;
+            bases(j, ka, va);
+            f32x16 s[2][2];
+            s_half(ka, 0, s[0]);
+            s_half(ka, 1, s[1]);
+            mask_half(s[0], j * kBN, 0);
+            mask_half(s[1], j * kBN, 1);
+            float mx0[2], mx1[2];
+            half_max(s[0], sl2, mx0);
+            half_max(s[1], sl2, mx1);
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) {
+                const float mx = fmaxf(mx0[cb], mx1[cb]);
+                if (mx > m[cb] + kLazy) m[cb] = mx;
+            }
+        }
+        __syncthreads();                                        // every wave is done with the stages
         lsum[0] = lsum[1] = 0.0f;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
