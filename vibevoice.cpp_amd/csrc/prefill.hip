@@ -13,12 +13,14 @@
 // can see; row tiles are issued heaviest-first for the causal imbalance.
 //
 // Staging.  K and V tiles go from HBM straight into LDS with buffer loads
-// that write LDS (no registers, no VALU), into a ring of three stages: the
-// loads of tile j + 2 are issued while tile j is computed.  Both tiles are
-// kept row-major ([key][dim], rows padded by 16 bytes against bank
-// conflicts); the V^T operand of the second product is read with
-// ds_read_b64_tr_b16, whose 16-lane transpose hands each lane 4 consecutive
-// keys of one dim.  Keys past L read as 0 through the buffer range check.
+// that write LDS (no registers, no VALU), into a ring of four stages: the
+// loads of tile j + 3 are issued, spread over the work of tile j, while
+// tile j is computed.  Both tiles are kept row-major ([key][dim]); K rows
+// are padded to 16 mod 256 bytes and V rows to 64 mod 256 bytes, which
+// keeps both operand reads free of bank conflicts.  The V^T operand of the
+// second product is read with ds_read_b64_tr_b16, whose 16-lane transpose
+// hands each lane 4 consecutive keys of one dim.  Keys past L read as 0
+// through the buffer range check.
 //
 // Per wave and key tile, with v_mfma_f32_32x32x16_{f16,bf16}:
 //   S^T[key][row] = K . Q^T  A = K rows from LDS (16 B per lane), B = Q^T
@@ -26,17 +28,23 @@
 //                            lane owns one query row (column) of S^T and the
 //                            softmax row reductions are in-register plus one
 //                            cross-half exchange;
-//   softmax                  fp32, exp2 domain; masks only on the tiles that
-//                            need them (interior tiles run a branch-free path);
+//   softmax                  fp32, exp2 domain;
 //   O^T[d][row] += V^T . P^T B = P^T converted in place from the S^T
 //                            accumulators: the key order of an MFMA step is
 //                            chosen to be the one the accumulator layout
 //                            already has, so no shuffle is needed.
-// The reference max m of a row is fixed by the first tile (key 0 is visible
-// to every row) and never moves inside the tile loop, so O stays in MFMA
-// accumulators with no rescale: p = 2^(x - m) may grow to 2^15 (f16).  A row
-// whose score exceeds m + 15 (rare: logits rarely grow by 2^15 after the
-// first tile) makes the workgroup restart its key loop with the raised m.
+// Tiles every row of the workgroup sees whole run a branch-free loop that is
+// pipelined across tiles: the scores of half 0 of tile j + 1 are computed
+// while P.V of tile j still runs, so that each group of 16 MFMAs has a
+// quarter of a softmax to overlap.  The diagonal and length-boundary tiles
+// at the end of a workgroup's range run a second loop with masks.
+// The reference max m of a row is taken from half 0 of the first tile (key 0
+// is visible to every row) and never moves inside the tile loop, so O stays
+// in MFMA accumulators with no rescale and no max is tracked per tile.  A
+// later score beyond m + 16 turns its f16 p into inf; the row sum shows it,
+// and the workgroup restarts its key loop with m raised to that tile's row
+// max (rare: logits rarely grow by 2^16 after the first tile).  With an
+// explicit mask the row max is tracked per tile instead (masked loop only).
 // P and V enter the second product as f16 (BF16 V is converted after the
 // transposing read): an 8-bit-mantissa P would cost up to ~4e-3 on short
 // rows, f16 P stays below 4e-4.  Q is rounded to K's type, as ggml's CPU
@@ -64,7 +72,7 @@ constexpr int kBN = 64;            // keys per tile
 constexpr int kRowsWave = 64;      // query rows per wave
 constexpr int kWaves = 4;
 constexpr int kRowsWG = kRowsWave * kWaves;
-constexpr int kStages = 3;
+constexpr int kStages = 4;         // LDS ring: tile j + 3 loads while tile j is computed
 constexpr int kMaxRestarts = 16;   // bound on key-loop restarts per workgroup
 
 // buffer_load_dwordx4 ... lds: each lane's 16 bytes land at LDS address
@@ -72,9 +80,11 @@ constexpr int kMaxRestarts = 16;   // bound on key-loop restarts per workgroup
 // reads on them; completion is waited for explicitly (wait_vmcnt) before the
 // workgroup barrier that publishes a stage.
 __device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t lds_addr, int voffset, int soffset) {
+    // lds_addr and soffset are wave-uniform; readfirstlane keeps them in SGPRs
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                  :
-                 : "s"(lds_addr), "v"(voffset), "s"(rsrc), "s"(soffset)
+                 : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voffset), "s"(rsrc),
+                   "s"(__builtin_amdgcn_readfirstlane(soffset))
                  : "memory", "m0");
 }
 
@@ -170,13 +180,16 @@ __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a) {
     // 64 mod 256 bytes puts the 4 rows on distinct banks.
     constexpr int KP = D * 2 + 16;
     constexpr int VP = D * 2 + 64;
-    constexpr int NIK = (kBN * KP + 4095) / 4096;  // 1 KB loads per wave per tile (K)
-    constexpr int NIV = (kBN * VP + 4095) / 4096;  // (V)
-    constexpr int KREG = NIK * 4096;               // LDS bytes per stage (K, then V)
-    constexpr int STAGE = KREG + NIV * 4096;
+    constexpr int NCK = (kBN * KP + 1023) / 1024;  // 1 KB chunks of a K tile
+    constexpr int NCV = (kBN * VP + 1023) / 1024;  // (V)
+    constexpr int NIK = (NCK + kWaves - 1) / kWaves;   // loads per wave per tile (K)
+    constexpr int NIV = (NCV + kWaves - 1) / kWaves;   // (V)
+    constexpr int KREG = NCK * 1024;               // LDS bytes per stage (K, then V)
+    constexpr int STAGE = KREG + NCV * 1024;
     constexpr int NLD = NIK + NIV;                 // loads per wave per tile
+    constexpr int JUNK = kStages * STAGE;          // 1 KB that loads past a tile's chunks write
 
-    __shared__ __attribute__((aligned(16))) char lds[kStages * STAGE];
+    __shared__ __attribute__((aligned(16))) char lds[kStages * STAGE + 1024];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, half = lane >> 5, l32 = lane & 31;
@@ -201,8 +214,10 @@ __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a) {
 
     // ---- tile loads: per lane and 1 KB chunk q = i * 4 + w of an operand,
     // the byte x = 1024 q + 16 lane of the padded tile is row x / pitch,
-    // column x % pitch; pad bytes and chunks past the tile load from an
-    // offset past the buffer (0 bytes read, zeros written)
+    // column x % pitch; pad bytes load from an offset past the buffer (0
+    // bytes read, zeros written), and a wave's loads past the last chunk
+    // write zeros to the junk kilobyte (every wave issues the same number
+    // of loads per tile, with no branch)
     const uint32_t nbk = (uint32_t)a.k_nb_tok, nbv = (uint32_t)a.v_nb_tok;
     const i32x4 krs = make_rsrc(a.k[b] + kvh * a.k_nb_head, (uint32_t)(L - 1) * nbk + 2 * D);
     const i32x4 vrs = make_rsrc(a.v[b] + kvh * a.v_nb_head, (uint32_t)(L - 1) * nbv + 2 * D);
@@ -220,14 +235,28 @@ __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a) {
         voff[i] = r < kBN && c < 2 * D ? (int)(r * nbv) + c : 0x40000000;
     }
     const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_char*)lds;
-    auto issue = [&](int j) {
+    // loads lo .. hi - 1 of this wave's NLD for tile j (K chunks, then V).
+    // A dead load (a tile past the last one, or any load once a restart is
+    // decided) reads from past the buffer (zeros, no memory traffic) into
+    // the junk kilobyte, so the count of loads per tile stays the same and
+    // no stage is touched.
+    auto issue_range = [&](int j, int lo, int hi, bool live) {
         const uint32_t st = lds0 + (j % kStages) * STAGE;
-        const int sk = (int)((uint32_t)(j * kBN) * nbk), sv = (int)((uint32_t)(j * kBN) * nbv);
+        const int sk = live ? (int)((uint32_t)(j * kBN) * nbk) : 0x40000000;
+        const int sv = live ? (int)((uint32_t)(j * kBN) * nbv) : 0x40000000;
 #pragma unroll
-        for (int i = 0; i < NIK; ++i) dma16(krs, st + (i * kWaves + w) * 1024, koff[i], sk);
-#pragma unroll
-        for (int i = 0; i < NIV; ++i) dma16(vrs, st + KREG + (i * kWaves + w) * 1024, voff[i], sv);
+        for (int i = 0; i < NLD; ++i) {
+            if (i < lo || i >= hi) continue;
+            if (i < NIK) {
+                const int c = i * kWaves + w;
+                dma16(krs, live && c < NCK ? st + c * 1024 : lds0 + JUNK, koff[i], sk);
+            } else {
+                const int c = (i - NIK) * kWaves + w;
+                dma16(vrs, live && c < NCV ? st + KREG + c * 1024 : lds0 + JUNK, voff[i - NIK], sv);
+            }
+        }
     };
+    auto issue = [&](int j) { issue_range(j, 0, NLD, j < n_tiles); };
     // workgroup OR of `flag` at the barrier that ends tile j: each wave
     // publishes its own word in a slot that alternates with j (a slot is
     // rewritten two tiles later, after every wave has read it)
@@ -425,45 +454,26 @@ __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a) {
                 for (int cb = 0; cb < 2; ++cb)
                     o[dt][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[dt][ks], pf[cb][ks], o[dt][cb], 0, 0, 0);
     };
-    // a tile every row of the workgroup sees whole: no masks, no branches.
-    // Four phases, each one scheduling region: K reads + S of half 0 | S of
-    // half 1 beside the softmax of half 0 (+ V reads of half 0) | P.V of
-    // half 0 beside the softmax of half 1 (+ V reads of half 1) | P.V of
-    // half 1
-    auto fast_tile = [&](const lds_char* ka, const lds_char* va) {
-        f32x16 s0[2], s1[2];
-        h8 p0[2][2], p1[2][2];
-        QF kf0[DS], kf1[DS];
-        h8 vf0[DT][2], vf1[DT][2];
-        load_k(ka, 0, kf0);
-        load_k(ka, 1, kf1);
-        mma_k(kf0, s0);
-        // S of each half moves to VGPRs in the phase that computes it, so
-        // the next half's MFMAs have accumulators of their own
-        asm volatile("" : "+v"(s0[0]), "+v"(s0[1]));
-        __builtin_amdgcn_sched_barrier(0);
-        load_v(va, 0, vf0);
-        mma_k(kf1, s1);
-        probs(s0, sl2, p0);
+    // softmax of k step ks (16 keys) of a half for both column blocks, with
+    // the fixed exponent offsets of the loop
+    float nbf[2];
+    auto probs_ks = [&](const f32x16 (&s)[2], int ks, h8 (&pf)[2][2]) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);       // VALU
-            if (i < 8) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);   // DS read
-        }
-        asm volatile("" : "+v"(s1[0]), "+v"(s1[1]));
-        __builtin_amdgcn_sched_barrier(0);
-        load_v(va, 1, vf1);
-        mma_v(vf0, p0);
-        probs(s1, sl2, p1);
+        for (int cb = 0; cb < 2; ++cb) {
+            float ps = lsum[cb];
+            h8 pv;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
-            if (i < 8) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+            for (int e = 0; e < 8; e += 2) {
+                const float p0 = __builtin_amdgcn_exp2f(fmaf(s[cb][ks * 8 + e], sl2, nbf[cb]));
+                const float p1 = __builtin_amdgcn_exp2f(fmaf(s[cb][ks * 8 + e + 1], sl2, nbf[cb]));
+                h2 pp = {(_Float16)p0, (_Float16)p1};
+                pv[e] = pp.x;
+                pv[e + 1] = pp.y;
+                ps = __builtin_amdgcn_fdot2(pp, h2{(_Float16)1.0f, (_Float16)1.0f}, ps, false);
+            }
+            pf[cb][ks] = pv;
+            lsum[cb] = ps;
         }
-        __builtin_amdgcn_sched_barrier(0);
-        mma_v(vf1, p1);
     };
     // a tile with masks: the implicit ones, or the explicit mask (scores
     // then carried in the exp2 domain, the row max tracked per tile: the
@@ -523,9 +533,10 @@ __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a) {
     const int j_fast = EXPL ? 0 : min(n_tiles, (causal ? min(L, past + t_lo_wg + 1) : L) / kBN);
 
     for (int restarts = 0;; ++restarts) {
-        if (n_tiles > 0) issue(0);
-        if (n_tiles > 1) issue(1);
-        if (n_tiles > 1) wait_vm_barrier<NLD>(); else wait_vm_barrier<0>();
+        issue(0);
+        issue(1);
+        issue(2);
+        wait_vm_barrier<2 * NLD>();                             // tile 0 is in LDS
         if (!EXPL && restarts == 0 && n_tiles > 0) {
             // m from half 0 of tile 0: key 0 is visible to every row
             const lds_char *ka, *va;
@@ -537,52 +548,145 @@ __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a) {
         }
         int j = 0;
         bool restart = false;
-        // end of tile j: publish this wave's restart flag, wait for tile j + 1
-        // (tile j + 2's loads may still fly) and OR the flags
-        auto end_tile = [&](int jj, bool flag) -> bool {
-            if (lane == 0) any_flag[jj & 1][w] = flag;
-            if (jj + 2 < n_tiles) wait_vm_barrier<NLD>(); else wait_vm_barrier<0>();
-            int any = 0;
-#pragma unroll
-            for (int i = 0; i < kWaves; ++i) any |= any_flag[jj & 1][i];
-            return any != 0;                                    // workgroup-uniform
-        };
         // (the loops leave through their conditions only: an exit from the
         // middle makes the compiler copy O through VGPRs on every tile)
         int jb = 0;                                             // the tile that asked for the restart
-        for (; j < j_fast && !restart; ++j) {
-            if (j + 2 < n_tiles) issue(j + 2);      // into the stage tile j - 1 used (free since the last barrier)
+        int bar = 0;                                            // barriers passed (flag slot parity)
+        nbf[0] = m[0] == -INFINITY ? 0.0f : -m[0];
+        nbf[1] = m[1] == -INFINITY ? 0.0f : -m[1];
+        // ---- tiles every row of the workgroup sees whole: no masks, no
+        // branches, pipelined across tiles.  Iteration j, in four scheduling
+        // regions (sched_barrier) of 16 MFMAs, each beside a quarter of a
+        // softmax that reads scores finished at least one region earlier:
+        //   1  S of half 1 of tile j         | softmax, 2nd k step of half 0
+        //      barrier: tile j + 1 in LDS, every wave done with tile j - 1
+        //   2  S of half 0 of tile j + 1     | softmax, 1st k step of half 1
+        //   3  P.V of half 0 of tile j       | softmax, 2nd k step of half 1
+        //   4  P.V of half 1 of tile j       | softmax, 1st k step of half 0
+        //                                      of tile j + 1
+        // The loads of tile j + 3 go, after the barrier, into the stage tile
+        // j - 1 used; a tile past the last, or any tile once a restart is
+        // decided (the restart re-reads the stage of the tile that asked for
+        // it), loads nothing.  A tile's overflow verdict is complete after
+        // region 3 and published at the next barrier.
+        f32x16 sc[2];                                           // S of half 0 of the current tile
+        h8 pc[2][2];                                            // its p, first k step filled
+        QF kf1[DS];                                             // K of half 1 of the current tile
+        bool verdict = false;                                   // overflow up to the previous tile
+        auto barrier_flags = [&](bool flag, bool two_ahead) -> bool {
+            if (lane == 0) any_flag[bar & 1][w] = flag;
+            if (two_ahead) wait_vm_barrier<2 * NLD>(); else wait_vm_barrier<NLD>();
+            int any = 0;
+#pragma unroll
+            for (int i = 0; i < kWaves; ++i) any |= any_flag[bar & 1][i];
+            ++bar;
+            return any != 0;                                    // workgroup-uniform
+        };
+        if (j_fast > 0) {
             const lds_char *ka, *va;
-            bases(j, ka, va);
+            bases(0, ka, va);
+            QF kf0[DS];
+            load_k(ka, 0, kf0);
+            mma_k(kf0, sc);
+            probs_ks(sc, 0, pc);
+            load_k(ka, 1, kf1);
+        }
+        // region 1 of tile j (shared by the loop and its last tile)
+        auto region1 = [&](const lds_char* va, f32x16 (&s1)[2], h8 (&vf0)[DT][2]) {
+            load_v(va, 0, vf0);
+            mma_k(kf1, s1);
+            probs_ks(sc, 1, pc);
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        for (; j + 1 < j_fast && !restart; ++j) {
             // O stays in AGPRs across the back-edge (without the hint the
             // compiler moves part of it through VGPRs on every tile)
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
                 for (int cb = 0; cb < 2; ++cb) asm volatile("" : "+a"(o[dt][cb]));
-            fast_tile(ka, va);
-            if (end_tile(j, __any(overflow(restarts)))) {
+            const lds_char *ka, *va, *kn, *vn;
+            bases(j, ka, va);
+            bases(j + 1, kn, vn);
+            f32x16 s1[2], sn[2];
+            h8 p1[2][2], pn[2][2], vf0[DT][2], vf1[DT][2];
+            QF kf0[DS];
+            region1(va, s1, vf0);
+            if (barrier_flags(verdict, false)) {
+                restart = true;
+                jb = j - 1;
+            }
+            const bool live = !restart && j + 3 < n_tiles;
+            // region 2
+            load_k(kn, 0, kf0);
+            issue_range(j + 3, 0, NLD / 2, live);
+            mma_k(kf0, sn);
+            probs_ks(s1, 0, p1);
+            __builtin_amdgcn_sched_barrier(0);
+            // region 3
+            load_v(va, 1, vf1);
+            issue_range(j + 3, NLD / 2, NLD, live);
+            mma_v(vf0, pc);
+            probs_ks(s1, 1, p1);
+            __builtin_amdgcn_sched_barrier(0);
+            verdict = __any(overflow(restarts));
+            // region 4
+            load_k(kn, 1, kf1);
+            mma_v(vf1, p1);
+            probs_ks(sn, 0, pn);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) {
+                sc[cb] = sn[cb];
+                pc[cb][0] = pn[cb][0];
+            }
+        }
+        if (j_fast > 0 && !restart) {
+            // the last of these tiles, j = j_fast - 1: no next tile to start;
+            // the barrier at its end makes its stage free for the masked loop
+            const lds_char *ka, *va;
+            bases(j, ka, va);
+            f32x16 s1[2];
+            h8 p1[2][2], vf0[DT][2], vf1[DT][2];
+            region1(va, s1, vf0);
+            if (barrier_flags(verdict, false)) {
+                restart = true;
+                jb = j - 1;
+            }
+            issue_range(j + 3, 0, NLD, !restart && j + 3 < n_tiles);
+            load_v(va, 1, vf1);
+            probs_ks(s1, 0, p1);
+            mma_v(vf0, pc);
+            probs_ks(s1, 1, p1);
+            mma_v(vf1, p1);
+            if (barrier_flags(__any(overflow(restarts)), true) && !restart) {
                 restart = true;
                 jb = j;
             }
+            ++j;
         }
         for (; j < n_tiles && !restart; ++j) {
-            if (j + 2 < n_tiles) issue(j + 2);
+            issue(j + 3);
             const lds_char *ka, *va;
             bases(j, ka, va);
             bool flag = false;
             if (j * kBN < kend_w) flag = slow_tile(ka, va, j * kBN, restarts) || overflow(restarts);
-            if (end_tile(j, __any(flag))) {
+            // end of tile j: publish the restart flags, wait for tile j + 1
+            // (the loads of tiles j + 2 and j + 3 may still fly)
+            if (barrier_flags(__any(flag), true)) {
                 restart = true;
                 jb = j;
             }
         }
-        if (!restart) break;
+        if (!restart) {
+            wait_vm_barrier<0>();                               // loads past the last tile
+            break;
+        }
         j = jb;
         wait_vm_barrier<0>();                                   // no load may land in a stage after the restart
         if (!EXPL && j * kBN < kend_w) {
             // raise m for the rows whose scores on tile j passed m + 15 (tile j
-            // is still in its stage: tile j + 3 was never issued)
+            // is still in its stage: tile j + 4 was never issued)
             const lds_char *ka, *va;
             bases(j, ka, va);
             f32x16 s[2][2];
