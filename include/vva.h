@@ -197,7 +197,9 @@ VVA_API int vva_supports(const vva_context* ctx, int head_dim, int n_q_heads, in
 /* ------------------------------------------------------------ debugging */
 
 /* Kernel path selection for tests: 0 = automatic (default), 1 = force the
- * VALU row kernel for every attention call.  Per context. */
+ * VALU row kernel for every attention call, 2 = automatic except that
+ * single-token calls on Q8_0 caches use the register-streamed decode kernel
+ * instead of the LDS-streamed one.  Per context. */
 VVA_API vva_status vva_set_attn_path(vva_context* ctx, int path);
 /* Number of key splits used by the last decode call (0 if none). */
 VVA_API int        vva_last_decode_splits(const vva_context* ctx);

@@ -1,0 +1,149 @@
+"""GPU parity of the LDS-streamed Q8_0 decode kernel (decode_stream.hip).
+
+Single-token attention over Q8_0 caches, through the C ABI, against the
+oracle on the exact cache bytes the GPU holds (downloaded).  Tolerance: the
+task's 2e-3 max-abs / 1e-3 mean-abs for Q8_0 caches, against both the exact
+fp64 oracle and the ggml-order oracle (Q quantized to Q8_0, integer block
+dots).  The cases cover every kv-head count the kernel takes (1, 2, 4, 8),
+both head dims, splits whose first row is not 16-byte aligned in memory,
+splits past a short sequence's end, explicit masks, each Q type, and the
+register-streamed kernel (decode.hip) on the same bytes.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import vva
+import vvo
+from gpu_util import as_f32, assert_close, err_stats, fill_cache, oracle_attn, to_gpu
+
+pytestmark = pytest.mark.gpu
+
+MAX_TOL, MEAN_TOL = 2e-3, 1e-3
+
+
+def _decode(ctx, torch, kv, Hq, q_type, seed, mask=None, wgs=None):
+    B = kv.n_seq
+    rng = np.random.default_rng(seed)
+    d = kv.head_dim
+    q = to_gpu(torch, rng.standard_normal((B, 1, Hq, d)), q_type)
+    out = torch.full((B, 1, Hq, d), float("nan"), dtype=torch.float32, device="cuda")
+    mask_t = None if mask is None else torch.from_numpy(mask.view(np.float16)).to("cuda")
+    if wgs is not None:
+        os.environ["VVA_DECODE_WGS"] = str(wgs)
+    try:
+        ctx.attn(kv, 0, q, out, d ** -0.5, mask=mask_t)
+        torch.cuda.synchronize()
+    finally:
+        if wgs is not None:
+            del os.environ["VVA_DECODE_WGS"]
+    return as_f32(torch, q), as_f32(torch, out), ctx.last_decode_splits()
+
+
+def _cache(ctx, d, Hkv, lens, seed):
+    kv = vva.KVCache(ctx, 1, Hkv, d, max(lens) + 8, len(lens), vva.Q8_0)
+    fill_cache(kv, lens, seed=seed)
+    for s, n in enumerate(lens):
+        kv.set_len(s, n - 1)                   # the last row is "the new token"
+    return kv
+
+
+CASES = [
+    # d, Hq, Hkv, lens (incl. the new token), q_type, workgroups (None = one per CU)
+    (128, 28, 4, [8193, 8193], vva.F32, None),     # 7B CFG decode shape, shorter window
+    (128, 28, 4, [33], vva.F32, None),             # one tile and one key
+    (128, 28, 4, [4097, 40], vva.F16, None),       # second stream ends in its first split
+    (128, 12, 2, [3001], vva.BF16, None),          # 1.5B heads: 64-key tiles
+    (128, 8, 1, [2500, 1999], vva.F32, 37),        # one kv head: 136-byte rows, unaligned splits
+    (128, 16, 8, [1777], vva.F32, None),           # eight kv heads: one wave each
+    (64, 14, 2, [3333, 1025], vva.F32, 21),        # 0.5B heads: 136-byte rows, unaligned splits
+    (64, 8, 4, [999], vva.F16, None),
+    (128, 28, 4, [700, 700], vva.F32, 1),          # one split: output written directly
+]
+
+
+@pytest.mark.parametrize("d,Hq,Hkv,lens,q_type,wgs", CASES)
+def test_stream_decode_matches_oracle(ctx, torch_gpu, d, Hq, Hkv, lens, q_type, wgs):
+    torch = torch_gpu
+    print(f"stream decode d={d} Hq={Hq} Hkv={Hkv} lens={lens} q={q_type} wgs={wgs}", flush=True)
+    kv = _cache(ctx, d, Hkv, lens, seed=d + Hkv + sum(lens))
+    q, out, splits = _decode(ctx, torch, kv, Hq, q_type, seed=5, wgs=wgs)
+    ref = oracle_attn(q, kv, 0, range(len(lens)), lens, 1, d ** -0.5)
+    mx, mn = assert_close(out, ref, MAX_TOL, MEAN_TOL, what="stream decode vs exact")
+    gg = oracle_attn(q, kv, 0, range(len(lens)), lens, 1, d ** -0.5, mode=vvo.GGML)
+    gmx, gmn = err_stats(out, gg)
+    print(f"  splits {splits}: vs exact max {mx:.2e} mean {mn:.2e}; vs ggml-order max {gmx:.2e} mean {gmn:.2e}")
+    assert gmx <= MAX_TOL and gmn <= MEAN_TOL
+    kv.free()
+
+
+def test_stream_decode_matches_register_kernel(ctx, torch_gpu):
+    """Same bytes, same Q: the LDS-streamed and the register-streamed kernels
+    differ only in where each split's running max sits (f16 p * d_v rounding)."""
+    torch = torch_gpu
+    lens = [6001, 5000]
+    kv = _cache(ctx, 128, 4, lens, seed=77)
+    _, a, sa = _decode(ctx, torch, kv, 28, vva.F32, seed=8)
+    ctx.set_attn_path(2)
+    try:
+        _, b, sb = _decode(ctx, torch, kv, 28, vva.F32, seed=8)
+    finally:
+        ctx.set_attn_path(0)
+    print(f"splits stream {sa}, register {sb}; max diff {np.abs(a - b).max():.2e}")
+    assert np.abs(a - b).max() < 2e-4
+    kv.free()
+
+
+def test_stream_decode_split_count_does_not_change_result(ctx, torch_gpu):
+    torch = torch_gpu
+    lens = [5000, 4321]
+    kv = _cache(ctx, 128, 4, lens, seed=3)
+    outs = []
+    for wgs in (2, 16, 100, 512):
+        _, out, splits = _decode(ctx, torch, kv, 28, vva.F32, seed=9, wgs=wgs)
+        outs.append((splits, out))
+    assert len({s for s, _ in outs}) == 4, [s for s, _ in outs]
+    for s, o in outs[1:]:
+        assert np.abs(o - outs[0][1]).max() < 2e-4, s
+    kv.free()
+
+
+def test_stream_decode_explicit_mask(ctx, torch_gpu):
+    torch = torch_gpu
+    L = 2000
+    kv = _cache(ctx, 128, 4, [L], seed=4)
+    m = np.zeros((1, 1, L), np.float32)
+    m[0, 0, 100:900] = -np.inf                 # a hole across several splits
+    m[0, 0, 1500:1503] = -np.inf
+    mbits = vvo.f16_bits(m)
+    q, out, _ = _decode(ctx, torch, kv, 28, vva.F32, seed=6, mask=mbits)
+    ref = oracle_attn(q, kv, 0, [0], [L], 1, 128 ** -0.5, mask=mbits)
+    assert_close(out, ref, MAX_TOL, MEAN_TOL, what="masked stream decode")
+    kv.free()
+
+
+def test_stream_decode_consecutive_steps(ctx, torch_gpu):
+    """Append-then-attend steps through rope_append, as the decode loop runs
+    them: each step's output matches the oracle on the grown cache."""
+    torch = torch_gpu
+    d, Hq, Hkv, L0 = 128, 28, 4, 3000
+    kv = vva.KVCache(ctx, 1, Hkv, d, L0 + 8, 2, vva.Q8_0)
+    fill_cache(kv, [L0, L0], seed=12)
+    rng = np.random.default_rng(13)
+    for step in range(3):
+        L = L0 + step
+        q = to_gpu(torch, rng.standard_normal((2, 1, Hq, d)), vva.F32)
+        k = to_gpu(torch, rng.standard_normal((2, 1, Hkv, d)), vva.F32)
+        v = to_gpu(torch, rng.standard_normal((2, 1, Hkv, d)), vva.F32)
+        pos = torch.full((1,), L, dtype=torch.int32, device="cuda")
+        qr = torch.empty_like(q)
+        ctx.rope_append(kv, 0, q, k, v, pos, qr)
+        out = torch.empty_like(q)
+        ctx.attn(kv, 0, qr, out, d ** -0.5)
+        torch.cuda.synchronize()
+        ref = oracle_attn(as_f32(torch, qr), kv, 0, [0, 1], [L + 1, L + 1], 1, d ** -0.5)
+        assert_close(as_f32(torch, out), ref, MAX_TOL, MEAN_TOL, what=f"step {step}")
+        for s in range(2):
+            kv.set_len(s, L + 1)
+    kv.free()

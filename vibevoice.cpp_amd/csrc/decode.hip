@@ -44,35 +44,11 @@ namespace vva {
 
 namespace {
 
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-typedef __amdgpu_buffer_rsrc_t BufRsrc;
+#include "wave_ops.hpp"
 
-// Raw buffer descriptor (stride 0, range `bytes`; word 3 = 0x00020000, the
-// gfx9 raw-buffer configuration): loads at offsets past the range return 0.
-__device__ __forceinline__ BufRsrc make_rsrc(const char* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), (short)0, (int)bytes, 0x00020000);
-}
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
-
-constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazy = 8.0f;      // running-max slack in log2 units: p <= 256
 constexpr int kWaves = 8;
 constexpr int kMaxSplits = 256;
-
-__device__ __forceinline__ float dot2_f16(uint32_t a, uint32_t b, float c) {
-    h2 x, y;
-    __builtin_memcpy(&x, &a, 4);
-    __builtin_memcpy(&y, &b, 4);
-    return __builtin_amdgcn_fdot2(x, y, c, false);
-}
-__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
-    bf2 x, y;
-    __builtin_memcpy(&x, &a, 4);
-    __builtin_memcpy(&y, &b, 4);
-    return __builtin_amdgcn_fdot2_f32_bf16(x, y, c, false);
-}
 
 template <int KT>
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
@@ -83,103 +59,6 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
 __device__ __forceinline__ float half_to_f32_rt(uint32_t v, int type) {
     return type == VVA_TYPE_BF16 ? bf16_to_f32((uint16_t)v) : f16_to_f32((uint16_t)v);
 }
-
-__device__ __forceinline__ void wave_lds_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-// Cross-lane steps without LDS: DPP within rows of 16 lanes, permlane swaps
-// across rows (v_permlane16_swap pairs rows 0-1 / 2-3, v_permlane32_swap the
-// two halves of the wave).
-template <int CTRL>
-__device__ __forceinline__ float dpp(float x) {
-    return __uint_as_float(__builtin_amdgcn_mov_dpp(__float_as_uint(x), CTRL, 0xf, 0xf, true));
-}
-constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
-__device__ __forceinline__ float max_swap16(float x) {
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float max_swap32(float x) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float add_swap16(float x) {
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-__device__ __forceinline__ float add_swap32(float x) {
-    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-// Sum over the LPT lanes of one key (aligned groups of 2, 4 or 8), for N
-// values at once so consecutive DPP steps do not wait on each other.
-template <int LPT, int N>
-__device__ __forceinline__ void key_sum(float (&x)[N]) {
-#pragma unroll
-    for (int i = 0; i < N; ++i) x[i] += dpp<kDppXor1>(x[i]);
-    if constexpr (LPT >= 4) {
-#pragma unroll
-        for (int i = 0; i < N; ++i) x[i] += dpp<kDppXor2>(x[i]);
-    }
-    if constexpr (LPT == 8) {
-#pragma unroll
-        for (int i = 0; i < N; ++i) x[i] += dpp<kDppHalfMirror>(x[i]);
-    }
-}
-// Max over all keys of the wave, for values equal within each LPT group.
-template <int LPT, int N>
-__device__ __forceinline__ void keys_max(float (&x)[N]) {
-    if constexpr (LPT == 2) {
-#pragma unroll
-        for (int i = 0; i < N; ++i) x[i] = fmaxf(x[i], dpp<kDppXor2>(x[i]));
-    }
-    if constexpr (LPT <= 4) {
-#pragma unroll
-        for (int i = 0; i < N; ++i) x[i] = fmaxf(x[i], dpp<kDppHalfMirror>(x[i]));
-    }
-#pragma unroll
-    for (int i = 0; i < N; ++i) x[i] = fmaxf(x[i], dpp<kDppMirror>(x[i]));
-#pragma unroll
-    for (int i = 0; i < N; ++i) x[i] = max_swap16(x[i]);
-#pragma unroll
-    for (int i = 0; i < N; ++i) x[i] = max_swap32(x[i]);
-}
-// Sum over all 64 lanes (every lane gets the total).
-__device__ __forceinline__ float wave_sum(float x) {
-    x += dpp<kDppXor1>(x);
-    x += dpp<kDppXor2>(x);
-    x += dpp<kDppHalfMirror>(x);
-    x += dpp<kDppMirror>(x);
-    x = add_swap16(x);
-    return add_swap32(x);
-}
-
-// First dot of a chain: the VOP3P form with an inline 0 accumulator (the
-// accumulate-in-place form would need the zero moved in first).
-__device__ __forceinline__ int sdot4_first(uint32_t a, uint32_t b) {
-    int r;
-    asm("v_dot4_i32_i8 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
-    return r;
-}
-
-// (int8 byte N of a, int8 byte N of b) -> f16 pair (exact): two SDWA
-// converts, the second writing the high half in place.
-#define VVA_I8_PAIR(N)                                                                          \
-    __device__ __forceinline__ uint32_t i8_pair_b##N(uint16_t a, uint16_t b) {                  \
-        uint32_t r;                                                                             \
-        asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_" #N "\n\t" \
-            "v_cvt_f16_i16_sdwa %0, sext(%2) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_" #N \
-            : "=&v"(r) : "v"(a), "v"(b));                                                       \
-        return r;                                                                               \
-    }
-VVA_I8_PAIR(0)
-VVA_I8_PAIR(1)
-VVA_I8_PAIR(2)
-VVA_I8_PAIR(3)
-#undef VVA_I8_PAIR
 
 template <int D, int G, int KT>
 struct Cfg {
@@ -697,6 +576,16 @@ hipError_t launch_dg(const AttnArgs& a, float* ws, int n_splits, int split_len, 
 }
 
 }  // namespace
+
+hipError_t launch_decode_merge(const AttnArgs& a, const float* ws, int n_splits, hipStream_t s) {
+    if (a.d == 64)
+        hipLaunchKernelGGL(decode_merge_kernel<64>, dim3(a.Hq, a.B), dim3(kMergeThreads), 0, s, a, ws, n_splits);
+    else if (a.d == 128)
+        hipLaunchKernelGGL(decode_merge_kernel<128>, dim3(a.Hq, a.B), dim3(kMergeThreads), 0, s, a, ws, n_splits);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
 
 int decode_waves(const AttnArgs&) { return kWaves; }
 int decode_max_splits() { return kMaxSplits; }

@@ -1,0 +1,490 @@
+// decode_stream.hip — split-K single-token attention (T == 1) over a dense
+// Q8_0 KV cache: the per-step attention of the ASR / TTS decode loops
+// (src/vibevoice_asr.cpp:760-800, src/vibevoice_tts.cpp:862-880), i.e.
+// ggml_flash_attn_ext with one query row per head (src/qwen2.cpp:332-334)
+// on Q8_0 K/V.
+//
+// Streaming.  Every workgroup (8 waves, one per CU) takes a contiguous key
+// range of one sequence and streams it through a 4-stage LDS ring filled by
+// buffer_load_dwordx4 ... lds, so three tiles (102 KB per CU) are on their
+// way from HBM while one is computed.  A tile is 512 (key, kv head, 32-dim
+// block) rows of the cache = 17,408 B of K plus the same of V, read as the
+// cache lays them out ([token][kv head][34-byte GGUF block]): one contiguous
+// byte range per operand, 1 KB per wave instruction.  The buffer ranges of
+// a split end at its last key, so chunks past it come back as zeros without
+// a memory access.
+//
+// Arithmetic on the matrix cores.  With g = 7 query heads per kv head, the
+// VALU form of this loop (v_dot4 scores, v_dot2 P.V) needs ~800 VALU lane
+// operations per (key, kv head) and runs VALU-bound at about a third of
+// HBM speed; on MFMA the VALU keeps only the conversions and the softmax.
+// Per tile, wave w takes kv head w % Hkv and 16 (d = 128) or 32 (d = 64) of
+// the tile's keys, in groups of 16 keys; lane = (g = lane / 16, n = lane % 16).
+// MFMA row/column m of a group stands for its key sigma(m) = 4 (m % 4) +
+// m / 4, so lane group g works on keys g, g + 4, g + 8, g + 12: with the
+// cache's 544-byte token rows the four groups' LDS reads then fall in
+// different banks.
+//   scores  S^T[key][row] per 32-dim block b with v_mfma_i32_16x16x32_i8:
+//           A = the K codes of block b (lane: key sigma(n), codes 8g..8g+7),
+//           B = Q quantized to Q8_0 (lane: row n, same codes), so each
+//           block's dot is ggml's exact integer Q8_0 x Q8_0 block sum; the
+//           lane receives keys sigma(4g + i) of row n and scales them by
+//           d_k * d_q in fp32.
+//   softmax fp32, exp2 domain, one row per lane (max over the row's 16 keys:
+//           in-lane, then two permlane swaps).  The running max is raised
+//           only when a score exceeds it by 2^8.
+//   P.V     O^T[dim][row] += V^T P'^T with v_mfma_f32_16x16x16_f16 per 16
+//           dims: A = V codes (exact in f16; lane: dims 2n, 2n+1 of block b,
+//           keys sigma(4g + i)), B = P' = p * d_v(key, b) as f16 — the score
+//           accumulator layout is already B's layout, so P never leaves the
+//           registers.  MFMA j = 2b + s holds dims 32b + 2m + s in its row m.
+// The waves of one kv head merge through LDS (log-sum-exp); the workgroup
+// writes (m, l, acc[d]) per query head, or the output when there is one
+// split, and decode_merge_kernel (decode.hip) combines the splits.
+#include "vva_internal.hpp"
+
+namespace vva {
+
+namespace {
+
+#include "wave_ops.hpp"
+
+typedef __attribute__((address_space(3))) char lds_char;
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kW = 8;                        // waves per workgroup
+constexpr int kStages = 4;                   // LDS ring depth (power of 2)
+constexpr int kTileOpBytes = 17408;          // one operand of a tile: 512 Q8_0 blocks
+constexpr int kOpChunks = 18;                // 1 KB chunks per operand: 17 KB + alignment slack
+constexpr int kOpBytes = kOpChunks * 1024;
+constexpr int kStage = 2 * kOpBytes;         // K, then V
+constexpr int kJunk = kStages * kStage;      // 1 KB target of the padding loads
+constexpr int kLdsBytes = kJunk + 1024;
+constexpr int kLoads = (2 * kOpChunks + kW - 1) / kW;   // DMA loads per wave per tile
+constexpr int kDead = 0x40000000;            // buffer offset past every range
+constexpr float kLazy = 8.0f;                // running-max slack in log2 units: p <= 256
+static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
+
+// buffer_load_dwordx4 ... lds: each lane's 16 bytes land at LDS address
+// m0 + 16 * lane.  Inline asm, so the compiler neither fences LDS reads on it
+// nor waits for it; completion is awaited explicitly (wait_vm_barrier).  The
+// whole offset is in the VGPR (soffset 0), so the range check sees all of it.
+__device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t lds_addr, int voffset) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voffset), "s"(rsrc)
+                 : "memory", "m0");
+}
+
+// wait until at most N of this wave's loads are outstanding (and its LDS
+// operations are done), then meet the workgroup at a barrier
+template <int N>
+__device__ __forceinline__ void wait_vm_barrier() {
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(N) : "memory");
+}
+
+// fp16 scale of Q8_0 block b of the head row at `row` (4-byte aligned): the
+// block starts at byte 34 b, so its scale is the low half of an aligned
+// dword for even b and the high half for odd b.
+template <int B>
+__device__ __forceinline__ uint16_t block_scale(const char* row) {
+    constexpr int off = B * kQ8Bytes;
+    if constexpr (off % 4 == 0) return (uint16_t)(*(const uint32_t*)(row + off));
+    else return (uint16_t)(*(const uint32_t*)(row + off - 2) >> 16);
+}
+
+template <int NB, int B = 0>
+__device__ __forceinline__ void load_scales(const char* row, uint16_t (&dst)[NB]) {
+    if constexpr (B < NB) {
+        dst[B] = block_scale<B>(row);
+        load_scales<NB, B + 1>(row, dst);
+    }
+}
+
+__device__ __forceinline__ h2 as_h2(uint16_t lo, uint16_t hi) {
+    const uint32_t u = (uint32_t)lo | ((uint32_t)hi << 16);
+    h2 v;
+    __builtin_memcpy(&v, &u, 4);
+    return v;
+}
+__device__ __forceinline__ h4 as_h4(uint32_t lo, uint32_t hi) {
+    const uint64_t u = (uint64_t)lo | ((uint64_t)hi << 32);
+    h4 v;
+    __builtin_memcpy(&v, &u, 8);
+    return v;
+}
+__device__ __forceinline__ h4 cat_h4(h2 lo, h2 hi) { return h4{lo[0], lo[1], hi[0], hi[1]}; }
+
+// D: head dim (64 / 128); G: query heads per kv head (<= 16).
+template <int D, int G>
+__global__ void __launch_bounds__(kW * 64)
+decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split_len) {
+    constexpr int NB = D / 32;                // Q8_0 blocks per head row
+    constexpr int HB = NB * kQ8Bytes;         // bytes per head row
+    constexpr int NSUB = 128 / D;             // groups of 16 keys per wave per tile
+    constexpr int KPW = 16 * NSUB;            // keys per wave per tile
+    constexpr int NJ = 2 * NB;                // P.V MFMAs (16 dims each) per key group
+    static_assert(KPW * kW * HB == kTileOpBytes, "tile size");
+    static_assert(G <= 16, "one query head per lane row");
+
+    __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
+
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4, n = lane & 15;
+    const int Hkv = a.Hkv;
+    const int R = kW / Hkv;                   // waves per kv head
+    const int h = w % Hkv, r = w / Hkv;
+    const int RB = Hkv * HB;                  // bytes per token row (all kv heads)
+    const int TT = KPW * R;                   // keys per tile
+    const int split = blockIdx.x, b = blockIdx.y;
+    const int L = a.L[b];
+    const int j0 = min(L, split * split_len);
+    const int j1 = min(L, j0 + split_len);
+    const int n_tiles = (j1 - j0 + TT - 1) / TT;
+
+    // One raw buffer per operand: from the 16-byte boundary at or below the
+    // split's first row to its last row.  delta = the row start's offset
+    // from that boundary (a multiple of 4), also its offset in the LDS tile.
+    const char* kfirst = a.k[b] + (int64_t)j0 * RB;
+    const char* vfirst = a.v[b] + (int64_t)j0 * RB;
+    const int dk = (int)((uintptr_t)kfirst & 15), dv = (int)((uintptr_t)vfirst & 15);
+    const uint32_t span = (uint32_t)(j1 - j0) * (uint32_t)RB;
+    const i32x4 krs = make_rsrc_sgpr(kfirst - dk, dk + span);
+    const i32x4 vrs = make_rsrc_sgpr(vfirst - dv, dv + span);
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_char*)lds;
+
+    // Tile t of an operand is bytes [t * 17408, t * 17408 + 18 KB) of its
+    // buffer, chunk c (1 KB) loaded by wave c % kW as its (c / kW)-th load.
+    // Every wave issues kLoads loads per tile: the 36 chunks of K and V, then
+    // padding loads (from past the range: zeros, no memory access) into the
+    // junk kilobyte.  A tile past the last one loads nothing but zeros; the
+    // 18th chunk of an operand is needed only when delta > 0.
+    auto issue = [&](int t) {
+        const bool live = t < n_tiles;
+        const uint32_t st = lds0 + (uint32_t)(t & (kStages - 1)) * kStage;
+        const int tb = t * kTileOpBytes + lane * 16;
+#pragma unroll
+        for (int i = 0; i < kLoads; ++i) {
+            const int c = i * kW + w;
+            if (c < kOpChunks) {
+                const bool need = live && (c < kOpChunks - 1 || dk > 0);
+                dma16(krs, st + c * 1024, need ? tb + c * 1024 : kDead);
+            } else if (c < 2 * kOpChunks) {
+                const int cc = c - kOpChunks;
+                const bool need = live && (cc < kOpChunks - 1 || dv > 0);
+                dma16(vrs, st + kOpBytes + cc * 1024, need ? tb + cc * 1024 : kDead);
+            } else {
+                dma16(krs, lds0 + kJunk, kDead);
+            }
+        }
+    };
+
+    // ---- Q: loaded first, then the first tiles go out, then Q is quantized
+    // to Q8_0 blocks (codes + fp16-rounded scale) into the ring's last stage,
+    // which the loop does not load before its first barrier.  Four adjacent
+    // lanes share a block (8 values each; the block max over the quad by
+    // DPP); with more than 128 blocks a thread takes a second quarter.
+    constexpr int QI = 2;                             // quarters per thread (Hq * NB <= 256)
+    const int nqi = a.Hq * NB * 4;
+    const int eb = (int)type_elem_bytes(a.q_type);
+    uint4 qraw[QI][2];
+#pragma unroll
+    for (int it = 0; it < QI; ++it) {
+        const int t = (int)threadIdx.x + it * kW * 64;
+        const int tt = t < nqi ? t : 0;
+        const int qh = tt / (NB * 4), qc = (tt >> 2) % NB, qp = tt & 3;
+        const char* src = a.q + b * a.q_nb_b + qh * a.q_nb_h + (int64_t)(qc * 32 + qp * 8) * eb;
+        qraw[it][0] = ((const uint4*)src)[0];
+        qraw[it][1] = a.q_type == VVA_TYPE_F32 ? ((const uint4*)src)[1] : qraw[it][0];
+    }
+#pragma unroll
+    for (int t = 0; t < kStages - 1; ++t) issue(t);
+
+    uint32_t* qlds = (uint32_t*)(lds + (kStages - 1) * kStage);
+#pragma unroll
+    for (int it = 0; it < QI; ++it) {
+        if (it * kW * 64 >= nqi) break;               // uniform
+        const int t = (int)threadIdx.x + it * kW * 64;
+        float x[8];
+        if (a.q_type == VVA_TYPE_F32) {
+            const uint4 u0 = qraw[it][0], u1 = qraw[it][1];
+            x[0] = __uint_as_float(u0.x); x[1] = __uint_as_float(u0.y);
+            x[2] = __uint_as_float(u0.z); x[3] = __uint_as_float(u0.w);
+            x[4] = __uint_as_float(u1.x); x[5] = __uint_as_float(u1.y);
+            x[6] = __uint_as_float(u1.z); x[7] = __uint_as_float(u1.w);
+        } else {
+            const bool bf = a.q_type == VVA_TYPE_BF16;
+            const uint32_t wv[4] = {qraw[it][0].x, qraw[it][0].y, qraw[it][0].z, qraw[it][0].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint16_t lo = (uint16_t)(wv[e] & 0xffffu), hi = (uint16_t)(wv[e] >> 16);
+                x[2 * e] = bf ? bf16_to_f32(lo) : f16_to_f32(lo);
+                x[2 * e + 1] = bf ? bf16_to_f32(hi) : f16_to_f32(hi);
+            }
+        }
+        float am = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(x[i]));
+        am = fmaxf(am, dpp<kDppXor1>(am));
+        am = fmaxf(am, dpp<kDppXor2>(am));
+        const float dq = am / 127.0f;
+        const float id = dq != 0.0f ? 1.0f / dq : 0.0f;
+        uint32_t c[2] = {0, 0};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) c[i >> 2] |= ((uint32_t)(uint8_t)(int8_t)roundf(x[i] * id)) << (8 * (i & 3));
+        if (t < nqi) {
+            uint32_t* dst = qlds + (t >> 2) * 9;
+            dst[2 * (t & 3)] = c[0];
+            dst[2 * (t & 3) + 1] = c[1];
+            if ((t & 3) == 0) dst[8] = __float_as_uint(f16_to_f32(f32_to_f16(dq)));
+        }
+    }
+    __syncthreads();
+
+    // B operand of the score MFMAs: row n's Q codes 8g..8g+7 of each block,
+    // and its block scales times scale * log2(e) (rows past g are zero)
+    long qb[NB];
+    float qd[NB];
+    {
+        const float sl2 = a.scale * kLog2e;          // scores come out in the exp2 domain
+#pragma unroll
+        for (int bb = 0; bb < NB; ++bb) {
+            qb[bb] = 0;
+            qd[bb] = 0.0f;
+            if (n < G) {
+                const uint32_t* src = qlds + ((h * G + n) * NB + bb) * 9;
+                qb[bb] = (long)((uint64_t)src[2 * g] | ((uint64_t)src[2 * g + 1] << 32));
+                qd[bb] = __uint_as_float(src[8]) * sl2;
+            }
+        }
+    }
+
+    float m = -INFINITY, l = 0.0f;            // row n's running max (log2 domain) and sum
+    f32x4 acc[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) acc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const char* mrow = a.mask_mode == kMaskExplicit ? a.mask + b * a.mask_nb_b : nullptr;   // query row 0
+
+    for (int t = 0; t < n_tiles; ++t) {
+        // tile t has landed in every wave's share; every wave is done with t - 1
+        wait_vm_barrier<(kStages - 2) * kLoads>();
+        issue(t + kStages - 1);
+        const char* kt = lds + (t & (kStages - 1)) * kStage + dk + h * HB;
+        const char* vt = lds + (t & (kStages - 1)) * kStage + kOpBytes + dv + h * HB;
+#pragma unroll
+        for (int u = 0; u < NSUB; ++u) {
+            const int kb = r * KPW + 16 * u;              // first key of the group in the tile
+            // ---- scores: per block, A = key (kb + sigma(n))'s codes 8g..8g+7
+            i32x4 cs[NB];
+            {
+                const char* ka = kt + (kb + 4 * (n & 3) + (n >> 2)) * RB;
+#pragma unroll
+                for (int bb = 0; bb < NB; ++bb) {
+                    const int off = bb * kQ8Bytes + 2 + 8 * g;       // 2 mod 4 for even blocks
+                    const uint32_t* p = (const uint32_t*)(ka + (off & ~3));
+                    const int sh = (bb & 1) ? 0 : 2;
+                    const uint32_t w0 = p[0], w1 = p[1];
+                    uint32_t lo = w0, hi = w1;
+                    if (sh) {
+                        const uint32_t w2 = p[2];
+                        lo = __builtin_amdgcn_alignbyte(w1, w0, 2);
+                        hi = __builtin_amdgcn_alignbyte(w2, w1, 2);
+                    }
+                    const long av = (long)((uint64_t)lo | ((uint64_t)hi << 32));
+                    cs[bb] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, qb[bb], i32x4{0, 0, 0, 0}, 0, 0, 0);
+                }
+            }
+            // the lane's output keys kb + sigma(4g + i) = kb + 4i + g: their K
+            // and V block scales and the V codes of dims 2n, 2n + 1 of every
+            // block
+            uint16_t dkh[4][NB], dvh[4][NB], vc[4][NB];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int key = kb + 4 * i + g;
+                load_scales<NB>(kt + key * RB, dkh[i]);
+                load_scales<NB>(vt + key * RB, dvh[i]);
+#pragma unroll
+                for (int bb = 0; bb < NB; ++bb)
+                    vc[i][bb] = *(const uint16_t*)(vt + key * RB + bb * kQ8Bytes + 2 + 2 * n);
+            }
+            float s[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float x = 0.0f;
+#pragma unroll
+                for (int bb = 0; bb < NB; ++bb) x = fmaf((float)cs[bb][i], f16_to_f32(dkh[i][bb]) * qd[bb], x);
+                const int j = j0 + t * TT + kb + 4 * i + g;
+                bool live = j < j1;
+                if (mrow) {
+                    const float mv = live ? f16_to_f32(*(const uint16_t*)(mrow + 2 * (int64_t)j)) * kLog2e : 0.0f;
+                    live = live && mv != -INFINITY;
+                    x += mv;
+                }
+                s[i] = live ? x : -INFINITY;
+            }
+
+            // ---- online softmax of row n, running max raised lazily
+            const bool raise = s[0] > m + kLazy || s[1] > m + kLazy || s[2] > m + kLazy || s[3] > m + kLazy;
+            if (__any(raise)) {
+                float cm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+                cm = max_swap32(max_swap16(cm));
+                if (cm > m + kLazy) {
+                    const float alpha = __builtin_amdgcn_exp2f(m - cm);     // 0 when m = -inf
+                    l *= alpha;
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j) acc[j] *= alpha;
+                    m = cm;
+                }
+            }
+            const float base = m == -INFINITY ? 0.0f : m;
+            float p[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(s[i] - base);   // 0 when masked
+            l += (p[0] + p[1]) + (p[2] + p[3]);
+            const h2 p01 = h2{(_Float16)p[0], (_Float16)p[1]};
+            const h2 p23 = h2{(_Float16)p[2], (_Float16)p[3]};
+
+            // ---- O^T += V^T P'^T per 16 dims
+#pragma unroll
+            for (int bb = 0; bb < NB; ++bb) {
+                const h4 pb = cat_h4(p01 * as_h2(dvh[0][bb], dvh[1][bb]), p23 * as_h2(dvh[2][bb], dvh[3][bb]));
+                const h4 a0 = as_h4(i8_pair_mfma_b0(vc[0][bb], vc[1][bb]), i8_pair_mfma_b0(vc[2][bb], vc[3][bb]));
+                const h4 a1 = as_h4(i8_pair_mfma_b1(vc[0][bb], vc[1][bb]), i8_pair_mfma_b1(vc[2][bb], vc[3][bb]));
+                acc[2 * bb] = __builtin_amdgcn_mfma_f32_16x16x16f16(a0, pb, acc[2 * bb], 0, 0, 0);
+                acc[2 * bb + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(a1, pb, acc[2 * bb + 1], 0, 0, 0);
+            }
+        }
+    }
+    // the padding tiles' loads land before the ring is reused
+    asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+    __syncthreads();
+
+    // row n's sum over the four lane groups
+    l = add_swap32(add_swap16(l));
+
+    // lane (g, n) holds O[row n][32 b + 8 g + 2 i + s] = acc[2 b + s][i]
+    auto dims = [&](int bb, int half) -> float4 {
+        const f32x4 e = acc[2 * bb], o = acc[2 * bb + 1];
+        return half == 0 ? make_float4(e[0], o[0], e[1], o[1]) : make_float4(e[2], o[2], e[3], o[3]);
+    };
+
+    // ---- merge the R waves of each kv head (log-sum-exp) through LDS
+    float (*abuf)[16][D] = (float (*)[16][D])lds;
+    float (*mbuf)[16] = (float (*)[16])(lds + kW * 16 * D * 4);
+    float (*lbuf)[16] = (float (*)[16])(lds + kW * 16 * D * 4 + kW * 16 * 4);
+    if (R > 1) {
+        if (r > 0) {
+            if (g == 0) { mbuf[w][n] = m; lbuf[w][n] = l; }
+#pragma unroll
+            for (int bb = 0; bb < NB; ++bb) {
+                *(float4*)&abuf[w][n][32 * bb + 8 * g] = dims(bb, 0);
+                *(float4*)&abuf[w][n][32 * bb + 8 * g + 4] = dims(bb, 1);
+            }
+        }
+        __syncthreads();
+        if (r > 0) return;
+        for (int rr = 1; rr < R; ++rr) {
+            const int ow = rr * Hkv + h;
+            const float mo = mbuf[ow][n];
+            const float mn = fmaxf(m, mo);
+            const float fa = mn == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - mn);
+            const float fb = mn == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mo - mn);
+            l = l * fa + lbuf[ow][n] * fb;
+#pragma unroll
+            for (int bb = 0; bb < NB; ++bb) {
+                const float4 x = *(const float4*)&abuf[ow][n][32 * bb + 8 * g];
+                const float4 y = *(const float4*)&abuf[ow][n][32 * bb + 8 * g + 4];
+                f32x4& e = acc[2 * bb];
+                f32x4& o = acc[2 * bb + 1];
+                e[0] = e[0] * fa + x.x * fb; o[0] = o[0] * fa + x.y * fb;
+                e[1] = e[1] * fa + x.z * fb; o[1] = o[1] * fa + x.w * fb;
+                e[2] = e[2] * fa + y.x * fb; o[2] = o[2] * fa + y.y * fb;
+                e[3] = e[3] * fa + y.z * fb; o[3] = o[3] * fa + y.w * fb;
+            }
+            m = mn;
+        }
+    }
+    if (n >= G) return;
+    const int hq = h * G + n;
+    if (n_splits == 1) {
+        const float inv = l == 0.0f ? 0.0f : 1.0f / l;
+        float* orow = (float*)((char*)a.out + b * a.o_nb_b + hq * a.o_nb_h);
+#pragma unroll
+        for (int bb = 0; bb < NB; ++bb) {
+            const float4 x = dims(bb, 0), y = dims(bb, 1);
+            *(float4*)(orow + 32 * bb + 8 * g) = make_float4(x.x * inv, x.y * inv, x.z * inv, x.w * inv);
+            *(float4*)(orow + 32 * bb + 8 * g + 4) = make_float4(y.x * inv, y.y * inv, y.z * inv, y.w * inv);
+        }
+        return;
+    }
+    // partials: acc [B][Hq][n_splits][D], then (m, l) [B][Hq][n_splits][2]
+    const size_t idx = ((size_t)b * a.Hq + hq) * n_splits + split;
+    float* wacc = ws + idx * D;
+#pragma unroll
+    for (int bb = 0; bb < NB; ++bb) {
+        *(float4*)(wacc + 32 * bb + 8 * g) = dims(bb, 0);
+        *(float4*)(wacc + 32 * bb + 8 * g + 4) = dims(bb, 1);
+    }
+    if (g == 0) *(float2*)(ws + (size_t)a.B * a.Hq * n_splits * D + idx * 2) = make_float2(m, l);
+}
+
+template <int D>
+hipError_t launch_ds(const AttnArgs& a, float* ws, int n_splits, int split_len, hipStream_t s) {
+    const dim3 grid(n_splits, a.B), block(kW * 64);
+    switch (a.Hq / a.Hkv) {
+#define VVA_DS(G) case G: hipLaunchKernelGGL((decode_stream_kernel<D, G>), grid, block, 0, s, a, ws, n_splits, split_len); break;
+        VVA_DS(1) VVA_DS(2) VVA_DS(3) VVA_DS(4) VVA_DS(5) VVA_DS(6) VVA_DS(7) VVA_DS(8)
+#undef VVA_DS
+        default: return hipErrorInvalidValue;
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || n_splits == 1) return e;
+    return launch_decode_merge(a, ws, n_splits, s);
+}
+
+}  // namespace
+
+bool decode_stream_supported(const AttnArgs& a) {
+    if (a.T != 1) return false;
+    if (a.d != 64 && a.d != 128) return false;
+    if (a.k_type != VVA_TYPE_Q8_0 || a.v_type != VVA_TYPE_Q8_0) return false;
+    if (a.Hkv < 1 || a.Hq % a.Hkv != 0 || a.Hq / a.Hkv > 8) return false;
+    if (kW % a.Hkv != 0) return false;
+    // dense rows: [token][kv head][blocks], as the resident cache stores them
+    const int64_t hb = (int64_t)(a.d / 32) * kQ8Bytes;
+    if (a.k_nb_head != hb || a.v_nb_head != hb) return false;
+    if (a.k_nb_tok != hb * a.Hkv || a.v_nb_tok != hb * a.Hkv) return false;
+    for (int b = 0; b < a.B; ++b) {
+        if (((uintptr_t)a.k[b] % 4) || ((uintptr_t)a.v[b] % 4)) return false;
+        // every buffer range and live offset stays below the padding offset
+        if ((int64_t)(a.L[b] + 1) * a.k_nb_tok + 2 * kOpBytes >= kDead) return false;
+    }
+    if (a.mask_mode == kMaskExplicit && (a.mask_nb_b % 2 != 0)) return false;
+    if (((uintptr_t)a.q % 16) || a.q_nb_h % 16 || a.q_nb_b % 16) return false;
+    if (((uintptr_t)a.out % 16) || a.o_nb_h % 16 || a.o_nb_b % 16) return false;
+    return true;
+}
+
+int decode_stream_plan(const AttnArgs& a, int n_cu, int* split_len) {
+    int Lmax = 1;
+    for (int b = 0; b < a.B; ++b) Lmax = a.L[b] > Lmax ? a.L[b] : Lmax;
+    // one workgroup per CU over (split, sequence); at least two tiles' worth
+    // of keys per split
+    int target = n_cu / a.B;
+    if (target < 1) target = 1;
+    int sl = (Lmax + target - 1) / target;
+    const int min_len = 2 * kTileOpBytes / (int)((a.d / 32) * kQ8Bytes * a.Hkv);
+    if (sl < min_len) sl = min_len;
+    *split_len = sl;
+    return (Lmax + sl - 1) / sl;
+}
+
+hipError_t launch_decode_stream(const AttnArgs& a, float* ws, int n_splits, int split_len, hipStream_t s) {
+    if (a.d == 64) return launch_ds<64>(a, ws, n_splits, split_len, s);
+    if (a.d == 128) return launch_ds<128>(a, ws, n_splits, split_len, s);
+    return hipErrorInvalidValue;
+}
+
+}  // namespace vva

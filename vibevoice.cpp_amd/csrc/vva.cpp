@@ -115,6 +115,19 @@ vva_status ensure_ws(vva_context* ctx, size_t bytes) {
 vva_status run_attention(vva_context* ctx, AttnArgs& a) {
     hipError_t e;
     ctx->last_splits = 0;
+    if (ctx->attn_path == 0 && a.T == 1 && decode_stream_supported(a)) {
+        int split_len = 0, wgs = ctx->n_cu;
+        if (const char* env = std::getenv("VVA_DECODE_WGS")) wgs = std::atoi(env);
+        const int n_splits = decode_stream_plan(a, wgs, &split_len);
+        if (n_splits > 1) {
+            vva_status st = ensure_ws(ctx, (size_t)n_splits * a.B * a.Hq * (a.d + 2) * sizeof(float));
+            if (st != VVA_OK) return st;
+        }
+        e = launch_decode_stream(a, ctx->ws, n_splits, split_len, ctx->stream);
+        if (e != hipSuccess) return hip_fail(ctx, e, "decode launch");
+        ctx->last_splits = n_splits;
+        return VVA_OK;
+    }
     if (ctx->attn_path != 1 && a.T == 1 && decode_supported(a)) {
         const int nw = decode_waves(a);
         int Lmax = 1;
@@ -232,7 +245,7 @@ extern "C" const char* vva_last_error(const vva_context* ctx) {
 extern "C" const char* vva_version(void) { return "vva 0.1.0 (gfx950)"; }
 
 extern "C" vva_status vva_set_attn_path(vva_context* ctx, int path) {
-    if (!ctx || path < 0 || path > 1) return VVA_ERR_INVALID_ARG;
+    if (!ctx || path < 0 || path > 2) return VVA_ERR_INVALID_ARG;
     ctx->attn_path = path;
     return VVA_OK;
 }

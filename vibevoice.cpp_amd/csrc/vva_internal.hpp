@@ -87,6 +87,16 @@ hipError_t launch_decode(const AttnArgs& a, float* ws, int n_splits, int split_l
 bool decode_supported(const AttnArgs& a);
 int decode_waves(const AttnArgs& a);            // waves per workgroup (one key sub-range each)
 int decode_max_splits();
+// Second pass of a split decode: combines the (m, l, acc) partials of `ws`
+// (layout of launch_decode) into the output rows.
+hipError_t launch_decode_merge(const AttnArgs& a, const float* ws, int n_splits, hipStream_t s);
+// LDS-streamed split-K decode over dense Q8_0 caches (T == 1): the cache
+// tiles of each split are DMA'd into a 4-stage LDS ring.  Partials use the
+// layout of launch_decode and are combined by launch_decode_merge.
+bool decode_stream_supported(const AttnArgs& a);
+// Key splits for one call: writes each split's length to *split_len.
+int decode_stream_plan(const AttnArgs& a, int n_cu, int* split_len);
+hipError_t launch_decode_stream(const AttnArgs& a, float* ws, int n_splits, int split_len, hipStream_t s);
 // MFMA flash prefill (F16 / BF16 caches).
 hipError_t launch_prefill(const AttnArgs& a, hipStream_t s);
 bool prefill_supported(const AttnArgs& a);
