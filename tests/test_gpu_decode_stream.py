@@ -147,3 +147,4 @@ def test_stream_decode_consecutive_steps(ctx, torch_gpu):
         for s in range(2):
             kv.set_len(s, L + 1)
     kv.free()
+

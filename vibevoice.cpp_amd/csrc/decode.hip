@@ -486,25 +486,28 @@ decode_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split_len) {
     }
 }
 
-// One workgroup of 256 threads per (query head, sequence): 256 / (D/4)
-// groups of D/4 threads each take every NG-th split, with up to kMergeDepth
-// partial rows (float4 per thread) in flight at once, fold them with a
-// running log-sum-exp, and the groups meet in LDS.  For n_splits <= NG *
-// kMergeDepth (128 at D = 128) every load goes out in one round trip.
+// One workgroup of 256 threads per (32-dim quarter, query head, sequence):
+// NG = 32 groups of 8 threads (one float4 of the quarter each) take every
+// NG-th split, with up to kMergeDepth partial rows in flight at once, fold
+// them with a running log-sum-exp, and the groups meet in LDS.  For
+// n_splits <= NG * kMergeDepth (128) every load goes out in one round trip;
+// the quarter split puts D/32 workgroups on each row so the round trips of
+// one row run on several CUs.
 constexpr int kMergeThreads = 256;
-constexpr int kMergeDepth = 16;
+constexpr int kMergeDepth = 4;
+constexpr int kMergeDims = 32;
 
 template <int D>
 __global__ void __launch_bounds__(kMergeThreads) decode_merge_kernel(AttnArgs a, const float* __restrict__ ws,
                                                                      int n_splits) {
-    constexpr int TPR = D / 4;                  // threads per partial row
+    constexpr int TPR = kMergeDims / 4;         // threads per partial row quarter
     constexpr int NG = kMergeThreads / TPR;     // row groups
     __shared__ float sm[NG], sden[NG];
     __shared__ float4 snum[NG][TPR];
-    const int h = blockIdx.x, b = blockIdx.y;
+    const int h = blockIdx.x, b = blockIdx.y, q4 = blockIdx.z;
     const int grp = threadIdx.x / TPR, i4 = threadIdx.x % TPR;
     const size_t base = ((size_t)b * a.Hq + h) * n_splits;
-    const float4* wacc = (const float4*)ws + base * TPR;
+    const float4* wacc = (const float4*)ws + base * (D / 4) + q4 * TPR;
     const float* wml = ws + (size_t)a.B * a.Hq * n_splits * D + base * 2;
     float M = -INFINITY, den = 0.0f;
     float4 num = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -514,7 +517,7 @@ __global__ void __launch_bounds__(kMergeThreads) decode_merge_kernel(AttnArgs a,
 #pragma unroll
         for (int k = 0; k < kMergeDepth; ++k) {
             const int s = min(s0 + k * NG, n_splits - 1);     // clamped: unconditional loads
-            av[k] = wacc[(size_t)s * TPR + i4];
+            av[k] = wacc[(size_t)s * (D / 4) + i4];
             const float2 ml = *(const float2*)(wml + 2 * s);
             mv[k] = s0 + k * NG < n_splits ? ml.x : -INFINITY;
             lv[k] = ml.y;
@@ -547,7 +550,7 @@ __global__ void __launch_bounds__(kMergeThreads) decode_merge_kernel(AttnArgs a,
     float4 n = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     float d = 0.0f;
     if (MM != -INFINITY) {
-#pragma unroll
+#pragma unroll 8
         for (int g = 0; g < NG; ++g) {
             const float f = __builtin_amdgcn_exp2f(sm[g] - MM);      // 0 for -inf
             const float4 v = snum[g][i4];
@@ -556,7 +559,7 @@ __global__ void __launch_bounds__(kMergeThreads) decode_merge_kernel(AttnArgs a,
         }
     }
     const float inv = d == 0.0f ? 0.0f : 1.0f / d;
-    float* orow = (float*)((char*)a.out + b * a.o_nb_b + h * a.o_nb_h);
+    float* orow = (float*)((char*)a.out + b * a.o_nb_b + h * a.o_nb_h) + q4 * kMergeDims;
     *(float4*)(orow + 4 * i4) = make_float4(n.x * inv, n.y * inv, n.z * inv, n.w * inv);
 }
 
@@ -571,7 +574,7 @@ hipError_t launch_dg(const AttnArgs& a, float* ws, int n_splits, int split_len, 
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || n_splits == 1) return e;
-    hipLaunchKernelGGL(decode_merge_kernel<D>, dim3(a.Hq, a.B), dim3(kMergeThreads), 0, s, a, ws, n_splits);
+    hipLaunchKernelGGL(decode_merge_kernel<D>, dim3(a.Hq, a.B, D / kMergeDims), dim3(kMergeThreads), 0, s, a, ws, n_splits);
     return hipGetLastError();
 }
 
@@ -579,9 +582,9 @@ hipError_t launch_dg(const AttnArgs& a, float* ws, int n_splits, int split_len, 
 
 hipError_t launch_decode_merge(const AttnArgs& a, const float* ws, int n_splits, hipStream_t s) {
     if (a.d == 64)
-        hipLaunchKernelGGL(decode_merge_kernel<64>, dim3(a.Hq, a.B), dim3(kMergeThreads), 0, s, a, ws, n_splits);
+        hipLaunchKernelGGL(decode_merge_kernel<64>, dim3(a.Hq, a.B, 64 / kMergeDims), dim3(kMergeThreads), 0, s, a, ws, n_splits);
     else if (a.d == 128)
-        hipLaunchKernelGGL(decode_merge_kernel<128>, dim3(a.Hq, a.B), dim3(kMergeThreads), 0, s, a, ws, n_splits);
+        hipLaunchKernelGGL(decode_merge_kernel<128>, dim3(a.Hq, a.B, 128 / kMergeDims), dim3(kMergeThreads), 0, s, a, ws, n_splits);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();

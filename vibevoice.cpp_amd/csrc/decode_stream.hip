@@ -43,6 +43,8 @@
 // split, and decode_merge_kernel (decode.hip) combines the splits.
 #include "vva_internal.hpp"
 
+#include <type_traits>
+
 namespace vva {
 
 namespace {
@@ -62,6 +64,8 @@ constexpr int kStage = 2 * kOpBytes;         // K, then V
 constexpr int kJunk = kStages * kStage;      // 1 KB target of the padding loads
 constexpr int kLdsBytes = kJunk + 1024;
 constexpr int kLoads = (2 * kOpChunks + kW - 1) / kW;   // DMA loads per wave per tile
+constexpr int kQLoads = 3;                   // DMA loads per wave for the raw Q rows
+constexpr int kQRawBytes = kQLoads * kW * 1024;   // raw Q area: up to 24 KB
 constexpr int kDead = 0x40000000;            // buffer offset past every range
 constexpr float kLazy = 8.0f;                // running-max slack in log2 units: p <= 256
 static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
@@ -100,6 +104,19 @@ __device__ __forceinline__ void load_scales(const char* row, uint16_t (&dst)[NB]
         dst[B] = block_scale<B>(row);
         load_scales<NB, B + 1>(row, dst);
     }
+}
+
+// f16 half HI of dword `h` times f32 `x` (v_fma_mix_f32 reads the half in
+// place: no conversion or extraction instruction).  The result feeds VALU
+// instructions only.
+template <int HI>
+__device__ __forceinline__ float mix_mul(uint32_t h, float x) {
+    float r;
+    if constexpr (HI)
+        asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h), "v"(x));
+    else
+        asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[0,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h), "v"(x));
+    return r;
 }
 
 __device__ __forceinline__ h2 as_h2(uint16_t lo, uint16_t hi) {
@@ -181,42 +198,49 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split
         }
     };
 
-    // ---- Q: loaded first, then the first tiles go out, then Q is quantized
-    // to Q8_0 blocks (codes + fp16-rounded scale) into the ring's last stage,
-    // which the loop does not load before its first barrier.  Four adjacent
-    // lanes share a block (8 values each; the block max over the quad by
-    // DPP); with more than 128 blocks a thread takes a second quarter.
+    // ---- Q: its rows (contiguous, at most 24 KB) are DMA'd first into the
+    // ring's last stage, which the loop does not load before its first
+    // barrier, then tile 0 goes out.  Once the wave's own Q loads have landed
+    // (they were issued first) and the workgroup has met, Q is quantized to
+    // Q8_0 blocks (codes + fp16-rounded scale) next to the raw rows, and
+    // tiles 1 and 2 go out.  Four adjacent lanes share a block (8 values each; the block max
+    // over the quad by DPP); with more than 128 blocks a thread takes a
+    // second quarter.
+    const int eb = (int)type_elem_bytes(a.q_type);
+    {
+        const i32x4 qrs = make_rsrc_sgpr(a.q + b * a.q_nb_b, (uint32_t)(a.Hq * D * eb));
+#pragma unroll
+        for (int i = 0; i < kQLoads; ++i) {
+            const int c = i * kW + w;
+            dma16(qrs, lds0 + (kStages - 1) * kStage + c * 1024, c * 1024 + lane * 16);
+        }
+    }
+    // only tile 0 goes out with Q: the fewer requests ahead of Q's, the
+    // sooner the quantization starts
+    issue(0);
+    wait_vm_barrier<kLoads>();
+
+    const char* qraw = lds + (kStages - 1) * kStage;
+    uint32_t* qlds = (uint32_t*)(lds + (kStages - 1) * kStage + kQRawBytes);
     constexpr int QI = 2;                             // quarters per thread (Hq * NB <= 256)
     const int nqi = a.Hq * NB * 4;
-    const int eb = (int)type_elem_bytes(a.q_type);
-    uint4 qraw[QI][2];
-#pragma unroll
-    for (int it = 0; it < QI; ++it) {
-        const int t = (int)threadIdx.x + it * kW * 64;
-        const int tt = t < nqi ? t : 0;
-        const int qh = tt / (NB * 4), qc = (tt >> 2) % NB, qp = tt & 3;
-        const char* src = a.q + b * a.q_nb_b + qh * a.q_nb_h + (int64_t)(qc * 32 + qp * 8) * eb;
-        qraw[it][0] = ((const uint4*)src)[0];
-        qraw[it][1] = a.q_type == VVA_TYPE_F32 ? ((const uint4*)src)[1] : qraw[it][0];
-    }
-#pragma unroll
-    for (int t = 0; t < kStages - 1; ++t) issue(t);
-
-    uint32_t* qlds = (uint32_t*)(lds + (kStages - 1) * kStage);
 #pragma unroll
     for (int it = 0; it < QI; ++it) {
         if (it * kW * 64 >= nqi) break;               // uniform
         const int t = (int)threadIdx.x + it * kW * 64;
+        const int tt = t < nqi ? t : 0;
+        const char* src = qraw + (int64_t)((tt >> 2) * 32 + (tt & 3) * 8) * eb;   // block tt/4, quarter tt%4
         float x[8];
         if (a.q_type == VVA_TYPE_F32) {
-            const uint4 u0 = qraw[it][0], u1 = qraw[it][1];
+            const uint4 u0 = ((const uint4*)src)[0], u1 = ((const uint4*)src)[1];
             x[0] = __uint_as_float(u0.x); x[1] = __uint_as_float(u0.y);
             x[2] = __uint_as_float(u0.z); x[3] = __uint_as_float(u0.w);
             x[4] = __uint_as_float(u1.x); x[5] = __uint_as_float(u1.y);
             x[6] = __uint_as_float(u1.z); x[7] = __uint_as_float(u1.w);
         } else {
             const bool bf = a.q_type == VVA_TYPE_BF16;
-            const uint32_t wv[4] = {qraw[it][0].x, qraw[it][0].y, qraw[it][0].z, qraw[it][0].w};
+            const uint4 u0 = ((const uint4*)src)[0];
+            const uint32_t wv[4] = {u0.x, u0.y, u0.z, u0.w};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const uint16_t lo = (uint16_t)(wv[e] & 0xffffu), hi = (uint16_t)(wv[e] >> 16);
@@ -241,7 +265,10 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split
             if ((t & 3) == 0) dst[8] = __float_as_uint(f16_to_f32(f32_to_f16(dq)));
         }
     }
-    __syncthreads();
+#pragma unroll
+    for (int t = 1; t < kStages - 1; ++t) issue(t);
+    // LDS only: the tile loads stay in flight
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory");
 
     // B operand of the score MFMAs: row n's Q codes 8g..8g+7 of each block,
     // and its block scales times scale * log2(e) (rows past g are zero)
@@ -262,10 +289,115 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split
     }
 
     float m = -INFINITY, l = 0.0f;            // row n's running max (log2 domain) and sum
+    float mb = 0.0f;                          // m, or 0 while m = -inf: the exp2 base
     f32x4 acc[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; ++j) acc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     const char* mrow = a.mask_mode == kMaskExplicit ? a.mask + b * a.mask_nb_b : nullptr;   // query row 0
+    const int ka_off = (4 * (n & 3) + (n >> 2)) * RB;       // A-operand key sigma(n) of a group
+    const int kc_off = g * RB;                              // C-layout keys 4i + g: i * 4 RB further
+    const int vc_off = g * RB + 2 + 2 * n;                  // their V codes of dims 2n, 2n + 1
+
+    // One group of 16 keys starting at tile key kb.  CHECK: the group may
+    // hold keys past the split or the caller passed a mask.
+    auto group = [&](const char* kt, const char* vt, int kb, int jt, auto check) {
+        constexpr bool CHECK = decltype(check)::value;
+        // ---- scores: per block, A = key (kb + sigma(n))'s codes 8g..8g+7
+        i32x4 cs[NB];
+        {
+            const char* ka = kt + kb * RB + ka_off;
+#pragma unroll
+            for (int bb = 0; bb < NB; ++bb) {
+                const int off = bb * kQ8Bytes + 2 + 8 * g;       // 2 mod 4 for even blocks
+                const uint32_t* p = (const uint32_t*)(ka + (off & ~3));
+                const uint32_t w0 = p[0], w1 = p[1];
+                uint32_t lo = w0, hi = w1;
+                if ((bb & 1) == 0) {
+                    const uint32_t w2 = p[2];
+                    lo = __builtin_amdgcn_alignbyte(w1, w0, 2);
+                    hi = __builtin_amdgcn_alignbyte(w2, w1, 2);
+                }
+                const long av = (long)((uint64_t)lo | ((uint64_t)hi << 32));
+                cs[bb] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, qb[bb], i32x4{0, 0, 0, 0}, 0, 0, 0);
+            }
+        }
+        // the lane's keys kb + sigma(4g + i) = kb + 4i + g: the dwords that
+        // hold their K and V block scales, and their V codes of dims 2n, 2n + 1
+        uint32_t kd[4][NB], vd[4][NB], vc[4][NB];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const char* kr = kt + (kb + 4 * i) * RB + kc_off;
+            const char* vr = vt + (kb + 4 * i) * RB + kc_off;
+            const char* vcr = vt + (kb + 4 * i) * RB + vc_off;
+#pragma unroll
+            for (int bb = 0; bb < NB; ++bb) {
+                const int dw = (bb * kQ8Bytes - (bb & 1) * 2) / 4;
+                kd[i][bb] = ((const uint32_t*)kr)[dw];
+                vd[i][bb] = ((const uint32_t*)vr)[dw];
+                vc[i][bb] = *(const uint16_t*)(vcr + bb * kQ8Bytes);
+            }
+        }
+        float s[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float x = 0.0f;
+#pragma unroll
+            for (int bb = 0; bb < NB; ++bb) {
+                const float e = (bb & 1) ? mix_mul<1>(kd[i][bb], qd[bb]) : mix_mul<0>(kd[i][bb], qd[bb]);
+                x = fmaf((float)cs[bb][i], e, x);
+            }
+            s[i] = x;
+        }
+        if constexpr (CHECK) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int j = jt + kb + 4 * i + g;
+                bool live = j < j1;
+                if (mrow) {
+                    const float mv = live ? f16_to_f32(*(const uint16_t*)(mrow + 2 * (int64_t)j)) * kLog2e : 0.0f;
+                    live = live && mv != -INFINITY;
+                    s[i] += mv;
+                }
+                s[i] = live ? s[i] : -INFINITY;
+            }
+        }
+
+        // ---- online softmax of row n, running max raised lazily
+        const float smax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+        if (__any(smax > m + kLazy)) {
+            const float cm = max_swap32(max_swap16(smax));
+            if (cm > m + kLazy) {
+                const float alpha = __builtin_amdgcn_exp2f(m - cm);     // 0 when m = -inf
+                l *= alpha;
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) acc[j] *= alpha;
+                m = cm;
+                mb = cm;
+            }
+        }
+        float p[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(s[i] - mb);   // 0 when masked
+        l += (p[0] + p[1]) + (p[2] + p[3]);
+        const h2 p01 = h2{(_Float16)p[0], (_Float16)p[1]};
+        const h2 p23 = h2{(_Float16)p[2], (_Float16)p[3]};
+
+        // ---- O^T += V^T P'^T per 16 dims
+#pragma unroll
+        for (int bb = 0; bb < NB; ++bb) {
+            const uint32_t sel = (bb & 1) ? 0x07060302u : 0x05040100u;      // high or low halves
+            h2 dv01, dv23;
+            const uint32_t u01 = __builtin_amdgcn_perm(vd[1][bb], vd[0][bb], sel);
+            const uint32_t u23 = __builtin_amdgcn_perm(vd[3][bb], vd[2][bb], sel);
+            __builtin_memcpy(&dv01, &u01, 4);
+            __builtin_memcpy(&dv23, &u23, 4);
+            const h4 pb = cat_h4(p01 * dv01, p23 * dv23);
+            const h4 a0 = as_h4(i8_pair_mfma_b0(vc[0][bb], vc[1][bb]), i8_pair_mfma_b0(vc[2][bb], vc[3][bb]));
+            const h4 a1 = as_h4(i8_pair_mfma_b1(vc[0][bb], vc[1][bb]), i8_pair_mfma_b1(vc[2][bb], vc[3][bb]));
+            acc[2 * bb] = __builtin_amdgcn_mfma_f32_16x16x16f16(a0, pb, acc[2 * bb], 0, 0, 0);
+            acc[2 * bb + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(a1, pb, acc[2 * bb + 1], 0, 0, 0);
+        }
+    };
 
     for (int t = 0; t < n_tiles; ++t) {
         // tile t has landed in every wave's share; every wave is done with t - 1
@@ -273,88 +405,14 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split
         issue(t + kStages - 1);
         const char* kt = lds + (t & (kStages - 1)) * kStage + dk + h * HB;
         const char* vt = lds + (t & (kStages - 1)) * kStage + kOpBytes + dv + h * HB;
+        const int jt = j0 + t * TT;
+        // only the split's last tile can hold keys past its end
+        const bool check = mrow != nullptr || jt + TT > j1;
 #pragma unroll
         for (int u = 0; u < NSUB; ++u) {
-            const int kb = r * KPW + 16 * u;              // first key of the group in the tile
-            // ---- scores: per block, A = key (kb + sigma(n))'s codes 8g..8g+7
-            i32x4 cs[NB];
-            {
-                const char* ka = kt + (kb + 4 * (n & 3) + (n >> 2)) * RB;
-#pragma unroll
-                for (int bb = 0; bb < NB; ++bb) {
-                    const int off = bb * kQ8Bytes + 2 + 8 * g;       // 2 mod 4 for even blocks
-                    const uint32_t* p = (const uint32_t*)(ka + (off & ~3));
-                    const int sh = (bb & 1) ? 0 : 2;
-                    const uint32_t w0 = p[0], w1 = p[1];
-                    uint32_t lo = w0, hi = w1;
-                    if (sh) {
-                        const uint32_t w2 = p[2];
-                        lo = __builtin_amdgcn_alignbyte(w1, w0, 2);
-                        hi = __builtin_amdgcn_alignbyte(w2, w1, 2);
-                    }
-                    const long av = (long)((uint64_t)lo | ((uint64_t)hi << 32));
-                    cs[bb] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, qb[bb], i32x4{0, 0, 0, 0}, 0, 0, 0);
-                }
-            }
-            // the lane's output keys kb + sigma(4g + i) = kb + 4i + g: their K
-            // and V block scales and the V codes of dims 2n, 2n + 1 of every
-            // block
-            uint16_t dkh[4][NB], dvh[4][NB], vc[4][NB];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int key = kb + 4 * i + g;
-                load_scales<NB>(kt + key * RB, dkh[i]);
-                load_scales<NB>(vt + key * RB, dvh[i]);
-#pragma unroll
-                for (int bb = 0; bb < NB; ++bb)
-                    vc[i][bb] = *(const uint16_t*)(vt + key * RB + bb * kQ8Bytes + 2 + 2 * n);
-            }
-            float s[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                float x = 0.0f;
-#pragma unroll
-                for (int bb = 0; bb < NB; ++bb) x = fmaf((float)cs[bb][i], f16_to_f32(dkh[i][bb]) * qd[bb], x);
-                const int j = j0 + t * TT + kb + 4 * i + g;
-                bool live = j < j1;
-                if (mrow) {
-                    const float mv = live ? f16_to_f32(*(const uint16_t*)(mrow + 2 * (int64_t)j)) * kLog2e : 0.0f;
-                    live = live && mv != -INFINITY;
-                    x += mv;
-                }
-                s[i] = live ? x : -INFINITY;
-            }
-
-            // ---- online softmax of row n, running max raised lazily
-            const bool raise = s[0] > m + kLazy || s[1] > m + kLazy || s[2] > m + kLazy || s[3] > m + kLazy;
-            if (__any(raise)) {
-                float cm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-                cm = max_swap32(max_swap16(cm));
-                if (cm > m + kLazy) {
-                    const float alpha = __builtin_amdgcn_exp2f(m - cm);     // 0 when m = -inf
-                    l *= alpha;
-#pragma unroll
-                    for (int j = 0; j < NJ; ++j) acc[j] *= alpha;
-                    m = cm;
-                }
-            }
-            const float base = m == -INFINITY ? 0.0f : m;
-            float p[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(s[i] - base);   // 0 when masked
-            l += (p[0] + p[1]) + (p[2] + p[3]);
-            const h2 p01 = h2{(_Float16)p[0], (_Float16)p[1]};
-            const h2 p23 = h2{(_Float16)p[2], (_Float16)p[3]};
-
-            // ---- O^T += V^T P'^T per 16 dims
-#pragma unroll
-            for (int bb = 0; bb < NB; ++bb) {
-                const h4 pb = cat_h4(p01 * as_h2(dvh[0][bb], dvh[1][bb]), p23 * as_h2(dvh[2][bb], dvh[3][bb]));
-                const h4 a0 = as_h4(i8_pair_mfma_b0(vc[0][bb], vc[1][bb]), i8_pair_mfma_b0(vc[2][bb], vc[3][bb]));
-                const h4 a1 = as_h4(i8_pair_mfma_b1(vc[0][bb], vc[1][bb]), i8_pair_mfma_b1(vc[2][bb], vc[3][bb]));
-                acc[2 * bb] = __builtin_amdgcn_mfma_f32_16x16x16f16(a0, pb, acc[2 * bb], 0, 0, 0);
-                acc[2 * bb + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(a1, pb, acc[2 * bb + 1], 0, 0, 0);
-            }
+            const int kb = r * KPW + 16 * u;
+            if (check) group(kt, vt, kb, jt, std::true_type{});
+            else group(kt, vt, kb, jt, std::false_type{});
         }
     }
     // the padding tiles' loads land before the ring is reused
@@ -384,50 +442,52 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split
             }
         }
         __syncthreads();
-        if (r > 0) return;
-        for (int rr = 1; rr < R; ++rr) {
-            const int ow = rr * Hkv + h;
-            const float mo = mbuf[ow][n];
-            const float mn = fmaxf(m, mo);
-            const float fa = mn == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - mn);
-            const float fb = mn == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mo - mn);
-            l = l * fa + lbuf[ow][n] * fb;
+        if (r == 0) {
+            for (int rr = 1; rr < R; ++rr) {
+                const int ow = rr * Hkv + h;
+                const float mo = mbuf[ow][n];
+                const float mn = fmaxf(m, mo);
+                const float fa = mn == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - mn);
+                const float fb = mn == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mo - mn);
+                l = l * fa + lbuf[ow][n] * fb;
+#pragma unroll
+                for (int bb = 0; bb < NB; ++bb) {
+                    const float4 x = *(const float4*)&abuf[ow][n][32 * bb + 8 * g];
+                    const float4 y = *(const float4*)&abuf[ow][n][32 * bb + 8 * g + 4];
+                    f32x4& e = acc[2 * bb];
+                    f32x4& o = acc[2 * bb + 1];
+                    e[0] = e[0] * fa + x.x * fb; o[0] = o[0] * fa + x.y * fb;
+                    e[1] = e[1] * fa + x.z * fb; o[1] = o[1] * fa + x.w * fb;
+                    e[2] = e[2] * fa + y.x * fb; o[2] = o[2] * fa + y.y * fb;
+                    e[3] = e[3] * fa + y.z * fb; o[3] = o[3] * fa + y.w * fb;
+                }
+                m = mn;
+            }
+        }
+    }
+    const int hq = h * G + n;
+    if (r == 0 && n < G) {
+        if (n_splits == 1) {
+            const float inv = l == 0.0f ? 0.0f : 1.0f / l;
+            float* orow = (float*)((char*)a.out + b * a.o_nb_b + hq * a.o_nb_h);
 #pragma unroll
             for (int bb = 0; bb < NB; ++bb) {
-                const float4 x = *(const float4*)&abuf[ow][n][32 * bb + 8 * g];
-                const float4 y = *(const float4*)&abuf[ow][n][32 * bb + 8 * g + 4];
-                f32x4& e = acc[2 * bb];
-                f32x4& o = acc[2 * bb + 1];
-                e[0] = e[0] * fa + x.x * fb; o[0] = o[0] * fa + x.y * fb;
-                e[1] = e[1] * fa + x.z * fb; o[1] = o[1] * fa + x.w * fb;
-                e[2] = e[2] * fa + y.x * fb; o[2] = o[2] * fa + y.y * fb;
-                e[3] = e[3] * fa + y.z * fb; o[3] = o[3] * fa + y.w * fb;
+                const float4 x = dims(bb, 0), y = dims(bb, 1);
+                *(float4*)(orow + 32 * bb + 8 * g) = make_float4(x.x * inv, x.y * inv, x.z * inv, x.w * inv);
+                *(float4*)(orow + 32 * bb + 8 * g + 4) = make_float4(y.x * inv, y.y * inv, y.z * inv, y.w * inv);
             }
-            m = mn;
+        } else {
+            // partials: acc [B][Hq][n_splits][D], then (m, l) [B][Hq][n_splits][2]
+            const size_t idx = ((size_t)b * a.Hq + hq) * n_splits + split;
+            float* wacc = ws + idx * D;
+#pragma unroll
+            for (int bb = 0; bb < NB; ++bb) {
+                *(float4*)(wacc + 32 * bb + 8 * g) = dims(bb, 0);
+                *(float4*)(wacc + 32 * bb + 8 * g + 4) = dims(bb, 1);
+            }
+            if (g == 0) *(float2*)(ws + (size_t)a.B * a.Hq * n_splits * D + idx * 2) = make_float2(m, l);
         }
     }
-    if (n >= G) return;
-    const int hq = h * G + n;
-    if (n_splits == 1) {
-        const float inv = l == 0.0f ? 0.0f : 1.0f / l;
-        float* orow = (float*)((char*)a.out + b * a.o_nb_b + hq * a.o_nb_h);
-#pragma unroll
-        for (int bb = 0; bb < NB; ++bb) {
-            const float4 x = dims(bb, 0), y = dims(bb, 1);
-            *(float4*)(orow + 32 * bb + 8 * g) = make_float4(x.x * inv, x.y * inv, x.z * inv, x.w * inv);
-            *(float4*)(orow + 32 * bb + 8 * g + 4) = make_float4(y.x * inv, y.y * inv, y.z * inv, y.w * inv);
-        }
-        return;
-    }
-    // partials: acc [B][Hq][n_splits][D], then (m, l) [B][Hq][n_splits][2]
-    const size_t idx = ((size_t)b * a.Hq + hq) * n_splits + split;
-    float* wacc = ws + idx * D;
-#pragma unroll
-    for (int bb = 0; bb < NB; ++bb) {
-        *(float4*)(wacc + 32 * bb + 8 * g) = dims(bb, 0);
-        *(float4*)(wacc + 32 * bb + 8 * g + 4) = dims(bb, 1);
-    }
-    if (g == 0) *(float2*)(ws + (size_t)a.B * a.Hq * n_splits * D + idx * 2) = make_float2(m, l);
 }
 
 template <int D>
@@ -463,6 +523,10 @@ bool decode_stream_supported(const AttnArgs& a) {
     }
     if (a.mask_mode == kMaskExplicit && (a.mask_nb_b % 2 != 0)) return false;
     if (((uintptr_t)a.q % 16) || a.q_nb_h % 16 || a.q_nb_b % 16) return false;
+    // Q rows contiguous and small enough for the raw-Q area, codes after them
+    const int64_t qrow = (int64_t)a.d * type_elem_bytes(a.q_type);
+    if (a.q_nb_h != qrow || a.Hq * qrow > kQRawBytes) return false;
+    if (kQRawBytes + (int64_t)a.Hq * (a.d / 32) * 36 > kStage) return false;
     if (((uintptr_t)a.out % 16) || a.o_nb_h % 16 || a.o_nb_b % 16) return false;
     return true;
 }

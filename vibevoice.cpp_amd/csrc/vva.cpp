@@ -26,7 +26,7 @@ struct vva_context {
     int n_cu = 256;
     int attn_path = 0;
     int last_splits = 0;
-    float* ws = nullptr;                 // decode split partials, after the ticket area
+    float* ws = nullptr;                 // decode split partials
     size_t ws_bytes = 0;
     std::set<vva_kv*> caches;            // released by vva_destroy if still alive
 };

@@ -145,7 +145,7 @@ VVA_I8_PAIR(3)
 // VALU instruction needs two wait states in between; the trailing s_nop 1
 // provides them whatever the compiler schedules next.
 #define VVA_I8_PAIR_MFMA(N)                                                                     \
-    __device__ __forceinline__ uint32_t i8_pair_mfma_b##N(uint16_t a, uint16_t b) {             \
+    __device__ __forceinline__ uint32_t i8_pair_mfma_b##N(uint32_t a, uint32_t b) {             \
         uint32_t r;                                                                             \
         asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_" #N "\n\t" \
             "v_cvt_f16_i16_sdwa %0, sext(%2) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_" #N "\n\t" \
