@@ -44,6 +44,14 @@ L_DECODE = 32768
 B_DECODE = 2
 THETA = 1.0e6
 
+# HBM bytes per launch of the dominant kernels, from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE
+# passes over this script (KiB per dispatch), each scaled by the counter's reading for a plain
+# 1 GiB device-to-device copy (`--only copy`): FETCH_SIZE read 512 MiB for 1 GiB (x 2.0),
+# WRITE_SIZE 1 GiB (x 1.0).  Counters and commands: profiles/prefill_kernel_7b_32k.md,
+# profiles/decode_stream_q8_0_7b_32k.md.
+TRAFFIC_PREFILL = (980169.7 * 2.0 + 458752.5 * 1.0) * 1024          # prefill_kernel<128,F16>
+TRAFFIC_DECODE = ((35058.0 + 1843.5) * 2.0 + (3808.0 + 28.0) * 1.0) * 1024   # stream + merge
+
 
 def prefill_flops_per_layer(T: int, past: int = 0) -> float:
     # 2 * d for QK^T and 2 * d for PV per visible (query, key) pair
@@ -269,7 +277,7 @@ def main() -> int:
         line["ms_per_step"] = round(pre["ms_per_step"], 3)
         line["roofline"] = {"bound": "mfma", "achieved": round(pre["attn_tflops"], 2), "peak": PEAK_F16_TFLOPS,
                             "unit": "TFLOP/s", "frac": round(pre["attn_tflops"] / PEAK_F16_TFLOPS, 4),
-                            "traffic": None, "kernel": "prefill_kernel<128,F16>",
+                            "traffic": TRAFFIC_PREFILL, "kernel": "prefill_kernel<128,F16>",
                             "avg_launch_ms": round(pre["attn_ms"], 4),
                             "flop_per_launch": pre["flops_per_layer"]}
         if not args.no_cpu:
@@ -283,7 +291,7 @@ def main() -> int:
             "value": round(dec["gbs"], 1), "unit": "GB/s", "steps": args.decode_steps,
             "ms_per_step": round(dec["ms_per_step"], 4), "dtype": "q8_0/f32",
             "roofline": {"bound": "hbm", "achieved": round(dec["attn_gbs"], 1), "peak": PEAK_HBM_GBS,
-                         "unit": "GB/s", "frac": round(dec["attn_gbs"] / PEAK_HBM_GBS, 4), "traffic": None,
+                         "unit": "GB/s", "frac": round(dec["attn_gbs"] / PEAK_HBM_GBS, 4), "traffic": TRAFFIC_DECODE,
                          "kernel": "decode_stream_kernel<128,7> + decode_merge_kernel<128>",
                          "avg_launch_us": round(dec["attn_us"], 3), "bytes_per_launch": dec["bytes_per_layer"],
                          "timing": "HIP events around each step's 28 back-to-back attention calls",
