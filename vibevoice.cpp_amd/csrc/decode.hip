@@ -488,75 +488,95 @@ decode_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split_len) {
 
 // One workgroup of 256 threads per (32-dim quarter, query head, sequence):
 // NG = 32 groups of 8 threads (one float4 of the quarter each) take every
-// NG-th split, with up to kMergeDepth partial rows in flight at once, fold
-// them with a running log-sum-exp, and the groups meet in LDS.  For
-// n_splits <= NG * kMergeDepth (128) every load goes out in one round trip;
-// the quarter split puts D/32 workgroups on each row so the round trips of
-// one row run on several CUs.
+// NG-th split, with up to kMergeDepth partial rows in flight at once.  The
+// row max M over all splits is found first (in-wave DPP / permlane steps,
+// then the 4 waves through LDS); each thread then weighs its rows by
+// exp2(m - M), and the 32 groups' sums meet by cross-lane adds within each
+// wave and one LDS step across the waves.  For n_splits <= NG * kMergeDepth
+// (128) every load goes out in one round trip; the quarter split puts D/32
+// workgroups on each row so the round trips of one row run on several CUs.
 constexpr int kMergeThreads = 256;
 constexpr int kMergeDepth = 4;
 constexpr int kMergeDims = 32;
+constexpr int kDppRowRor8 = 0x128;
 
 template <int D>
 __global__ void __launch_bounds__(kMergeThreads) decode_merge_kernel(AttnArgs a, const float* __restrict__ ws,
                                                                      int n_splits) {
     constexpr int TPR = kMergeDims / 4;         // threads per partial row quarter
     constexpr int NG = kMergeThreads / TPR;     // row groups
-    __shared__ float sm[NG], sden[NG];
-    __shared__ float4 snum[NG][TPR];
+    constexpr int NW = kMergeThreads / 64;
+    __shared__ float smax[NW];
+    __shared__ float4 snum[NW][TPR];
+    __shared__ float sden[NW];
     const int h = blockIdx.x, b = blockIdx.y, q4 = blockIdx.z;
     const int grp = threadIdx.x / TPR, i4 = threadIdx.x % TPR;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const size_t base = ((size_t)b * a.Hq + h) * n_splits;
     const float4* wacc = (const float4*)ws + base * (D / 4) + q4 * TPR;
     const float* wml = ws + (size_t)a.B * a.Hq * n_splits * D + base * 2;
     float M = -INFINITY, den = 0.0f;
     float4 num = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (int s0 = grp; s0 < n_splits; s0 += NG * kMergeDepth) {
-        float4 av[kMergeDepth];
-        float mv[kMergeDepth], lv[kMergeDepth];
+    // first round (all rows when n_splits <= 128): loads, then the global max
+    float4 av[kMergeDepth];
+    float mv[kMergeDepth], lv[kMergeDepth];
 #pragma unroll
-        for (int k = 0; k < kMergeDepth; ++k) {
-            const int s = min(s0 + k * NG, n_splits - 1);     // clamped: unconditional loads
-            av[k] = wacc[(size_t)s * (D / 4) + i4];
-            const float2 ml = *(const float2*)(wml + 2 * s);
-            mv[k] = s0 + k * NG < n_splits ? ml.x : -INFINITY;
-            lv[k] = ml.y;
-        }
-        float mn = M;
-#pragma unroll
-        for (int k = 0; k < kMergeDepth; ++k) mn = fmaxf(mn, mv[k]);
-        if (mn == -INFINITY) continue;                        // nothing visible yet
-        const float f0 = M == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(M - mn);
-        num.x *= f0; num.y *= f0; num.z *= f0; num.w *= f0;
-        den *= f0;
-#pragma unroll
-        for (int k = 0; k < kMergeDepth; ++k) {
-            const float f = __builtin_amdgcn_exp2f(mv[k] - mn);   // 0 for -inf
-            num.x = fmaf(av[k].x, f, num.x);
-            num.y = fmaf(av[k].y, f, num.y);
-            num.z = fmaf(av[k].z, f, num.z);
-            num.w = fmaf(av[k].w, f, num.w);
-            den = fmaf(lv[k], f, den);
-        }
-        M = mn;
+    for (int k = 0; k < kMergeDepth; ++k) {
+        const int s = min(grp + k * NG, n_splits - 1);     // clamped: unconditional loads
+        av[k] = wacc[(size_t)s * (D / 4) + i4];
+        const float2 ml = *(const float2*)(wml + 2 * s);
+        mv[k] = grp + k * NG < n_splits ? ml.x : -INFINITY;
+        lv[k] = ml.y;
     }
-    if (i4 == 0) { sm[grp] = M; sden[grp] = den; }
-    snum[grp][i4] = num;
-    __syncthreads();
-    if (grp != 0) return;
-    float MM = -INFINITY;
+    float mt = -INFINITY;
 #pragma unroll
-    for (int g = 0; g < NG; ++g) MM = fmaxf(MM, sm[g]);
-    float4 n = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    float d = 0.0f;
-    if (MM != -INFINITY) {
-#pragma unroll 8
-        for (int g = 0; g < NG; ++g) {
-            const float f = __builtin_amdgcn_exp2f(sm[g] - MM);      // 0 for -inf
-            const float4 v = snum[g][i4];
-            n.x = fmaf(v.x, f, n.x); n.y = fmaf(v.y, f, n.y); n.z = fmaf(v.z, f, n.z); n.w = fmaf(v.w, f, n.w);
-            d = fmaf(sden[g], f, d);
+    for (int k = 0; k < kMergeDepth; ++k) mt = fmaxf(mt, mv[k]);
+    for (int s0 = grp + NG * kMergeDepth; s0 < n_splits; s0 += NG) {   // more than 128 splits
+        const float2 ml = *(const float2*)(wml + 2 * s0);
+        mt = fmaxf(mt, ml.x);
+    }
+    mt = fmaxf(mt, dpp<kDppRowRor8>(mt));
+    mt = max_swap32(max_swap16(mt));
+    if (lane == 0) smax[wv] = mt;
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, smax[w]);
+    if (M != -INFINITY) {
+        auto add = [&](float m, float l, const float4& v) {
+            const float f = __builtin_amdgcn_exp2f(m - M);     // 0 for -inf
+            num.x = fmaf(v.x, f, num.x);
+            num.y = fmaf(v.y, f, num.y);
+            num.z = fmaf(v.z, f, num.z);
+            num.w = fmaf(v.w, f, num.w);
+            den = fmaf(l, f, den);
+        };
+#pragma unroll
+        for (int k = 0; k < kMergeDepth; ++k) add(mv[k], lv[k], av[k]);
+        for (int s0 = grp + NG * kMergeDepth; s0 < n_splits; s0 += NG) {
+            const float2 ml = *(const float2*)(wml + 2 * s0);
+            add(ml.x, ml.y, wacc[(size_t)s0 * (D / 4) + i4]);
         }
+    }
+    // sum over the 8 groups of the wave (lanes i4, i4 + 8, ..., i4 + 56)
+    auto gsum = [](float x) { return add_swap32(add_swap16(x + dpp<kDppRowRor8>(x))); };
+    num.x = gsum(num.x);
+    num.y = gsum(num.y);
+    num.z = gsum(num.z);
+    num.w = gsum(num.w);
+    den = gsum(den);
+    if (lane < TPR) {
+        snum[wv][lane] = num;
+        if (lane == 0) sden[wv] = den;
+    }
+    __syncthreads();
+    if (threadIdx.x >= TPR) return;
+    float4 n = snum[0][i4];
+    float d = sden[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) {
+        const float4 v = snum[w][i4];
+        n.x += v.x; n.y += v.y; n.z += v.z; n.w += v.w;
+        d += sden[w];
     }
     const float inv = d == 0.0f ? 0.0f : 1.0f / d;
     float* orow = (float*)((char*)a.out + b * a.o_nb_b + h * a.o_nb_h) + q4 * kMergeDims;

@@ -74,11 +74,20 @@ static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
 // m0 + 16 * lane.  Inline asm, so the compiler neither fences LDS reads on it
 // nor waits for it; completion is awaited explicitly (wait_vm_barrier).  The
 // whole offset is in the VGPR (soffset 0), so the range check sees all of it.
+// STREAM marks the load non-temporal: the cache is read once, so its lines
+// should not displace what the next call reads again (Q, the partials).
+template <bool STREAM = false>
 __device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t lds_addr, int voffset) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                 :
-                 : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voffset), "s"(rsrc)
-                 : "memory", "m0");
+    if constexpr (STREAM)
+        asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
+                     :
+                     : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voffset), "s"(rsrc)
+                     : "memory", "m0");
+    else
+        asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                     :
+                     : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voffset), "s"(rsrc)
+                     : "memory", "m0");
 }
 
 // wait until at most N of this wave's loads are outstanding (and its LDS
@@ -86,24 +95,6 @@ __device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t lds_addr, int voffset
 template <int N>
 __device__ __forceinline__ void wait_vm_barrier() {
     asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(N) : "memory");
-}
-
-// fp16 scale of Q8_0 block b of the head row at `row` (4-byte aligned): the
-// block starts at byte 34 b, so its scale is the low half of an aligned
-// dword for even b and the high half for odd b.
-template <int B>
-__device__ __forceinline__ uint16_t block_scale(const char* row) {
-    constexpr int off = B * kQ8Bytes;
-    if constexpr (off % 4 == 0) return (uint16_t)(*(const uint32_t*)(row + off));
-    else return (uint16_t)(*(const uint32_t*)(row + off - 2) >> 16);
-}
-
-template <int NB, int B = 0>
-__device__ __forceinline__ void load_scales(const char* row, uint16_t (&dst)[NB]) {
-    if constexpr (B < NB) {
-        dst[B] = block_scale<B>(row);
-        load_scales<NB, B + 1>(row, dst);
-    }
 }
 
 // f16 half HI of dword `h` times f32 `x` (v_fma_mix_f32 reads the half in
@@ -133,8 +124,9 @@ __device__ __forceinline__ h4 as_h4(uint32_t lo, uint32_t hi) {
 }
 __device__ __forceinline__ h4 cat_h4(h2 lo, h2 hi) { return h4{lo[0], lo[1], hi[0], hi[1]}; }
 
-// D: head dim (64 / 128); G: query heads per kv head (<= 16).
-template <int D, int G>
+// D: head dim (64 / 128); HKV: kv heads (1, 2, 4, 8), which fixes the token
+// row pitch, so every LDS offset inside a tile is a constant.
+template <int D, int HKV>
 __global__ void __launch_bounds__(kW * 64)
 decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split_len) {
     constexpr int NB = D / 32;                // Q8_0 blocks per head row
@@ -143,17 +135,17 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split
     constexpr int KPW = 16 * NSUB;            // keys per wave per tile
     constexpr int NJ = 2 * NB;                // P.V MFMAs (16 dims each) per key group
     static_assert(KPW * kW * HB == kTileOpBytes, "tile size");
-    static_assert(G <= 16, "one query head per lane row");
+    static_assert(kW % HKV == 0, "whole waves per kv head");
 
     __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
 
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, n = lane & 15;
-    const int Hkv = a.Hkv;
-    const int R = kW / Hkv;                   // waves per kv head
-    const int h = w % Hkv, r = w / Hkv;
-    const int RB = Hkv * HB;                  // bytes per token row (all kv heads)
+    constexpr int R = kW / HKV;               // waves per kv head
+    constexpr int RB = HKV * HB;              // bytes per token row (all kv heads)
+    const int G = a.Hq / HKV;                 // query heads per kv head (<= 16)
+    const int h = w % HKV, r = w / HKV;
     const int TT = KPW * R;                   // keys per tile
     const int split = blockIdx.x, b = blockIdx.y;
     const int L = a.L[b];
@@ -177,25 +169,31 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split
     // Every wave issues kLoads loads per tile: the 36 chunks of K and V, then
     // padding loads (from past the range: zeros, no memory access) into the
     // junk kilobyte.  A tile past the last one loads nothing but zeros; the
-    // 18th chunk of an operand is needed only when delta > 0.
+    // 18th chunk of an operand is needed only when delta > 0.  The plan of
+    // each of the wave's loads (operand, LDS offset, whether it ever fetches)
+    // is fixed for the kernel, so a tile's issue has no branches.
+    i32x4 lrs[kLoads];
+    uint32_t llds[kLoads], lstage[kLoads];
+    int loff[kLoads];
+    bool lvalid[kLoads];
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+        const int c = i * kW + w;
+        const bool isk = c < kOpChunks, isv = !isk && c < 2 * kOpChunks;
+        const int cc = isk ? c : c - kOpChunks;
+        lrs[i] = isv ? vrs : krs;
+        llds[i] = isk ? (uint32_t)(c * 1024) : isv ? (uint32_t)(kOpBytes + cc * 1024) : (uint32_t)kJunk;
+        lstage[i] = isk || isv ? 0xffffffffu : 0u;
+        loff[i] = cc * 1024;
+        lvalid[i] = (isk && (cc < kOpChunks - 1 || dk > 0)) || (isv && (cc < kOpChunks - 1 || dv > 0));
+    }
     auto issue = [&](int t) {
         const bool live = t < n_tiles;
-        const uint32_t st = lds0 + (uint32_t)(t & (kStages - 1)) * kStage;
+        const uint32_t st = (uint32_t)(t & (kStages - 1)) * kStage;
         const int tb = t * kTileOpBytes + lane * 16;
 #pragma unroll
-        for (int i = 0; i < kLoads; ++i) {
-            const int c = i * kW + w;
-            if (c < kOpChunks) {
-                const bool need = live && (c < kOpChunks - 1 || dk > 0);
-                dma16(krs, st + c * 1024, need ? tb + c * 1024 : kDead);
-            } else if (c < 2 * kOpChunks) {
-                const int cc = c - kOpChunks;
-                const bool need = live && (cc < kOpChunks - 1 || dv > 0);
-                dma16(vrs, st + kOpBytes + cc * 1024, need ? tb + cc * 1024 : kDead);
-            } else {
-                dma16(krs, lds0 + kJunk, kDead);
-            }
-        }
+        for (int i = 0; i < kLoads; ++i)
+            dma16<true>(lrs[i], lds0 + (st & lstage[i]) + llds[i], live && lvalid[i] ? tb + loff[i] : kDead);
     };
 
     // ---- Q: its rows (contiguous, at most 24 KB) are DMA'd first into the
@@ -335,6 +333,7 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split
                 kd[i][bb] = ((const uint32_t*)kr)[dw];
                 vd[i][bb] = ((const uint32_t*)vr)[dw];
                 vc[i][bb] = *(const uint16_t*)(vcr + bb * kQ8Bytes);
+                asm("" : "+v"(vc[i][bb]));     // widened here, next to its load: no masking later
             }
         }
         float s[4];
@@ -392,29 +391,30 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split
             __builtin_memcpy(&dv01, &u01, 4);
             __builtin_memcpy(&dv23, &u23, 4);
             const h4 pb = cat_h4(p01 * dv01, p23 * dv23);
-            const h4 a0 = as_h4(i8_pair_mfma_b0(vc[0][bb], vc[1][bb]), i8_pair_mfma_b0(vc[2][bb], vc[3][bb]));
-            const h4 a1 = as_h4(i8_pair_mfma_b1(vc[0][bb], vc[1][bb]), i8_pair_mfma_b1(vc[2][bb], vc[3][bb]));
+            uint32_t c0, c1, c2, c3;
+            i8_quad_mfma(vc[0][bb], vc[1][bb], vc[2][bb], vc[3][bb], c0, c1, c2, c3);
+            const h4 a0 = as_h4(c0, c1), a1 = as_h4(c2, c3);
             acc[2 * bb] = __builtin_amdgcn_mfma_f32_16x16x16f16(a0, pb, acc[2 * bb], 0, 0, 0);
             acc[2 * bb + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(a1, pb, acc[2 * bb + 1], 0, 0, 0);
         }
     };
 
-    for (int t = 0; t < n_tiles; ++t) {
-        // tile t has landed in every wave's share; every wave is done with t - 1
+    // tile t has landed in every wave's share; every wave is done with t - 1
+    auto tile = [&](int t, auto check) {
         wait_vm_barrier<(kStages - 2) * kLoads>();
         issue(t + kStages - 1);
         const char* kt = lds + (t & (kStages - 1)) * kStage + dk + h * HB;
         const char* vt = lds + (t & (kStages - 1)) * kStage + kOpBytes + dv + h * HB;
         const int jt = j0 + t * TT;
-        // only the split's last tile can hold keys past its end
-        const bool check = mrow != nullptr || jt + TT > j1;
 #pragma unroll
-        for (int u = 0; u < NSUB; ++u) {
-            const int kb = r * KPW + 16 * u;
-            if (check) group(kt, vt, kb, jt, std::true_type{});
-            else group(kt, vt, kb, jt, std::false_type{});
-        }
-    }
+        for (int u = 0; u < NSUB; ++u) group(kt, vt, r * KPW + 16 * u, jt, check);
+    };
+    // tiles whose keys all lie inside the split run without checks; only the
+    // last can hold keys past its end (all tiles are checked under a mask)
+    const int n_plain = mrow != nullptr ? 0 : (j1 - j0) / TT;
+    int t = 0;
+    for (; t < n_plain; ++t) tile(t, std::false_type{});
+    for (; t < n_tiles; ++t) tile(t, std::true_type{});
     // the padding tiles' loads land before the ring is reused
     asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
     __syncthreads();
@@ -444,7 +444,7 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split
         __syncthreads();
         if (r == 0) {
             for (int rr = 1; rr < R; ++rr) {
-                const int ow = rr * Hkv + h;
+                const int ow = rr * HKV + h;
                 const float mo = mbuf[ow][n];
                 const float mn = fmaxf(m, mo);
                 const float fa = mn == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - mn);
@@ -493,9 +493,9 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split
 template <int D>
 hipError_t launch_ds(const AttnArgs& a, float* ws, int n_splits, int split_len, hipStream_t s) {
     const dim3 grid(n_splits, a.B), block(kW * 64);
-    switch (a.Hq / a.Hkv) {
-#define VVA_DS(G) case G: hipLaunchKernelGGL((decode_stream_kernel<D, G>), grid, block, 0, s, a, ws, n_splits, split_len); break;
-        VVA_DS(1) VVA_DS(2) VVA_DS(3) VVA_DS(4) VVA_DS(5) VVA_DS(6) VVA_DS(7) VVA_DS(8)
+    switch (a.Hkv) {
+#define VVA_DS(H) case H: hipLaunchKernelGGL((decode_stream_kernel<D, H>), grid, block, 0, s, a, ws, n_splits, split_len); break;
+        VVA_DS(1) VVA_DS(2) VVA_DS(4) VVA_DS(8)
 #undef VVA_DS
         default: return hipErrorInvalidValue;
     }

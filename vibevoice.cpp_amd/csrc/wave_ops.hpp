@@ -140,19 +140,24 @@ VVA_I8_PAIR(2)
 VVA_I8_PAIR(3)
 #undef VVA_I8_PAIR
 
-// The same conversion for an MFMA operand.  The compiler's hazard checks do
-// not look inside inline asm, and an MFMA that reads a VGPR written by a
-// VALU instruction needs two wait states in between; the trailing s_nop 1
-// provides them whatever the compiler schedules next.
-#define VVA_I8_PAIR_MFMA(N)                                                                     \
-    __device__ __forceinline__ uint32_t i8_pair_mfma_b##N(uint32_t a, uint32_t b) {             \
-        uint32_t r;                                                                             \
-        asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_" #N "\n\t" \
-            "v_cvt_f16_i16_sdwa %0, sext(%2) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_" #N "\n\t" \
-            "s_nop 1"                                                                           \
-            : "=&v"(r) : "v"(a), "v"(b));                                                       \
-        return r;                                                                               \
-    }
-VVA_I8_PAIR_MFMA(0)
-VVA_I8_PAIR_MFMA(1)
-#undef VVA_I8_PAIR_MFMA
+// The two f16 MFMA A operands of one Q8_0 block from the code words of four
+// keys (c0..c3, each holding dims 2n and 2n + 1 in bytes 0 and 1): r0:r1 =
+// dim 2n of keys 0-3, r2:r3 = dim 2n + 1 (exact).  The compiler's hazard
+// checks do not look inside inline asm, and an MFMA that reads a VGPR written
+// by a VALU instruction needs two wait states in between; the trailing
+// s_nop 1 provides them for the last register written, whatever the compiler
+// schedules next (the others are further back).
+__device__ __forceinline__ void i8_quad_mfma(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3,
+                                             uint32_t& r0, uint32_t& r1, uint32_t& r2, uint32_t& r3) {
+    asm("v_cvt_f16_i16_sdwa %0, sext(%4) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
+        "v_cvt_f16_i16_sdwa %0, sext(%5) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_0\n\t"
+        "v_cvt_f16_i16_sdwa %1, sext(%6) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_0\n\t"
+        "v_cvt_f16_i16_sdwa %1, sext(%7) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_0\n\t"
+        "v_cvt_f16_i16_sdwa %2, sext(%4) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_1\n\t"
+        "v_cvt_f16_i16_sdwa %2, sext(%5) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1\n\t"
+        "v_cvt_f16_i16_sdwa %3, sext(%6) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_1\n\t"
+        "v_cvt_f16_i16_sdwa %3, sext(%7) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1\n\t"
+        "s_nop 1"
+        : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3)
+        : "v"(c0), "v"(c1), "v"(c2), "v"(c3));
+}
