@@ -4,43 +4,49 @@
 // ggml_flash_attn_ext with one query row per head (src/qwen2.cpp:332-334)
 // on Q8_0 K/V.
 //
-// Streaming.  Every workgroup (8 waves, one per CU) takes a contiguous key
-// range of one sequence and streams it through a 4-stage LDS ring filled by
-// buffer_load_dwordx4 ... lds, so three tiles (102 KB per CU) are on their
-// way from HBM while one is computed.  A tile is 512 (key, kv head, 32-dim
-// block) rows of the cache = 17,408 B of K plus the same of V, read as the
-// cache lays them out ([token][kv head][34-byte GGUF block]): one contiguous
-// byte range per operand, 1 KB per wave instruction.  The buffer ranges of
-// a split end at its last key, so chunks past it come back as zeros without
-// a memory access.
+// Streaming.  Every workgroup (4 waves, one per SIMD; one workgroup per CU)
+// takes a contiguous key range of one sequence and streams it through a
+// 4-stage LDS ring filled by buffer_load_dwordx4 ... lds (non-temporal: the
+// cache is read once), so three tiles (102 KB per CU) are on their way from
+// HBM while one is computed.  A tile is 512 (key, kv head, 32-dim block)
+// rows of the cache = 17,408 B of K plus the same of V, read as the cache
+// lays them out ([token][kv head][34-byte GGUF block]): one contiguous byte
+// range per operand, 1 KB per wave instruction.  The buffer ranges of a
+// split end at its last key, so chunks past it come back as zeros without a
+// memory access.
 //
-// Arithmetic on the matrix cores.  With g = 7 query heads per kv head, the
-// VALU form of this loop (v_dot4 scores, v_dot2 P.V) needs ~800 VALU lane
-// operations per (key, kv head) and runs VALU-bound at about a third of
-// HBM speed; on MFMA the VALU keeps only the conversions and the softmax.
-// Per tile, wave w takes kv head w % Hkv and 16 (d = 128) or 32 (d = 64) of
-// the tile's keys, in groups of 16 keys; lane = (g = lane / 16, n = lane % 16).
-// MFMA row/column m of a group stands for its key sigma(m) = 4 (m % 4) +
-// m / 4, so lane group g works on keys g, g + 4, g + 8, g + 12: with the
-// cache's 544-byte token rows the four groups' LDS reads then fall in
-// different banks.
-//   scores  S^T[key][row] per 32-dim block b with v_mfma_i32_16x16x32_i8:
-//           A = the K codes of block b (lane: key sigma(n), codes 8g..8g+7),
-//           B = Q quantized to Q8_0 (lane: row n, same codes), so each
+// Arithmetic on the matrix cores.  With g <= 8 query heads per kv head, a
+// 16 x 16 MFMA tile with one kv head's query rows would leave half its
+// columns idle; instead each wave packs two slots into the 16 columns:
+// rows 0-7 are the query heads of kv head 2p and rows 8-15 those of kv head
+// 2p + 1 (or, with one kv head, the same heads over a second group of 16
+// keys), over the same 16 keys.  Lane = (g = lane / 16, n = lane % 16).
+// MFMA row m of a group stands for its key sigma(m) = 4 (m % 4) + m / 4, so
+// lane group g works on keys g, g + 4, g + 8, g + 12: with the cache's
+// 544-byte token rows the four groups' LDS reads then fall in different
+// banks.
+//   scores  S^T[key][row] per 32-dim Q8_0 block with two
+//           v_mfma_i32_16x16x32_i8, block-diagonal over k: in the MFMA for
+//           dims 16j .. 16j + 15, k 0-15 carry slot 0's K codes and slot
+//           0's Q codes (zero in slot 1's columns), k 16-31 slot 1's.  Each
 //           block's dot is ggml's exact integer Q8_0 x Q8_0 block sum; the
-//           lane receives keys sigma(4g + i) of row n and scales them by
+//           lane receives keys sigma(4g + i) of its row n and scales them by
 //           d_k * d_q in fp32.
 //   softmax fp32, exp2 domain, one row per lane (max over the row's 16 keys:
 //           in-lane, then two permlane swaps).  The running max is raised
 //           only when a score exceeds it by 2^8.
 //   P.V     O^T[dim][row] += V^T P'^T with v_mfma_f32_16x16x16_f16 per 16
-//           dims: A = V codes (exact in f16; lane: dims 2n, 2n+1 of block b,
-//           keys sigma(4g + i)), B = P' = p * d_v(key, b) as f16 — the score
-//           accumulator layout is already B's layout, so P never leaves the
-//           registers.  MFMA j = 2b + s holds dims 32b + 2m + s in its row m.
-// The waves of one kv head merge through LDS (log-sum-exp); the workgroup
-// writes (m, l, acc[d]) per query head, or the output when there is one
-// split, and decode_merge_kernel (decode.hip) combines the splits.
+//           dims and slot: A = that slot's V codes (exact in f16; lane: dims
+//           2n, 2n+1 of block b, keys sigma(4g + i)), B = P' = p * d_v(key,
+//           b) as f16 — the score accumulator layout is already B's layout,
+//           so P never leaves the registers.  Each slot's MFMA is right for
+//           its own 8 columns; a lane keeps the accumulator of its slot.
+// A tile's P.V runs one tile late, beside the next tile's scores (its V
+// codes wait in registers), so the two dependency chains overlap.
+// The workgroup's records merge through LDS (log-sum-exp) into one row per
+// query head; the workgroup writes (m, l, acc[d]) per query head, or the
+// output when there is one split, and decode_merge_kernel (decode.hip)
+// combines the splits.
 #include "vva_internal.hpp"
 
 #include <type_traits>
@@ -55,7 +61,7 @@ typedef __attribute__((address_space(3))) char lds_char;
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kW = 8;                        // waves per workgroup
+constexpr int kW = 4;                        // waves per workgroup (one per SIMD)
 constexpr int kStages = 4;                   // LDS ring depth (power of 2)
 constexpr int kTileOpBytes = 17408;          // one operand of a tile: 512 Q8_0 blocks
 constexpr int kOpChunks = 18;                // 1 KB chunks per operand: 17 KB + alignment slack
@@ -63,8 +69,9 @@ constexpr int kOpBytes = kOpChunks * 1024;
 constexpr int kStage = 2 * kOpBytes;         // K, then V
 constexpr int kJunk = kStages * kStage;      // 1 KB target of the padding loads
 constexpr int kLdsBytes = kJunk + 1024;
-constexpr int kLoads = (2 * kOpChunks + kW - 1) / kW;   // DMA loads per wave per tile
-constexpr int kQLoads = 3;                   // DMA loads per wave for the raw Q rows
+constexpr int kOpLoads = (kOpChunks + kW - 1) / kW;     // DMA loads per wave, operand and tile
+constexpr int kLoads = 2 * kOpLoads;         // DMA loads per wave per tile
+constexpr int kQLoads = 6;                   // DMA loads per wave for the raw Q rows
 constexpr int kQRawBytes = kQLoads * kW * 1024;   // raw Q area: up to 24 KB
 constexpr int kDead = 0x40000000;            // buffer offset past every range
 constexpr float kLazy = 8.0f;                // running-max slack in log2 units: p <= 256
@@ -72,8 +79,11 @@ static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
 
 // buffer_load_dwordx4 ... lds: each lane's 16 bytes land at LDS address
 // m0 + 16 * lane.  Inline asm, so the compiler neither fences LDS reads on it
-// nor waits for it; completion is awaited explicitly (wait_vm_barrier).  The
-// whole offset is in the VGPR (soffset 0), so the range check sees all of it.
+// nor waits for it; completion is awaited explicitly (wait_vm_barrier, whose
+// memory clobber is what orders LDS reads after the data lands).  No memory
+// clobber here: a load writes a stage nobody reads until a later barrier, so
+// the compiler may move the current tile's LDS reads across it.  The whole
+// offset is in the VGPR (soffset 0), so the range check sees all of it.
 // STREAM marks the load non-temporal: the cache is read once, so its lines
 // should not displace what the next call reads again (Q, the partials).
 template <bool STREAM = false>
@@ -82,12 +92,12 @@ __device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t lds_addr, int voffset
         asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
                      :
                      : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voffset), "s"(rsrc)
-                     : "memory", "m0");
+                     : "m0");
     else
         asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                      :
                      : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voffset), "s"(rsrc)
-                     : "memory", "m0");
+                     : "m0");
 }
 
 // wait until at most N of this wave's loads are outstanding (and its LDS
@@ -127,26 +137,39 @@ __device__ __forceinline__ h4 cat_h4(h2 lo, h2 hi) { return h4{lo[0], lo[1], hi[
 // D: head dim (64 / 128); HKV: kv heads (1, 2, 4, 8), which fixes the token
 // row pitch, so every LDS offset inside a tile is a constant.
 template <int D, int HKV>
-__global__ void __launch_bounds__(kW * 64)
+__global__ void __launch_bounds__(kW * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
 decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split_len) {
     constexpr int NB = D / 32;                // Q8_0 blocks per head row
     constexpr int HB = NB * kQ8Bytes;         // bytes per head row
-    constexpr int NSUB = 128 / D;             // groups of 16 keys per wave per tile
-    constexpr int KPW = 16 * NSUB;            // keys per wave per tile
-    constexpr int NJ = 2 * NB;                // P.V MFMAs (16 dims each) per key group
-    static_assert(KPW * kW * HB == kTileOpBytes, "tile size");
-    static_assert(kW % HKV == 0, "whole waves per kv head");
+    constexpr int RB = HKV * HB;              // bytes per token row (all kv heads)
+    constexpr int TT = kTileOpBytes / RB;     // keys per tile
+    constexpr int NPAIR = TT * HKV / 32;      // slot pairs (2 slots of 16 keys x 1 kv head) per tile
+    constexpr int NSUB = NPAIR / kW;          // slot pairs per wave per tile
+    constexpr int HP = HKV >= 2 ? HKV / 2 : 1;    // kv head pairs
+    constexpr int NJ = 2 * NB;                // P.V MFMAs (16 dims each) per slot
+    static_assert(TT * RB == kTileOpBytes && NSUB * kW == NPAIR && NSUB >= 1, "tile size");
+    static_assert(kW % HP == 0, "a wave keeps its head pair across its slot pairs");
 
     __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
 
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, n = lane & 15;
-    constexpr int R = kW / HKV;               // waves per kv head
-    constexpr int RB = HKV * HB;              // bytes per token row (all kv heads)
-    const int G = a.Hq / HKV;                 // query heads per kv head (<= 16)
-    const int h = w % HKV, r = w / HKV;
-    const int TT = KPW * R;                   // keys per tile
+    const int G = a.Hq / HKV;                 // query heads per kv head (<= 8)
+    // The wave's two slots: kv heads 2 hp and 2 hp + 1 over the same 16 keys,
+    // or (HKV = 1) the one kv head over two consecutive groups of 16 keys.
+    // Column n of the MFMAs is query row n & 7 of slot n >> 3.
+    const int hp = w % HP;
+    auto slot_head = [&](int s) { return HKV >= 2 ? 2 * hp + s : 0; };
+    constexpr int SK = HKV >= 2 ? 0 : 16;     // key offset of slot 1 from slot 0
+    // first key of slot 0 of the wave's slot pair u in a tile
+    auto pair_key = [&](int u) {
+        const int p = w + kW * u;
+        return HKV >= 2 ? 16 * (p / HP) : 32 * p;
+    };
+    const int sr = n >> 3, rr = n & 7;        // the lane's slot and query row in it
+    const bool rvalid = rr < G;
+    const int hq_row = slot_head(sr) * G + rr;
     const int split = blockIdx.x, b = blockIdx.y;
     const int L = a.L[b];
     const int j0 = min(L, split * split_len);
@@ -165,35 +188,25 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split
     const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_char*)lds;
 
     // Tile t of an operand is bytes [t * 17408, t * 17408 + 18 KB) of its
-    // buffer, chunk c (1 KB) loaded by wave c % kW as its (c / kW)-th load.
-    // Every wave issues kLoads loads per tile: the 36 chunks of K and V, then
-    // padding loads (from past the range: zeros, no memory access) into the
+    // buffer: 18 chunks of 1 KB, chunk c loaded by wave c % kW.  Every wave
+    // issues kOpLoads loads per operand and tile; a chunk index past 17 is a
+    // padding load (from past the range: zeros, no memory access) into the
     // junk kilobyte.  A tile past the last one loads nothing but zeros; the
-    // 18th chunk of an operand is needed only when delta > 0.  The plan of
-    // each of the wave's loads (operand, LDS offset, whether it ever fetches)
-    // is fixed for the kernel, so a tile's issue has no branches.
-    i32x4 lrs[kLoads];
-    uint32_t llds[kLoads], lstage[kLoads];
-    int loff[kLoads];
-    bool lvalid[kLoads];
-#pragma unroll
-    for (int i = 0; i < kLoads; ++i) {
-        const int c = i * kW + w;
-        const bool isk = c < kOpChunks, isv = !isk && c < 2 * kOpChunks;
-        const int cc = isk ? c : c - kOpChunks;
-        lrs[i] = isv ? vrs : krs;
-        llds[i] = isk ? (uint32_t)(c * 1024) : isv ? (uint32_t)(kOpBytes + cc * 1024) : (uint32_t)kJunk;
-        lstage[i] = isk || isv ? 0xffffffffu : 0u;
-        loff[i] = cc * 1024;
-        lvalid[i] = (isk && (cc < kOpChunks - 1 || dk > 0)) || (isv && (cc < kOpChunks - 1 || dv > 0));
-    }
+    // 18th chunk of an operand is needed only when delta > 0.
     auto issue = [&](int t) {
         const bool live = t < n_tiles;
-        const uint32_t st = (uint32_t)(t & (kStages - 1)) * kStage;
+        const uint32_t st = lds0 + (uint32_t)(t & (kStages - 1)) * kStage;
         const int tb = t * kTileOpBytes + lane * 16;
 #pragma unroll
-        for (int i = 0; i < kLoads; ++i)
-            dma16<true>(lrs[i], lds0 + (st & lstage[i]) + llds[i], live && lvalid[i] ? tb + loff[i] : kDead);
+        for (int op = 0; op < 2; ++op)
+#pragma unroll
+            for (int i = 0; i < kOpLoads; ++i) {
+                const int c = w + kW * i;
+                const bool have = c < kOpChunks;
+                const bool need = live && have && (c < kOpChunks - 1 || (op ? dv : dk) > 0);
+                const uint32_t dst = have ? st + op * kOpBytes + c * 1024 : lds0 + kJunk;
+                dma16<true>(op ? vrs : krs, dst, need ? tb + c * 1024 : kDead);
+            }
     };
 
     // ---- Q: its rows (contiguous, at most 24 KB) are DMA'd first into the
@@ -201,9 +214,9 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split
     // barrier, then tile 0 goes out.  Once the wave's own Q loads have landed
     // (they were issued first) and the workgroup has met, Q is quantized to
     // Q8_0 blocks (codes + fp16-rounded scale) next to the raw rows, and
-    // tiles 1 and 2 go out.  Four adjacent lanes share a block (8 values each; the block max
-    // over the quad by DPP); with more than 128 blocks a thread takes a
-    // second quarter.
+    // tiles 1 and 2 go out.  Four adjacent lanes share a block (8 values
+    // each; the block max over the quad by DPP); a thread takes every
+    // (kW * 64)-th quarter block.
     const int eb = (int)type_elem_bytes(a.q_type);
     {
         const i32x4 qrs = make_rsrc_sgpr(a.q + b * a.q_nb_b, (uint32_t)(a.Hq * D * eb));
@@ -220,7 +233,7 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split
 
     const char* qraw = lds + (kStages - 1) * kStage;
     uint32_t* qlds = (uint32_t*)(lds + (kStages - 1) * kStage + kQRawBytes);
-    constexpr int QI = 2;                             // quarters per thread (Hq * NB <= 256)
+    constexpr int QI = 1024 / (kW * 64);              // quarters per thread (Hq * NB <= 256)
     const int nqi = a.Hq * NB * 4;
 #pragma unroll
     for (int it = 0; it < QI; ++it) {
@@ -268,153 +281,243 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split
     // LDS only: the tile loads stay in flight
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory");
 
-    // B operand of the score MFMAs: row n's Q codes 8g..8g+7 of each block,
-    // and its block scales times scale * log2(e) (rows past g are zero)
-    long qb[NB];
+    // B operands of the score MFMAs, block-diagonal over k: per block and
+    // 16-dim half j, lane (g, n) holds codes 16 j + 8 (g & 1) .. + 7 of row
+    // n's Q block when its k range (slot g >> 1) is row n's slot, else 0.
+    // qd: row n's block scales times scale * log2(e).
+    long qb[NB][2];
     float qd[NB];
     {
         const float sl2 = a.scale * kLog2e;          // scores come out in the exp2 domain
+        const bool mine = (g >> 1) == sr && rvalid;
+        const uint32_t* src = qlds + hq_row * NB * 9;
 #pragma unroll
         for (int bb = 0; bb < NB; ++bb) {
-            qb[bb] = 0;
-            qd[bb] = 0.0f;
-            if (n < G) {
-                const uint32_t* src = qlds + ((h * G + n) * NB + bb) * 9;
-                qb[bb] = (long)((uint64_t)src[2 * g] | ((uint64_t)src[2 * g + 1] << 32));
-                qd[bb] = __uint_as_float(src[8]) * sl2;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int wd = bb * 9 + 4 * j + 2 * (g & 1);
+                qb[bb][j] = mine ? (long)((uint64_t)src[wd] | ((uint64_t)src[wd + 1] << 32)) : 0;
             }
+            qd[bb] = rvalid ? __uint_as_float(src[bb * 9 + 8]) * sl2 : 0.0f;
         }
     }
 
     float m = -INFINITY, l = 0.0f;            // row n's running max (log2 domain) and sum
     float mb = 0.0f;                          // m, or 0 while m = -inf: the exp2 base
-    f32x4 acc[NJ];
+    f32x4 acc[2][NJ];                         // per slot's V: only the lane's own slot is kept
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) acc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) acc[s][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     const char* mrow = a.mask_mode == kMaskExplicit ? a.mask + b * a.mask_nb_b : nullptr;   // query row 0
-    const int ka_off = (4 * (n & 3) + (n >> 2)) * RB;       // A-operand key sigma(n) of a group
-    const int kc_off = g * RB;                              // C-layout keys 4i + g: i * 4 RB further
-    const int vc_off = g * RB + 2 + 2 * n;                  // their V codes of dims 2n, 2n + 1
-
-    // One group of 16 keys starting at tile key kb.  CHECK: the group may
-    // hold keys past the split or the caller passed a mask.
-    auto group = [&](const char* kt, const char* vt, int kb, int jt, auto check) {
-        constexpr bool CHECK = decltype(check)::value;
-        // ---- scores: per block, A = key (kb + sigma(n))'s codes 8g..8g+7
-        i32x4 cs[NB];
-        {
-            const char* ka = kt + kb * RB + ka_off;
+    // LDS offsets from a slot pair's first key.  Score A operand: key
+    // sigma(n) = 4 (n % 4) + n / 4 of slot g >> 1, codes 8 (g & 1) .. of each
+    // 16-dim half; the 4-byte word at or below them.
+    const int ka_off = (4 * (n & 3) + (n >> 2) + SK * (g >> 1)) * RB + slot_head(g >> 1) * HB + 8 * (g & 1);
+    // C layout: keys 4i + g of the lane's own slot (i * 4 RB further)
+    const int kc_off = (g + SK * sr) * RB + slot_head(sr) * HB;
+    // P.V A operands: V codes of dims 2n, 2n + 1 of keys 4i + g of each slot
+    int vc_off[2];
 #pragma unroll
-            for (int bb = 0; bb < NB; ++bb) {
-                const int off = bb * kQ8Bytes + 2 + 8 * g;       // 2 mod 4 for even blocks
-                const uint32_t* p = (const uint32_t*)(ka + (off & ~3));
-                const uint32_t w0 = p[0], w1 = p[1];
-                uint32_t lo = w0, hi = w1;
-                if ((bb & 1) == 0) {
-                    const uint32_t w2 = p[2];
-                    lo = __builtin_amdgcn_alignbyte(w1, w0, 2);
-                    hi = __builtin_amdgcn_alignbyte(w2, w1, 2);
-                }
-                const long av = (long)((uint64_t)lo | ((uint64_t)hi << 32));
-                cs[bb] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, qb[bb], i32x4{0, 0, 0, 0}, 0, 0, 0);
+    for (int s = 0; s < 2; ++s) vc_off[s] = (g + SK * s) * RB + slot_head(s) * HB + 2 + 2 * n;
+
+    // A slot pair's P.V operands, carried from its scores to the P.V step one
+    // tile later: the V codes (in registers, so the stage can be refilled)
+    // and P' = p * d_v per block.
+    struct PendingPV {
+        uint32_t vc[2][4][NB];
+        h4 pb[NB];
+    };
+    // O^T += V^T P'^T per 16 dims, once with each slot's V
+    auto pv = [&](const PendingPV& q) {
+#pragma unroll
+        for (int bb = 0; bb < NB; ++bb)
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                uint32_t c0, c1, c2, c3;
+                i8_quad_mfma(q.vc[s][0][bb], q.vc[s][1][bb], q.vc[s][2][bb], q.vc[s][3][bb], c0, c1, c2, c3);
+                acc[s][2 * bb] = __builtin_amdgcn_mfma_f32_16x16x16f16(as_h4(c0, c1), q.pb[bb], acc[s][2 * bb], 0, 0, 0);
+                acc[s][2 * bb + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(as_h4(c2, c3), q.pb[bb], acc[s][2 * bb + 1], 0, 0, 0);
             }
-        }
-        // the lane's keys kb + sigma(4g + i) = kb + 4i + g: the dwords that
-        // hold their K and V block scales, and their V codes of dims 2n, 2n + 1
-        uint32_t kd[4][NB], vd[4][NB], vc[4][NB];
+    };
+    // The LDS operands of one slot pair (2 x 16 keys) starting at tile key
+    // kb: the score A operands per block and 16-dim half, the dwords that
+    // hold the K and V block scales of the lane's keys 4i + g of its slot,
+    // and both slots' V codes of dims 2n, 2n + 1.  Read right after the
+    // barrier, before the next tile's loads are issued (an asm volatile the
+    // compiler does not move LDS reads across).
+    struct PairOps {
+        uint32_t aw[NB][2][3];                // A words (the third only for even blocks)
+        uint32_t kd[4][NB], vd[4][NB], vc[2][4][NB];
+    };
+    auto read_pair = [&](const char* kt, const char* vt, int kb, PairOps& o) {
+        const char* ka = kt + kb * RB + ka_off;
+#pragma unroll
+        for (int bb = 0; bb < NB; ++bb)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int off = bb * kQ8Bytes + 2 + 16 * j;      // 2 mod 4 for even blocks
+                const uint32_t* p = (const uint32_t*)(ka + (off & ~3));
+                o.aw[bb][j][0] = p[0];
+                o.aw[bb][j][1] = p[1];
+                o.aw[bb][j][2] = (bb & 1) == 0 ? p[2] : 0u;
+            }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const char* kr = kt + (kb + 4 * i) * RB + kc_off;
             const char* vr = vt + (kb + 4 * i) * RB + kc_off;
-            const char* vcr = vt + (kb + 4 * i) * RB + vc_off;
 #pragma unroll
             for (int bb = 0; bb < NB; ++bb) {
                 const int dw = (bb * kQ8Bytes - (bb & 1) * 2) / 4;
-                kd[i][bb] = ((const uint32_t*)kr)[dw];
-                vd[i][bb] = ((const uint32_t*)vr)[dw];
-                vc[i][bb] = *(const uint16_t*)(vcr + bb * kQ8Bytes);
-                asm("" : "+v"(vc[i][bb]));     // widened here, next to its load: no masking later
+                o.kd[i][bb] = ((const uint32_t*)kr)[dw];
+                o.vd[i][bb] = ((const uint32_t*)vr)[dw];
+#pragma unroll
+                for (int s = 0; s < 2; ++s) {
+                    o.vc[s][i][bb] = *(const uint16_t*)(vt + (kb + 4 * i) * RB + vc_off[s] + bb * kQ8Bytes);
+                    asm("" : "+v"(o.vc[s][i][bb]));     // widened here, next to its load: no masking later
+                }
             }
         }
-        float s[4];
+    };
+    // Scores and softmax of one slot pair (keys kb .. of the tile at key jt)
+    // from its operands, with the P.V of the previous tile's pair (pend;
+    // zeros before the first tile) in the same instruction stream: the two
+    // are independent until a rescale, which comes after both.  The pair's
+    // own P.V operands replace pend.  CHECK: the group may hold keys past the
+    // split or the caller passed a mask.
+    auto group = [&](const PairOps& o, int kb, int jt, auto check, const PendingPV& prev, PendingPV& cur) {
+        constexpr bool CHECK = decltype(check)::value;
+        pv(prev);
+        // ---- scores: per block, two block-diagonal halves into one sum
+        i32x4 cs[NB];
+#pragma unroll
+        for (int bb = 0; bb < NB; ++bb) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                uint32_t lo = o.aw[bb][j][0], hi = o.aw[bb][j][1];
+                if ((bb & 1) == 0) {
+                    lo = __builtin_amdgcn_alignbyte(o.aw[bb][j][1], o.aw[bb][j][0], 2);
+                    hi = __builtin_amdgcn_alignbyte(o.aw[bb][j][2], o.aw[bb][j][1], 2);
+                }
+                const long av = (long)((uint64_t)lo | ((uint64_t)hi << 32));
+                cs[bb] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, qb[bb][j], j == 0 ? i32x4{0, 0, 0, 0} : cs[bb], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int bb = 0; bb < NB; ++bb) cur.vc[s][i][bb] = o.vc[s][i][bb];
+        float sc[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             float x = 0.0f;
 #pragma unroll
             for (int bb = 0; bb < NB; ++bb) {
-                const float e = (bb & 1) ? mix_mul<1>(kd[i][bb], qd[bb]) : mix_mul<0>(kd[i][bb], qd[bb]);
+                const float e = (bb & 1) ? mix_mul<1>(o.kd[i][bb], qd[bb]) : mix_mul<0>(o.kd[i][bb], qd[bb]);
                 x = fmaf((float)cs[bb][i], e, x);
             }
-            s[i] = x;
+            sc[i] = x;
         }
         if constexpr (CHECK) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int j = jt + kb + 4 * i + g;
+                const int j = jt + kb + SK * sr + 4 * i + g;
                 bool live = j < j1;
                 if (mrow) {
                     const float mv = live ? f16_to_f32(*(const uint16_t*)(mrow + 2 * (int64_t)j)) * kLog2e : 0.0f;
                     live = live && mv != -INFINITY;
-                    s[i] += mv;
+                    sc[i] += mv;
                 }
-                s[i] = live ? s[i] : -INFINITY;
+                sc[i] = live ? sc[i] : -INFINITY;
             }
         }
 
-        // ---- online softmax of row n, running max raised lazily
-        const float smax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+        // ---- online softmax of row n, running max raised lazily (after
+        // the previous pair's P.V has gone into acc)
+        const float smax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
         if (__any(smax > m + kLazy)) {
             const float cm = max_swap32(max_swap16(smax));
             if (cm > m + kLazy) {
                 const float alpha = __builtin_amdgcn_exp2f(m - cm);     // 0 when m = -inf
                 l *= alpha;
 #pragma unroll
-                for (int j = 0; j < NJ; ++j) acc[j] *= alpha;
+                for (int s = 0; s < 2; ++s)
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j) acc[s][j] *= alpha;
                 m = cm;
                 mb = cm;
             }
         }
         float p[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(s[i] - mb);   // 0 when masked
+        for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(sc[i] - mb);   // 0 when masked
         l += (p[0] + p[1]) + (p[2] + p[3]);
         const h2 p01 = h2{(_Float16)p[0], (_Float16)p[1]};
         const h2 p23 = h2{(_Float16)p[2], (_Float16)p[3]};
 
-        // ---- O^T += V^T P'^T per 16 dims
 #pragma unroll
         for (int bb = 0; bb < NB; ++bb) {
             const uint32_t sel = (bb & 1) ? 0x07060302u : 0x05040100u;      // high or low halves
             h2 dv01, dv23;
-            const uint32_t u01 = __builtin_amdgcn_perm(vd[1][bb], vd[0][bb], sel);
-            const uint32_t u23 = __builtin_amdgcn_perm(vd[3][bb], vd[2][bb], sel);
+            const uint32_t u01 = __builtin_amdgcn_perm(o.vd[1][bb], o.vd[0][bb], sel);
+            const uint32_t u23 = __builtin_amdgcn_perm(o.vd[3][bb], o.vd[2][bb], sel);
             __builtin_memcpy(&dv01, &u01, 4);
             __builtin_memcpy(&dv23, &u23, 4);
-            const h4 pb = cat_h4(p01 * dv01, p23 * dv23);
-            uint32_t c0, c1, c2, c3;
-            i8_quad_mfma(vc[0][bb], vc[1][bb], vc[2][bb], vc[3][bb], c0, c1, c2, c3);
-            const h4 a0 = as_h4(c0, c1), a1 = as_h4(c2, c3);
-            acc[2 * bb] = __builtin_amdgcn_mfma_f32_16x16x16f16(a0, pb, acc[2 * bb], 0, 0, 0);
-            acc[2 * bb + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(a1, pb, acc[2 * bb + 1], 0, 0, 0);
+            cur.pb[bb] = cat_h4(p01 * dv01, p23 * dv23);
         }
     };
 
     // tile t has landed in every wave's share; every wave is done with t - 1
-    auto tile = [&](int t, auto check) {
-        wait_vm_barrier<(kStages - 2) * kLoads>();
-        issue(t + kStages - 1);
-        const char* kt = lds + (t & (kStages - 1)) * kStage + dk + h * HB;
-        const char* vt = lds + (t & (kStages - 1)) * kStage + kOpBytes + dv + h * HB;
-        const int jt = j0 + t * TT;
+    // (whose V codes wait in registers for their P.V).  The pending P.V
+    // operands alternate between two sets, tile by tile, so they stay put.
+    PendingPV pa[NSUB], pz[NSUB];
 #pragma unroll
-        for (int u = 0; u < NSUB; ++u) group(kt, vt, r * KPW + 16 * u, jt, check);
+    for (int u = 0; u < NSUB; ++u) {
+#pragma unroll
+        for (int bb = 0; bb < NB; ++bb) {
+            pz[u].pb[bb] = h4{};
+#pragma unroll
+            for (int s = 0; s < 2; ++s)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) pz[u].vc[s][i][bb] = 0;
+        }
+    }
+    auto tile = [&](int t, auto check, const PendingPV (&prev)[NSUB], PendingPV (&cur)[NSUB]) {
+        wait_vm_barrier<(kStages - 2) * kLoads>();
+        const char* kt = lds + (t & (kStages - 1)) * kStage + dk;
+        const char* vt = lds + (t & (kStages - 1)) * kStage + kOpBytes + dv;
+        const int jt = j0 + t * TT;
+        PairOps ops[NSUB];
+#pragma unroll
+        for (int u = 0; u < NSUB; ++u) read_pair(kt, vt, pair_key(u), ops[u]);
+        issue(t + kStages - 1);
+#pragma unroll
+        for (int u = 0; u < NSUB; ++u) group(ops[u], pair_key(u), jt, check, prev[u], cur[u]);
     };
     // tiles whose keys all lie inside the split run without checks; only the
-    // last can hold keys past its end (all tiles are checked under a mask)
+    // last can hold keys past its end (all tiles are checked under a mask).
+    // Tiles go in pairs (pz -> pa, pa -> pz); an odd count ends with one
+    // more tile into pa, whose P.V is the last.
     const int n_plain = mrow != nullptr ? 0 : (j1 - j0) / TT;
     int t = 0;
-    for (; t < n_plain; ++t) tile(t, std::false_type{});
-    for (; t < n_tiles; ++t) tile(t, std::true_type{});
+    for (; t + 1 < n_plain; t += 2) {
+        tile(t, std::false_type{}, pz, pa);
+        tile(t + 1, std::false_type{}, pa, pz);
+    }
+    for (; t + 1 < n_tiles; t += 2) {
+        tile(t, std::true_type{}, pz, pa);
+        tile(t + 1, std::true_type{}, pa, pz);
+    }
+    if (t < n_tiles) {
+        tile(t, std::true_type{}, pz, pa);
+#pragma unroll
+        for (int u = 0; u < NSUB; ++u) pv(pa[u]);
+    } else {
+#pragma unroll
+        for (int u = 0; u < NSUB; ++u) pv(pz[u]);
+    }
     // the padding tiles' loads land before the ring is reused
     asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
     __syncthreads();
@@ -422,70 +525,61 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split
     // row n's sum over the four lane groups
     l = add_swap32(add_swap16(l));
 
-    // lane (g, n) holds O[row n][32 b + 8 g + 2 i + s] = acc[2 b + s][i]
-    auto dims = [&](int bb, int half) -> float4 {
-        const f32x4 e = acc[2 * bb], o = acc[2 * bb + 1];
-        return half == 0 ? make_float4(e[0], o[0], e[1], o[1]) : make_float4(e[2], o[2], e[3], o[3]);
-    };
-
-    // ---- merge the R waves of each kv head (log-sum-exp) through LDS
-    float (*abuf)[16][D] = (float (*)[16][D])lds;
-    float (*mbuf)[16] = (float (*)[16])(lds + kW * 16 * D * 4);
-    float (*lbuf)[16] = (float (*)[16])(lds + kW * 16 * D * 4 + kW * 16 * 4);
-    if (R > 1) {
-        if (r > 0) {
-            if (g == 0) { mbuf[w][n] = m; lbuf[w][n] = l; }
+    // ---- every (wave, row) result to LDS: (m, l, O[D]) of query row rr of
+    // slot sr.  Lane (g, n) holds O[32 b + 8 g + 2 i + s] = acc[sr][2 b + s][i].
+    constexpr int PS = D + 4;                 // floats per (wave, row) record
+    float* part = (float*)lds;
+    {
+        float* prow = part + (w * 16 + n) * PS;
 #pragma unroll
-            for (int bb = 0; bb < NB; ++bb) {
-                *(float4*)&abuf[w][n][32 * bb + 8 * g] = dims(bb, 0);
-                *(float4*)&abuf[w][n][32 * bb + 8 * g + 4] = dims(bb, 1);
-            }
+        for (int bb = 0; bb < NB; ++bb) {
+            const f32x4 e = sr ? acc[1][2 * bb] : acc[0][2 * bb];
+            const f32x4 o = sr ? acc[1][2 * bb + 1] : acc[0][2 * bb + 1];
+            *(float4*)(prow + 32 * bb + 8 * g) = make_float4(e[0], o[0], e[1], o[1]);
+            *(float4*)(prow + 32 * bb + 8 * g + 4) = make_float4(e[2], o[2], e[3], o[3]);
         }
-        __syncthreads();
-        if (r == 0) {
-            for (int rr = 1; rr < R; ++rr) {
-                const int ow = rr * HKV + h;
-                const float mo = mbuf[ow][n];
-                const float mn = fmaxf(m, mo);
-                const float fa = mn == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - mn);
-                const float fb = mn == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mo - mn);
-                l = l * fa + lbuf[ow][n] * fb;
-#pragma unroll
-                for (int bb = 0; bb < NB; ++bb) {
-                    const float4 x = *(const float4*)&abuf[ow][n][32 * bb + 8 * g];
-                    const float4 y = *(const float4*)&abuf[ow][n][32 * bb + 8 * g + 4];
-                    f32x4& e = acc[2 * bb];
-                    f32x4& o = acc[2 * bb + 1];
-                    e[0] = e[0] * fa + x.x * fb; o[0] = o[0] * fa + x.y * fb;
-                    e[1] = e[1] * fa + x.z * fb; o[1] = o[1] * fa + x.w * fb;
-                    e[2] = e[2] * fa + y.x * fb; o[2] = o[2] * fa + y.y * fb;
-                    e[3] = e[3] * fa + y.z * fb; o[3] = o[3] * fa + y.w * fb;
-                }
-                m = mn;
-            }
-        }
+        if (g == 0) { prow[D] = m; prow[D + 1] = l; }
     }
-    const int hq = h * G + n;
-    if (r == 0 && n < G) {
-        if (n_splits == 1) {
-            const float inv = l == 0.0f ? 0.0f : 1.0f / l;
-            float* orow = (float*)((char*)a.out + b * a.o_nb_b + hq * a.o_nb_h);
+    __syncthreads();
+
+    // ---- per (query head, 4 dims): log-sum-exp over the records of its
+    // rows: the waves of its head pair (HKV >= 2: row 8 (h & 1) + r) or all
+    // waves and both slots (HKV = 1: rows r and 8 + r)
+    constexpr int NREC = HKV >= 2 ? kW / HP : 2 * kW;
+    const int ntask = a.Hq * (D / 4);
+    for (int task = threadIdx.x; task < ntask; task += kW * 64) {
+        const int hq = task / (D / 4), d4 = task % (D / 4);
+        const int h = hq / G, r = hq % G;
+        float M = -INFINITY, den = 0.0f;
+        float4 num = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-            for (int bb = 0; bb < NB; ++bb) {
-                const float4 x = dims(bb, 0), y = dims(bb, 1);
-                *(float4*)(orow + 32 * bb + 8 * g) = make_float4(x.x * inv, x.y * inv, x.z * inv, x.w * inv);
-                *(float4*)(orow + 32 * bb + 8 * g + 4) = make_float4(y.x * inv, y.y * inv, y.z * inv, y.w * inv);
-            }
+        for (int k = 0; k < NREC; ++k) {
+            const int ww = HKV >= 2 ? h / 2 + HP * k : k >> 1;
+            const int nn = HKV >= 2 ? 8 * (h & 1) + r : 8 * (k & 1) + r;
+            const float* rec = part + (ww * 16 + nn) * PS;
+            const float mm = rec[D];
+            if (mm == -INFINITY) continue;                  // nothing visible in this record
+            const float ll = rec[D + 1];
+            const float4 v = *(const float4*)(rec + 4 * d4);
+            const float mn = fmaxf(M, mm);
+            const float fa = __builtin_amdgcn_exp2f(M - mn);   // 0 while M = -inf
+            const float fb = __builtin_amdgcn_exp2f(mm - mn);
+            den = den * fa + ll * fb;
+            num.x = num.x * fa + v.x * fb;
+            num.y = num.y * fa + v.y * fb;
+            num.z = num.z * fa + v.z * fb;
+            num.w = num.w * fa + v.w * fb;
+            M = mn;
+        }
+        if (n_splits == 1) {
+            const float inv = den == 0.0f ? 0.0f : 1.0f / den;
+            float* orow = (float*)((char*)a.out + b * a.o_nb_b + hq * a.o_nb_h);
+            *(float4*)(orow + 4 * d4) = make_float4(num.x * inv, num.y * inv, num.z * inv, num.w * inv);
         } else {
             // partials: acc [B][Hq][n_splits][D], then (m, l) [B][Hq][n_splits][2]
             const size_t idx = ((size_t)b * a.Hq + hq) * n_splits + split;
-            float* wacc = ws + idx * D;
-#pragma unroll
-            for (int bb = 0; bb < NB; ++bb) {
-                *(float4*)(wacc + 32 * bb + 8 * g) = dims(bb, 0);
-                *(float4*)(wacc + 32 * bb + 8 * g + 4) = dims(bb, 1);
-            }
-            if (g == 0) *(float2*)(ws + (size_t)a.B * a.Hq * n_splits * D + idx * 2) = make_float2(m, l);
+            *(float4*)(ws + idx * D + 4 * d4) = num;
+            if (d4 == 0) *(float2*)(ws + (size_t)a.B * a.Hq * n_splits * D + idx * 2) = make_float2(M, den);
         }
     }
 }
@@ -511,7 +605,7 @@ bool decode_stream_supported(const AttnArgs& a) {
     if (a.d != 64 && a.d != 128) return false;
     if (a.k_type != VVA_TYPE_Q8_0 || a.v_type != VVA_TYPE_Q8_0) return false;
     if (a.Hkv < 1 || a.Hq % a.Hkv != 0 || a.Hq / a.Hkv > 8) return false;
-    if (kW % a.Hkv != 0) return false;
+    if (a.Hkv != 1 && a.Hkv != 2 && a.Hkv != 4 && a.Hkv != 8) return false;
     // dense rows: [token][kv head][blocks], as the resident cache stores them
     const int64_t hb = (int64_t)(a.d / 32) * kQ8Bytes;
     if (a.k_nb_head != hb || a.v_nb_head != hb) return false;
