@@ -159,6 +159,12 @@ class Context:
     def synchronize(self):
         self.check(self.lib.vva_synchronize(self.h))
 
+    def set_stream(self, stream):
+        """Enqueue later calls on `stream` (a torch.cuda.Stream), e.g. the
+        stream a torch.cuda.graph capture records."""
+        self.check(self.lib.vva_set_stream(self.h, ctypes.c_void_p(stream.cuda_stream)))
+        self.stream = stream
+
     def set_attn_path(self, path: int):
         self.check(self.lib.vva_set_attn_path(self.h, path))
 
