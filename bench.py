@@ -43,6 +43,9 @@ T_PREFILL = 32768
 L_DECODE = 32768
 B_DECODE = 2
 THETA = 1.0e6
+CHUNK = 512                      # ASR prefill chunk (64 chunks cover 32768 tokens)
+# 0.5B TTS CFG decode: 14 q / 2 kv heads, d = 64, F16 caches at 1024, 24 layers
+S_D, S_HQ, S_HKV, S_LAYERS, S_L = 64, 14, 2, 24, 1024
 
 # HBM bytes per launch of the dominant kernels, from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE
 # passes over this script (KiB per dispatch), each scaled by the counter's reading for a plain
@@ -192,6 +195,122 @@ def run_decode(torch, vva, ctx, steps: int, warmup: int):
     return res, kv
 
 
+def run_prefill_chunked(torch, vva, ctx, layers: int):
+    """The ASR prefill as the reference runs it: 64 chunks of 512 tokens per
+    layer, chunk c attending to its 512 rows plus the 512 c rows before it
+    (same total FLOPs as the single-shot prefill).  HIP events around each
+    chunk's attention launch."""
+    rng = torch.Generator(device="cuda").manual_seed(99)
+    q = torch.randn((1, CHUNK, HQ, D), generator=rng, device="cuda").to(torch.bfloat16)
+    k = torch.randn((1, CHUNK, HKV, D), generator=rng, device="cuda").to(torch.bfloat16)
+    v = torch.randn((1, CHUNK, HKV, D), generator=rng, device="cuda").to(torch.bfloat16)
+    qr = torch.empty((1, CHUNK, HQ, D), dtype=torch.float16, device="cuda")
+    out = torch.empty((1, CHUNK, HQ, D), dtype=torch.float32, device="cuda")
+    kv = vva.KVCache(ctx, layers + 1, HKV, D, T_PREFILL, 1, vva.F16)
+    n_chunks = T_PREFILL // CHUNK
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(layers * n_chunks)]
+    scale = D ** -0.5
+    pos_all = torch.arange(T_PREFILL, dtype=torch.int32, device="cuda")
+    for layer in range(layers + 1):                  # layer 0: untimed warm-up (sizes the workspace)
+        for c in range(n_chunks):
+            kv.set_len(0, c * CHUNK)
+            ctx.rope_append(kv, layer, q, k, v, pos_all[c * CHUNK:(c + 1) * CHUNK], qr, freq_base=THETA)
+            if layer > 0:
+                ev[(layer - 1) * n_chunks + c][0].record()
+            ctx.attn(kv, layer, qr, out, scale)
+            if layer > 0:
+                ev[(layer - 1) * n_chunks + c][1].record()
+    torch.cuda.synchronize()
+    ms = [a.elapsed_time(b) for a, b in ev]
+    attn_ms = float(np.sum(ms)) / layers
+    flops = sum(4.0 * HQ * D * (CHUNK * c * CHUNK + CHUNK * (CHUNK + 1) / 2) for c in range(n_chunks))
+    kv.free()
+    return {"workload": f"Qwen2.5-7B-shaped ASR prefill: {n_chunks} chunks of {CHUNK} tokens, past 0..{T_PREFILL - CHUNK}, "
+                        f"F16 cache, {layers} layers",
+            "value": round(flops / (attn_ms * 1e-3) / 1e12, 1), "unit": "TFLOP/s",
+            "frac_of_mfma_peak": round(flops / (attn_ms * 1e-3) / 1e12 / PEAK_F16_TFLOPS, 4),
+            "attn_ms_per_layer": round(attn_ms, 3), "flop_per_layer": flops,
+            "splits_last_chunk": ctx.last_decode_splits(),
+            "first_chunk_ms": round(float(np.mean(ms[::n_chunks])), 4),
+            "last_chunk_ms": round(float(np.mean(ms[n_chunks - 1::n_chunks])), 4),
+            "timing": "HIP events around each chunk's attention launch"}
+
+
+def run_decode_small(torch, vva, ctx, steps: int):
+    """The 0.5B TTS CFG decode step (B = 2, 14 q / 2 kv heads, d = 64, F16
+    caches at 1024, 24 layers of RoPE + append + attention), timed as eager
+    launches from prebuilt descriptors and as one captured HIP graph per
+    step.  The graph's kernel arguments (cache lengths) are fixed at capture,
+    so each replay repeats the captured step at the same positions."""
+    rng = torch.Generator(device="cuda").manual_seed(5)
+    B = 2
+    kv = vva.KVCache(ctx, S_LAYERS, S_HKV, S_D, S_L + 8, B, vva.F16)
+    for layer in range(S_LAYERS):
+        for s_ in range(B):
+            kv.set_len(s_, 0)
+        kk = torch.randn((B, S_L, S_HKV, S_D), generator=rng, device="cuda")
+        vv = torch.randn((B, S_L, S_HKV, S_D), generator=rng, device="cuda")
+        qq = torch.empty((B, S_L, S_HKV, S_D), device="cuda")
+        pos = torch.arange(S_L, dtype=torch.int32, device="cuda")
+        ctx.rope_append(kv, layer, qq, kk, vv, pos, qq, freq_base=THETA)
+    for s_ in range(B):
+        kv.set_len(s_, S_L)
+    q = torch.randn((B, 1, S_HQ, S_D), generator=rng, device="cuda")
+    k = torch.randn((B, 1, S_HKV, S_D), generator=rng, device="cuda")
+    v = torch.randn((B, 1, S_HKV, S_D), generator=rng, device="cuda")
+    qr = torch.empty_like(q)
+    out = torch.empty((B, 1, S_HQ, S_D), dtype=torch.float32, device="cuda")
+    pos = torch.full((B, 1), S_L, dtype=torch.int32, device="cuda")
+    scale = S_D ** -0.5
+    lib, h, kvh = ctx.lib, ctx.h, kv.h
+    byref = ctypes.byref
+    qv, kv_, vv_, pv, qrv, ov = (vva.view(t) for t in (q, k, v, pos, qr, out))
+
+    def step():
+        for layer in range(S_LAYERS):
+            ctx.check(lib.vva_rope_append(h, kvh, layer, byref(qv), byref(kv_), byref(vv_), byref(pv), None, THETA,
+                                          byref(qrv)))
+            ctx.check(lib.vva_attn(h, kvh, layer, byref(qrv), None, None, scale, byref(ov)))
+
+    for _ in range(3):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    eager_us = e0.elapsed_time(e1) * 1e3 / steps
+    g = torch.cuda.CUDAGraph()
+    default = torch.cuda.current_stream()
+    try:
+        with torch.cuda.graph(g):
+            ctx.set_stream(torch.cuda.current_stream())
+            step()
+    finally:
+        ctx.set_stream(default)
+    g.replay()
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(steps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    graph_us = e0.elapsed_time(e1) * 1e3 / steps
+    del g
+    L = S_L + 1
+    attn_bytes = B * L * S_HKV * 2 * S_D * 2 + 2 * B * S_HQ * S_D * 4
+    kv.free()
+    return {"workload": f"Qwen2.5-0.5B-shaped TTS CFG decode: B=2, {S_HQ}q/{S_HKV}kv d={S_D}, F16 cache at {S_L}, "
+                        f"{S_LAYERS} layers of RoPE + append + attention",
+            "eager_us_per_step": round(eager_us, 2), "graph_us_per_step": round(graph_us, 2),
+            "eager_us_per_layer": round(eager_us / S_LAYERS, 3), "graph_us_per_layer": round(graph_us / S_LAYERS, 3),
+            "attn_bytes_per_layer": attn_bytes, "steps": steps,
+            "timing": "HIP events around `steps` back-to-back steps; graph: one captured step replayed"}
+
+
 def cpu_baseline_prefill(torch, vva, vvo, kv, qr):
     """Oracle (ggml-order mode, all host cores) on layer 0: 1024 query rows spread over [0, 32k)."""
     rows = np.linspace(0, T_PREFILL - 1, 1024).astype(np.int32)
@@ -239,6 +358,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--decode-steps", type=int, default=512)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--extra", action="store_true",
+                    help="also report the chunked ASR prefill (64 x 512) and the 0.5B F16 decode step (eager and graph)")
     ap.add_argument("--only", choices=["prefill", "decode", "both", "copy"], default="both",
                     help="copy: a plain 1 GiB device-to-device copy, the reference for FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
@@ -305,6 +426,10 @@ def main() -> int:
             line["value"], line["unit"] = line["decode"]["value"], "GB/s"
             line["ms_per_step"] = line["decode"]["ms_per_step"]
             line["roofline"] = line["decode"]["roofline"]
+    if args.extra:
+        line["prefill_chunked"] = run_prefill_chunked(torch, vva, ctx, layers=2)
+        torch.cuda.empty_cache()
+        line["decode_small"] = run_decode_small(torch, vva, ctx, steps=200)
     ctx.close()
     print(json.dumps(line), flush=True)
     return 0

@@ -201,7 +201,9 @@ VVA_API int vva_supports(const vva_context* ctx, int head_dim, int n_q_heads, in
  * single-token calls on Q8_0 caches use the register-streamed decode kernel
  * instead of the LDS-streamed one.  Per context. */
 VVA_API vva_status vva_set_attn_path(vva_context* ctx, int path);
-/* Number of key splits used by the last decode call (0 if none). */
+/* Number of key splits used by the last attention call: per (sequence, kv
+ * head) for a single-token call, per row tile for a prefill; 0 for the row
+ * kernel.  Diagnostics for tests and benchmarks. */
 VVA_API int        vva_last_decode_splits(const vva_context* ctx);
 
 #ifdef __cplusplus

@@ -74,6 +74,7 @@ constexpr int kWaves = 4;
 constexpr int kRowsWG = kRowsWave * kWaves;
 constexpr int kStages = 4;         // LDS ring: tile j + 3 loads while tile j is computed
 constexpr int kMaxRestarts = 16;   // bound on key-loop restarts per workgroup
+constexpr int kMaxKeySplits = 32;  // key splits per row tile
 
 // buffer_load_dwordx4 ... lds: each lane's 16 bytes land at LDS address
 // m0 + 16 * lane.  Issued as inline asm so the compiler does not fence LDS
@@ -169,7 +170,7 @@ __device__ __forceinline__ const lds_char* lds_at(uint32_t addr) { return (const
 
 // EXPL: explicit F16 mask (otherwise implicit causal / length masking only).
 template <int D, int KT, bool EXPL>
-__global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a) {
+__global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a, float* __restrict__ ws, int n_ks) {
     using F = Frag<KT>;
     using QF = typename F::type;
     constexpr int DS = D / 16;                     // 16-dim MFMA steps of Q.K
@@ -198,7 +199,8 @@ __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a) {
     const int g = a.Hq / a.Hkv;
     const int nrows = a.T * g;
     const int n_rt = (nrows + kRowsWG - 1) / kRowsWG;
-    const int R0 = (n_rt - 1 - (int)blockIdx.x) * kRowsWG;    // heaviest tiles first
+    const int ks = (int)blockIdx.x % n_ks;                       // key split of the row tile
+    const int R0 = (n_rt - 1 - (int)blockIdx.x / n_ks) * kRowsWG;   // heaviest tiles first
     const int wr0 = R0 + w * kRowsWave;
     const int L = a.L[b], past = a.past[b];
     const bool causal = !EXPL && a.mask_mode == kMaskCausal;
@@ -206,7 +208,12 @@ __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a) {
     // key range of the workgroup and of this wave
     const int t_hi_wg = min(a.T - 1, (min(R0 + kRowsWG, nrows) - 1) / g);
     const int kend = causal ? min(L, past + t_hi_wg + 1) : L;
-    const int n_tiles = (kend + kBN - 1) / kBN;
+    // the workgroup's share of the row tile's key tiles: [j_lo, j_lo + n_tiles);
+    // tile j below is local, its first key kb0 + j * kBN
+    const int n_tiles_rt = (kend + kBN - 1) / kBN;
+    const int j_lo = (int)((int64_t)ks * n_tiles_rt / n_ks);
+    const int n_tiles = (int)((int64_t)(ks + 1) * n_tiles_rt / n_ks) - j_lo;
+    const int kb0 = j_lo * kBN;
     const bool wave_live = wr0 < nrows;
     const int t_lo_w = min(a.T - 1, wr0 / g);
     const int t_hi_w = min(a.T - 1, (min(wr0 + kRowsWave, nrows) - 1) / g);
@@ -219,8 +226,9 @@ __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a) {
     // write zeros to the junk kilobyte (every wave issues the same number
     // of loads per tile, with no branch)
     const uint32_t nbk = (uint32_t)a.k_nb_tok, nbv = (uint32_t)a.v_nb_tok;
-    const i32x4 krs = make_rsrc(a.k[b] + kvh * a.k_nb_head, (uint32_t)(L - 1) * nbk + 2 * D);
-    const i32x4 vrs = make_rsrc(a.v[b] + kvh * a.v_nb_head, (uint32_t)(L - 1) * nbv + 2 * D);
+    const int kl = max(L - kb0, 1);                           // rows from the split's first key
+    const i32x4 krs = make_rsrc(a.k[b] + kvh * a.k_nb_head + (int64_t)kb0 * nbk, (uint32_t)(kl - 1) * nbk + 2 * D);
+    const i32x4 vrs = make_rsrc(a.v[b] + kvh * a.v_nb_head + (int64_t)kb0 * nbv, (uint32_t)(kl - 1) * nbv + 2 * D);
     int koff[NIK], voff[NIV];
 #pragma unroll
     for (int i = 0; i < NIK; ++i) {
@@ -530,7 +538,7 @@ __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a) {
     };
     // all tiles before j_fast are seen whole by every row of the workgroup
     const int t_lo_wg = min(a.T - 1, R0 / g);
-    const int j_fast = EXPL ? 0 : min(n_tiles, (causal ? min(L, past + t_lo_wg + 1) : L) / kBN);
+    const int j_fast = EXPL ? 0 : max(0, min(n_tiles, (causal ? min(L, past + t_lo_wg + 1) : L) / kBN - j_lo));
 
     for (int restarts = 0;; ++restarts) {
         issue(0);
@@ -538,12 +546,15 @@ __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a) {
         issue(2);
         wait_vm_barrier<2 * NLD>();                             // tile 0 is in LDS
         if (!EXPL && restarts == 0 && n_tiles > 0) {
-            // m from half 0 of tile 0: key 0 is visible to every row
+            // m from half 0 of the first tile: visible to every row when it
+            // lies in the fully visible range (the single-split case: key 0);
+            // a row that cannot see it keeps m = -inf (exponent offset 0)
+            // and a restart raises m should a later p overflow f16
             const lds_char *ka, *va;
             bases(0, ka, va);
             f32x16 s0[2];
             s_half(ka, 0, s0);
-            mask_half(s0, 0, 0);
+            mask_half(s0, kb0, 0);
             half_max(s0, sl2, m);
         }
         int j = 0;
@@ -670,7 +681,7 @@ __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a) {
             const lds_char *ka, *va;
             bases(j, ka, va);
             bool flag = false;
-            if (j * kBN < kend_w) flag = slow_tile(ka, va, j * kBN, restarts) || overflow(restarts);
+            if (kb0 + j * kBN < kend_w) flag = slow_tile(ka, va, kb0 + j * kBN, restarts) || overflow(restarts);
             // end of tile j: publish the restart flags, wait for tile j + 1
             // (the loads of tiles j + 2 and j + 3 may still fly)
             if (barrier_flags(__any(flag), true)) {
@@ -684,7 +695,7 @@ __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a) {
         }
         j = jb;
         wait_vm_barrier<0>();                                   // no load may land in a stage after the restart
-        if (!EXPL && j * kBN < kend_w) {
+        if (!EXPL && kb0 + j * kBN < kend_w) {
             // raise m for the rows whose scores on tile j passed m + 15 (tile j
             // is still in its stage: tile j + 4 was never issued)
             const lds_char *ka, *va;
@@ -692,8 +703,8 @@ __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a) {
             f32x16 s[2][2];
             s_half(ka, 0, s[0]);
             s_half(ka, 1, s[1]);
-            mask_half(s[0], j * kBN, 0);
-            mask_half(s[1], j * kBN, 1);
+            mask_half(s[0], kb0 + j * kBN, 0);
+            mask_half(s[1], kb0 + j * kBN, 1);
             float mx0[2], mx1[2];
             half_max(s[0], sl2, mx0);
             half_max(s[1], sl2, mx1);
@@ -711,15 +722,30 @@ __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a) {
             for (int cb = 0; cb < 2; ++cb) o[dt][cb] = f32x16{};
     }
 
-    // ---- normalize and write (each lane owns one row per column block)
+    // ---- normalize and write (each lane owns one row per column block);
+    // with several key splits, write the split's partial instead: O
+    // unnormalized, and (exponent base, row sum) of the row
+    const int64_t nr_all = (int64_t)a.B * a.T * a.Hq;
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
         const int row = wr0 + cb * 32 + l32;
         const float lt = lsum[cb] + __shfl_xor(lsum[cb], 32, 64);
         if (row >= nrows) continue;
-        const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
         const int t = row / g, h = kvh * g + row % g;
-        float* orow = (float*)((char*)a.out + b * a.o_nb_b + t * a.o_nb_t + h * a.o_nb_h);
+        float* orow;
+        float inv = 1.0f;
+        if (n_ks == 1) {
+            inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+            orow = (float*)((char*)a.out + b * a.o_nb_b + t * a.o_nb_t + h * a.o_nb_h);
+        } else {
+            const int64_t rg = ((int64_t)b * a.T + t) * a.Hq + h;
+            orow = ws + ((int64_t)ks * nr_all + rg) * D;
+            if (half == 0) {
+                // p = 2^(s - base): base = m, or 0 while m = -inf; an empty row is -inf
+                const float base = m[cb] != -INFINITY ? m[cb] : (lt > 0.0f ? 0.0f : -INFINITY);
+                *(float2*)(ws + nr_all * D * n_ks + ((int64_t)ks * nr_all + rg) * 2) = make_float2(base, lt);
+            }
+        }
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
@@ -732,15 +758,51 @@ __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a) {
     }
 }
 
+// Combines the key splits of every query row: one thread per (row, 4 dims),
+// log-sum-exp over the n_ks partials (exp2 domain), normalized into out.
+template <int D>
+__global__ void __launch_bounds__(256) prefill_merge_kernel(AttnArgs a, const float* __restrict__ ws, int n_ks) {
+    const int64_t nr_all = (int64_t)a.B * a.T * a.Hq;
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t rg = idx / (D / 4);
+    const int d4 = (int)(idx % (D / 4));
+    if (rg >= nr_all) return;
+    const float* ml = ws + nr_all * D * n_ks;
+    float M = -INFINITY;
+    for (int k = 0; k < n_ks; ++k) M = fmaxf(M, ml[((int64_t)k * nr_all + rg) * 2]);
+    float den = 0.0f;
+    float4 num = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (M != -INFINITY) {
+        for (int k = 0; k < n_ks; ++k) {
+            const float2 e = *(const float2*)(ml + ((int64_t)k * nr_all + rg) * 2);
+            const float f = __builtin_amdgcn_exp2f(e.x - M);          // 0 for an empty split
+            const float4 v = *(const float4*)(ws + ((int64_t)k * nr_all + rg) * D + 4 * d4);
+            num.x = fmaf(v.x, f, num.x);
+            num.y = fmaf(v.y, f, num.y);
+            num.z = fmaf(v.z, f, num.z);
+            num.w = fmaf(v.w, f, num.w);
+            den = fmaf(e.y, f, den);
+        }
+    }
+    const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+    const int h = (int)(rg % a.Hq), t = (int)((rg / a.Hq) % a.T), b = (int)(rg / ((int64_t)a.Hq * a.T));
+    float* orow = (float*)((char*)a.out + b * a.o_nb_b + t * a.o_nb_t + h * a.o_nb_h);
+    *(float4*)(orow + 4 * d4) = make_float4(num.x * inv, num.y * inv, num.z * inv, num.w * inv);
+}
+
 template <int D, int KT>
-hipError_t launch_pf(const AttnArgs& a, hipStream_t s) {
+hipError_t launch_pf(const AttnArgs& a, float* ws, int n_ks, hipStream_t s) {
     const int g = a.Hq / a.Hkv;
     const int nrows = a.T * g;
-    dim3 grid((nrows + kRowsWG - 1) / kRowsWG, a.Hkv, a.B);
+    dim3 grid((nrows + kRowsWG - 1) / kRowsWG * n_ks, a.Hkv, a.B);
     if (a.mask_mode == kMaskExplicit)
-        hipLaunchKernelGGL((prefill_kernel<D, KT, true>), grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((prefill_kernel<D, KT, true>), grid, dim3(256), 0, s, a, ws, n_ks);
     else
-        hipLaunchKernelGGL((prefill_kernel<D, KT, false>), grid, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((prefill_kernel<D, KT, false>), grid, dim3(256), 0, s, a, ws, n_ks);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || n_ks == 1) return e;
+    const int64_t threads = (int64_t)a.B * a.T * a.Hq * (D / 4);
+    hipLaunchKernelGGL(prefill_merge_kernel<D>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, a, ws, n_ks);
     return hipGetLastError();
 }
 
@@ -767,11 +829,33 @@ bool prefill_supported(const AttnArgs& a) {
     return true;
 }
 
-hipError_t launch_prefill(const AttnArgs& a, hipStream_t s) {
+int prefill_plan(const AttnArgs& a, int n_cu) {
+    // Key splits per row tile: only when the row tiles alone leave CUs idle
+    // (a short chunk over a long past); about two workgroups per CU, each
+    // split at least 4 key tiles of the longest row tile.
+    const int g = a.Hq / a.Hkv;
+    const int64_t base = (int64_t)((a.T * g + kRowsWG - 1) / kRowsWG) * a.Hkv * a.B;
+    if (base >= n_cu) return 1;
+    int Lmax = 1;
+    for (int b = 0; b < a.B; ++b) Lmax = a.L[b] > Lmax ? a.L[b] : Lmax;
+    const int max_ks = ((Lmax + kBN - 1) / kBN) / 4;
+    int n_ks = (int)(2 * (int64_t)n_cu / base);
+    if (n_ks > max_ks) n_ks = max_ks;
+    if (n_ks > kMaxKeySplits) n_ks = kMaxKeySplits;
+    return n_ks < 1 ? 1 : n_ks;
+}
+
+size_t prefill_ws_bytes(const AttnArgs& a, int n_ks) {
+    return n_ks <= 1 ? 0 : (size_t)n_ks * a.B * a.T * a.Hq * (a.d + 2) * sizeof(float);
+}
+
+hipError_t launch_prefill(const AttnArgs& a, float* ws, int n_ks, hipStream_t s) {
     if (a.d == 64) {
-        return a.k_type == VVA_TYPE_F16 ? launch_pf<64, VVA_TYPE_F16>(a, s) : launch_pf<64, VVA_TYPE_BF16>(a, s);
+        return a.k_type == VVA_TYPE_F16 ? launch_pf<64, VVA_TYPE_F16>(a, ws, n_ks, s)
+                                        : launch_pf<64, VVA_TYPE_BF16>(a, ws, n_ks, s);
     }
-    return a.k_type == VVA_TYPE_F16 ? launch_pf<128, VVA_TYPE_F16>(a, s) : launch_pf<128, VVA_TYPE_BF16>(a, s);
+    return a.k_type == VVA_TYPE_F16 ? launch_pf<128, VVA_TYPE_F16>(a, ws, n_ks, s)
+                                    : launch_pf<128, VVA_TYPE_BF16>(a, ws, n_ks, s);
 }
 
 }  // namespace vva

@@ -155,8 +155,15 @@ vva_status run_attention(vva_context* ctx, AttnArgs& a) {
         return VVA_OK;
     }
     if (ctx->attn_path != 1 && a.T > 1 && prefill_supported(a)) {
-        e = launch_prefill(a, ctx->stream);
+        int n_ks = prefill_plan(a, ctx->n_cu);
+        if (const char* env = std::getenv("VVA_PREFILL_SPLITS")) n_ks = std::atoi(env) > 0 ? std::atoi(env) : 1;
+        if (n_ks > 1) {
+            vva_status st = ensure_ws(ctx, prefill_ws_bytes(a, n_ks));
+            if (st != VVA_OK) return st;
+        }
+        e = launch_prefill(a, ctx->ws, n_ks, ctx->stream);
         if (e != hipSuccess) return hip_fail(ctx, e, "prefill launch");
+        ctx->last_splits = n_ks;
         return VVA_OK;
     }
     e = launch_attn_rows(a, ctx->stream);

@@ -97,9 +97,13 @@ bool decode_stream_supported(const AttnArgs& a);
 // Key splits for one call: writes each split's length to *split_len.
 int decode_stream_plan(const AttnArgs& a, int n_cu, int* split_len);
 hipError_t launch_decode_stream(const AttnArgs& a, float* ws, int n_splits, int split_len, hipStream_t s);
-// MFMA flash prefill (F16 / BF16 caches).
-hipError_t launch_prefill(const AttnArgs& a, hipStream_t s);
+// MFMA flash prefill (F16 / BF16 caches).  n_ks > 1 splits each row
+// tile's keys over n_ks workgroups, with partials in ws
+// (prefill_ws_bytes) merged by a second kernel.
+hipError_t launch_prefill(const AttnArgs& a, float* ws, int n_ks, hipStream_t s);
 bool prefill_supported(const AttnArgs& a);
+int prefill_plan(const AttnArgs& a, int n_cu);
+size_t prefill_ws_bytes(const AttnArgs& a, int n_ks);
 
 }  // namespace vva
 
