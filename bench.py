@@ -16,6 +16,13 @@ Workloads (synthetic, seeded):
            x Hkv x 2 x 136 B) + f32 Q read + f32 O write; the whole-step rate
            also counts the RoPE + append traffic.
 
+  prefill_chunked  the ASR prefill as the reference runs it: 64 chunks of 512
+           tokens over a growing past, 7B heads (same FLOPs as the single
+           shot); reported beside the single-shot line.
+  decode_small  the 0.5B TTS CFG decode step (B = 2, 14 q / 2 kv heads,
+           d = 64, F16 caches at 1024, 24 layers), eager and as one captured
+           HIP graph per step.
+
 Prints one JSON line: `value` is the prefill throughput (TFLOP/s), `decode`
 holds the decode throughput (GB/s); each carries a roofline entry measured
 with HIP events around every attention launch on the library's stream.
@@ -358,8 +365,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--decode-steps", type=int, default=512)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--extra", action="store_true",
-                    help="also report the chunked ASR prefill (64 x 512) and the 0.5B F16 decode step (eager and graph)")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the chunked ASR prefill (64 x 512) and the 0.5B F16 decode step (eager and graph)")
     ap.add_argument("--only", choices=["prefill", "decode", "both", "copy"], default="both",
                     help="copy: a plain 1 GiB device-to-device copy, the reference for FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
@@ -426,7 +433,7 @@ def main() -> int:
             line["value"], line["unit"] = line["decode"]["value"], "GB/s"
             line["ms_per_step"] = line["decode"]["ms_per_step"]
             line["roofline"] = line["decode"]["roofline"]
-    if args.extra:
+    if not args.no_extra and args.only in ("prefill", "decode", "both"):
         line["prefill_chunked"] = run_prefill_chunked(torch, vva, ctx, layers=2)
         torch.cuda.empty_cache()
         line["decode_small"] = run_decode_small(torch, vva, ctx, steps=200)

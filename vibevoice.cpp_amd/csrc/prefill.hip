@@ -831,15 +831,17 @@ bool prefill_supported(const AttnArgs& a) {
 
 int prefill_plan(const AttnArgs& a, int n_cu) {
     // Key splits per row tile: only when the row tiles alone leave CUs idle
-    // (a short chunk over a long past); about two workgroups per CU, each
-    // split at least 4 key tiles of the longest row tile.
+    // (a short chunk over a long past); as many as keep every workgroup in
+    // one round on the CUs (a partial second round costs more than the
+    // idle CUs it fills), each split at least 4 key tiles of the longest row
+    // tile.
     const int g = a.Hq / a.Hkv;
     const int64_t base = (int64_t)((a.T * g + kRowsWG - 1) / kRowsWG) * a.Hkv * a.B;
     if (base >= n_cu) return 1;
     int Lmax = 1;
     for (int b = 0; b < a.B; ++b) Lmax = a.L[b] > Lmax ? a.L[b] : Lmax;
     const int max_ks = ((Lmax + kBN - 1) / kBN) / 4;
-    int n_ks = (int)(2 * (int64_t)n_cu / base);
+    int n_ks = (int)(n_cu / base);
     if (n_ks > max_ks) n_ks = max_ks;
     if (n_ks > kMaxKeySplits) n_ks = kMaxKeySplits;
     return n_ks < 1 ? 1 : n_ks;
