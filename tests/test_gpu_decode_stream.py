@@ -59,6 +59,8 @@ CASES = [
     (128, 16, 8, [1777], vva.F32, None),           # eight kv heads: one wave each
     (64, 14, 2, [3333, 1025], vva.F32, 21),        # 0.5B heads: 136-byte rows, unaligned splits
     (64, 8, 4, [999], vva.F16, None),
+    (64, 8, 1, [2222, 901], vva.F32, None),        # 0.5B-like d, one kv head: two key groups per wave
+    (64, 16, 8, [1500], vva.BF16, 9),              # d = 64, eight kv heads
     (128, 28, 4, [700, 700], vva.F32, 1),          # one split: output written directly
 ]
 

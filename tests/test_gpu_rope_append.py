@@ -111,3 +111,39 @@ def test_errors_are_reported_not_raised_in_native_code(ctx, torch_gpu):
     with pytest.raises(vva.VvaError):
         ctx.rope_append(kv, 3, q, k, k, pos, q)     # bad layer
     kv.free()
+
+
+@pytest.mark.parametrize("in_t,cache_t", [(vva.BF16, vva.F16), (vva.F32, vva.BF16), (vva.F16, vva.F32)])
+def test_vector_and_scalar_paths_agree_bit_for_bit(ctx, torch_gpu, in_t, cache_t):
+    """Rows on 16-byte boundaries take the vector path (8 pairs per lane), a
+    view 8 bytes off a boundary the scalar one; both compute the same fp32
+    operations, so Q and the cache bytes must be identical."""
+    torch = torch_gpu
+    d, Hq, Hkv, T, B = 128, 28, 4, 21, 2
+    rng = np.random.default_rng(17)
+    vals = [rng.standard_normal((B, T, H, d)) for H in (Hq, Hkv, Hkv)]
+    aligned = [to_gpu(torch, x, in_t) for x in vals]
+    eb = 4 if in_t == vva.F32 else 2
+    off = 8 // eb                                          # 8 bytes: off every 16-byte boundary
+    shifted = []
+    for x in aligned:
+        big = torch.zeros(x.shape[:-1] + (d + 8,), dtype=x.dtype, device="cuda")
+        big[..., off:off + d] = x
+        shifted.append(big[..., off:off + d])
+    assert shifted[0].data_ptr() % 16 == 8
+    pos = torch.tensor(np.array([[100 * b + t for t in range(T)] for b in range(B)], np.int32)).to("cuda")
+    kv = vva.KVCache(ctx, 2, Hkv, d, T + 8, B, cache_t)
+    outs = []
+    for layer, (q, k, v) in enumerate((aligned, shifted)):
+        for s in range(B):
+            kv.set_len(s, 0)
+        q_out = torch.empty((B, T, Hq, d), dtype=torch.float16, device="cuda")
+        ctx.rope_append(kv, layer, q, k, v, pos, q_out)
+        outs.append(q_out)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    for b in range(B):
+        a0, a1 = kv.download(0, b, T), kv.download(1, b, T)
+        np.testing.assert_array_equal(a0[0], a1[0])
+        np.testing.assert_array_equal(a0[1], a1[1])
+    kv.free()

@@ -20,7 +20,8 @@ Q8_BLOCK_BYTES = 34
 OK, ERR_GENERIC, ERR_INVALID_ARG, ERR_OOM, ERR_NOT_IMPLEMENTED, ERR_DEVICE = 0, -1, -2, -5, -6, -9
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "lib", "libvva.so")
+# VVA_LIB names another build of the library (same ABI), e.g. to compare kernel variants.
+LIB_PATH = os.environ.get("VVA_LIB") or os.path.join(_HERE, "lib", "libvva.so")
 
 # Symbols declared in include/vva.h (checked by the CPU test suite).
 EXPORTS = [
