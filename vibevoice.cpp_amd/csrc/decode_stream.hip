@@ -134,14 +134,21 @@ __device__ __forceinline__ h4 as_h4(uint32_t lo, uint32_t hi) {
 }
 __device__ __forceinline__ h4 cat_h4(h2 lo, h2 hi) { return h4{lo[0], lo[1], hi[0], hi[1]}; }
 
-// D: head dim (64 / 128); HKV: kv heads (1, 2, 4, 8), which fixes the token
-// row pitch, so every LDS offset inside a tile is a constant.
-template <int D, int HKV>
+// D: head dim (64 / 128); HKV: kv heads of the workgroup's tile (1, 2, 4,
+// 8), which fixes the row pitch in LDS, so every LDS offset inside a tile is
+// a constant; NHG: head groups of the cache row (the cache holds HKV * NHG kv
+// heads per token).  With NHG > 1 workgroup (split, b * NHG + group) gathers
+// its group's slice of every cache row (RB bytes, a multiple of 16, at
+// group * RB in a row of NHG * RB bytes): the split partials then cover HKV
+// kv heads over NHG times the keys, NHG times fewer of them.
+template <int D, int HKV, int NHG>
 __global__ void __launch_bounds__(kW * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
 decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split_len) {
     constexpr int NB = D / 32;                // Q8_0 blocks per head row
     constexpr int HB = NB * kQ8Bytes;         // bytes per head row
-    constexpr int RB = HKV * HB;              // bytes per token row (all kv heads)
+    constexpr int RB = HKV * HB;              // bytes per token row in LDS (the group's kv heads)
+    constexpr int RBM = NHG * RB;             // bytes per token row in the cache
+    static_assert(NHG == 1 || RB % 16 == 0, "16-byte pieces of a row slice");
     constexpr int TT = kTileOpBytes / RB;     // keys per tile
     constexpr int NPAIR = TT * HKV / 32;      // slot pairs (2 slots of 16 keys x 1 kv head) per tile
     constexpr int NSUB = NPAIR / kW;          // slot pairs per wave per tile
@@ -155,7 +162,8 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, n = lane & 15;
-    const int G = a.Hq / HKV;                 // query heads per kv head (<= 8)
+    const int G = a.Hq / (HKV * NHG);         // query heads per kv head (<= 8)
+    const int HQL = HKV * G;                  // the workgroup's query heads
     // The wave's two slots: kv heads 2 hp and 2 hp + 1 over the same 16 keys,
     // or (HKV = 1) the one kv head over two consecutive groups of 16 keys.
     // Column n of the MFMAs is query row n & 7 of slot n >> 3.
@@ -170,7 +178,8 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split
     const int sr = n >> 3, rr = n & 7;        // the lane's slot and query row in it
     const bool rvalid = rr < G;
     const int hq_row = slot_head(sr) * G + rr;
-    const int split = blockIdx.x, b = blockIdx.y;
+    const int split = blockIdx.x, b = blockIdx.y / NHG, hgrp = blockIdx.y % NHG;
+    const int hq0 = hgrp * HQL;               // first query head of the group
     const int L = a.L[b];
     const int j0 = min(L, split * split_len);
     const int j1 = min(L, j0 + split_len);
@@ -179,10 +188,11 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split
     // One raw buffer per operand: from the 16-byte boundary at or below the
     // split's first row to its last row.  delta = the row start's offset
     // from that boundary (a multiple of 4), also its offset in the LDS tile.
-    const char* kfirst = a.k[b] + (int64_t)j0 * RB;
-    const char* vfirst = a.v[b] + (int64_t)j0 * RB;
+    // (NHG > 1: the cache rows are 16-byte aligned, delta = 0)
+    const char* kfirst = a.k[b] + (int64_t)j0 * RBM;
+    const char* vfirst = a.v[b] + (int64_t)j0 * RBM;
     const int dk = (int)((uintptr_t)kfirst & 15), dv = (int)((uintptr_t)vfirst & 15);
-    const uint32_t span = (uint32_t)(j1 - j0) * (uint32_t)RB;
+    const uint32_t span = (uint32_t)(j1 - j0) * (uint32_t)RBM;
     const i32x4 krs = make_rsrc_sgpr(kfirst - dk, dk + span);
     const i32x4 vrs = make_rsrc_sgpr(vfirst - dv, dv + span);
     const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_char*)lds;
@@ -193,10 +203,19 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split
     // padding load (from past the range: zeros, no memory access) into the
     // junk kilobyte.  A tile past the last one loads nothing but zeros; the
     // 18th chunk of an operand is needed only when delta > 0.
+    // Byte offset, in the split's buffer, of this lane's 16 bytes of chunk c
+    // of tile 0: the tile is contiguous in the cache (NHG = 1), or the group's
+    // RB-byte slice of each of its rows (NHG > 1).  Tile t is t * TT rows on.
+    int loff[kOpLoads];
+#pragma unroll
+    for (int i = 0; i < kOpLoads; ++i) {
+        const int bt = (w + kW * i) * 1024 + lane * 16;
+        loff[i] = NHG == 1 ? bt : (bt / RB) * RBM + hgrp * RB + bt % RB;
+    }
     auto issue = [&](int t) {
         const bool live = t < n_tiles;
         const uint32_t st = lds0 + (uint32_t)(t & (kStages - 1)) * kStage;
-        const int tb = t * kTileOpBytes + lane * 16;
+        const int tb = t * TT * RBM;
 #pragma unroll
         for (int op = 0; op < 2; ++op)
 #pragma unroll
@@ -205,7 +224,7 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split
                 const bool have = c < kOpChunks;
                 const bool need = live && have && (c < kOpChunks - 1 || (op ? dv : dk) > 0);
                 const uint32_t dst = have ? st + op * kOpBytes + c * 1024 : lds0 + kJunk;
-                dma16<true>(op ? vrs : krs, dst, need ? tb + c * 1024 : kDead);
+                dma16<true>(op ? vrs : krs, dst, need ? tb + loff[i] : kDead);
             }
     };
 
@@ -219,7 +238,7 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split
     // (kW * 64)-th quarter block.
     const int eb = (int)type_elem_bytes(a.q_type);
     {
-        const i32x4 qrs = make_rsrc_sgpr(a.q + b * a.q_nb_b, (uint32_t)(a.Hq * D * eb));
+        const i32x4 qrs = make_rsrc_sgpr(a.q + b * a.q_nb_b + (int64_t)hq0 * D * eb, (uint32_t)(HQL * D * eb));
 #pragma unroll
         for (int i = 0; i < kQLoads; ++i) {
             const int c = i * kW + w;
@@ -234,7 +253,7 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split
     const char* qraw = lds + (kStages - 1) * kStage;
     uint32_t* qlds = (uint32_t*)(lds + (kStages - 1) * kStage + kQRawBytes);
     constexpr int QI = 1024 / (kW * 64);              // quarters per thread (Hq * NB <= 256)
-    const int nqi = a.Hq * NB * 4;
+    const int nqi = HQL * NB * 4;
 #pragma unroll
     for (int it = 0; it < QI; ++it) {
         if (it * kW * 64 >= nqi) break;               // uniform
@@ -546,10 +565,11 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split
     // rows: the waves of its head pair (HKV >= 2: row 8 (h & 1) + r) or all
     // waves and both slots (HKV = 1: rows r and 8 + r)
     constexpr int NREC = HKV >= 2 ? kW / HP : 2 * kW;
-    const int ntask = a.Hq * (D / 4);
+    const int ntask = HQL * (D / 4);
     for (int task = threadIdx.x; task < ntask; task += kW * 64) {
-        const int hq = task / (D / 4), d4 = task % (D / 4);
-        const int h = hq / G, r = hq % G;
+        const int hql = task / (D / 4), d4 = task % (D / 4);
+        const int hq = hq0 + hql;                    // global query head
+        const int h = hql / G, r = hql % G;
         float M = -INFINITY, den = 0.0f;
         float4 num = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
@@ -584,18 +604,36 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split
     }
 }
 
+// Head groups of the cache rows: d = 128 caches with 4 or 8 kv heads are
+// split into pairs (272-byte row slices) when every row is 16-byte aligned.
+int stream_groups(const AttnArgs& a) {
+    if (a.d != 128 || a.Hkv < 4) return 1;
+    for (int b = 0; b < a.B; ++b)
+        if (((uintptr_t)a.k[b] % 16) || ((uintptr_t)a.v[b] % 16)) return 1;
+    return a.Hkv / 2;
+}
+
 template <int D>
 hipError_t launch_ds(const AttnArgs& a, float* ws, int n_splits, int split_len, hipStream_t s) {
-    const dim3 grid(n_splits, a.B), block(kW * 64);
-    switch (a.Hkv) {
-#define VVA_DS(H) case H: hipLaunchKernelGGL((decode_stream_kernel<D, H>), grid, block, 0, s, a, ws, n_splits, split_len); break;
-        VVA_DS(1) VVA_DS(2) VVA_DS(4) VVA_DS(8)
-#undef VVA_DS
-        default: return hipErrorInvalidValue;
+    const int ng = stream_groups(a);
+    const dim3 grid(n_splits, a.B * ng), block(kW * 64);
+    auto finish = [&]() -> hipError_t {
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess || n_splits == 1) return e;
+        return launch_decode_merge(a, ws, n_splits, s);
+    };
+#define VVA_DS(H, NG) hipLaunchKernelGGL((decode_stream_kernel<D, H, NG>), grid, block, 0, s, a, ws, n_splits, split_len)
+    if constexpr (D == 128) {
+        if (ng == 2) { VVA_DS(2, 2); return finish(); }
+        if (ng == 4) { VVA_DS(2, 4); return finish(); }
     }
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess || n_splits == 1) return e;
-    return launch_decode_merge(a, ws, n_splits, s);
+    if (a.Hkv == 1) VVA_DS(1, 1);
+    else if (a.Hkv == 2) VVA_DS(2, 1);
+    else if (a.Hkv == 4) VVA_DS(4, 1);
+    else if (a.Hkv == 8) VVA_DS(8, 1);
+    else return hipErrorInvalidValue;
+#undef VVA_DS
+    return finish();
 }
 
 }  // namespace
@@ -630,10 +668,11 @@ int decode_stream_plan(const AttnArgs& a, int n_cu, int* split_len) {
     for (int b = 0; b < a.B; ++b) Lmax = a.L[b] > Lmax ? a.L[b] : Lmax;
     // one workgroup per CU over (split, sequence); at least two tiles' worth
     // of keys per split
-    int target = n_cu / a.B;
+    const int ng = stream_groups(a);
+    int target = n_cu / (a.B * ng);
     if (target < 1) target = 1;
     int sl = (Lmax + target - 1) / target;
-    const int min_len = 2 * kTileOpBytes / (int)((a.d / 32) * kQ8Bytes * a.Hkv);
+    const int min_len = 2 * kTileOpBytes / (int)((a.d / 32) * kQ8Bytes * (a.Hkv / ng));
     if (sl < min_len) sl = min_len;
     *split_len = sl;
     return (Lmax + sl - 1) / sl;
