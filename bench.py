@@ -60,7 +60,7 @@ S_D, S_HQ, S_HKV, S_LAYERS, S_L = 64, 14, 2, 24, 1024
 # WRITE_SIZE 1 GiB (x 1.0).  Counters and commands: profiles/prefill_kernel_7b_32k.md,
 # profiles/decode_stream_q8_0_7b_32k.md.
 TRAFFIC_PREFILL = (972114.1 * 2.0 + 458752.5 * 1.0) * 1024          # prefill_kernel<128,F16>
-TRAFFIC_DECODE = ((35157.3 + 1843.5) * 2.0 + (3808.0 + 28.0) * 1.0) * 1024   # stream + merge
+TRAFFIC_DECODE = ((35171.1 + 933.5) * 2.0 + (1904.0 + 28.0) * 1.0) * 1024    # stream + merge
 
 
 def prefill_flops_per_layer(T: int, past: int = 0) -> float:
@@ -420,7 +420,7 @@ def main() -> int:
             "ms_per_step": round(dec["ms_per_step"], 4), "dtype": "q8_0/f32",
             "roofline": {"bound": "hbm", "achieved": round(dec["attn_gbs"], 1), "peak": PEAK_HBM_GBS,
                          "unit": "GB/s", "frac": round(dec["attn_gbs"] / PEAK_HBM_GBS, 4), "traffic": TRAFFIC_DECODE,
-                         "kernel": "decode_stream_kernel<128,4> + decode_merge_kernel<128>",
+                         "kernel": "decode_stream_kernel<128,2,2> + decode_merge_kernel<128>",
                          "avg_launch_us": round(dec["attn_us"], 3), "bytes_per_launch": dec["bytes_per_layer"],
                          "timing": "HIP events around each step's 28 back-to-back attention calls",
                          "splits": dec["splits"]},

@@ -119,7 +119,7 @@ def test_vector_and_scalar_paths_agree_bit_for_bit(ctx, torch_gpu, in_t, cache_t
     view 8 bytes off a boundary the scalar one; both compute the same fp32
     operations, so Q and the cache bytes must be identical."""
     torch = torch_gpu
-    d, Hq, Hkv, T, B = 128, 28, 4, 21, 2
+    d, Hq, Hkv, T, B = 128, 28, 4, 40, 2           # T * B >= 64: the vector path when aligned
     rng = np.random.default_rng(17)
     vals = [rng.standard_normal((B, T, H, d)) for H in (Hq, Hkv, Hkv)]
     aligned = [to_gpu(torch, x, in_t) for x in vals]

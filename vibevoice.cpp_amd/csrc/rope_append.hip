@@ -234,7 +234,9 @@ hipError_t launch_rope_append(const RopeAppendArgs& a, hipStream_t s) {
     if (a.T <= 0 || a.B <= 0) return hipSuccess;
     const int items = ((a.do_q ? a.Hq : 0) + (a.do_kv ? 2 * a.Hkv : 0)) * (a.d / 2);
     if (items <= 0) return hipSuccess;
-    if (rope_vec_ok(a)) {
+    // the vector path for many tokens; a few-token call (decode) is launch-
+    // bound and spreads wider over the scalar kernel's item slices
+    if ((int64_t)a.T * a.B >= 64 && rope_vec_ok(a)) {
         const dim3 grid((a.T + kRopeTokens - 1) / kRopeTokens, a.B);
         if (a.d == 64)
             hipLaunchKernelGGL(rope_append_vec_kernel<32>, grid, dim3(256), 0, s, a);
