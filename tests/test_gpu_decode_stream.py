@@ -150,3 +150,66 @@ def test_stream_decode_consecutive_steps(ctx, torch_gpu):
             kv.set_len(s, L + 1)
     kv.free()
 
+
+
+def _decode_splits(ctx, torch, kv, Hq, seed, splits):
+    os.environ["VVA_DECODE_SPLITS"] = str(splits)
+    try:
+        return _decode(ctx, torch, kv, Hq, vva.F32, seed=seed)
+    finally:
+        del os.environ["VVA_DECODE_SPLITS"]
+
+
+@pytest.mark.parametrize("d,Hq,Hkv,lens", [
+    (128, 28, 4, [5000, 1234]),    # kv-head pairs gathered (272-byte slices), 64-key tiles
+    (64, 14, 2, [3001, 77]),       # whole 136-byte rows, 128-key tiles
+    (128, 8, 1, [2049, 2048]),     # 136-byte rows of one kv head
+])
+def test_stream_decode_round_robin_tiles(ctx, torch_gpu, d, Hq, Hkv, lens):
+    """Split s takes tiles s, s + n, s + 2n, ... of its sequence.  Forced
+    split counts from 1 (every tile in one workgroup) to far more splits than
+    tiles (splits with no key at all, the short sequence's only partial tile
+    in one split) give the oracle's result."""
+    torch = torch_gpu
+    kv = _cache(ctx, d, Hkv, lens, seed=d * Hkv + len(lens))
+    for splits in (1, 3, 7, 64, 200, 1024):
+        print(f"round-robin d={d} Hq={Hq} Hkv={Hkv} lens={lens} splits={splits}", flush=True)
+        q, out, used = _decode_splits(ctx, torch, kv, Hq, seed=splits, splits=splits)
+        assert used == splits
+        ref = oracle_attn(q, kv, 0, range(len(lens)), lens, 1, d ** -0.5)
+        assert_close(out, ref, MAX_TOL, MEAN_TOL, what=f"{splits} splits")
+    kv.free()
+
+
+def test_stream_decode_unaligned_window(ctx, torch_gpu):
+    """ggml_flash_attn_ext over a window of a Q8_0 cache that starts 5 rows in
+    (136-byte rows: 8 bytes past a 16-byte boundary), no mask: every tile is
+    loaded from the 16-byte boundary below it."""
+    torch = torch_gpu
+    d, Hq, Hkv, r0, L = 64, 14, 2, 5, 3001
+    kv = vva.KVCache(ctx, 1, Hkv, d, r0 + L + 8, 1, vva.Q8_0)
+    fill_cache(kv, [r0 + L], seed=99)
+    kview, vview = kv.views(0, 0)
+    for t_ in (kview, vview):
+        t_.data += r0 * t_.nb[2]
+        t_.ne[1], t_.ne[2] = t_.ne[2], t_.ne[1]        # ne = [d, L, Hkv, 1]
+        t_.nb[1], t_.nb[2] = t_.nb[2], t_.nb[1]
+        t_.ne[1] = L
+    assert (kview.data % 16) == 8
+    rng = np.random.default_rng(98)
+    q = to_gpu(torch, rng.standard_normal((1, 1, Hq, d)), vva.F32)
+    out = torch.full((1, 1, Hq, d), float("nan"), dtype=torch.float32, device="cuda")
+    kraw, vraw = kv.download(0, 0, r0 + L)
+    ref = vvo.attn(as_f32(torch, q), [kraw[r0:].reshape(-1)], [vraw[r0:].reshape(-1)], vva.Q8_0, vva.Q8_0,
+                   [L], n_kv_heads=Hkv, scale=d ** -0.5, mask_mode=vvo.MASK_NONE)
+    for splits in (5, 64):
+        print(f"unaligned window splits={splits}", flush=True)
+        os.environ["VVA_DECODE_SPLITS"] = str(splits)
+        try:
+            ctx.flash_attn_ext(q.permute(0, 2, 1, 3), None, None, out, d ** -0.5, k_view=kview, v_view=vview)
+            torch.cuda.synchronize()
+        finally:
+            del os.environ["VVA_DECODE_SPLITS"]
+        assert ctx.last_decode_splits() == splits
+        assert_close(as_f32(torch, out), ref, MAX_TOL, MEAN_TOL, what=f"unaligned window, {splits} splits")
+    kv.free()

@@ -5,14 +5,15 @@
 // on Q8_0 K/V.
 //
 // Streaming.  Every workgroup (4 waves, one per SIMD; one workgroup per CU)
-// takes a contiguous key range of one sequence and streams it through a
-// 4-stage LDS ring filled by buffer_load_dwordx4 ... lds (non-temporal: the
-// cache is read once), so three tiles (102 KB per CU) are on their way from
-// HBM while one is computed.  A tile is 512 (key, kv head, 32-dim block)
-// rows of the cache = 17,408 B of K plus the same of V, read as the cache
-// lays them out ([token][kv head][34-byte GGUF block]): one contiguous byte
-// range per operand, 1 KB per wave instruction.  The buffer ranges of a
-// split end at its last key, so chunks past it come back as zeros without a
+// takes every n_splits-th tile of one sequence (split s: tiles s, s +
+// n_splits, ...) and streams them through a 4-stage LDS ring filled by
+// buffer_load_dwordx4 ... lds (non-temporal: the cache is read once), so
+// three tiles (102 KB per CU) are on their way from HBM while one is
+// computed.  A tile is 512 (key, kv head, 32-dim block) rows of the cache =
+// 17,408 B of K plus the same of V, read as the cache lays them out
+// ([token][kv head][34-byte GGUF block]): one contiguous byte range per
+// operand, 1 KB per wave instruction.  The buffer ranges end at the
+// sequence's last key, so chunks past it come back as zeros without a
 // memory access.
 //
 // Arithmetic on the matrix cores.  With g <= 8 query heads per kv head, a
@@ -143,7 +144,7 @@ __device__ __forceinline__ h4 cat_h4(h2 lo, h2 hi) { return h4{lo[0], lo[1], hi[
 // kv heads over NHG times the keys, NHG times fewer of them.
 template <int D, int HKV, int NHG>
 __global__ void __launch_bounds__(kW * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
-decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split_len) {
+decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits) {
     constexpr int NB = D / 32;                // Q8_0 blocks per head row
     constexpr int HB = NB * kQ8Bytes;         // bytes per head row
     constexpr int RB = HKV * HB;              // bytes per token row in LDS (the group's kv heads)
@@ -181,18 +182,27 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split
     const int split = blockIdx.x, b = blockIdx.y / NHG, hgrp = blockIdx.y % NHG;
     const int hq0 = hgrp * HQL;               // first query head of the group
     const int L = a.L[b];
-    const int j0 = min(L, split * split_len);
-    const int j1 = min(L, j0 + split_len);
-    const int n_tiles = (j1 - j0 + TT - 1) / TT;
+    // Tiles are dealt round-robin: the split's tile t is tile split + t *
+    // n_splits of the sequence, so at any moment the workgroups of a sequence
+    // stream neighbouring tiles of the cache (measured 4 % faster than a
+    // contiguous key range per split).  Only the sequence's last tile can
+    // hold keys past L.
+    const int j1 = L;
+    const int all_tiles = (L + TT - 1) / TT;
+    const int n_tiles = split < all_tiles ? (all_tiles - split + n_splits - 1) / n_splits : 0;
+    const int n_full = L / TT;                // tiles without keys past L
+    const int n_whole = split < n_full ? (n_full - split + n_splits - 1) / n_splits : 0;
+    auto tile_key = [&](int t) { return (split + t * n_splits) * TT; };   // first key of tile t
 
     // One raw buffer per operand: from the 16-byte boundary at or below the
-    // split's first row to its last row.  delta = the row start's offset
-    // from that boundary (a multiple of 4), also its offset in the LDS tile.
-    // (NHG > 1: the cache rows are 16-byte aligned, delta = 0)
-    const char* kfirst = a.k[b] + (int64_t)j0 * RBM;
-    const char* vfirst = a.v[b] + (int64_t)j0 * RBM;
+    // sequence's row 0 to its row L - 1.  delta = row 0's offset from that
+    // boundary (a multiple of 4), also a tile's offset in its LDS stage
+    // (tiles start TT * RBM = 17,408 bytes apart).  (NHG > 1: the cache rows
+    // are 16-byte aligned, delta = 0)
+    const char* kfirst = a.k[b];
+    const char* vfirst = a.v[b];
     const int dk = (int)((uintptr_t)kfirst & 15), dv = (int)((uintptr_t)vfirst & 15);
-    const uint32_t span = (uint32_t)(j1 - j0) * (uint32_t)RBM;
+    const uint32_t span = (uint32_t)L * (uint32_t)RBM;
     const i32x4 krs = make_rsrc_sgpr(kfirst - dk, dk + span);
     const i32x4 vrs = make_rsrc_sgpr(vfirst - dv, dv + span);
     const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_char*)lds;
@@ -215,7 +225,7 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split
     auto issue = [&](int t) {
         const bool live = t < n_tiles;
         const uint32_t st = lds0 + (uint32_t)(t & (kStages - 1)) * kStage;
-        const int tb = t * TT * RBM;
+        const int tb = tile_key(t) * RBM;
 #pragma unroll
         for (int op = 0; op < 2; ++op)
 #pragma unroll
@@ -507,7 +517,7 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split
         wait_vm_barrier<(kStages - 2) * kLoads>();
         const char* kt = lds + (t & (kStages - 1)) * kStage + dk;
         const char* vt = lds + (t & (kStages - 1)) * kStage + kOpBytes + dv;
-        const int jt = j0 + t * TT;
+        const int jt = tile_key(t);
         PairOps ops[NSUB];
 #pragma unroll
         for (int u = 0; u < NSUB; ++u) read_pair(kt, vt, pair_key(u), ops[u]);
@@ -519,7 +529,7 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split
     // last can hold keys past its end (all tiles are checked under a mask).
     // Tiles go in pairs (pz -> pa, pa -> pz); an odd count ends with one
     // more tile into pa, whose P.V is the last.
-    const int n_plain = mrow != nullptr ? 0 : (j1 - j0) / TT;
+    const int n_plain = mrow != nullptr ? 0 : n_whole;
     int t = 0;
     for (; t + 1 < n_plain; t += 2) {
         tile(t, std::false_type{}, pz, pa);
@@ -614,7 +624,7 @@ int stream_groups(const AttnArgs& a) {
 }
 
 template <int D>
-hipError_t launch_ds(const AttnArgs& a, float* ws, int n_splits, int split_len, hipStream_t s) {
+hipError_t launch_ds(const AttnArgs& a, float* ws, int n_splits, hipStream_t s) {
     const int ng = stream_groups(a);
     const dim3 grid(n_splits, a.B * ng), block(kW * 64);
     auto finish = [&]() -> hipError_t {
@@ -622,7 +632,7 @@ hipError_t launch_ds(const AttnArgs& a, float* ws, int n_splits, int split_len, 
         if (e != hipSuccess || n_splits == 1) return e;
         return launch_decode_merge(a, ws, n_splits, s);
     };
-#define VVA_DS(H, NG) hipLaunchKernelGGL((decode_stream_kernel<D, H, NG>), grid, block, 0, s, a, ws, n_splits, split_len)
+#define VVA_DS(H, NG) hipLaunchKernelGGL((decode_stream_kernel<D, H, NG>), grid, block, 0, s, a, ws, n_splits)
     if constexpr (D == 128) {
         if (ng == 2) { VVA_DS(2, 2); return finish(); }
         if (ng == 4) { VVA_DS(2, 4); return finish(); }
@@ -663,24 +673,23 @@ bool decode_stream_supported(const AttnArgs& a) {
     return true;
 }
 
-int decode_stream_plan(const AttnArgs& a, int n_cu, int* split_len) {
+int decode_stream_plan(const AttnArgs& a, int n_cu) {
     int Lmax = 1;
     for (int b = 0; b < a.B; ++b) Lmax = a.L[b] > Lmax ? a.L[b] : Lmax;
-    // one workgroup per CU over (split, sequence); at least two tiles' worth
-    // of keys per split
+    // one workgroup per CU over (split, sequence, head group); at least two
+    // tiles' worth of keys per split
     const int ng = stream_groups(a);
     int target = n_cu / (a.B * ng);
     if (target < 1) target = 1;
     int sl = (Lmax + target - 1) / target;
     const int min_len = 2 * kTileOpBytes / (int)((a.d / 32) * kQ8Bytes * (a.Hkv / ng));
     if (sl < min_len) sl = min_len;
-    *split_len = sl;
     return (Lmax + sl - 1) / sl;
 }
 
-hipError_t launch_decode_stream(const AttnArgs& a, float* ws, int n_splits, int split_len, hipStream_t s) {
-    if (a.d == 64) return launch_ds<64>(a, ws, n_splits, split_len, s);
-    if (a.d == 128) return launch_ds<128>(a, ws, n_splits, split_len, s);
+hipError_t launch_decode_stream(const AttnArgs& a, float* ws, int n_splits, hipStream_t s) {
+    if (a.d == 64) return launch_ds<64>(a, ws, n_splits, s);
+    if (a.d == 128) return launch_ds<128>(a, ws, n_splits, s);
     return hipErrorInvalidValue;
 }
 

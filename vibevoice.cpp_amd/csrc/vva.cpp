@@ -6,6 +6,7 @@
 // message is kept per context, nothing aborts.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -116,14 +117,16 @@ vva_status run_attention(vva_context* ctx, AttnArgs& a) {
     hipError_t e;
     ctx->last_splits = 0;
     if (ctx->attn_path == 0 && a.T == 1 && decode_stream_supported(a)) {
-        int split_len = 0, wgs = ctx->n_cu;
+        int wgs = ctx->n_cu;
         if (const char* env = std::getenv("VVA_DECODE_WGS")) wgs = std::atoi(env);
-        const int n_splits = decode_stream_plan(a, wgs, &split_len);
+        int n_splits = decode_stream_plan(a, wgs);
+        // tests: any split count in [1, 1024]
+        if (const char* env = std::getenv("VVA_DECODE_SPLITS")) n_splits = std::min(1024, std::max(1, std::atoi(env)));
         if (n_splits > 1) {
             vva_status st = ensure_ws(ctx, (size_t)n_splits * a.B * a.Hq * (a.d + 2) * sizeof(float));
             if (st != VVA_OK) return st;
         }
-        e = launch_decode_stream(a, ctx->ws, n_splits, split_len, ctx->stream);
+        e = launch_decode_stream(a, ctx->ws, n_splits, ctx->stream);
         if (e != hipSuccess) return hip_fail(ctx, e, "decode launch");
         ctx->last_splits = n_splits;
         return VVA_OK;

@@ -94,9 +94,10 @@ hipError_t launch_decode_merge(const AttnArgs& a, const float* ws, int n_splits,
 // tiles of each split are DMA'd into a 4-stage LDS ring.  Partials use the
 // layout of launch_decode and are combined by launch_decode_merge.
 bool decode_stream_supported(const AttnArgs& a);
-// Key splits for one call: writes each split's length to *split_len.
-int decode_stream_plan(const AttnArgs& a, int n_cu, int* split_len);
-hipError_t launch_decode_stream(const AttnArgs& a, float* ws, int n_splits, int split_len, hipStream_t s);
+// Key splits for one call (workgroups per sequence and head group); split s
+// takes the sequence's tiles s, s + n_splits, s + 2 n_splits, ...
+int decode_stream_plan(const AttnArgs& a, int n_cu);
+hipError_t launch_decode_stream(const AttnArgs& a, float* ws, int n_splits, hipStream_t s);
 // MFMA flash prefill (F16 / BF16 caches).  n_ks > 1 splits each row
 // tile's keys over n_ks workgroups, with partials in ws
 // (prefill_ws_bytes) merged by a second kernel.
