@@ -571,45 +571,56 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits) {
     }
     __syncthreads();
 
-    // ---- per (query head, 4 dims): log-sum-exp over the records of its
+    // ---- per (query head, 8 dims): log-sum-exp over the records of its
     // rows: the waves of its head pair (HKV >= 2: row 8 (h & 1) + r) or all
-    // waves and both slots (HKV = 1: rows r and 8 + r)
+    // waves and both slots (HKV = 1: rows r and 8 + r).  Every record is
+    // read first (one LDS round trip), then weighed by exp2(m - M): a record
+    // with nothing visible has m = -inf, weight 0, and zero l and O.
     constexpr int NREC = HKV >= 2 ? kW / HP : 2 * kW;
-    const int ntask = HQL * (D / 4);
+    constexpr int D8 = D / 8;
+    const int ntask = HQL * D8;
     for (int task = threadIdx.x; task < ntask; task += kW * 64) {
-        const int hql = task / (D / 4), d4 = task % (D / 4);
+        const int hql = task / D8, d8 = task % D8;
         const int hq = hq0 + hql;                    // global query head
         const int h = hql / G, r = hql % G;
-        float M = -INFINITY, den = 0.0f;
-        float4 num = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        float mm[NREC], ll[NREC];
+        float4 v0[NREC], v1[NREC];
 #pragma unroll
         for (int k = 0; k < NREC; ++k) {
             const int ww = HKV >= 2 ? h / 2 + HP * k : k >> 1;
             const int nn = HKV >= 2 ? 8 * (h & 1) + r : 8 * (k & 1) + r;
             const float* rec = part + (ww * 16 + nn) * PS;
-            const float mm = rec[D];
-            if (mm == -INFINITY) continue;                  // nothing visible in this record
-            const float ll = rec[D + 1];
-            const float4 v = *(const float4*)(rec + 4 * d4);
-            const float mn = fmaxf(M, mm);
-            const float fa = __builtin_amdgcn_exp2f(M - mn);   // 0 while M = -inf
-            const float fb = __builtin_amdgcn_exp2f(mm - mn);
-            den = den * fa + ll * fb;
-            num.x = num.x * fa + v.x * fb;
-            num.y = num.y * fa + v.y * fb;
-            num.z = num.z * fa + v.z * fb;
-            num.w = num.w * fa + v.w * fb;
-            M = mn;
+            mm[k] = rec[D];
+            ll[k] = rec[D + 1];
+            v0[k] = *(const float4*)(rec + 8 * d8);
+            v1[k] = *(const float4*)(rec + 8 * d8 + 4);
+        }
+        float M = mm[0];
+#pragma unroll
+        for (int k = 1; k < NREC; ++k) M = fmaxf(M, mm[k]);
+        const float Mb = M == -INFINITY ? 0.0f : M;  // all records empty: every weight 0
+        float den = 0.0f;
+        float4 n0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), n1 = n0;
+#pragma unroll
+        for (int k = 0; k < NREC; ++k) {
+            const float f = __builtin_amdgcn_exp2f(mm[k] - Mb);
+            den = fmaf(ll[k], f, den);
+            n0.x = fmaf(v0[k].x, f, n0.x); n0.y = fmaf(v0[k].y, f, n0.y);
+            n0.z = fmaf(v0[k].z, f, n0.z); n0.w = fmaf(v0[k].w, f, n0.w);
+            n1.x = fmaf(v1[k].x, f, n1.x); n1.y = fmaf(v1[k].y, f, n1.y);
+            n1.z = fmaf(v1[k].z, f, n1.z); n1.w = fmaf(v1[k].w, f, n1.w);
         }
         if (n_splits == 1) {
             const float inv = den == 0.0f ? 0.0f : 1.0f / den;
-            float* orow = (float*)((char*)a.out + b * a.o_nb_b + hq * a.o_nb_h);
-            *(float4*)(orow + 4 * d4) = make_float4(num.x * inv, num.y * inv, num.z * inv, num.w * inv);
+            float* orow = (float*)((char*)a.out + b * a.o_nb_b + hq * a.o_nb_h) + 8 * d8;
+            *(float4*)orow = make_float4(n0.x * inv, n0.y * inv, n0.z * inv, n0.w * inv);
+            *(float4*)(orow + 4) = make_float4(n1.x * inv, n1.y * inv, n1.z * inv, n1.w * inv);
         } else {
             // partials: acc [B][Hq][n_splits][D], then (m, l) [B][Hq][n_splits][2]
             const size_t idx = ((size_t)b * a.Hq + hq) * n_splits + split;
-            *(float4*)(ws + idx * D + 4 * d4) = num;
-            if (d4 == 0) *(float2*)(ws + (size_t)a.B * a.Hq * n_splits * D + idx * 2) = make_float2(M, den);
+            *(float4*)(ws + idx * D + 8 * d8) = n0;
+            *(float4*)(ws + idx * D + 8 * d8 + 4) = n1;
+            if (d8 == 0) *(float2*)(ws + (size_t)a.B * a.Hq * n_splits * D + idx * 2) = make_float2(M, den);
         }
     }
 }
