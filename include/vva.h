@@ -61,7 +61,9 @@ typedef enum {
 /* ggml-shaped strided view of a device tensor.
  * ne[0] is the fastest dimension; nb[i] is the byte stride of dimension i.
  * For VVA_TYPE_Q8_0, ne[0] counts elements (a multiple of 32) and nb[0] is
- * the block size (34). */
+ * the block size (34).  Every ne[i] must be >= 1 and data non-NULL: a call
+ * with an empty tensor (e.g. zero new tokens) returns VVA_ERR_INVALID_ARG
+ * and enqueues nothing. */
 typedef struct {
     void*    data;
     int32_t  type;

@@ -173,3 +173,21 @@ def test_unsupported_options_are_rejected(ctx, torch_gpu):
                                         vva.ctypes.byref(vva.view(out)))
         ctx.check(st)
     assert e.value.status == vva.ERR_NOT_IMPLEMENTED
+
+
+def test_empty_calls_are_rejected(ctx, torch_gpu):
+    """Zero new tokens (ne[2] = 0; torch gives such tensors no storage) are
+    argument errors, not silent no-ops, and leave the cache length alone."""
+    torch = torch_gpu
+    d, Hq, Hkv = 64, 14, 2
+    kv = vva.KVCache(ctx, 1, Hkv, d, 16, 1, vva.F16)
+    q = torch.zeros((1, 0, Hq, d), dtype=torch.float32, device="cuda")
+    k = torch.zeros((1, 0, Hkv, d), dtype=torch.float32, device="cuda")
+    out = torch.zeros((1, 0, Hq, d), dtype=torch.float32, device="cuda")
+    pos = torch.zeros((0,), dtype=torch.int32, device="cuda")
+    for call in (lambda: ctx.rope_append(kv, 0, q, k, k, pos, q), lambda: ctx.attn(kv, 0, q, out, d ** -0.5)):
+        with pytest.raises(vva.VvaError) as err:
+            call()
+        assert err.value.status == vva.ERR_INVALID_ARG, err.value
+    assert kv.get_len(0) == 0
+    kv.free()
