@@ -62,6 +62,7 @@ CASES = [
     (64, 8, 1, [2222, 901], vva.F32, None),        # 0.5B-like d, one kv head: two key groups per wave
     (64, 16, 8, [1500], vva.BF16, 9),              # d = 64, eight kv heads
     (128, 28, 4, [700, 700], vva.F32, 1),          # one split: output written directly
+    (128, 28, 4, [32769, 32769], vva.F32, None),   # the 7B CFG decode at full size: 32768 past + 1
 ]
 
 
