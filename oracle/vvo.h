@@ -17,6 +17,12 @@
  *   VVO_GGML   — ggml CPU flash_attn_ext one-chunk order: per-key online
  *                softmax in fp32 with expf, F16 running V accumulator when V
  *                is F16, F32 otherwise.
+ *
+ * Parity unpinned: the bit-level ggml choices VVO_GGML encodes (the fp32
+ * theta recurrence of VVO_THETA_RECURRENCE, Q rounded to K's dot type, the
+ * F16 V accumulator, expf per key) cannot be checked against ggml itself,
+ * which is absent; the tests bound VVO_GGML against VVO_EXACT, which closed
+ * forms, invariants and fp64 brute force do pin.
  */
 #ifndef VVO_H
 #define VVO_H
