@@ -125,7 +125,7 @@ def run_prefill(torch, vva, ctx, steps: int, warmup: int):
 def run_decode(torch, vva, ctx, steps: int, warmup: int):
     rng = torch.Generator(device="cuda").manual_seed(4321)
     kv = vva.KVCache(ctx, LAYERS, HKV, D, L_DECODE + steps + warmup + 8, B_DECODE, vva.Q8_0)
-    # fill every layer's caches by appending 32768 random rows (RoPE'd K, raw V)
+    # fill every layer's caches by appending L_DECODE random rows (RoPE'd K, raw V)
     chunk = 8192
     for layer in range(LAYERS):
         for c0 in range(0, L_DECODE, chunk):
@@ -364,6 +364,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=3, help="timed prefill steps (28 layers each)")
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--decode-steps", type=int, default=512)
+    ap.add_argument("--decode-len", type=int, default=L_DECODE,
+                    help="cache positions before the first decode step (the metric is quoted at 32768)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the chunked ASR prefill (64 x 512) and the 0.5B F16 decode step (eager and graph)")
@@ -413,9 +415,10 @@ def main() -> int:
         kv.free()
         torch.cuda.empty_cache()
     if args.only in ("decode", "both"):
+        globals()["L_DECODE"] = args.decode_len      # read by run_decode
         dec, kvd = run_decode(torch, vva, ctx, args.decode_steps, max(1, args.warmup))
         line["decode"] = {
-            "workload": "Qwen2.5-7B-shaped CFG decode, batch 2, Q8_0 KV cache 32768 positions, 28 layers",
+            "workload": f"Qwen2.5-7B-shaped CFG decode, batch 2, Q8_0 KV cache {args.decode_len} positions, 28 layers",
             "value": round(dec["gbs"], 1), "unit": "GB/s", "steps": args.decode_steps,
             "ms_per_step": round(dec["ms_per_step"], 4), "dtype": "q8_0/f32",
             "roofline": {"bound": "hbm", "achieved": round(dec["attn_gbs"], 1), "peak": PEAK_HBM_GBS,
