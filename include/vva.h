@@ -82,7 +82,8 @@ typedef struct vva_kv      vva_kv;
  * (src/backend.cpp:64-133). */
 VVA_API vva_status  vva_create(int device, void* stream, vva_context** out);
 /* Destroys the context and every cache created on it that is still alive
- * (their handles become invalid). */
+ * (their handles become invalid: vva_kv_free ignores them, other calls
+ * return VVA_ERR_INVALID_ARG). */
 VVA_API void        vva_destroy(vva_context* ctx);
 /* Rebind the context to another stream (NULL = the null stream) after
  * waiting for the work already queued on the current one. */
@@ -114,7 +115,8 @@ typedef struct {
 /* Allocate (hipMalloc, one slab) and zero a cache.
  * Replaces ResidentKV::init (src/qwen2.cpp:207-229). */
 VVA_API vva_status vva_kv_create(vva_context* ctx, const vva_kv_desc* desc, vva_kv** out);
-/* Replaces ResidentKV::free (src/qwen2.cpp:231-244). */
+/* Replaces ResidentKV::free (src/qwen2.cpp:231-244).  A handle already
+ * released, by vva_kv_free or by vva_destroy of its context, is ignored. */
 VVA_API void       vva_kv_free(vva_kv* kv);
 /* Number of valid rows of sequence `seq` — ResidentKV::past_len
  * (src/qwen2.hpp:83), owned and advanced by the caller
@@ -207,6 +209,15 @@ VVA_API vva_status vva_set_attn_path(vva_context* ctx, int path);
  * head) for a single-token call, per row tile for a prefill; 0 for the row
  * kernel.  Diagnostics for tests and benchmarks. */
 VVA_API int        vva_last_decode_splits(const vva_context* ctx);
+/* Scheduling overrides for tests and benchmarks, per context; 0 restores the
+ * automatic choice:
+ *   decode_wgs      workgroups a single-token call is planned for (default:
+ *                   the device's CU count);
+ *   decode_splits   key splits per (sequence, head group) of the LDS-streamed
+ *                   Q8_0 decode, 1..1024;
+ *   prefill_splits  key splits per row tile of the MFMA prefill, 1..32.
+ * No counterpart in the reference (ggml chooses its own schedule). */
+VVA_API vva_status vva_set_schedule(vva_context* ctx, int decode_wgs, int decode_splits, int prefill_splits);
 
 #ifdef __cplusplus
 }

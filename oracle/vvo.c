@@ -295,8 +295,8 @@ static void attn_exact_one(const vvo_attn_args* a, int b, int t, int h,
 
 /* ggml CPU flash_attn_ext, one query row: keys in order, online softmax in
  * fp32 with expf; the running V sum is F16 when V is F16 (scaled and
- * accumulated with an f16 rounding per step), F32 otherwise; 1/S with S == 0
- * treated as 0. */
+ * accumulated with an f16 rounding per step), F32 otherwise (and always F32
+ * in VVO_GGML_F32ACC mode); 1/S with S == 0 treated as 0. */
 static void attn_ggml_one(const vvo_attn_args* a, int b, int t, int h,
                           float* vkq, uint16_t* vkq16, float* qr, uint8_t* q8, float* krow) {
     const int d = a->d, g = a->n_q_heads / a->n_kv_heads, kvh = h / g;
@@ -306,7 +306,7 @@ static void attn_ggml_one(const vvo_attn_args* a, int b, int t, int h,
     float* o = a->out + (((int64_t)b * a->T + t) * a->n_q_heads + h) * d;
     round_q(q, a->k_type, d, qr, q8);
     const int L = a->L[b];
-    const int v16 = a->v_type == VVO_F16;
+    const int v16 = a->v_type == VVO_F16 && a->mode == VVO_GGML;
     for (int i = 0; i < d; ++i) { vkq[i] = 0.0f; vkq16[i] = 0; }
     float S = 0.0f, M = -INFINITY;
     for (int j = 0; j < L; ++j) {

@@ -17,6 +17,11 @@
  *   VVO_GGML   — ggml CPU flash_attn_ext one-chunk order: per-key online
  *                softmax in fp32 with expf, F16 running V accumulator when V
  *                is F16, F32 otherwise.
+ *   VVO_GGML_F32ACC — the same order with an F32 running V accumulator for
+ *                every V type (identical to VVO_GGML unless V is F16): it
+ *                separates the F16 accumulator's own rounding, which grows
+ *                with the number of keys a row sees, from the rest of
+ *                ggml's order.
  *
  * Parity unpinned: the bit-level ggml choices VVO_GGML encodes (the fp32
  * theta recurrence of VVO_THETA_RECURRENCE, Q rounded to K's dot type, the
@@ -35,7 +40,7 @@ extern "C" {
 
 /* Type numbering = ggml_type (and vva_type). */
 enum { VVO_F32 = 0, VVO_F16 = 1, VVO_Q8_0 = 8, VVO_BF16 = 30 };
-enum { VVO_EXACT = 0, VVO_GGML = 1 };
+enum { VVO_EXACT = 0, VVO_GGML = 1, VVO_GGML_F32ACC = 2 };
 enum { VVO_MASK_NONE = 0, VVO_MASK_EXPLICIT = 1, VVO_MASK_CAUSAL = 2 };
 enum { VVO_THETA_RECURRENCE = 0, VVO_THETA_POW = 1 };
 
@@ -76,7 +81,7 @@ typedef struct {
     int32_t mask_mode;
     float   scale;
     float*  out;                     /* F32 [B][T][Hq][d] */
-    int32_t mode;                    /* VVO_EXACT / VVO_GGML */
+    int32_t mode;                    /* VVO_EXACT / VVO_GGML / VVO_GGML_F32ACC */
     int32_t q_round;                 /* 1: round Q to K's dot type first */
     int32_t n_threads;               /* <= 0: all cores */
     const int32_t* rows;             /* optional subset of flattened rows b*T+t (NULL: all) */

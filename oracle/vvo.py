@@ -12,7 +12,7 @@ import os
 import numpy as np
 
 F32, F16, Q8_0, BF16 = 0, 1, 8, 30
-EXACT, GGML = 0, 1
+EXACT, GGML, GGML_F32ACC = 0, 1, 2
 MASK_NONE, MASK_EXPLICIT, MASK_CAUSAL = 0, 1, 2
 THETA_RECURRENCE, THETA_POW = 0, 1
 MAX_B = 16

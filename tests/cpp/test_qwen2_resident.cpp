@@ -443,6 +443,24 @@ int test_supports(vva_context* ctx) {
     return 0;
 }
 
+// Destruction order: a ResidentKV that outlives its context.  vva_destroy
+// releases the cache; the ResidentKV's later free() (and its destructor)
+// must be no-ops, and calls with the released handle must fail cleanly.
+int test_order(vva_context*) {
+    vva_context* own = nullptr;
+    if (vva_create(0, nullptr, &own) != VVA_OK) return 70;
+    vva::ResidentKV kvs;
+    if (!kvs.init(own, 2, 64, 2, 32, 1, VVA_TYPE_F16)) return 71;
+    vva_kv* released = kvs.kv;
+    vva_destroy(own);
+    int32_t len = -1;
+    if (vva_kv_get_len(released, 0, &len) != VVA_ERR_INVALID_ARG) return 72;
+    kvs.free();                                              // handle already released: ignored
+    kvs.free();
+    printf("  context destroyed first: released handle refused, ResidentKV::free a no-op\n");
+    return 0;
+}
+
 struct Case {
     const char* name;
     std::function<int(vva_context*)> fn;
@@ -452,7 +470,8 @@ struct Case {
 
 int main(int argc, char** argv) {
     const std::vector<Case> cases = {{"chunks", test_chunks}, {"stack", test_stack}, {"cfg", test_cfg},
-                                     {"q8", test_q8},         {"errors", test_errors}, {"supports", test_supports}};
+                                     {"q8", test_q8},         {"errors", test_errors}, {"supports", test_supports},
+                                     {"order", test_order}};
     std::vector<std::string> want;
     for (int i = 1; i < argc; ++i) {
         if (!strcmp(argv[i], "--list")) {

@@ -7,14 +7,13 @@ path, 2e-3 max-abs / 1e-3 mean-abs for F16 / BF16 / Q8_0 caches.  Each case
 also reports the distance to the ggml-order oracle mode (per-key online
 softmax, F16 running sum for F16 V).
 """
-import os
 
 import numpy as np
 import pytest
 
 import vva
 import vvo
-from gpu_util import as_f32, assert_close, err_stats, fill_cache, oracle_attn, to_gpu
+from gpu_util import as_f32, assert_close, check_ggml_order, err_stats, fill_cache, oracle_attn, to_gpu
 
 pytestmark = pytest.mark.gpu
 
@@ -59,11 +58,9 @@ def test_decode_matches_oracle(ctx, torch_gpu, d, Hq, Hkv, t, lens, q_type):
     q, out = run_attn(ctx, torch, kv, 0, 1, B, Hq, q_type, seed=7)
     ref = oracle_attn(q, kv, 0, range(B), lens, 1, d ** -0.5)
     mx, mn = assert_close(out, ref, *TOL[t], what="decode vs exact")
-    gg = oracle_attn(q, kv, 0, range(B), lens, 1, d ** -0.5, mode=vvo.GGML)
-    gmx, gmn = err_stats(out, gg)
-    print(f"  vs exact max {mx:.2e} mean {mn:.2e}; vs ggml-order max {gmx:.2e} mean {gmn:.2e}; "
-          f"splits {ctx.last_decode_splits()}")
-    assert gmx <= TOL[t][0] and gmn <= TOL[t][1]
+    (gmx, gmn), (hmx, hmn) = check_ggml_order(out, q, kv, 0, range(B), lens, 1, d ** -0.5, *TOL[t], what="decode")
+    print(f"  vs exact max {mx:.2e} mean {mn:.2e}; vs ggml order max {gmx:.2e} mean {gmn:.2e} "
+          f"(F16 V sum: max {hmx:.2e} mean {hmn:.2e}); splits {ctx.last_decode_splits()}")
     kv.free()
 
 
@@ -75,12 +72,9 @@ def test_decode_split_count_does_not_change_result(ctx, torch_gpu):
     for s, n in enumerate(lens):
         kv.set_len(s, n - 1)
     outs = []
-    for wgs in ("2", "16", "100", "512"):
-        os.environ["VVA_DECODE_WGS"] = wgs
-        try:
+    for wgs in (2, 16, 100, 512):
+        with ctx.schedule(decode_wgs=wgs):
             _, out = run_attn(ctx, torch, kv, 0, 1, 2, 28, vva.F32, seed=9)
-        finally:
-            del os.environ["VVA_DECODE_WGS"]
         outs.append((ctx.last_decode_splits(), out))
     assert len({s for s, _ in outs}) == 4, [s for s, _ in outs]
     # each split has its own running max, so the f16 p * v products (2^-12

@@ -9,8 +9,6 @@ both head dims, splits whose first row is not 16-byte aligned in memory,
 splits past a short sequence's end, explicit masks, each Q type, and the
 register-streamed kernel (decode.hip) on the same bytes.
 """
-import os
-
 import numpy as np
 import pytest
 
@@ -23,21 +21,16 @@ pytestmark = pytest.mark.gpu
 MAX_TOL, MEAN_TOL = 2e-3, 1e-3
 
 
-def _decode(ctx, torch, kv, Hq, q_type, seed, mask=None, wgs=None):
+def _decode(ctx, torch, kv, Hq, q_type, seed, mask=None, wgs=None, splits=None, q_scale=1.0):
     B = kv.n_seq
     rng = np.random.default_rng(seed)
     d = kv.head_dim
-    q = to_gpu(torch, rng.standard_normal((B, 1, Hq, d)), q_type)
+    q = to_gpu(torch, rng.standard_normal((B, 1, Hq, d)) * q_scale, q_type)
     out = torch.full((B, 1, Hq, d), float("nan"), dtype=torch.float32, device="cuda")
     mask_t = None if mask is None else torch.from_numpy(mask.view(np.float16)).to("cuda")
-    if wgs is not None:
-        os.environ["VVA_DECODE_WGS"] = str(wgs)
-    try:
+    with ctx.schedule(decode_wgs=wgs or 0, decode_splits=splits or 0):
         ctx.attn(kv, 0, q, out, d ** -0.5, mask=mask_t)
         torch.cuda.synchronize()
-    finally:
-        if wgs is not None:
-            del os.environ["VVA_DECODE_WGS"]
     return as_f32(torch, q), as_f32(torch, out), ctx.last_decode_splits()
 
 
@@ -154,11 +147,7 @@ def test_stream_decode_consecutive_steps(ctx, torch_gpu):
 
 
 def _decode_splits(ctx, torch, kv, Hq, seed, splits):
-    os.environ["VVA_DECODE_SPLITS"] = str(splits)
-    try:
-        return _decode(ctx, torch, kv, Hq, vva.F32, seed=seed)
-    finally:
-        del os.environ["VVA_DECODE_SPLITS"]
+    return _decode(ctx, torch, kv, Hq, vva.F32, seed=seed, splits=splits)
 
 
 @pytest.mark.parametrize("d,Hq,Hkv,lens", [
@@ -205,12 +194,89 @@ def test_stream_decode_unaligned_window(ctx, torch_gpu):
                    [L], n_kv_heads=Hkv, scale=d ** -0.5, mask_mode=vvo.MASK_NONE)
     for splits in (5, 64):
         print(f"unaligned window splits={splits}", flush=True)
-        os.environ["VVA_DECODE_SPLITS"] = str(splits)
-        try:
+        with ctx.schedule(decode_splits=splits):
             ctx.flash_attn_ext(q.permute(0, 2, 1, 3), None, None, out, d ** -0.5, k_view=kview, v_view=vview)
             torch.cuda.synchronize()
-        finally:
-            del os.environ["VVA_DECODE_SPLITS"]
         assert ctx.last_decode_splits() == splits
         assert_close(as_f32(torch, out), ref, MAX_TOL, MEAN_TOL, what=f"unaligned window, {splits} splits")
+    kv.free()
+
+
+def _tile_keys(d, Hkv):
+    """Keys per LDS tile of the streamed kernel: 17,408 bytes of one operand
+    over the kv heads a workgroup takes (a pair of them for d = 128 caches
+    with 4 or 8 kv heads)."""
+    heads = 2 if (d == 128 and Hkv >= 4) else Hkv
+    return 17408 // (heads * (d // 32) * 34)
+
+
+@pytest.mark.parametrize("d,Hq,Hkv,L", [
+    (64, 14, 2, 4097),     # 0.5B heads: 128-key tiles, two slot pairs per wave per tile
+    (64, 8, 1, 6001),      # one kv head: 256-key tiles, two slot pairs per wave per tile
+    (128, 28, 4, 8193),    # 7B heads: 64-key tiles, one slot pair per wave per tile
+])
+def test_stream_decode_peaked_scores(ctx, torch_gpu, d, Hq, Hkv, L):
+    """Peaked attention, where a running-max raise inside a tile is certain.
+
+    Q is N(0,1) * 4 (scores spread ~4 nats), and in every 3rd tile a key is
+    planted at 80 % of the tile (for d = 64, in the second slot pair of its
+    wave) whose score for the first query head of each group is 23-27 nats,
+    about 10 nats above every random score.  The split that meets it raises
+    its running max after the tile's first slot pair has formed its p, the
+    case where p formed on the old base must be rescaled too.  Checked
+    against the ggml-order oracle (Q quantized to Q8_0 per block, as ggml
+    does for Q8_0 K: the peaked softmax amplifies the Q rounding, so the
+    exact-Q oracle is reported only) for several split counts, and against
+    the register-streamed kernel on the same bytes."""
+    torch = torch_gpu
+    G = Hq // Hkv
+    B = 2
+    kv = _cache(ctx, d, Hkv, [L, L - 500], seed=d * 7 + Hkv)
+    rng = np.random.default_rng(2024 + d + Hkv)
+    q = (rng.standard_normal((B, 1, Hq, d)) * 4.0).astype(np.float32)
+    TT = _tile_keys(d, Hkv)
+    planted = 0
+    for b in range(B):
+        Lb = L if b == 0 else L - 500
+        for t in range(0, (Lb - 1) // TT, 3):
+            j = t * TT + (4 * TT) // 5
+            if j >= Lb - 1:
+                break
+            target = 23.0 + 4.0 * rng.random()            # nats, for query head h * G
+            k_row = np.empty((1, Hkv, d), np.float32)
+            for h in range(Hkv):
+                q0 = q[b, 0, h * G]
+                k_row[0, h] = q0 * (target / (d ** -0.5 * float(q0 @ q0)))
+            v_row = rng.standard_normal((1, Hkv, d)).astype(np.float32)
+            kv.upload(0, b, j, k_row, v_row)
+            planted += 1
+    assert planted >= 6
+    qg = torch.from_numpy(q).cuda()
+    ggml_ref = None
+    outs = {}
+    for splits in (0, 3, 17, 64):
+        out = torch.full((B, 1, Hq, d), float("nan"), dtype=torch.float32, device="cuda")
+        with ctx.schedule(decode_splits=splits):
+            ctx.attn(kv, 0, qg, out, d ** -0.5)
+            torch.cuda.synchronize()
+        used = ctx.last_decode_splits()
+        o = as_f32(torch, out)
+        if ggml_ref is None:
+            ggml_ref = oracle_attn(q, kv, 0, range(B), [L, L - 500], 1, d ** -0.5, mode=vvo.GGML)
+            exact = oracle_attn(q, kv, 0, range(B), [L, L - 500], 1, d ** -0.5)
+            emx, emn = err_stats(o, exact)
+            print(f"  vs exact-Q oracle (reported): max {emx:.2e} mean {emn:.2e}")
+        mx, mn = assert_close(o, ggml_ref, MAX_TOL, MEAN_TOL, what=f"peaked decode, {used} splits vs ggml-order")
+        print(f"peaked d={d} Hq={Hq} Hkv={Hkv} L={L} planted={planted} splits={used}: max {mx:.2e} mean {mn:.2e}",
+              flush=True)
+        outs[used] = o
+    ctx.set_attn_path(2)
+    try:
+        out = torch.full((B, 1, Hq, d), float("nan"), dtype=torch.float32, device="cuda")
+        ctx.attn(kv, 0, qg, out, d ** -0.5)
+        torch.cuda.synchronize()
+    finally:
+        ctx.set_attn_path(0)
+    reg = as_f32(torch, out)
+    assert_close(reg, ggml_ref, MAX_TOL, MEAN_TOL, what="peaked decode, register kernel vs ggml-order")
     kv.free()

@@ -11,7 +11,9 @@ Checks, each independent of the oracle's code path:
     single-shot (tests/test_qwen2_resident.cpp paths B-D), decode equals the
     last prefill row, an explicit causal mask equals the implicit one, a row
     with no visible key is 0;
-  * the ggml-order mode stays within the path's tolerances of the exact mode.
+  * the ggml-order mode stays within the path's tolerances of the exact mode,
+    and its F32-accumulator variant differs from it only through the F16
+    running V sum.
 """
 import os
 
@@ -103,6 +105,32 @@ def test_ggml_mode_within_tolerance_of_exact(vvo, ktype, tol):
     ex = vvo.attn(q, [kraw], [vraw], t, t, [L], n_kv_heads=Hkv, scale=d ** -0.5, mode=vvo.EXACT)
     gg = vvo.attn(q, [kraw], [vraw], t, t, [L], n_kv_heads=Hkv, scale=d ** -0.5, mode=vvo.GGML)
     assert np.abs(ex - gg).max() < tol
+
+
+@pytest.mark.parametrize("ktype", ["f32", "f16", "bf16", "q8_0"])
+def test_ggml_f32acc_mode_isolates_the_f16_accumulator(vvo, ktype):
+    """GGML_F32ACC is ggml's order with an F32 running V sum.  It equals GGML
+    bit for bit unless V is F16; with F16 V it sits within fp32 rounding of
+    the exact mode while GGML (F16 running sum) is far further away, so the
+    two modes differ by the F16 accumulator and nothing else."""
+    rng = np.random.default_rng(23)
+    Hq, Hkv, d, T, past = 14, 2, 64, 4, 700
+    t = TYPES[ktype]
+    L = past + T
+    q = rng.standard_normal((1, T, Hq, d)).astype(np.float32)
+    kraw, _ = make_cache(vvo, rng.standard_normal((L, Hkv, d)).astype(np.float32), t)
+    vraw, _ = make_cache(vvo, rng.standard_normal((L, Hkv, d)).astype(np.float32), t)
+    args = dict(n_kv_heads=Hkv, scale=d ** -0.5)
+    ex = vvo.attn(q, [kraw], [vraw], t, t, [L], mode=vvo.EXACT, **args)
+    gg = vvo.attn(q, [kraw], [vraw], t, t, [L], mode=vvo.GGML, **args)
+    g32 = vvo.attn(q, [kraw], [vraw], t, t, [L], mode=vvo.GGML_F32ACC, **args)
+    if ktype != "f16":
+        assert np.array_equal(gg, g32)
+    else:
+        e32 = np.abs(g32 - ex).max()
+        e16 = np.abs(gg - ex).max()
+        assert e32 < 2e-5, e32
+        assert e16 > 20 * e32, (e16, e32)
 
 
 def _rand_case(vvo, rng, T, past, Hq=4, Hkv=2, d=32, t=0):

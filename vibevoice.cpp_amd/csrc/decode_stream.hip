@@ -408,13 +408,13 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits) {
             }
         }
     };
-    // Scores and softmax of one slot pair (keys kb .. of the tile at key jt)
-    // from its operands, with the P.V of the previous tile's pair (pend;
-    // zeros before the first tile) in the same instruction stream: the two
-    // are independent until a rescale, which comes after both.  The pair's
-    // own P.V operands replace pend.  CHECK: the group may hold keys past the
-    // split or the caller passed a mask.
-    auto group = [&](const PairOps& o, int kb, int jt, auto check, const PendingPV& prev, PendingPV& cur) {
+    // Scores of one slot pair (keys kb .. of the tile at key jt) from its
+    // operands, with the P.V of the previous tile's pair (prev; zeros before
+    // the first tile) in the same instruction stream: the two are
+    // independent.  The pair's V codes go to cur.  CHECK: the group may hold
+    // keys past the split or the caller passed a mask.
+    auto group_scores = [&](const PairOps& o, int kb, int jt, auto check, const PendingPV& prev, PendingPV& cur,
+                            float (&sc)[4]) {
         constexpr bool CHECK = decltype(check)::value;
         pv(prev);
         // ---- scores: per block, two block-diagonal halves into one sum
@@ -438,7 +438,6 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits) {
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int bb = 0; bb < NB; ++bb) cur.vc[s][i][bb] = o.vc[s][i][bb];
-        float sc[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             float x = 0.0f;
@@ -462,10 +461,12 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits) {
                 sc[i] = live ? sc[i] : -INFINITY;
             }
         }
-
-        // ---- online softmax of row n, running max raised lazily (after
-        // the previous pair's P.V has gone into acc)
-        const float smax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+    };
+    // Running max of row n, raised lazily to the row's max over smax (the
+    // lane's scores of every slot pair of the tile).  Called once per tile,
+    // after every pending P.V has gone into acc and before any of the tile's
+    // P' is formed, so acc and l are the only quantities on the old base.
+    auto rescale = [&](float smax) {
         if (__any(smax > m + kLazy)) {
             const float cm = max_swap32(max_swap16(smax));
             if (cm > m + kLazy) {
@@ -479,6 +480,9 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits) {
                 mb = cm;
             }
         }
+    };
+    // p = 2^(s - mb) of one slot pair, its row sums, and its P' = p * d_v.
+    auto group_probs = [&](const PairOps& o, const float (&sc)[4], PendingPV& cur) {
         float p[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(sc[i] - mb);   // 0 when masked
@@ -522,8 +526,19 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits) {
 #pragma unroll
         for (int u = 0; u < NSUB; ++u) read_pair(kt, vt, pair_key(u), ops[u]);
         issue(t + kStages - 1);
+        // every pending P.V into acc and every score of the tile first, then
+        // one rescale decision, then the tile's P' on the final base: with
+        // NSUB > 1 (d = 64) a raise decided per slot pair would leave P'
+        // formed on the old base unscaled
+        float sc[NSUB][4];
 #pragma unroll
-        for (int u = 0; u < NSUB; ++u) group(ops[u], pair_key(u), jt, check, prev[u], cur[u]);
+        for (int u = 0; u < NSUB; ++u) group_scores(ops[u], pair_key(u), jt, check, prev[u], cur[u], sc[u]);
+        float smax = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < NSUB; ++u) smax = fmaxf(smax, fmaxf(fmaxf(sc[u][0], sc[u][1]), fmaxf(sc[u][2], sc[u][3])));
+        rescale(smax);
+#pragma unroll
+        for (int u = 0; u < NSUB; ++u) group_probs(ops[u], sc[u], cur[u]);
     };
     // tiles whose keys all lie inside the split run without checks; only the
     // last can hold keys past its end (all tiles are checked under a mask).

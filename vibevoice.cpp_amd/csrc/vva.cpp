@@ -12,6 +12,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <set>
 #include <string>
 #include <vector>
@@ -27,8 +28,14 @@ struct vva_context {
     int n_cu = 256;
     int attn_path = 0;
     int last_splits = 0;
-    float* ws = nullptr;                 // decode split partials
+    // scheduling overrides (vva_set_schedule); 0 = automatic
+    int sched_decode_wgs = 0, sched_decode_splits = 0, sched_prefill_splits = 0;
+    float* ws = nullptr;                 // split partials (decode and key-split prefill)
     size_t ws_bytes = 0;
+    // Workspaces outgrown by a later call.  A kernel already enqueued, or a
+    // HIP graph captured earlier, may still hold their address, so they stay
+    // allocated until vva_destroy.
+    std::vector<float*> ws_retired;
     std::set<vva_kv*> caches;            // released by vva_destroy if still alive
 };
 
@@ -45,6 +52,17 @@ struct vva_kv {
 namespace {
 
 thread_local std::string g_create_err;
+
+// Every live cache handle of every context.  vva_kv_free of a handle that is
+// not here (already freed, or released by vva_destroy of its context) does
+// nothing, so a caller that destroys the context first cannot double-free.
+std::mutex g_kv_mu;
+std::set<const vva_kv*> g_kv_live;
+
+bool kv_live(const vva_kv* kv) {
+    std::lock_guard<std::mutex> lk(g_kv_mu);
+    return g_kv_live.count(kv) != 0;
+}
 
 struct DeviceGuard {
     int prev = -1;
@@ -97,17 +115,24 @@ vva_status check_tensor(vva_context* ctx, const vva_tensor* t, const char* name)
     return VVA_OK;
 }
 
+// Grows the context's split workspace to at least `bytes`.  Growing
+// allocates, which a stream under HIP graph capture must not do: such a call
+// fails with VVA_ERR_INVALID_ARG (run one call of the largest shape before
+// capturing).  The outgrown workspace is retired, not freed (see
+// vva_context::ws_retired).
 vva_status ensure_ws(vva_context* ctx, size_t bytes) {
     if (bytes <= ctx->ws_bytes) return VVA_OK;
-    if (ctx->ws) {
-        (void)hipStreamSynchronize(ctx->stream);
-        (void)hipFree(ctx->ws);
-        ctx->ws = nullptr;
-        ctx->ws_bytes = 0;
-    }
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(ctx->stream, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone)
+        return fail(ctx, VVA_ERR_INVALID_ARG,
+                    "split workspace must grow to %zu bytes during stream capture; run one call of this "
+                    "shape before capturing", bytes);
     size_t sz = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
-    hipError_t e = hipMalloc(&ctx->ws, sz);
-    if (e != hipSuccess) return hip_fail(ctx, e, "hipMalloc(decode workspace)");
+    float* p = nullptr;
+    hipError_t e = hipMalloc(&p, sz);
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipMalloc(split workspace)");
+    if (ctx->ws) ctx->ws_retired.push_back(ctx->ws);
+    ctx->ws = p;
     ctx->ws_bytes = sz;
     return VVA_OK;
 }
@@ -117,11 +142,9 @@ vva_status run_attention(vva_context* ctx, AttnArgs& a) {
     hipError_t e;
     ctx->last_splits = 0;
     if (ctx->attn_path == 0 && a.T == 1 && decode_stream_supported(a)) {
-        int wgs = ctx->n_cu;
-        if (const char* env = std::getenv("VVA_DECODE_WGS")) wgs = std::atoi(env);
+        const int wgs = ctx->sched_decode_wgs > 0 ? ctx->sched_decode_wgs : ctx->n_cu;
         int n_splits = decode_stream_plan(a, wgs);
-        // tests: any split count in [1, 1024]
-        if (const char* env = std::getenv("VVA_DECODE_SPLITS")) n_splits = std::min(1024, std::max(1, std::atoi(env)));
+        if (ctx->sched_decode_splits > 0) n_splits = ctx->sched_decode_splits;
         if (n_splits > 1) {
             vva_status st = ensure_ws(ctx, (size_t)n_splits * a.B * a.Hq * (a.d + 2) * sizeof(float));
             if (st != VVA_OK) return st;
@@ -138,12 +161,9 @@ vva_status run_attention(vva_context* ctx, AttnArgs& a) {
         // about one workgroup per CU over (split, sequence); each of the
         // nw / Hkv waves of a kv head takes at least 32 keys
         const int R = nw / a.Hkv;
-        int target = ctx->n_cu / a.B;
-        if (const char* env = std::getenv("VVA_DECODE_WGS")) target = std::atoi(env) / a.B;
+        int target = (ctx->sched_decode_wgs > 0 ? ctx->sched_decode_wgs : ctx->n_cu) / a.B;
         if (target < 1) target = 1;
-        int min_sub = 32;
-        if (const char* env = std::getenv("VVA_DECODE_MIN_SUB")) min_sub = std::atoi(env);
-        if (min_sub < 1) min_sub = 1;
+        constexpr int min_sub = 32;
         int sub_len = (Lmax + target * R - 1) / (target * R);
         if (sub_len < min_sub) sub_len = min_sub;
         const int split_len = sub_len * R;
@@ -159,7 +179,7 @@ vva_status run_attention(vva_context* ctx, AttnArgs& a) {
     }
     if (ctx->attn_path != 1 && a.T > 1 && prefill_supported(a)) {
         int n_ks = prefill_plan(a, ctx->n_cu);
-        if (const char* env = std::getenv("VVA_PREFILL_SPLITS")) n_ks = std::atoi(env) > 0 ? std::atoi(env) : 1;
+        if (ctx->sched_prefill_splits > 0) n_ks = ctx->sched_prefill_splits;
         if (n_ks > 1) {
             vva_status st = ensure_ws(ctx, prefill_ws_bytes(a, n_ks));
             if (st != VVA_OK) return st;
@@ -222,12 +242,17 @@ extern "C" void vva_destroy(vva_context* ctx) {
     if (!ctx) return;
     DeviceGuard g(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    {
+        std::lock_guard<std::mutex> lk(g_kv_mu);
+        for (vva_kv* kv : ctx->caches) g_kv_live.erase(kv);
+    }
     for (vva_kv* kv : ctx->caches) {
         (void)hipFree(kv->base);
         delete kv;
     }
     ctx->caches.clear();
     if (ctx->ws) (void)hipFree(ctx->ws);
+    for (float* p : ctx->ws_retired) (void)hipFree(p);
     delete ctx;
 }
 
@@ -262,6 +287,17 @@ extern "C" vva_status vva_set_attn_path(vva_context* ctx, int path) {
 
 extern "C" int vva_last_decode_splits(const vva_context* ctx) { return ctx ? ctx->last_splits : 0; }
 
+extern "C" vva_status vva_set_schedule(vva_context* ctx, int decode_wgs, int decode_splits, int prefill_splits) {
+    if (!ctx) return VVA_ERR_INVALID_ARG;
+    if (decode_wgs < 0 || decode_splits < 0 || decode_splits > 1024 || prefill_splits < 0 || prefill_splits > 32)
+        return fail(ctx, VVA_ERR_INVALID_ARG, "set_schedule: out of range (%d, %d, %d)", decode_wgs, decode_splits,
+                    prefill_splits);
+    ctx->sched_decode_wgs = decode_wgs;
+    ctx->sched_decode_splits = decode_splits;
+    ctx->sched_prefill_splits = prefill_splits;
+    return VVA_OK;
+}
+
 // ----------------------------------------------------------------- KV cache
 
 extern "C" vva_status vva_kv_create(vva_context* ctx, const vva_kv_desc* d, vva_kv** out) {
@@ -288,12 +324,21 @@ extern "C" vva_status vva_kv_create(vva_context* ctx, const vva_kv_desc* d, vva_
     if (e != hipSuccess) { (void)hipFree(kv->base); delete kv; return hip_fail(ctx, e, "kv_create: memset"); }
     kv->len.assign(d->n_seq, 0);
     ctx->caches.insert(kv);
+    {
+        std::lock_guard<std::mutex> lk(g_kv_mu);
+        g_kv_live.insert(kv);
+    }
     *out = kv;
     return VVA_OK;
 }
 
 extern "C" void vva_kv_free(vva_kv* kv) {
     if (!kv) return;
+    {
+        // a handle already released (by vva_kv_free or vva_destroy) is ignored
+        std::lock_guard<std::mutex> lk(g_kv_mu);
+        if (!g_kv_live.erase(kv)) return;
+    }
     vva_context* ctx = kv->ctx;
     DeviceGuard g(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
@@ -303,19 +348,19 @@ extern "C" void vva_kv_free(vva_kv* kv) {
 }
 
 extern "C" vva_status vva_kv_get_len(const vva_kv* kv, int seq, int32_t* len) {
-    if (!kv || !len || seq < 0 || seq >= kv->desc.n_seq) return VVA_ERR_INVALID_ARG;
+    if (!kv || !kv_live(kv) || !len || seq < 0 || seq >= kv->desc.n_seq) return VVA_ERR_INVALID_ARG;
     *len = kv->len[seq];
     return VVA_OK;
 }
 
 extern "C" vva_status vva_kv_set_len(vva_kv* kv, int seq, int32_t len) {
-    if (!kv || seq < 0 || seq >= kv->desc.n_seq || len < 0 || len > kv->desc.max_seq) return VVA_ERR_INVALID_ARG;
+    if (!kv || !kv_live(kv) || seq < 0 || seq >= kv->desc.n_seq || len < 0 || len > kv->desc.max_seq) return VVA_ERR_INVALID_ARG;
     kv->len[seq] = len;
     return VVA_OK;
 }
 
 extern "C" vva_status vva_kv_view(const vva_kv* kv, int layer, int seq, vva_tensor* k, vva_tensor* v) {
-    if (!kv || layer < 0 || layer >= kv->desc.n_layers || seq < 0 || seq >= kv->desc.n_seq)
+    if (!kv || !kv_live(kv) || layer < 0 || layer >= kv->desc.n_layers || seq < 0 || seq >= kv->desc.n_seq)
         return VVA_ERR_INVALID_ARG;
     for (int which = 0; which < 2; ++which) {
         vva_tensor* t = which == 0 ? k : v;
@@ -337,7 +382,8 @@ extern "C" vva_status vva_kv_view(const vva_kv* kv, int layer, int seq, vva_tens
 extern "C" vva_status vva_kv_upload(vva_context* ctx, vva_kv* kv, int layer, int seq, int32_t start,
                                     int32_t len, const float* k_host, const float* v_host) {
     if (!ctx) return VVA_ERR_INVALID_ARG;
-    if (!kv || layer < 0 || layer >= kv->desc.n_layers || seq < 0 || seq >= kv->desc.n_seq)
+    if (!kv || !kv_live(kv) || kv->ctx != ctx || layer < 0 || layer >= kv->desc.n_layers || seq < 0 ||
+        seq >= kv->desc.n_seq)
         return fail(ctx, VVA_ERR_INVALID_ARG, "kv_upload: bad cache / layer / seq");
     if (start < 0 || len < 0 || (int64_t)start + len > kv->desc.max_seq)
         return fail(ctx, VVA_ERR_INVALID_ARG, "kv_upload: rows [%d,%d) outside max_seq %d", start, start + len,
@@ -448,7 +494,8 @@ extern "C" vva_status vva_rope_append(vva_context* ctx, vva_kv* kv, int layer, c
                                       const vva_tensor* k, const vva_tensor* v, const vva_tensor* pos,
                                       const int32_t* seq_ids, float freq_base, const vva_tensor* q_out) {
     if (!ctx) return VVA_ERR_INVALID_ARG;
-    if (!kv || kv->ctx == nullptr) return fail(ctx, VVA_ERR_INVALID_ARG, "rope_append: null cache");
+    if (!kv || !kv_live(kv) || kv->ctx != ctx)
+        return fail(ctx, VVA_ERR_INVALID_ARG, "rope_append: cache is null, released or of another context");
     if (layer < 0 || layer >= kv->desc.n_layers) return fail(ctx, VVA_ERR_INVALID_ARG, "rope_append: layer %d", layer);
     vva_status st = check_tensor(ctx, q, "q");
     if (st != VVA_OK) return st;
@@ -499,7 +546,8 @@ extern "C" vva_status vva_rope_append(vva_context* ctx, vva_kv* kv, int layer, c
 extern "C" vva_status vva_attn(vva_context* ctx, const vva_kv* kv, int layer, const vva_tensor* q,
                                const int32_t* seq_ids, const vva_tensor* mask, float scale, const vva_tensor* out) {
     if (!ctx) return VVA_ERR_INVALID_ARG;
-    if (!kv) return fail(ctx, VVA_ERR_INVALID_ARG, "attn: null cache");
+    if (!kv || !kv_live(kv) || kv->ctx != ctx)
+        return fail(ctx, VVA_ERR_INVALID_ARG, "attn: cache is null, released or of another context");
     if (layer < 0 || layer >= kv->desc.n_layers) return fail(ctx, VVA_ERR_INVALID_ARG, "attn: layer %d", layer);
     vva_status st = check_tensor(ctx, q, "q");
     if (st != VVA_OK) return st;

@@ -43,6 +43,10 @@ struct Qwen2Hparams {
 // Resident K/V of a layer stack: one K and one V tensor per (layer,
 // sequence), ne=[hd, n_kv, max_seq, 1] in the chosen cache type, in one
 // device allocation owned by the library (src/qwen2.cpp:207-229).
+// Destruction order: free (or destroy) every ResidentKV before
+// vva_destroy of its context.  vva_destroy releases the caches still alive,
+// and a later free() or destructor of such a ResidentKV is then a no-op
+// (the library ignores released handles), but its views are dangling.
 struct ResidentKV {
     vva_context*     ctx      = nullptr;     // borrowed
     vva_kv*          kv       = nullptr;
@@ -57,9 +61,13 @@ struct ResidentKV {
     ~ResidentKV();
 
     // ResidentKV::init (src/qwen2.cpp:207-229), plus the sequence count and
-    // the cache type (the reference stores F32).  Zeroes the cache.
+    // the cache type.  Zeroes the cache.  The reference stores F32 and casts
+    // the whole window to F16 before every flash-attention call
+    // (src/qwen2.cpp:328-331); an F16 cache rounds each row once, at append,
+    // to the same F16 values, so F16 is the default: the attention sees the
+    // reference's operands at half the memory and without the per-call cast.
     bool init(vva_context* c, int n_layers, int hd, int n_kv, int max_seq, int n_seq = 1,
-              int type = VVA_TYPE_F32);
+              int type = VVA_TYPE_F16);
     // ResidentKV::free (src/qwen2.cpp:231-244).
     void free();
     // kvs.k[layer] / kvs.v[layer] (src/qwen2.cpp:293-294) of one sequence.

@@ -8,6 +8,8 @@ raise.
 """
 from __future__ import annotations
 
+import atexit
+import contextlib
 import ctypes
 import os
 import weakref
@@ -29,6 +31,7 @@ EXPORTS = [
     "vva_version", "vva_kv_create", "vva_kv_free", "vva_kv_get_len", "vva_kv_set_len",
     "vva_kv_view", "vva_kv_upload", "vva_rope_ext", "vva_rope_append", "vva_attn",
     "vva_flash_attn_ext", "vva_supports", "vva_set_attn_path", "vva_last_decode_splits",
+    "vva_set_schedule",
 ]
 
 
@@ -50,6 +53,20 @@ class KVDesc(ctypes.Structure):
 
 
 _lib = None
+# Contexts still open when the interpreter exits are destroyed by an atexit
+# hook, which runs before the C-level exit handlers of the HIP runtime and
+# of any profiler attached to the process: no vva_destroy (stream
+# synchronize, hipFree) then runs during or after their teardown.
+_live_contexts = weakref.WeakSet()
+
+
+@atexit.register
+def _close_live_contexts():
+    for c in list(_live_contexts):
+        try:
+            c.close()
+        except Exception:  # noqa: BLE001 — best effort at exit
+            pass
 
 
 def load_library(path: str = LIB_PATH):
@@ -82,6 +99,7 @@ def load_library(path: str = LIB_PATH):
         "vva_supports": (I, [P, I, I, I, I, I]),
         "vva_set_attn_path": (I, [P, I]),
         "vva_last_decode_splits": (I, [P]),
+        "vva_set_schedule": (I, [P, I, I, I]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -139,6 +157,7 @@ class Context:
             raise VvaError(st, self.lib.vva_last_error(None).decode())
         self.h = h
         self.caches = weakref.WeakSet()
+        _live_contexts.add(self)
 
     def check(self, st: int):
         if st != OK:
@@ -171,6 +190,19 @@ class Context:
 
     def last_decode_splits(self) -> int:
         return int(self.lib.vva_last_decode_splits(self.h))
+
+    def set_schedule(self, decode_wgs: int = 0, decode_splits: int = 0, prefill_splits: int = 0):
+        """Scheduling overrides for tests and benchmarks (0 = automatic)."""
+        self.check(self.lib.vva_set_schedule(self.h, decode_wgs, decode_splits, prefill_splits))
+
+    @contextlib.contextmanager
+    def schedule(self, decode_wgs: int = 0, decode_splits: int = 0, prefill_splits: int = 0):
+        """`with ctx.schedule(...)`: overrides for the block, automatic after."""
+        self.set_schedule(decode_wgs, decode_splits, prefill_splits)
+        try:
+            yield self
+        finally:
+            self.set_schedule(0, 0, 0)
 
     def supports(self, head_dim, n_q_heads, n_kv_heads, q_type, kv_type) -> bool:
         return bool(self.lib.vva_supports(self.h, head_dim, n_q_heads, n_kv_heads, q_type, kv_type))
