@@ -180,6 +180,23 @@ VVA_API vva_status vva_attn(vva_context* ctx, const vva_kv* kv, int layer,
                             const vva_tensor* q, const int32_t* seq_ids,
                             const vva_tensor* mask, float scale, const vva_tensor* out);
 
+/* vva_attn without any allocation, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  No counterpart in the reference.  Same arguments,
+ * kernels and results as vva_attn; the split partials of decode and of
+ * key-split prefill go to a static per-device scratch array of 36 MiB
+ * (resolved once per device by vva_create) instead of the context's
+ * workspace, so the call makes no hipMalloc / hipFree.  A call whose
+ * partials would exceed 36 MiB returns VVA_ERR_INVALID_ARG (the automatic
+ * schedule stays below 32.5 MiB for head_dim <= 128 on MI355X; forced
+ * split counts of vva_set_schedule may not).  Every call on one GPU shares
+ * that GPU's scratch, whose contents persist from call to call: calls that
+ * overlap in time on one GPU (other streams or contexts) race; calls
+ * ordered on one stream do not. */
+VVA_API vva_status vva_attn_noalloc(vva_context* ctx, const vva_kv* kv, int layer,
+                                    const vva_tensor* q, const int32_t* seq_ids,
+                                    const vva_tensor* mask, float scale, const vva_tensor* out);
+
 /* ggml_flash_attn_ext on arbitrary strided device tensors (ggml.h semantics):
  *   q: ne = [d, T, Hq, B] (F32 / F16 / BF16)  — the permuted q_p of
  *      src/qwen2.cpp:320;

@@ -36,6 +36,7 @@ struct vva_context {
     // HIP graph captured earlier, may still hold their address, so they stay
     // allocated until vva_destroy.
     std::vector<float*> ws_retired;
+    float* scratch = nullptr;            // this device's `scratch` (vva_attn_noalloc)
     std::set<vva_kv*> caches;            // released by vva_destroy if still alive
 };
 
@@ -49,9 +50,24 @@ struct vva_kv {
     std::vector<int32_t> len;
 };
 
+// Split-partial scratch of vva_attn_noalloc, one copy per GPU, held until
+// the process ends.  Its size covers every split count the planners choose
+// at head_dim <= 128 on a 256-CU device (at most 32.5 MiB: key-split
+// prefill partials n_ks * B * T * Hq * (d + 2) floats with n_ks * row tiles
+// <= 256).  In host code `scratch` only names the symbol: its device address
+// comes from hipGetSymbolAddress (scratch_addr below).
+constexpr size_t kScratchBytes = (size_t)36 << 20;
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
 namespace {
 
 thread_local std::string g_create_err;
+
+// Device address of `scratch` per device, resolved once per device by
+// vva_create with that device current.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch[kMaxDevices] = {};
 
 // Every live cache handle of every context.  vva_kv_free of a handle that is
 // not here (already freed, or released by vva_destroy of its context) does
@@ -137,19 +153,38 @@ vva_status ensure_ws(vva_context* ctx, size_t bytes) {
     return VVA_OK;
 }
 
-// Shared by vva_attn and vva_flash_attn_ext once AttnArgs is filled.
-vva_status run_attention(vva_context* ctx, AttnArgs& a) {
+// Split workspace of one call: the context's, grown on demand, or (fixed)
+// the device's static scratch, which never allocates and refuses sizes
+// beyond kScratchBytes.
+vva_status get_ws(vva_context* ctx, bool fixed, size_t bytes, float** ws) {
+    if (fixed) {
+        if (bytes > kScratchBytes)
+            return fail(ctx, VVA_ERR_INVALID_ARG,
+                        "attn_noalloc: this call needs %zu bytes of split workspace, more than the %zu-byte "
+                        "static scratch", bytes, kScratchBytes);
+        *ws = ctx->scratch;
+        return VVA_OK;
+    }
+    vva_status st = ensure_ws(ctx, bytes);
+    *ws = ctx->ws;
+    return st;
+}
+
+// Shared by vva_attn, vva_attn_noalloc (fixed) and vva_flash_attn_ext once
+// AttnArgs is filled.
+vva_status run_attention(vva_context* ctx, AttnArgs& a, bool fixed = false) {
     hipError_t e;
+    float* ws = nullptr;
     ctx->last_splits = 0;
     if (ctx->attn_path == 0 && a.T == 1 && decode_stream_supported(a)) {
         const int wgs = ctx->sched_decode_wgs > 0 ? ctx->sched_decode_wgs : ctx->n_cu;
         int n_splits = decode_stream_plan(a, wgs);
         if (ctx->sched_decode_splits > 0) n_splits = ctx->sched_decode_splits;
         if (n_splits > 1) {
-            vva_status st = ensure_ws(ctx, (size_t)n_splits * a.B * a.Hq * (a.d + 2) * sizeof(float));
+            vva_status st = get_ws(ctx, fixed, (size_t)n_splits * a.B * a.Hq * (a.d + 2) * sizeof(float), &ws);
             if (st != VVA_OK) return st;
         }
-        e = launch_decode_stream(a, ctx->ws, n_splits, ctx->stream);
+        e = launch_decode_stream(a, ws, n_splits, ctx->stream);
         if (e != hipSuccess) return hip_fail(ctx, e, "decode launch");
         ctx->last_splits = n_splits;
         return VVA_OK;
@@ -169,10 +204,10 @@ vva_status run_attention(vva_context* ctx, AttnArgs& a) {
         const int split_len = sub_len * R;
         const int n_splits = (Lmax + split_len - 1) / split_len;
         if (n_splits > 1) {
-            vva_status st = ensure_ws(ctx, (size_t)n_splits * a.B * a.Hq * (a.d + 2) * sizeof(float));
+            vva_status st = get_ws(ctx, fixed, (size_t)n_splits * a.B * a.Hq * (a.d + 2) * sizeof(float), &ws);
             if (st != VVA_OK) return st;
         }
-        e = launch_decode(a, ctx->ws, n_splits, split_len, ctx->stream);
+        e = launch_decode(a, ws, n_splits, split_len, ctx->stream);
         if (e != hipSuccess) return hip_fail(ctx, e, "decode launch");
         ctx->last_splits = n_splits;
         return VVA_OK;
@@ -181,10 +216,10 @@ vva_status run_attention(vva_context* ctx, AttnArgs& a) {
         int n_ks = prefill_plan(a, ctx->n_cu);
         if (ctx->sched_prefill_splits > 0) n_ks = ctx->sched_prefill_splits;
         if (n_ks > 1) {
-            vva_status st = ensure_ws(ctx, prefill_ws_bytes(a, n_ks));
+            vva_status st = get_ws(ctx, fixed, prefill_ws_bytes(a, n_ks), &ws);
             if (st != VVA_OK) return st;
         }
-        e = launch_prefill(a, ctx->ws, n_ks, ctx->stream);
+        e = launch_prefill(a, ws, n_ks, ctx->stream);
         if (e != hipSuccess) return hip_fail(ctx, e, "prefill launch");
         ctx->last_splits = n_ks;
         return VVA_OK;
@@ -230,10 +265,24 @@ extern "C" vva_status vva_create(int device, void* stream, vva_context** out) {
     if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(nullptr, VVA_ERR_NOT_IMPLEMENTED, "kernels are built for gfx950, device is %s", prop.gcnArchName);
     DeviceGuard g(device);
+    float* scr = nullptr;
+    if (device < kMaxDevices) {
+        std::lock_guard<std::mutex> lk(g_scratch_mu);
+        if (!g_scratch[device]) {
+            e = hipGetSymbolAddress((void**)&g_scratch[device], HIP_SYMBOL(scratch));
+            if (e != hipSuccess) {
+                g_scratch[device] = nullptr;
+                return fail(nullptr, VVA_ERR_DEVICE, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+            }
+        }
+        scr = g_scratch[device];
+    }
     auto* ctx = new vva_context();
     ctx->device = device;
     ctx->n_cu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
     ctx->stream = (hipStream_t)stream;
+    ctx->scratch = scr;
+    ctx->err.reserve(512);               // error messages (< 512 bytes) then never allocate
     *out = ctx;
     return VVA_OK;
 }
@@ -543,9 +592,13 @@ extern "C" vva_status vva_rope_append(vva_context* ctx, vva_kv* kv, int layer, c
     return e == hipSuccess ? VVA_OK : hip_fail(ctx, e, "rope_append launch");
 }
 
-extern "C" vva_status vva_attn(vva_context* ctx, const vva_kv* kv, int layer, const vva_tensor* q,
-                               const int32_t* seq_ids, const vva_tensor* mask, float scale, const vva_tensor* out) {
+namespace {
+
+vva_status attn_impl(vva_context* ctx, const vva_kv* kv, int layer, const vva_tensor* q, const int32_t* seq_ids,
+                     const vva_tensor* mask, float scale, const vva_tensor* out, bool fixed) {
     if (!ctx) return VVA_ERR_INVALID_ARG;
+    if (fixed && !ctx->scratch)
+        return fail(ctx, VVA_ERR_NOT_IMPLEMENTED, "attn_noalloc: no static scratch on device %d", ctx->device);
     if (!kv || !kv_live(kv) || kv->ctx != ctx)
         return fail(ctx, VVA_ERR_INVALID_ARG, "attn: cache is null, released or of another context");
     if (layer < 0 || layer >= kv->desc.n_layers) return fail(ctx, VVA_ERR_INVALID_ARG, "attn: layer %d", layer);
@@ -584,7 +637,20 @@ extern "C" vva_status vva_attn(vva_context* ctx, const vva_kv* kv, int layer, co
     a.o_nb_h = out->nb[1]; a.o_nb_t = out->nb[2]; a.o_nb_b = out->nb[3];
     a.d = (int)d; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.T = (int)T; a.B = (int)B;
     DeviceGuard g(ctx->device);
-    return run_attention(ctx, a);
+    return run_attention(ctx, a, fixed);
+}
+
+}  // namespace
+
+extern "C" vva_status vva_attn(vva_context* ctx, const vva_kv* kv, int layer, const vva_tensor* q,
+                               const int32_t* seq_ids, const vva_tensor* mask, float scale, const vva_tensor* out) {
+    return attn_impl(ctx, kv, layer, q, seq_ids, mask, scale, out, false);
+}
+
+extern "C" vva_status vva_attn_noalloc(vva_context* ctx, const vva_kv* kv, int layer, const vva_tensor* q,
+                                       const int32_t* seq_ids, const vva_tensor* mask, float scale,
+                                       const vva_tensor* out) {
+    return attn_impl(ctx, kv, layer, q, seq_ids, mask, scale, out, true);
 }
 
 extern "C" vva_status vva_flash_attn_ext(vva_context* ctx, const vva_tensor* q, const vva_tensor* k,

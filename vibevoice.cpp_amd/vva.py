@@ -31,7 +31,7 @@ EXPORTS = [
     "vva_version", "vva_kv_create", "vva_kv_free", "vva_kv_get_len", "vva_kv_set_len",
     "vva_kv_view", "vva_kv_upload", "vva_rope_ext", "vva_rope_append", "vva_attn",
     "vva_flash_attn_ext", "vva_supports", "vva_set_attn_path", "vva_last_decode_splits",
-    "vva_set_schedule",
+    "vva_set_schedule", "vva_attn_noalloc",
 ]
 
 
@@ -95,6 +95,7 @@ def load_library(path: str = LIB_PATH):
         "vva_rope_ext": (I, [P, TP, TP, I, I, F, TP]),
         "vva_rope_append": (I, [P, P, I, TP, TP, TP, TP, P, F, TP]),
         "vva_attn": (I, [P, P, I, TP, P, TP, F, TP]),
+        "vva_attn_noalloc": (I, [P, P, I, TP, P, TP, F, TP]),
         "vva_flash_attn_ext": (I, [P, TP, TP, TP, TP, F, F, F, TP]),
         "vva_supports": (I, [P, I, I, I, I, I]),
         "vva_set_attn_path": (I, [P, I]),
@@ -229,6 +230,14 @@ class Context:
         mp = ctypes.byref(_mask_view(mask)) if mask is not None else None
         self.check(self.lib.vva_attn(self.h, kv.h, layer, ctypes.byref(view(q)), ids, mp, scale,
                                      ctypes.byref(view(out))))
+
+    def attn_noalloc(self, kv: "KVCache", layer: int, q, out, scale: float, seq_ids=None, mask=None):
+        """vva_attn_noalloc: as attn, with the split partials in the device's
+        static scratch (no device allocation)."""
+        ids = _ids(seq_ids)
+        mp = ctypes.byref(_mask_view(mask)) if mask is not None else None
+        self.check(self.lib.vva_attn_noalloc(self.h, kv.h, layer, ctypes.byref(view(q)), ids, mp, scale,
+                                             ctypes.byref(view(out))))
 
     def flash_attn_ext(self, q, k, v, out, scale: float, mask=None, k_view=None, v_view=None):
         """ggml layout: q torch [B, Hq, T, d] (ne=[d,T,Hq,B]); k, v torch [B, Hkv, L, d] or
