@@ -209,6 +209,40 @@ VVA_API vva_status vva_flash_attn_ext(vva_context* ctx, const vva_tensor* q, con
                                       const vva_tensor* v, const vva_tensor* mask, float scale,
                                       float max_bias, float logit_softcap, const vva_tensor* dst);
 
+/* Fused Q/K/V projection + bias + RoPE + KV append: the three linear()
+ * calls (ggml_mul_mat + ggml_add of the bias, src/qwen2.cpp:19-25, :273-275)
+ * and everything vva_rope_append does (src/qwen2.cpp:282-306), in one GEMM
+ * whose epilogue rotates and stores:
+ *   x:  ne = [hidden, T, B] (F32 / F16 / BF16), the normed layer input xn;
+ *   wq: ne = [hidden, Hq*d], wk, wv: ne = [hidden, Hkv*d], all F16 or all
+ *       Q8_0 (GGUF blocks along hidden), rows contiguous (F16: 16-byte
+ *       aligned rows, Q8_0: 4-byte aligned);
+ *   bq, bk, bv: F32 ne = [Hq*d] / [Hkv*d], or NULL (no bias);
+ *   pos, seq_ids, freq_base: as vva_rope_append;
+ *   q_out: ne = [d, Hq, T, B] (F32 / F16 / BF16), receives RoPE(x wq^T + bq).
+ * Writes RoPE(x wk^T + bk) and x wv^T + bv into cache rows [len(seq_b),
+ * len(seq_b) + T) of (layer, seq_b) in the cache type; does not advance len.
+ * Numerics of ggml's CPU mul_mat: x is rounded to f16 (F16 weights) or
+ * quantized to Q8_0 blocks (Q8_0 weights) before the dot products.
+ * Requires hidden % 64 == 0, Hq*d and Hkv*d multiples of 128, d = 64 or 128;
+ * otherwise VVA_ERR_NOT_IMPLEMENTED. */
+VVA_API vva_status vva_qkv_rope_append(vva_context* ctx, vva_kv* kv, int layer, const vva_tensor* x,
+                                       const vva_tensor* wq, const vva_tensor* wk, const vva_tensor* wv,
+                                       const vva_tensor* bq, const vva_tensor* bk, const vva_tensor* bv,
+                                       const vva_tensor* pos, const int32_t* seq_ids, float freq_base,
+                                       const vva_tensor* q_out);
+
+/* Output projection + residual: h = o w_o^T + x, the ggml_mul_mat(attn_o)
+ * and ggml_add(x, o) of src/qwen2.cpp:348-349:
+ *   o:   ne = [Hq*d, T, B] (F32 / F16 / BF16), e.g. vva_attn's output viewed
+ *        as rows of Hq*d;
+ *   w_o: ne = [Hq*d, hidden], F16 or Q8_0 (same layout rules as above);
+ *   x:   F32 ne = [hidden, T, B], the layer input (residual);
+ *   h:   F32 ne = [hidden, T, B], may alias x.
+ * Requires Hq*d % 64 == 0 and hidden % 128 == 0. */
+VVA_API vva_status vva_out_proj_residual(vva_context* ctx, const vva_tensor* o, const vva_tensor* w_o,
+                                         const vva_tensor* x, const vva_tensor* h);
+
 /* Capability probe — analogue of backend_supports_flash_attn()
  * (src/backend.cpp:157-196).  Returns 1 if vva_attn / vva_flash_attn_ext can
  * run this combination on the context's device, 0 otherwise. */

@@ -423,3 +423,97 @@ int vvo_attn(const vvo_attn_args* a) {
     for (int i = 0; i < started; ++i) pthread_join(th[i], NULL);
     return job.err ? -5 : 0;
 }
+
+/* ------------------------------------------------------------ linear */
+
+typedef struct {
+    const uint8_t* w; int w_type; int64_t w_row_bytes;
+    const float* bias; const float* x; float* y;
+    int64_t N, K, M; int mode;
+    const float* xr;          /* GGML, F16: x rounded to f16 (as f32) [N][K] */
+    const uint8_t* xq;        /* GGML, Q8_0: x as Q8_0 blocks [N][K/32 * 34] */
+    int64_t next;
+} linear_job;
+
+static void* linear_worker(void* arg) {
+    linear_job* j = (linear_job*)arg;
+    const int64_t K = j->K, nb = K / VVO_QK8_0;
+    double* wd = (double*)malloc(sizeof(double) * K);
+    float* wf = (float*)malloc(sizeof(float) * K);
+    if (!wd || !wf) { free(wd); free(wf); return NULL; }
+    for (;;) {
+        const int64_t m = __atomic_fetch_add(&j->next, 1, __ATOMIC_RELAXED);
+        if (m >= j->M) break;
+        const uint8_t* wr = j->w + m * j->w_row_bytes;
+        vvo_to_f32(wr, j->w_type, wf, K);
+        for (int64_t k = 0; k < K; ++k) wd[k] = wf[k];
+        for (int64_t n = 0; n < j->N; ++n) {
+            float out;
+            if (j->mode == VVO_EXACT) {
+                const float* xn = j->x + n * K;
+                double acc = 0.0;
+                for (int64_t k = 0; k < K; ++k) acc += wd[k] * (double)xn[k];
+                if (j->bias) acc += (double)j->bias[m];
+                out = (float)acc;
+            } else if (j->w_type == VVO_Q8_0) {
+                const uint8_t* xb = j->xq + n * nb * 34;
+                float acc = 0.0f;
+                for (int64_t b = 0; b < nb; ++b) {
+                    uint16_t dw, dx;
+                    memcpy(&dw, wr + b * 34, 2);
+                    memcpy(&dx, xb + b * 34, 2);
+                    int sumi = 0;
+                    for (int i = 0; i < VVO_QK8_0; ++i)
+                        sumi += (int)(int8_t)wr[b * 34 + 2 + i] * (int)(int8_t)xb[b * 34 + 2 + i];
+                    acc += (float)sumi * (h2f(dw) * h2f(dx));
+                }
+                out = j->bias ? acc + j->bias[m] : acc;
+            } else {
+                const float* xn = j->xr + n * K;
+                float acc = 0.0f;
+                for (int64_t k = 0; k < K; ++k) acc = fmaf(wf[k], xn[k], acc);
+                out = j->bias ? acc + j->bias[m] : acc;
+            }
+            j->y[n * j->M + m] = out;
+        }
+    }
+    free(wd);
+    free(wf);
+    return NULL;
+}
+
+int vvo_linear(const void* w, int w_type, int64_t w_row_bytes, const float* bias, const float* x, float* y,
+               int64_t N, int64_t K, int64_t M, int mode, int n_threads) {
+    if (!w || !x || !y || N <= 0 || K <= 0 || M <= 0) return -2;
+    if (w_type != VVO_F16 && w_type != VVO_Q8_0) return -2;
+    if (w_type == VVO_Q8_0 && K % VVO_QK8_0) return -2;
+    if (w_row_bytes < vvo_row_bytes(w_type, K)) return -2;
+    pthread_once(&g_f16_once, f16_table_init);
+    linear_job j = {(const uint8_t*)w, w_type, w_row_bytes, bias, x, y, N, K, M, mode, NULL, NULL, 0};
+    float* xr = NULL;
+    uint8_t* xq = NULL;
+    if (mode != VVO_EXACT) {
+        if (w_type == VVO_F16) {
+            xr = (float*)malloc(sizeof(float) * N * K);
+            if (!xr) return -5;
+            for (int64_t i = 0; i < N * K; ++i) xr[i] = h2f(vvo_f32_to_f16(x[i]));
+            j.xr = xr;
+        } else {
+            xq = (uint8_t*)malloc((size_t)(N * (K / VVO_QK8_0) * 34));
+            if (!xq) return -5;
+            for (int64_t n = 0; n < N; ++n) vvo_quantize_q8_0(x + n * K, xq + n * (K / VVO_QK8_0) * 34, K);
+            j.xq = xq;
+        }
+    }
+    int nt = n_threads > 0 ? n_threads : vvo_n_cores();
+    if (nt > 256) nt = 256;
+    pthread_t th[256];
+    int started = 0;
+    for (int i = 1; i < nt; ++i)
+        if (pthread_create(&th[started], NULL, linear_worker, &j) == 0) ++started;
+    linear_worker(&j);
+    for (int i = 0; i < started; ++i) pthread_join(th[i], NULL);
+    free(xr);
+    free(xq);
+    return 0;
+}

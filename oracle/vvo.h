@@ -91,6 +91,23 @@ typedef struct {
 int      vvo_attn(const vvo_attn_args* a);
 int      vvo_n_cores(void);
 
+/* Linear layer y = x W^T (+ bias): ggml_mul_mat(W, x) followed by ggml_add
+ * of the bias (linear(), src/qwen2.cpp:19-25), as used for the q/k/v
+ * projections (src/qwen2.cpp:273-275) and the output projection
+ * (src/qwen2.cpp:348).
+ *   w: M rows of K elements of w_type (F16, or Q8_0 blocks along K), row
+ *      stride w_row_bytes;  x: F32 [N][K];  bias: F32 [M] or NULL;
+ *   y: F32 [N][M].
+ * VVO_EXACT: fp64 sum of dequantized w times unrounded x.
+ * VVO_GGML:  ggml's CPU vec-dot order: x converted to W's vec-dot type
+ *            first (F16: rounded to f16, products summed in fp32 in k
+ *            order; Q8_0: x quantized to Q8_0 blocks, integer block sums
+ *            times d_w * d_x summed in fp32 in block order), then the bias
+ *            added in fp32.
+ * Returns 0, or -2 on bad arguments. */
+int      vvo_linear(const void* w, int w_type, int64_t w_row_bytes, const float* bias, const float* x,
+                    float* y, int64_t N, int64_t K, int64_t M, int mode, int n_threads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -68,6 +68,10 @@ def lib():
         L.vvo_attn.restype = ctypes.c_int
         L.vvo_attn.argtypes = [ctypes.POINTER(AttnArgs)]
         L.vvo_n_cores.restype = ctypes.c_int
+        L.vvo_linear.restype = ctypes.c_int
+        L.vvo_linear.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
+                                 ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int,
+                                 ctypes.c_int]
         _lib = L
     return _lib
 
@@ -159,3 +163,22 @@ def attn(q: np.ndarray, k_caches, v_caches, k_type: int, v_type: int, L, *, n_kv
 
 def n_cores() -> int:
     return int(lib().vvo_n_cores())
+
+
+def linear(x: np.ndarray, w_raw: np.ndarray, w_type: int, M: int, bias: np.ndarray | None = None,
+           mode: int = GGML, n_threads: int = 0) -> np.ndarray:
+    """y = x W^T + bias.  x: f32 [..., K]; w_raw: raw bytes of M rows of K
+    elements of w_type (F16 or Q8_0); bias f32 [M] or None -> f32 [..., M]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    K = x.shape[-1]
+    N = x.size // K
+    w_raw = np.ascontiguousarray(w_raw).reshape(-1)
+    rb = row_bytes(w_type, K)
+    assert w_raw.size == M * rb
+    y = np.empty(x.shape[:-1] + (M,), dtype=np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    rc = lib().vvo_linear(_ptr(w_raw), w_type, rb, None if b is None else _ptr(b), _ptr(x), _ptr(y),
+                          N, K, M, mode, n_threads)
+    if rc != 0:
+        raise RuntimeError(f"vvo_linear failed: {rc}")
+    return y

@@ -1,0 +1,339 @@
+// proj.hip — the linear layers on either side of the attention, on CDNA4
+// MFMA, with their neighbouring elementwise ops fused into the epilogue:
+//   * q/k/v projections (linear(): ggml_mul_mat + bias, src/qwen2.cpp:19-25,
+//     :273-275), NeoX RoPE of q and k (:282-287) and the append of k and v to
+//     the resident cache (:293-306) — one GEMM over the stacked weights whose
+//     epilogue writes RoPE(q) and the cache rows;
+//   * the output projection plus the residual add (src/qwen2.cpp:348-349).
+//
+// Numerics follow ggml's CPU mul_mat: x is first converted to the weight's
+// vec-dot type by proj_prep_kernel (F16 weights: x rounded to f16; Q8_0
+// weights: x quantized to Q8_0 blocks, kept as f16 d_x * q values), then
+// every product of f16 operands is exact in the fp32 MFMA accumulators.
+// Q8_0 weight blocks are dequantized to f16 d_w * q values while the tile is
+// staged in LDS.  (The two f16 roundings of d * q are the only departure from
+// ggml's integer block sums; each is below 2^-12 relative.)
+//
+// GEMM.  D[m][n] = sum_k W[m][k] X[n][k]: m = output feature, n = token row
+// (b * T + t), k = input feature.  A workgroup computes a 128 x 128 tile
+// over k in steps of 64 with 4 waves, each a 64 x 64 quadrant of 2 x 2
+// v_mfma_f32_32x32x16_f16 blocks.  Both operands are k-contiguous rows, so
+// every MFMA fragment is one 16-byte LDS read; rows are padded to 144 bytes
+// (16 mod 256: conflict-free fragment reads).  Tiles are staged through
+// registers into two LDS stages (the loads of tile j + 1 fly while tile j is
+// computed); the compiler tracks every load.  Workgroups are ordered so that
+// each XCD (workgroups are dealt to the 8 XCDs round-robin) walks a
+// contiguous run of tiles: the 36 weight tiles of one token tile share its
+// X tile in that XCD's L2.
+//
+// Epilogue.  The accumulators go through LDS as a [token][feature] tile, so
+// the epilogue threads see whole head rows: bias, then the NeoX rotation of
+// pair (i, i + d/2) with the token's (cos, sin) row written by the prep
+// kernel (the fp32 theta recurrence of rope_append.hip), then stores in the
+// q_out / cache types (Q8_0 rows quantized per 32-dim block).
+#include "vva_internal.hpp"
+
+namespace vva {
+
+namespace {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kTM = 128;                    // output features per tile
+constexpr int kTN = 128;                    // token rows per tile
+constexpr int kTK = 64;                     // inputs per k step
+constexpr int kPitch = kTK * 2 + 16;        // LDS bytes per operand row
+constexpr int kOpBytes = 128 * kPitch;      // one operand tile: 18,432
+constexpr int kStage = 2 * kOpBytes;        // A (weights) then B (x)
+constexpr int kCPitch = kTM + 4;            // floats per token row of the epilogue tile
+static_assert(2 * kStage >= kTN * kCPitch * 4, "the epilogue tile reuses the two stages");
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// ------------------------------------------------------------ prep
+
+// One workgroup per token row n = b * T + t: the row in the weights'
+// vec-dot type, as f16 (F16 weights: x rounded; Q8_0 weights: the Q8_0
+// round trip, d * q with the fp16 d), and, for the q/k/v projections, the
+// row's RoPE (cos, sin) pairs with the fp32 theta recurrence.
+__global__ void __launch_bounds__(256) proj_prep_kernel(ProjPrepArgs a) {
+    const int n = blockIdx.x;
+    const int b = n / a.T, t = n - b * a.T;
+    const char* src = a.x + b * a.x_nb_b + t * a.x_nb_t;
+    const int64_t es = type_elem_bytes(a.x_type);
+    uint16_t* dst = a.xh + (int64_t)n * a.K;
+    // 8 consecutive elements per thread; four threads make one 32-block
+    for (int k0 = threadIdx.x * 8; k0 < a.K; k0 += 256 * 8) {
+        float x[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = load_elem(src + (k0 + e) * es, a.x_type);
+        uint16_t h[8];
+        if (a.q8) {
+            float am = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) am = fmaxf(am, fabsf(x[e]));
+            am = fmaxf(am, __shfl_xor(am, 1, 4));
+            am = fmaxf(am, __shfl_xor(am, 2, 4));
+            const float d = am / 127.0f;
+            const float id = d != 0.0f ? 1.0f / d : 0.0f;
+            const float dh = f16_to_f32(f32_to_f16(d));
+#pragma unroll
+            for (int e = 0; e < 8; ++e) h[e] = f32_to_f16(dh * roundf(x[e] * id));
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) h[e] = f32_to_f16(x[e]);
+        }
+        uint4 v;
+        v.x = (uint32_t)h[0] | ((uint32_t)h[1] << 16);
+        v.y = (uint32_t)h[2] | ((uint32_t)h[3] << 16);
+        v.z = (uint32_t)h[4] | ((uint32_t)h[5] << 16);
+        v.w = (uint32_t)h[6] | ((uint32_t)h[7] << 16);
+        *(uint4*)(dst + k0) = v;
+    }
+    if (a.rope) {
+        const float p = (float)a.pos[b * a.pos_stride_b + t];
+        for (int i = threadIdx.x; i < a.P; i += 256) {
+            float th = p;
+            for (int k = 0; k < i; ++k) th *= a.theta_scale;
+            a.rope[(int64_t)n * a.P + i] = make_float2(cosf(th), sinf(th));
+        }
+    }
+}
+
+// ------------------------------------------------------------ GEMM
+
+// WQ8: Q8_0 weights (else F16).  MODE: kProjQKV or kProjResidual.
+template <bool WQ8, int MODE>
+__global__ void __launch_bounds__(256) proj_gemm_kernel(ProjArgs a) {
+    __shared__ __attribute__((aligned(16))) char lds[2 * kStage];
+
+    const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5, l32 = lane & 31;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = w & 1, wn = w >> 1;             // the wave's 64 x 64 quadrant
+
+    // Workgroup i runs on XCD i % 8; XCD x takes the contiguous run of tiles
+    // [x * q + min(x, r), ...) of its c_x = q + (x < r) workgroups.
+    const int n_mt = a.M / kTM;
+    const int tiles = gridDim.x;
+    const int q = tiles / 8, r = tiles % 8, x = blockIdx.x % 8;
+    const int tile = x * q + min(x, r) + (int)blockIdx.x / 8;
+    const int mt = tile % n_mt, nt = tile / n_mt;
+    const int m0 = mt * kTM, n0 = nt * kTN;
+    const int mat = m0 < a.m_end[0] ? 0 : (m0 < a.m_end[1] ? 1 : 2);
+    const int mrow0 = m0 - (mat ? a.m_end[mat - 1] : 0);     // first row in its matrix
+    const char* wbase = a.w[mat] + (int64_t)mrow0 * a.w_nb[mat];
+    const int64_t wnb = a.w_nb[mat];
+
+    // x rows past N read as zeros through the buffer range
+    const __amdgpu_buffer_rsrc_t xrs = rsrc(a.xh + (int64_t)n0 * a.K, (uint32_t)(min(a.N - n0, kTN) * a.K * 2));
+    const __amdgpu_buffer_rsrc_t wrs = rsrc(wbase, (uint32_t)(kTM * wnb));
+
+    // per thread and k step: 4 x 16 bytes of B (and of an F16 A): chunk c =
+    // tid + 256 i is row c / 8, 16-byte column c % 8
+    u32x4 breg[4], areg[4];
+    uint32_t qreg[9];
+    auto load = [&](int kt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int c = tid + 256 * i, row = c >> 3, col = c & 7;
+            breg[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (row * a.K + kt * kTK) * 2 + col * 16, 0, 0);
+        }
+        if constexpr (!WQ8) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int c = tid + 256 * i, row = c >> 3, col = c & 7;
+                areg[i] = __builtin_amdgcn_raw_buffer_load_b128(wrs, (uint32_t)(row * wnb) + kt * kTK * 2 + col * 16, 0, 0);
+            }
+        } else {
+            // block kt * 2 + (tid & 1) of row tid / 2: 34 bytes from the
+            // 4-byte boundary at or below it (9 dwords; the block of an odd
+            // index starts 2 bytes in, an even one's 9th dword is the next
+            // block's scale, always inside the row)
+            const uint32_t off = (uint32_t)((tid >> 1) * wnb) + (uint32_t)(kt * 2 + (tid & 1)) * kQ8Bytes;
+#pragma unroll
+            for (int i = 0; i < 9; ++i) qreg[i] = __builtin_amdgcn_raw_buffer_load_b32(wrs, (off & ~3u) + 4 * i, 0, 0);
+        }
+    };
+    auto store = [&](int st) {
+        char* sa = lds + st * kStage;
+        char* sb = sa + kOpBytes;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int c = tid + 256 * i, row = c >> 3, col = c & 7;
+            *(u32x4*)(sb + row * kPitch + col * 16) = breg[i];
+        }
+        if constexpr (!WQ8) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int c = tid + 256 * i, row = c >> 3, col = c & 7;
+                *(u32x4*)(sa + row * kPitch + col * 16) = areg[i];
+            }
+        } else {
+            const bool odd = tid & 1;                  // the block starts 2 bytes into dword 0
+            const uint32_t dbits = odd ? (qreg[0] >> 16) : (qreg[0] & 0xffffu);
+            _Float16 dh;
+            const uint16_t d16 = (uint16_t)dbits;
+            __builtin_memcpy(&dh, &d16, 2);
+            const h2 dd = {dh, dh};
+            uint32_t codes[8];                         // the 32 codes, 4 per dword
+#pragma unroll
+            for (int i = 0; i < 8; ++i) codes[i] = odd ? qreg[i + 1] : __builtin_amdgcn_alignbyte(qreg[i + 1], qreg[i], 2);
+            uint32_t outw[16];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t c = codes[i];
+                const h2 lo = {(_Float16)(int8_t)(c & 0xff), (_Float16)(int8_t)((c >> 8) & 0xff)};
+                const h2 hi = {(_Float16)(int8_t)((c >> 16) & 0xff), (_Float16)(int8_t)(c >> 24)};
+                const h2 plo = lo * dd, phi = hi * dd;   // exact product rounded once to f16
+                __builtin_memcpy(&outw[2 * i], &plo, 4);
+                __builtin_memcpy(&outw[2 * i + 1], &phi, 4);
+            }
+            char* dst = sa + (tid >> 1) * kPitch + (tid & 1) * 64;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                *(u32x4*)(dst + 16 * i) = u32x4{outw[4 * i], outw[4 * i + 1], outw[4 * i + 2], outw[4 * i + 3]};
+        }
+    };
+
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+
+    const int nk = a.K / kTK;
+    load(0);
+    store(0);
+    if (nk > 1) load(1);
+    __syncthreads();
+    // fragment offsets within a stage: row l32 of each 32-row block, the
+    // lane's 8-element k group
+    const int a_rd = (wm * 64 + l32) * kPitch + half * 16;
+    const int b_rd = kOpBytes + (wn * 64 + l32) * kPitch + half * 16;
+    for (int kt = 0; kt < nk; ++kt) {
+        const char* st = lds + (kt & 1) * kStage;
+#pragma unroll
+        for (int ks = 0; ks < kTK / 16; ++ks) {
+            h8 af[2], bf[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const u32x4 ua = *(const u32x4*)(st + a_rd + i * 32 * kPitch + ks * 32);
+                const u32x4 ub = *(const u32x4*)(st + b_rd + i * 32 * kPitch + ks * 32);
+                __builtin_memcpy(&af[i], &ua, 16);
+                __builtin_memcpy(&bf[i], &ub, 16);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+        if (kt + 1 < nk) {
+            store((kt + 1) & 1);      // that stage held tile kt - 1: every wave is past it
+            if (kt + 2 < nk) load(kt + 2);
+        }
+        __syncthreads();
+    }
+
+    // ---- accumulators to LDS as C[token][feature]: lane (half, l32) of
+    // block (i, j) holds features 8 (r / 4) + 4 half + r % 4 of token l32
+    float* C = (float*)lds;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            float* crow = C + (wn * 64 + 32 * j + l32) * kCPitch + wm * 64 + 32 * i + 4 * half;
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                *(float4*)(crow + 8 * g) = make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                                                       acc[i][j][4 * g + 3]);
+        }
+    __syncthreads();
+
+    if constexpr (MODE == kProjQKV) {
+        // 64 rotation pairs per token (one head of d = 128, two of d = 64):
+        // thread (token tid / 64 + 4 pass, pair tid % 64)
+        const int d = a.d, P = d >> 1;
+        const int pi = tid & 63, hl = pi / P, i = pi - hl * P;
+        const int head = (mrow0 + hl * d) / d;
+        const float* bias = a.bias[mat];
+        const float b0 = bias ? bias[mrow0 + hl * d + i] : 0.0f;
+        const float b1 = bias ? bias[mrow0 + hl * d + i + P] : 0.0f;
+        for (int nl = tid >> 6; nl < kTN; nl += 4) {
+            const int n = n0 + nl;
+            if (n >= a.N) break;                       // wave-uniform
+            float y0 = C[nl * kCPitch + hl * d + i] + b0;
+            float y1 = C[nl * kCPitch + hl * d + i + P] + b1;
+            if (mat < 2) {
+                const float2 cs = a.rope[(int64_t)n * P + i];
+                const float r0 = fmaf(y0, cs.x, -(y1 * cs.y));
+                const float r1 = fmaf(y0, cs.y, y1 * cs.x);
+                y0 = r0;
+                y1 = r1;
+            }
+            const int b = n / a.T, t = n - b * a.T;
+            if (mat == 0) {
+                const int64_t eo = type_elem_bytes(a.q_out_type);
+                char* dst = a.q_out + b * a.qo_nb_b + t * a.qo_nb_t + head * a.qo_nb_h;
+                store_elem(dst + i * eo, a.q_out_type, y0);
+                store_elem(dst + (i + P) * eo, a.q_out_type, y1);
+            } else {
+                char* row = (mat == 1 ? a.k_dst[b] : a.v_dst[b]) + t * a.cache_row_bytes + head * a.cache_head_bytes;
+                if (a.cache_type == VVA_TYPE_Q8_0) {
+                    store_q8_pair(row, i, P, y0, y1);
+                } else {
+                    const int64_t ec = type_elem_bytes(a.cache_type);
+                    store_elem(row + i * ec, a.cache_type, y0);
+                    store_elem(row + (i + P) * ec, a.cache_type, y1);
+                }
+            }
+        }
+    } else {
+        // h = y + x, 4 features per thread: thread (token tid / 32 + 8 pass,
+        // features 4 (tid % 32) ..)
+        const int c4 = (tid & 31) * 4;
+        for (int nl = tid >> 5; nl < kTN; nl += 8) {
+            const int n = n0 + nl;
+            if (n >= a.N) break;
+            const int b = n / a.T, t = n - b * a.T;
+            const float4 xr = *(const float4*)(a.res + b * a.res_nb_b + t * a.res_nb_t + (int64_t)(m0 + c4) * 4);
+            const float* cr = C + nl * kCPitch + c4;
+            *(float4*)(a.h + b * a.h_nb_b + t * a.h_nb_t + (int64_t)(m0 + c4) * 4) =
+                make_float4(cr[0] + xr.x, cr[1] + xr.y, cr[2] + xr.z, cr[3] + xr.w);
+        }
+    }
+}
+
+}  // namespace
+
+size_t proj_ws_bytes(int N, int K, int P) {
+    const size_t xh = ((size_t)N * K * 2 + 255) / 256 * 256;
+    return xh + (size_t)N * P * sizeof(float2);
+}
+
+hipError_t launch_proj(ProjPrepArgs& p, ProjArgs& a, void* ws, hipStream_t s) {
+    p.xh = (uint16_t*)ws;
+    p.rope = p.P > 0 ? (float2*)((char*)ws + ((size_t)p.N * p.K * 2 + 255) / 256 * 256) : nullptr;
+    a.xh = p.xh;
+    a.rope = p.rope;
+    hipLaunchKernelGGL(proj_prep_kernel, dim3(p.N), dim3(256), 0, s, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int tiles = (a.M / kTM) * ((a.N + kTN - 1) / kTN);
+    const bool q8 = a.w_type == VVA_TYPE_Q8_0;
+    if (a.mode == kProjQKV) {
+        if (q8) hipLaunchKernelGGL((proj_gemm_kernel<true, kProjQKV>), dim3(tiles), dim3(256), 0, s, a);
+        else    hipLaunchKernelGGL((proj_gemm_kernel<false, kProjQKV>), dim3(tiles), dim3(256), 0, s, a);
+    } else {
+        if (q8) hipLaunchKernelGGL((proj_gemm_kernel<true, kProjResidual>), dim3(tiles), dim3(256), 0, s, a);
+        else    hipLaunchKernelGGL((proj_gemm_kernel<false, kProjResidual>), dim3(tiles), dim3(256), 0, s, a);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace vva

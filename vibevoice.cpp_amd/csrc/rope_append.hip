@@ -23,29 +23,6 @@ namespace vva {
 
 namespace {
 
-__device__ __forceinline__ void store_q8_pair(char* row, int i, int P, float y0, float y1) {
-    // elements i (block i/32) and i + P (block (i+P)/32); the 32 lanes of
-    // this aligned group cover both blocks completely
-    float a0 = fabsf(y0), a1 = fabsf(y1);
-#pragma unroll
-    for (int m = 16; m >= 1; m >>= 1) {
-        a0 = fmaxf(a0, __shfl_xor(a0, m, 32));
-        a1 = fmaxf(a1, __shfl_xor(a1, m, 32));
-    }
-    const float d0 = a0 / 127.0f, d1 = a1 / 127.0f;
-    const float id0 = d0 != 0.0f ? 1.0f / d0 : 0.0f;
-    const float id1 = d1 != 0.0f ? 1.0f / d1 : 0.0f;
-    const int j0 = i, j1 = i + P;
-    char* b0 = row + (j0 / kQK8) * kQ8Bytes;
-    char* b1 = row + (j1 / kQK8) * kQ8Bytes;
-    if ((j0 & (kQK8 - 1)) == 0) {
-        *(uint16_t*)b0 = f32_to_f16(d0);
-        *(uint16_t*)b1 = f32_to_f16(d1);
-    }
-    b0[2 + (j0 & (kQK8 - 1))] = (char)(int8_t)roundf(y0 * id0);
-    b1[2 + (j1 & (kQK8 - 1))] = (char)(int8_t)roundf(y1 * id1);
-}
-
 __global__ void __launch_bounds__(256) rope_append_kernel(RopeAppendArgs a, int items_per_block) {
     const int t = blockIdx.x, b = blockIdx.y;
     const int P = a.d >> 1;

@@ -711,3 +711,185 @@ extern "C" int vva_supports(const vva_context* ctx, int head_dim, int n_q_heads,
     if (!float_type(q_type) || !cache_type(kv_type)) return 0;
     return head_dim_ok(head_dim, kv_type) ? 1 : 0;
 }
+
+// ------------------------------------------------------------ projections
+
+namespace {
+
+// A weight matrix ne = [K, M] of F16 or Q8_0 rows.
+vva_status check_weight(vva_context* ctx, const vva_tensor* w, const char* name, int64_t K, int64_t M, int type) {
+    vva_status st = check_tensor(ctx, w, name);
+    if (st != VVA_OK) return st;
+    if (w->type != type) return fail(ctx, VVA_ERR_INVALID_ARG, "%s: type %d, expected %d", name, w->type, type);
+    if (w->ne[0] != K || w->ne[1] != M || w->ne[2] != 1 || w->ne[3] != 1)
+        return fail(ctx, VVA_ERR_INVALID_ARG, "%s: ne=[%lld,%lld,%lld,%lld], expected [%lld,%lld,1,1]", name,
+                    (long long)w->ne[0], (long long)w->ne[1], (long long)w->ne[2], (long long)w->ne[3],
+                    (long long)K, (long long)M);
+    if ((int64_t)w->nb[0] != type_elem_bytes(type) || (int64_t)w->nb[1] < type_row_bytes(type, K))
+        return fail(ctx, VVA_ERR_INVALID_ARG, "%s: rows must be contiguous", name);
+    const size_t al = type == VVA_TYPE_F16 ? 16 : 4;
+    if ((uintptr_t)w->data % al || w->nb[1] % al)
+        return fail(ctx, VVA_ERR_INVALID_ARG, "%s: rows must be %zu-byte aligned", name, al);
+    if ((uint64_t)w->nb[1] * 128 >= ((uint64_t)1 << 31))
+        return fail(ctx, VVA_ERR_NOT_IMPLEMENTED, "%s: row stride too large", name);
+    return VVA_OK;
+}
+
+vva_status check_bias(vva_context* ctx, const vva_tensor* b, const char* name, int64_t M) {
+    if (!b) return VVA_OK;
+    vva_status st = check_tensor(ctx, b, name);
+    if (st != VVA_OK) return st;
+    if (b->type != VVA_TYPE_F32 || b->ne[0] != M || b->nb[0] != 4 || b->ne[1] * b->ne[2] * b->ne[3] != 1)
+        return fail(ctx, VVA_ERR_INVALID_ARG, "%s: must be F32 ne=[%lld]", name, (long long)M);
+    return VVA_OK;
+}
+
+// x / o rows: ne = [K, T, B, 1] (or [K, T, 1, 1]), contiguous rows of a float type.
+vva_status check_act(vva_context* ctx, const vva_tensor* x, const char* name, int64_t K, int64_t T, int64_t B) {
+    vva_status st = check_tensor(ctx, x, name);
+    if (st != VVA_OK) return st;
+    if (!float_type(x->type) || (int64_t)x->nb[0] != type_elem_bytes(x->type))
+        return fail(ctx, VVA_ERR_INVALID_ARG, "%s: F32/F16/BF16 with contiguous rows", name);
+    if (x->ne[0] != K || x->ne[1] != T || x->ne[2] != B || x->ne[3] != 1)
+        return fail(ctx, VVA_ERR_INVALID_ARG, "%s: ne=[%lld,%lld,%lld,%lld], expected [%lld,%lld,%lld,1]", name,
+                    (long long)x->ne[0], (long long)x->ne[1], (long long)x->ne[2], (long long)x->ne[3],
+                    (long long)K, (long long)T, (long long)B);
+    return VVA_OK;
+}
+
+}  // namespace
+
+extern "C" vva_status vva_qkv_rope_append(vva_context* ctx, vva_kv* kv, int layer, const vva_tensor* x,
+                                          const vva_tensor* wq, const vva_tensor* wk, const vva_tensor* wv,
+                                          const vva_tensor* bq, const vva_tensor* bk, const vva_tensor* bv,
+                                          const vva_tensor* pos, const int32_t* seq_ids, float freq_base,
+                                          const vva_tensor* q_out) {
+    if (!ctx) return VVA_ERR_INVALID_ARG;
+    if (!kv || !kv_live(kv) || kv->ctx != ctx)
+        return fail(ctx, VVA_ERR_INVALID_ARG, "qkv_rope_append: cache is null, released or of another context");
+    if (layer < 0 || layer >= kv->desc.n_layers) return fail(ctx, VVA_ERR_INVALID_ARG, "qkv_rope_append: layer %d", layer);
+    vva_status st;
+    if ((st = check_tensor(ctx, x, "x")) != VVA_OK) return st;
+    if ((st = check_tensor(ctx, q_out, "q_out")) != VVA_OK) return st;
+    if ((st = check_tensor(ctx, wq, "wq")) != VVA_OK) return st;
+    const int64_t d = kv->desc.head_dim, Hkv = kv->desc.n_kv_heads;
+    const int64_t K = x->ne[0], T = x->ne[1], B = x->ne[2];
+    const int64_t Hq = q_out->ne[1];
+    if (Hq < 1 || Hq % Hkv) return fail(ctx, VVA_ERR_INVALID_ARG, "qkv_rope_append: Hq %% Hkv != 0");
+    if (B > VVA_MAX_BATCH) return fail(ctx, VVA_ERR_INVALID_ARG, "qkv_rope_append: B > %d", VVA_MAX_BATCH);
+    const int wt = wq->type;
+    if (wt != VVA_TYPE_F16 && wt != VVA_TYPE_Q8_0)
+        return fail(ctx, VVA_ERR_NOT_IMPLEMENTED, "qkv_rope_append: weights must be F16 or Q8_0");
+    if (K % 64 || (Hq * d) % 128 || (Hkv * d) % 128 || (d != 64 && d != 128))
+        return fail(ctx, VVA_ERR_NOT_IMPLEMENTED,
+                    "qkv_rope_append: needs hidden %% 64 == 0, Hq*d and Hkv*d multiples of 128, head_dim 64 or 128");
+    if ((st = check_act(ctx, x, "x", K, T, B)) != VVA_OK) return st;
+    if ((st = check_weight(ctx, wq, "wq", K, Hq * d, wt)) != VVA_OK) return st;
+    if ((st = check_weight(ctx, wk, "wk", K, Hkv * d, wt)) != VVA_OK) return st;
+    if ((st = check_weight(ctx, wv, "wv", K, Hkv * d, wt)) != VVA_OK) return st;
+    if ((st = check_bias(ctx, bq, "bq", Hq * d)) != VVA_OK) return st;
+    if ((st = check_bias(ctx, bk, "bk", Hkv * d)) != VVA_OK) return st;
+    if ((st = check_bias(ctx, bv, "bv", Hkv * d)) != VVA_OK) return st;
+    if ((st = check_rows(ctx, q_out, "q_out", d, Hq, T, B)) != VVA_OK) return st;
+    int64_t ps = 0;
+    if ((st = check_pos(ctx, pos, T, B, &ps)) != VVA_OK) return st;
+    const int64_t N = T * B;
+    if (N * K * 2 >= ((int64_t)1 << 31) || 128 * K * 2 >= ((int64_t)1 << 31))
+        return fail(ctx, VVA_ERR_NOT_IMPLEMENTED, "qkv_rope_append: %lld x %lld inputs exceed 2 GiB", (long long)N,
+                    (long long)K);
+    ProjArgs a{};
+    for (int b = 0; b < B; ++b) {
+        const int seq = seq_ids ? seq_ids[b] : b;
+        if (seq < 0 || seq >= kv->desc.n_seq) return fail(ctx, VVA_ERR_INVALID_ARG, "qkv_rope_append: seq %d", seq);
+        for (int b2 = 0; b2 < b; ++b2)
+            if ((seq_ids ? seq_ids[b2] : b2) == seq)
+                return fail(ctx, VVA_ERR_INVALID_ARG, "qkv_rope_append: sequence %d appears twice", seq);
+        const int64_t past = kv->len[seq];
+        if (past + T > kv->desc.max_seq)
+            return fail(ctx, VVA_ERR_INVALID_ARG, "qkv_rope_append: seq %d: %lld + %lld rows exceed max_seq %d", seq,
+                        (long long)past, (long long)T, kv->desc.max_seq);
+        a.k_dst[b] = kv_tensor(kv, layer, seq, 0) + past * kv->row_bytes;
+        a.v_dst[b] = kv_tensor(kv, layer, seq, 1) + past * kv->row_bytes;
+    }
+    const vva_tensor* ws_[3] = {wq, wk, wv};
+    const vva_tensor* bs_[3] = {bq, bk, bv};
+    const int64_t rows[3] = {Hq * d, Hkv * d, Hkv * d};
+    int64_t m_end = 0;
+    for (int i = 0; i < 3; ++i) {
+        a.w[i] = (const char*)ws_[i]->data;
+        a.w_nb[i] = (int64_t)ws_[i]->nb[1];
+        m_end += rows[i];
+        a.m_end[i] = (int)m_end;
+        a.bias[i] = bs_[i] ? (const float*)bs_[i]->data : nullptr;
+    }
+    a.w_type = wt;
+    a.N = (int)N; a.K = (int)K; a.M = (int)m_end;
+    a.mode = kProjQKV;
+    a.q_out = (char*)q_out->data; a.q_out_type = q_out->type;
+    a.qo_nb_h = q_out->nb[1]; a.qo_nb_t = q_out->nb[2]; a.qo_nb_b = q_out->nb[3];
+    a.cache_row_bytes = kv->row_bytes;
+    a.cache_head_bytes = kv->head_bytes;
+    a.cache_type = kv->desc.type;
+    a.d = (int)d; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.T = (int)T;
+    ProjPrepArgs p{};
+    p.x = (const char*)x->data; p.x_type = x->type;
+    p.x_nb_t = (int64_t)x->nb[1]; p.x_nb_b = (int64_t)x->nb[2];
+    p.K = (int)K; p.T = (int)T; p.N = (int)N;
+    p.q8 = wt == VVA_TYPE_Q8_0;
+    p.pos = (const int32_t*)pos->data; p.pos_stride_b = ps;
+    p.P = (int)(d / 2);
+    p.theta_scale = powf(freq_base, -2.0f / (float)d);
+    DeviceGuard g(ctx->device);
+    if ((st = ensure_ws(ctx, proj_ws_bytes((int)N, (int)K, p.P))) != VVA_OK) return st;
+    hipError_t e = launch_proj(p, a, ctx->ws, ctx->stream);
+    return e == hipSuccess ? VVA_OK : hip_fail(ctx, e, "qkv_rope_append launch");
+}
+
+extern "C" vva_status vva_out_proj_residual(vva_context* ctx, const vva_tensor* o, const vva_tensor* w_o,
+                                            const vva_tensor* x, const vva_tensor* h) {
+    if (!ctx) return VVA_ERR_INVALID_ARG;
+    vva_status st;
+    if ((st = check_tensor(ctx, o, "o")) != VVA_OK) return st;
+    if ((st = check_tensor(ctx, w_o, "w_o")) != VVA_OK) return st;
+    if ((st = check_tensor(ctx, x, "x")) != VVA_OK) return st;
+    if ((st = check_tensor(ctx, h, "h")) != VVA_OK) return st;
+    const int64_t K = o->ne[0], T = o->ne[1], B = o->ne[2], M = w_o->ne[1];
+    const int wt = w_o->type;
+    if (wt != VVA_TYPE_F16 && wt != VVA_TYPE_Q8_0)
+        return fail(ctx, VVA_ERR_NOT_IMPLEMENTED, "out_proj_residual: weights must be F16 or Q8_0");
+    if (K % 64 || M % 128)
+        return fail(ctx, VVA_ERR_NOT_IMPLEMENTED, "out_proj_residual: needs in %% 64 == 0 and out %% 128 == 0");
+    if ((st = check_act(ctx, o, "o", K, T, B)) != VVA_OK) return st;
+    if ((st = check_weight(ctx, w_o, "w_o", K, M, wt)) != VVA_OK) return st;
+    if ((st = check_act(ctx, x, "x", M, T, B)) != VVA_OK) return st;
+    if ((st = check_act(ctx, h, "h", M, T, B)) != VVA_OK) return st;
+    if (x->type != VVA_TYPE_F32 || h->type != VVA_TYPE_F32)
+        return fail(ctx, VVA_ERR_INVALID_ARG, "out_proj_residual: x and h must be F32");
+    if ((uintptr_t)x->data % 16 || x->nb[1] % 16 || x->nb[2] % 16 || (uintptr_t)h->data % 16 || h->nb[1] % 16 ||
+        h->nb[2] % 16)
+        return fail(ctx, VVA_ERR_INVALID_ARG, "out_proj_residual: x and h rows must be 16-byte aligned");
+    const int64_t N = T * B;
+    if (N * K * 2 >= ((int64_t)1 << 31) || 128 * K * 2 >= ((int64_t)1 << 31))
+        return fail(ctx, VVA_ERR_NOT_IMPLEMENTED, "out_proj_residual: %lld x %lld inputs exceed 2 GiB", (long long)N,
+                    (long long)K);
+    ProjArgs a{};
+    a.w[0] = a.w[1] = a.w[2] = (const char*)w_o->data;
+    a.w_nb[0] = a.w_nb[1] = a.w_nb[2] = (int64_t)w_o->nb[1];
+    a.m_end[0] = a.m_end[1] = a.m_end[2] = (int)M;
+    a.w_type = wt;
+    a.N = (int)N; a.K = (int)K; a.M = (int)M;
+    a.mode = kProjResidual;
+    a.T = (int)T;
+    a.res = (const char*)x->data; a.res_nb_t = (int64_t)x->nb[1]; a.res_nb_b = (int64_t)x->nb[2];
+    a.h = (char*)h->data; a.h_nb_t = (int64_t)h->nb[1]; a.h_nb_b = (int64_t)h->nb[2];
+    ProjPrepArgs p{};
+    p.x = (const char*)o->data; p.x_type = o->type;
+    p.x_nb_t = (int64_t)o->nb[1]; p.x_nb_b = (int64_t)o->nb[2];
+    p.K = (int)K; p.T = (int)T; p.N = (int)N;
+    p.q8 = wt == VVA_TYPE_Q8_0;
+    p.P = 0;
+    DeviceGuard g(ctx->device);
+    if ((st = ensure_ws(ctx, proj_ws_bytes((int)N, (int)K, 0))) != VVA_OK) return st;
+    hipError_t e = launch_proj(p, a, ctx->ws, ctx->stream);
+    return e == hipSuccess ? VVA_OK : hip_fail(ctx, e, "out_proj_residual launch");
+}

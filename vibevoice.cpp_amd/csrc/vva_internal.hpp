@@ -77,6 +77,37 @@ struct AttnArgs {
 
 enum { kMaskNone = 0, kMaskExplicit = 1, kMaskCausal = 2 };
 
+// Linear layers around the attention (proj.hip).  Token row n = b * T + t.
+enum { kProjQKV = 0, kProjResidual = 1 };
+struct ProjPrepArgs {
+    const char* x; int x_type; int64_t x_nb_t, x_nb_b;   // rows of K elements (F32 / F16 / BF16)
+    int K, T, N;
+    int q8;                                              // Q8_0 round trip (Q8_0 weights)
+    uint16_t* xh;                                        // out: f16 [N][K]
+    const int32_t* pos; int64_t pos_stride_b;            // RoPE table (P > 0)
+    int P; float theta_scale;
+    float2* rope;                                        // out: [N][P] (cos, sin)
+};
+struct ProjArgs {
+    const char* w[3];            // weight matrices stacked along the output rows
+    int64_t w_nb[3];             // row stride in bytes
+    int m_end[3];                // first row past matrix i (cumulative)
+    const float* bias[3];        // F32 per output row, or null
+    int w_type;                  // F16 or Q8_0
+    const uint16_t* xh;          // the prep kernel's rows
+    int N, K, M;
+    int mode;
+    // kProjQKV: rows [0, Hq d) are q, then k, then v
+    const float2* rope;
+    char* q_out; int q_out_type; int64_t qo_nb_h, qo_nb_t, qo_nb_b;
+    char* k_dst[kMaxBatch]; char* v_dst[kMaxBatch];      // row 0 of this call's cache slots
+    int64_t cache_row_bytes, cache_head_bytes; int cache_type;
+    int d, Hq, Hkv, T;
+    // kProjResidual: h = y + res (F32 rows; may alias)
+    const char* res; int64_t res_nb_t, res_nb_b;
+    char* h; int64_t h_nb_t, h_nb_b;
+};
+
 // --------------------------------------------------------- host launchers
 
 hipError_t launch_rope_append(const RopeAppendArgs& a, hipStream_t s);
@@ -105,6 +136,9 @@ hipError_t launch_prefill(const AttnArgs& a, float* ws, int n_ks, hipStream_t s)
 bool prefill_supported(const AttnArgs& a);
 int prefill_plan(const AttnArgs& a, int n_cu);
 size_t prefill_ws_bytes(const AttnArgs& a, int n_ks);
+// Prep + GEMM of a linear layer; ws holds proj_ws_bytes(N, K, P) bytes.
+size_t proj_ws_bytes(int N, int K, int P);
+hipError_t launch_proj(ProjPrepArgs& p, ProjArgs& a, void* ws, hipStream_t s);
 
 }  // namespace vva
 
@@ -141,6 +175,32 @@ __device__ __forceinline__ float load_elem(const char* p, int type) {
 __device__ __forceinline__ void store_elem(char* p, int type, float f) {
     if (type == VVA_TYPE_F32) { *(float*)p = f; return; }
     *(uint16_t*)p = type == VVA_TYPE_F16 ? f32_to_f16(f) : f32_to_bf16(f);
+}
+
+// Q8_0 store of a NeoX rotation pair: elements i (block i/32) and i + P
+// (block (i+P)/32) of one head row.  Called by the 32 lanes of an aligned
+// group holding i = 32k .. 32k + 31, which cover both blocks completely, so
+// each block's amax is a 32-lane butterfly.  GGUF rule: d = amax / 127 (fp16),
+// codes round(x / d) with the fp32 d.
+__device__ __forceinline__ void store_q8_pair(char* row, int i, int P, float y0, float y1) {
+    float a0 = fabsf(y0), a1 = fabsf(y1);
+#pragma unroll
+    for (int m = 16; m >= 1; m >>= 1) {
+        a0 = fmaxf(a0, __shfl_xor(a0, m, 32));
+        a1 = fmaxf(a1, __shfl_xor(a1, m, 32));
+    }
+    const float d0 = a0 / 127.0f, d1 = a1 / 127.0f;
+    const float id0 = d0 != 0.0f ? 1.0f / d0 : 0.0f;
+    const float id1 = d1 != 0.0f ? 1.0f / d1 : 0.0f;
+    const int j0 = i, j1 = i + P;
+    char* b0 = row + (j0 / kQK8) * kQ8Bytes;
+    char* b1 = row + (j1 / kQK8) * kQ8Bytes;
+    if ((j0 & (kQK8 - 1)) == 0) {
+        *(uint16_t*)b0 = f32_to_f16(d0);
+        *(uint16_t*)b1 = f32_to_f16(d1);
+    }
+    b0[2 + (j0 & (kQK8 - 1))] = (char)(int8_t)roundf(y0 * id0);
+    b1[2 + (j1 & (kQK8 - 1))] = (char)(int8_t)roundf(y1 * id1);
 }
 
 }  // namespace vva

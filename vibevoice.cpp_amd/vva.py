@@ -31,7 +31,7 @@ EXPORTS = [
     "vva_version", "vva_kv_create", "vva_kv_free", "vva_kv_get_len", "vva_kv_set_len",
     "vva_kv_view", "vva_kv_upload", "vva_rope_ext", "vva_rope_append", "vva_attn",
     "vva_flash_attn_ext", "vva_supports", "vva_set_attn_path", "vva_last_decode_splits",
-    "vva_set_schedule", "vva_attn_noalloc",
+    "vva_set_schedule", "vva_attn_noalloc", "vva_qkv_rope_append", "vva_out_proj_residual",
 ]
 
 
@@ -96,6 +96,8 @@ def load_library(path: str = LIB_PATH):
         "vva_rope_append": (I, [P, P, I, TP, TP, TP, TP, P, F, TP]),
         "vva_attn": (I, [P, P, I, TP, P, TP, F, TP]),
         "vva_attn_noalloc": (I, [P, P, I, TP, P, TP, F, TP]),
+        "vva_qkv_rope_append": (I, [P, P, I, TP, TP, TP, TP, TP, TP, TP, TP, P, F, TP]),
+        "vva_out_proj_residual": (I, [P, TP, TP, TP, TP]),
         "vva_flash_attn_ext": (I, [P, TP, TP, TP, TP, F, F, F, TP]),
         "vva_supports": (I, [P, I, I, I, I, I]),
         "vva_set_attn_path": (I, [P, I]),
@@ -239,6 +241,22 @@ class Context:
         self.check(self.lib.vva_attn_noalloc(self.h, kv.h, layer, ctypes.byref(view(q)), ids, mp, scale,
                                              ctypes.byref(view(out))))
 
+    def qkv_rope_append(self, kv: "KVCache", layer: int, x, wq: "Weight", wk: "Weight", wv: "Weight", pos,
+                        q_out, bq=None, bk=None, bv=None, seq_ids=None, freq_base: float = 1.0e6):
+        """x: [B, T, hidden]; weights: Weight; biases f32 [rows] or None; q_out [B, T, Hq, d]."""
+        ids = _ids(seq_ids)
+        bref = [ctypes.byref(view(t)) if t is not None else None for t in (bq, bk, bv)]
+        self.check(self.lib.vva_qkv_rope_append(self.h, kv.h, layer, ctypes.byref(view(x)), ctypes.byref(wq.t),
+                                                ctypes.byref(wk.t), ctypes.byref(wv.t), bref[0], bref[1], bref[2],
+                                                ctypes.byref(view(pos)), ids, freq_base, ctypes.byref(view(q_out))))
+
+    def out_proj_residual(self, o, w_o: "Weight", x, h):
+        """o: [B, T, Hq*d] (or [B, T, Hq, d], viewed as rows); x, h: f32 [B, T, hidden]."""
+        if o.dim() == 4:
+            o = o.reshape(o.shape[0], o.shape[1], -1)
+        self.check(self.lib.vva_out_proj_residual(self.h, ctypes.byref(view(o)), ctypes.byref(w_o.t),
+                                                  ctypes.byref(view(x)), ctypes.byref(view(h))))
+
     def flash_attn_ext(self, q, k, v, out, scale: float, mask=None, k_view=None, v_view=None):
         """ggml layout: q torch [B, Hq, T, d] (ne=[d,T,Hq,B]); k, v torch [B, Hkv, L, d] or
         explicit Tensor views; out f32 [B, T, Hq, d] (ne=[d,Hq,T,B])."""
@@ -330,6 +348,19 @@ class KVCache:
         self.ctx.check(self.ctx.lib.vva_kv_upload(self.ctx.h, self.h, layer, seq, start, k_rows.shape[0],
                                                   ctypes.c_void_p(k_rows.ctypes.data),
                                                   ctypes.c_void_p(v_rows.ctypes.data)))
+
+
+class Weight:
+    """A linear layer's weight on the device: M rows of K elements, F16 or
+    Q8_0 (GGUF blocks along K), as ggml stores it (ne = [K, M]).  `raw` is a
+    uint8 torch tensor holding the rows back to back."""
+
+    def __init__(self, raw, w_type: int, K: int, M: int):
+        self.raw, self.w_type, self.K, self.M = raw, w_type, K, M
+        rb = K * 2 if w_type == F16 else K // 32 * Q8_BLOCK_BYTES
+        assert raw.numel() == rb * M
+        es = 2 if w_type == F16 else Q8_BLOCK_BYTES
+        self.t = view(raw, ggml_ne=[K, M, 1, 1], ggml_nb=[es, rb, rb * M, rb * M], type_=w_type)
 
 
 _hip_lib = None
