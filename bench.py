@@ -318,6 +318,110 @@ def run_decode_small(torch, vva, ctx, steps: int):
             "timing": "HIP events around `steps` back-to-back steps; graph: one captured step replayed"}
 
 
+def run_proj(torch, vva, vvo, reps: int = 10):
+    """The fused projections at 7B shapes (hidden 3584, 28 q / 4 kv heads,
+    d = 128), F16 and Q8_0 weights: vva_qkv_rope_append (q/k/v GEMM + bias +
+    RoPE + F16 cache append) and vva_out_proj_residual, each on a 4096-token
+    prefill chunk (MFMA-bound; FLOP = 2 N K M) and on the CFG decode step
+    (2 tokens; bound by streaming the weights: bytes = weight bytes).  HIP
+    events around `reps` back-to-back calls."""
+    ctx = vva.Context(0)
+    rng = np.random.default_rng(17)
+    hidden, M_qkv = HQ * D, (HQ + 2 * HKV) * D
+    out = {}
+    for wt, name in ((vva.F16, "f16"), (vva.Q8_0, "q8_0")):
+        wraw = {}
+        for key, (m, k) in {"q": (HQ * D, hidden), "k": (HKV * D, hidden), "v": (HKV * D, hidden),
+                            "o": (hidden, HQ * D)}.items():
+            w = (rng.standard_normal((m, k)) * k ** -0.5).astype(np.float32)
+            wraw[key] = vva.Weight(torch.from_numpy(vvo.from_f32(w, wt)).cuda(), wt, k, m)
+        wbytes_qkv = sum(wraw[k_].raw.numel() for k_ in "qkv")
+        wbytes_o = wraw["o"].raw.numel()
+        for T, B in ((4096, 1), (1, 2)):
+            kv = vva.KVCache(ctx, 1, HKV, D, T + 8, B, vva.F16)
+            x = torch.randn((B, T, hidden), device="cuda")
+            q_out = torch.empty((B, T, HQ, D), dtype=torch.float16, device="cuda")
+            o = torch.randn((B, T, HQ * D), device="cuda")
+            h = torch.empty((B, T, hidden), device="cuda")
+            pos = torch.arange(T, dtype=torch.int32, device="cuda")
+            calls = {
+                "qkv": lambda: ctx.qkv_rope_append(kv, 0, x, wraw["q"], wraw["k"], wraw["v"], pos, q_out),
+                "o": lambda: ctx.out_proj_residual(o, wraw["o"], x, h),
+            }
+            for op, fn in calls.items():
+                for _ in range(3):
+                    fn()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                torch.cuda.synchronize()
+                e0.record()
+                for _ in range(reps):
+                    fn()
+                e1.record()
+                torch.cuda.synchronize()
+                us = e0.elapsed_time(e1) * 1e3 / reps
+                M = M_qkv if op == "qkv" else hidden
+                flops = 2.0 * B * T * hidden * M
+                entry = {"us_per_call": round(us, 2), "tflops": round(flops / us / 1e6, 1)}
+                if T > 1:
+                    entry["frac_of_mfma_peak"] = round(flops / us / 1e6 / PEAK_F16_TFLOPS, 4)
+                else:
+                    wb = wbytes_qkv if op == "qkv" else wbytes_o
+                    entry["weight_gbs"] = round(wb / us / 1e3, 1)
+                    entry["frac_of_hbm_peak"] = round(wb / us / 1e3 / PEAK_HBM_GBS, 4)
+                out[f"{op}_{name}_T{T}xB{B}"] = entry
+            kv.free()
+    ctx.close()
+    return {"workload": "Qwen2.5-7B-shaped projections: q/k/v GEMM + bias + RoPE + F16 cache append "
+                        "(vva_qkv_rope_append) and output projection + residual (vva_out_proj_residual), "
+                        "F16 and Q8_0 weights, 4096-token chunk and 2-token CFG decode step",
+            "timing": f"HIP events around {reps} back-to-back calls (prep + GEMM kernels)", **out}
+
+
+def run_small_prefills(torch, vva, reps: int = 20):
+    """The two short prefill configurations, attention launch only (after the
+    RoPE + append), HIP events around `reps` launches per layer of a 28- (or
+    24-) layer stack:
+      C1  0.5B heads (14 q / 2 kv, d = 64), 256 tokens, F32 Q/K/V and F32
+          cache: the fp32 path (eager semantics, 1e-4 tolerance);
+      C3  1.5B heads (12 q / 2 kv, d = 128), 4096 tokens, bf16 Q/K/V, F16
+          cache: the MFMA flash prefill."""
+    ctx = vva.Context(0)
+    res = {}
+    for name, (d, hq, hkv, T, layers, qt, ct) in {
+            "c1_0p5b_fp32_T256": (64, 14, 2, 256, 24, torch.float32, vva.F32),
+            "c3_1p5b_T4096": (128, 12, 2, 4096, 28, torch.bfloat16, vva.F16)}.items():
+        kv = vva.KVCache(ctx, layers, hkv, d, T, 1, ct)
+        q = torch.randn((1, T, hq, d), device="cuda").to(qt)
+        k = torch.randn((1, T, hkv, d), device="cuda").to(qt)
+        v = torch.randn((1, T, hkv, d), device="cuda").to(qt)
+        qr = torch.empty((1, T, hq, d), dtype=torch.float32 if ct == vva.F32 else torch.float16, device="cuda")
+        out = torch.empty((1, T, hq, d), dtype=torch.float32, device="cuda")
+        pos = torch.arange(T, dtype=torch.int32, device="cuda")
+        kv.set_len(0, 0)
+        for layer in range(layers):
+            ctx.rope_append(kv, layer, q, k, v, pos, qr, freq_base=THETA)
+        ev = []
+        for rep in range(reps + 2):
+            for layer in range(layers):
+                e = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                e[0].record()
+                ctx.attn(kv, layer, qr, out, d ** -0.5)
+                e[1].record()
+                if rep >= 2:
+                    ev.append(e)
+        torch.cuda.synchronize()
+        ms = float(np.mean([a.elapsed_time(b) for a, b in ev]))
+        flops = 4.0 * hq * d * T * (T + 1) / 2
+        peak = 157.3 if ct == vva.F32 else PEAK_F16_TFLOPS
+        res[name] = {"attn_ms_per_layer": round(ms, 4), "tflops": round(flops / ms / 1e9, 2),
+                     "peak_tflops": peak, "frac": round(flops / ms / 1e9 / peak, 4), "layers": layers,
+                     "flop_per_layer": flops}
+        kv.free()
+    ctx.close()
+    res["timing"] = "HIP events around each attention launch, mean over layers x reps"
+    return res
+
+
 def cpu_baseline_prefill(torch, vva, vvo, kv, qr):
     """Oracle (ggml-order mode, all host cores) on layer 0: 1024 query rows spread over [0, 32k)."""
     rows = np.linspace(0, T_PREFILL - 1, 1024).astype(np.int32)
@@ -369,7 +473,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the chunked ASR prefill (64 x 512) and the 0.5B F16 decode step (eager and graph)")
-    ap.add_argument("--only", choices=["prefill", "decode", "both", "copy"], default="both",
+    ap.add_argument("--only", choices=["prefill", "decode", "both", "copy", "proj", "small"], default="both",
                     help="copy: a plain 1 GiB device-to-device copy, the reference for FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -390,6 +494,10 @@ def main() -> int:
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_per_launch": n, "launches": 3}), flush=True)
+        return 0
+    if args.only in ("proj", "small"):
+        r = run_proj(torch, vva, vvo) if args.only == "proj" else run_small_prefills(torch, vva)
+        print(json.dumps({args.only: r}), flush=True)
         return 0
     ctx = vva.Context(0)
     line = {
@@ -440,6 +548,9 @@ def main() -> int:
         line["prefill_chunked"] = run_prefill_chunked(torch, vva, ctx, layers=2)
         torch.cuda.empty_cache()
         line["decode_small"] = run_decode_small(torch, vva, ctx, steps=200)
+        line["prefill_small"] = run_small_prefills(torch, vva)
+        torch.cuda.empty_cache()
+        line["proj"] = run_proj(torch, vva, vvo)
     ctx.close()
     print(json.dumps(line), flush=True)
     return 0
