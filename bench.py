@@ -473,7 +473,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the chunked ASR prefill (64 x 512) and the 0.5B F16 decode step (eager and graph)")
-    ap.add_argument("--only", choices=["prefill", "decode", "both", "copy", "proj", "small"], default="both",
+    ap.add_argument("--only", choices=["prefill", "decode", "both", "copy", "proj", "small", "chunked"],
+                    default="both",
                     help="copy: a plain 1 GiB device-to-device copy, the reference for FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -495,8 +496,13 @@ def main() -> int:
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_per_launch": n, "launches": 3}), flush=True)
         return 0
-    if args.only in ("proj", "small"):
-        r = run_proj(torch, vva, vvo) if args.only == "proj" else run_small_prefills(torch, vva)
+    if args.only in ("proj", "small", "chunked"):
+        if args.only == "chunked":
+            c = vva.Context(0)
+            r = run_prefill_chunked(torch, vva, c, layers=2)
+            c.close()
+        else:
+            r = run_proj(torch, vva, vvo) if args.only == "proj" else run_small_prefills(torch, vva)
         print(json.dumps({args.only: r}), flush=True)
         return 0
     ctx = vva.Context(0)

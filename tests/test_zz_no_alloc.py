@@ -5,9 +5,10 @@ Two calls in a row per path, the second with a smaller input, so the second
 reads a scratch that still holds the first call's partials.  The same
 kernels run with the same split counts, so the outputs must agree to the
 path's tolerance (2e-3 max-abs / 1e-3 mean-abs for F16 / Q8_0 caches); the
-test also reports whether they are bit-identical.  A forced split count
-whose partials exceed the scratch is refused with VVA_ERR_INVALID_ARG before
-anything is enqueued.
+test also reports whether they are bit-identical.  The prefill planner
+keeps the no-alloc call's partials within the scratch (it may choose fewer
+key splits); a forced split count whose partials exceed the scratch is
+refused with VVA_ERR_INVALID_ARG before anything is enqueued.
 """
 import numpy as np
 import pytest
@@ -64,9 +65,11 @@ def test_noalloc_prefill_key_splits_match_attn(ctx, torch_gpu, T, past):
     rng = np.random.default_rng(T)
     q = to_gpu(torch, rng.standard_normal((1, T, Hq, d)), vva.F16)
     (a, sa), (b, sb) = _both(ctx, torch, kv, q, d ** -0.5)
-    assert sa == sb and sa > 1, (sa, sb)
+    # the planner keeps the no-alloc call's partials within the scratch, so
+    # its split count may be smaller: equal to the split-count tolerance
+    assert sa > 1 and sb > 1, (sa, sb)
     mx, mn = assert_close(b, a, *TOL, what="noalloc prefill vs attn")
-    print(f"  key splits {sa}: max {mx:.2e} mean {mn:.2e}; bit-identical {np.array_equal(a, b)}")
+    print(f"  key splits {sa} / {sb}: max {mx:.2e} mean {mn:.2e}; bit-identical {np.array_equal(a, b)}")
     kv.free()
 
 

@@ -51,6 +51,10 @@
 // flash attention does.
 #include "vva_internal.hpp"
 
+#include <algorithm>
+#include <functional>
+#include <vector>
+
 namespace vva {
 
 namespace {
@@ -67,14 +71,30 @@ typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) char lds_char;
 
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kLazy = 15.0f;     // headroom of p over 2^0 in log2 units: p <= 2^15 (f16-safe)
+constexpr float kLazy = 8.0f;      // running-max slack in log2 units: p <= 2^8 (f16-safe, rare rescales)
 constexpr int kBN = 64;            // keys per tile
-constexpr int kRowsWave = 64;      // query rows per wave
-constexpr int kWaves = 4;
+constexpr int kRowsWave = 32;      // query rows per wave: one 32-wide MFMA column block
+constexpr int kWaves = 8;          // two per SIMD
 constexpr int kRowsWG = kRowsWave * kWaves;
 constexpr int kStages = 4;         // LDS ring: tile j + 3 loads while tile j is computed
-constexpr int kMaxRestarts = 16;   // bound on key-loop restarts per workgroup
 constexpr int kMaxKeySplits = 32;  // key splits per row tile
+
+// Key tiles of row tile rt (rows rt * kRowsWG ..) of sequence b: the keys
+// its last row sees (causal), or all of them.
+__host__ __device__ inline int rt_key_tiles(const AttnArgs& a, int b, int rt, bool causal) {
+    const int g = a.Hq / a.Hkv, nrows = a.T * g;
+    const int t_hi = min(a.T - 1, (min((rt + 1) * kRowsWG, nrows) - 1) / g);
+    const int kend = causal ? min(a.L[b], a.past[b] + t_hi + 1) : a.L[b];
+    return (kend + kBN - 1) / kBN;
+}
+// Workgroups row tile rt is split over.
+__host__ __device__ inline int rt_splits(const PrefillPlan& p, int rt) {
+    return p.forced > 0 ? p.forced : (rt >= p.R ? p.n : 1);
+}
+// Pieces (workgroups per kv head and sequence) of a plan over n_rt row tiles.
+__host__ __device__ inline int plan_pieces(const PrefillPlan& p, int n_rt) {
+    return p.forced > 0 ? n_rt * p.forced : (n_rt - p.R) * p.n + p.R;
+}
 
 // buffer_load_dwordx4 ... lds: each lane's 16 bytes land at LDS address
 // m0 + 16 * lane.  Issued as inline asm so the compiler does not fence LDS
@@ -89,14 +109,14 @@ __device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t lds_addr, int voffset
                  : "memory", "m0");
 }
 
+// Raw buffer descriptor as four wave-uniform dwords (kept in SGPRs for the
+// inline-asm loads): base address (48 bits, stride 0), range in bytes, and
+// the gfx9 raw-buffer configuration word; loads past the range return 0.
 __device__ __forceinline__ i32x4 make_rsrc(const char* base, uint32_t bytes) {
-    const __amdgpu_buffer_rsrc_t r =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), (short)0, (int)bytes, 0x00020000);
-    i32x4 v;
-    __builtin_memcpy(&v, &r, 16);
-    // wave-uniform: keep it in SGPRs for the inline-asm loads
-    return i32x4{__builtin_amdgcn_readfirstlane(v.x), __builtin_amdgcn_readfirstlane(v.y),
-                 __builtin_amdgcn_readfirstlane(v.z), __builtin_amdgcn_readfirstlane(v.w)};
+    const uint64_t p = (uint64_t)(uintptr_t)base;
+    return i32x4{__builtin_amdgcn_readfirstlane((int)(uint32_t)p),
+                 __builtin_amdgcn_readfirstlane((int)((uint32_t)(p >> 32) & 0xffffu)),
+                 __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000};
 }
 
 // wait until at most N of this wave's loads are outstanding (and its LDS
@@ -170,7 +190,7 @@ __device__ __forceinline__ const lds_char* lds_at(uint32_t addr) { return (const
 
 // EXPL: explicit F16 mask (otherwise implicit causal / length masking only).
 template <int D, int KT, bool EXPL>
-__global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a, float* __restrict__ ws, int n_ks) {
+__global__ void __launch_bounds__(kWaves * 64) prefill_kernel(AttnArgs a, float* __restrict__ ws, PrefillPlan plan) {
     using F = Frag<KT>;
     using QF = typename F::type;
     constexpr int DS = D / 16;                     // 16-dim MFMA steps of Q.K
@@ -195,15 +215,26 @@ __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a, float* __restr
     const int tid = threadIdx.x;
     const int lane = tid & 63, half = lane >> 5, l32 = lane & 31;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int b = blockIdx.z, kvh = blockIdx.y;
+    const int b = blockIdx.z;
     const int g = a.Hq / a.Hkv;
     const int nrows = a.T * g;
     const int n_rt = (nrows + kRowsWG - 1) / kRowsWG;
-    const int ks = (int)blockIdx.x % n_ks;                       // key split of the row tile
-    const int R0 = (n_rt - 1 - (int)blockIdx.x / n_ks) * kRowsWG;   // heaviest tiles first
+    const bool causal = !EXPL && a.mask_mode == kMaskCausal;
+    // Workgroups go out heaviest row tile first, the kv heads innermost (so
+    // every head's heaviest tiles start in the first round), then the row
+    // tile's key splits: piece x of the sequence is found by walking the row
+    // tiles from the last (heaviest) down.
+    const int kvh = (int)blockIdx.x % a.Hkv;
+    const int x = (int)blockIdx.x / a.Hkv;
+    const int nh = plan.forced > 0 ? plan.forced : plan.n;                // splits of a heavy row tile
+    const int R = plan.forced > 0 ? 0 : plan.R;
+    const int heavy = (n_rt - R) * nh;                                   // pieces of the heavy row tiles
+    const int rt = x < heavy ? n_rt - 1 - x / nh : R - 1 - (x - heavy);
+    const int ks = x < heavy ? x % nh : 0;                               // key split of the row tile
+    const int n_ks = x < heavy ? nh : 1;
+    const int R0 = rt * kRowsWG;
     const int wr0 = R0 + w * kRowsWave;
     const int L = a.L[b], past = a.past[b];
-    const bool causal = !EXPL && a.mask_mode == kMaskCausal;
 
     // key range of the workgroup and of this wave
     const int t_hi_wg = min(a.T - 1, (min(R0 + kRowsWG, nrows) - 1) / g);
@@ -217,14 +248,17 @@ __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a, float* __restr
     const bool wave_live = wr0 < nrows;
     const int t_lo_w = min(a.T - 1, wr0 / g);
     const int t_hi_w = min(a.T - 1, (min(wr0 + kRowsWave, nrows) - 1) / g);
+    // keys [0, kend_w) are seen by some row of the wave; keys up to lim_w by
+    // every row (a tile whose last key is at most lim_w needs no mask)
     const int kend_w = !wave_live ? 0 : (causal ? min(L, past + t_hi_w + 1) : L);
+    const int lim_w = causal ? min(L - 1, past + t_lo_w) : L - 1;
 
-    // ---- tile loads: per lane and 1 KB chunk q = i * 4 + w of an operand,
-    // the byte x = 1024 q + 16 lane of the padded tile is row x / pitch,
-    // column x % pitch; pad bytes load from an offset past the buffer (0
-    // bytes read, zeros written), and a wave's loads past the last chunk
-    // write zeros to the junk kilobyte (every wave issues the same number
-    // of loads per tile, with no branch)
+    // ---- tile loads: per lane and 1 KB chunk q = i * kWaves + w of an
+    // operand, the byte x = 1024 q + 16 lane of the padded tile is row x /
+    // pitch, column x % pitch; pad bytes load from an offset past the buffer
+    // (0 bytes read, zeros written), and a wave's loads past the last chunk
+    // write zeros to the junk kilobyte (every wave issues the same number of
+    // loads per tile, with no branch)
     const uint32_t nbk = (uint32_t)a.k_nb_tok, nbv = (uint32_t)a.v_nb_tok;
     const int kl = max(L - kb0, 1);                           // rows from the split's first key
     const i32x4 krs = make_rsrc(a.k[b] + kvh * a.k_nb_head + (int64_t)kb0 * nbk, (uint32_t)(kl - 1) * nbk + 2 * D);
@@ -243,18 +277,16 @@ __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a, float* __restr
         voff[i] = r < kBN && c < 2 * D ? (int)(r * nbv) + c : 0x40000000;
     }
     const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_char*)lds;
-    // loads lo .. hi - 1 of this wave's NLD for tile j (K chunks, then V).
-    // A dead load (a tile past the last one, or any load once a restart is
-    // decided) reads from past the buffer (zeros, no memory traffic) into
-    // the junk kilobyte, so the count of loads per tile stays the same and
-    // no stage is touched.
-    auto issue_range = [&](int j, int lo, int hi, bool live) {
+    // the loads of tile j (K chunks, then V); a tile past the last one reads
+    // from past the buffer (zeros, no memory traffic) into the junk
+    // kilobyte, so the count of loads per tile stays the same
+    auto issue = [&](int j) {
+        const bool live = j < n_tiles;
         const uint32_t st = lds0 + (j % kStages) * STAGE;
         const int sk = live ? (int)((uint32_t)(j * kBN) * nbk) : 0x40000000;
         const int sv = live ? (int)((uint32_t)(j * kBN) * nbv) : 0x40000000;
 #pragma unroll
         for (int i = 0; i < NLD; ++i) {
-            if (i < lo || i >= hi) continue;
             if (i < NIK) {
                 const int c = i * kWaves + w;
                 dma16(krs, live && c < NCK ? st + c * 1024 : lds0 + JUNK, koff[i], sk);
@@ -264,510 +296,227 @@ __global__ void __launch_bounds__(256) prefill_kernel(AttnArgs a, float* __restr
             }
         }
     };
-    auto issue = [&](int j) { issue_range(j, 0, NLD, j < n_tiles); };
-    // workgroup OR of `flag` at the barrier that ends tile j: each wave
-    // publishes its own word in a slot that alternates with j (a slot is
-    // rewritten two tiles later, after every wave has read it)
-    __shared__ int any_flag[2][kWaves];
+    // tile 0 goes out before Q is loaded: the wait for Q then covers it
+    // (the loads complete in order), and tiles 1 and 2 follow once Q is in
+    // registers
+    issue(0);
 
-    // ---- this lane's query rows (one per 32-row column block) and Q^T
-    // fragments, rounded to K's type; one loop nest per Q type so the loads
-    // of a nest issue back to back
-    int tcol[2];
-    const char* qrow[2];
-    bool qok[2];
-#pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
-        const int row = wr0 + cb * 32 + l32;
-        qok[cb] = row < nrows;
-        const int t = qok[cb] ? row / g : 0;
-        const int h = kvh * g + (qok[cb] ? row % g : 0);
-        tcol[cb] = qok[cb] ? t : a.T - 1;
-        qrow[cb] = a.q + b * a.q_nb_b + t * a.q_nb_t + h * a.q_nb_h;
-    }
-    QF qf[2][DS];
-    u32x4 qraw[2][DS];
-    if (a.q_type == VVA_TYPE_F32) {
-        float4 x[2][DS][2];
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb)
+    // ---- this lane's query row (column l32 of the wave's 32-row block) and
+    // its Q^T fragments, rounded to K's type
+    const int row = wr0 + l32;
+    const bool qok = row < nrows;
+    const int tcol = qok ? row / g : a.T - 1;
+    const char* qrow = a.q + b * a.q_nb_b + (int64_t)(qok ? row / g : 0) * a.q_nb_t +
+                       (int64_t)(kvh * g + (qok ? row % g : 0)) * a.q_nb_h;
+    QF qf[DS];
+    {
+        u32x4 qraw[DS];
+        if (a.q_type == VVA_TYPE_F32) {
+            float4 x[DS][2];
 #pragma unroll
             for (int ds = 0; ds < DS; ++ds) {
                 const int d0 = ds * 16 + half * 8;
-                x[cb][ds][0] = *(const float4*)(qrow[cb] + d0 * 4);
-                x[cb][ds][1] = *(const float4*)(qrow[cb] + d0 * 4 + 16);
+                x[ds][0] = *(const float4*)(qrow + d0 * 4);
+                x[ds][1] = *(const float4*)(qrow + d0 * 4 + 16);
             }
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
             for (int ds = 0; ds < DS; ++ds) {
-                const float4 x0 = x[cb][ds][0], x1 = x[cb][ds][1];
-                qraw[cb][ds] = u32x4{F::cvt(x0.x) | ((uint32_t)F::cvt(x0.y) << 16), F::cvt(x0.z) | ((uint32_t)F::cvt(x0.w) << 16),
-                                     F::cvt(x1.x) | ((uint32_t)F::cvt(x1.y) << 16), F::cvt(x1.z) | ((uint32_t)F::cvt(x1.w) << 16)};
+                const float4 x0 = x[ds][0], x1 = x[ds][1];
+                qraw[ds] = u32x4{F::cvt(x0.x) | ((uint32_t)F::cvt(x0.y) << 16), F::cvt(x0.z) | ((uint32_t)F::cvt(x0.w) << 16),
+                                 F::cvt(x1.x) | ((uint32_t)F::cvt(x1.y) << 16), F::cvt(x1.z) | ((uint32_t)F::cvt(x1.w) << 16)};
             }
-    } else {
+        } else {
 #pragma unroll
-        for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-            for (int ds = 0; ds < DS; ++ds) qraw[cb][ds] = *(const u32x4*)(qrow[cb] + (ds * 16 + half * 8) * 2);
-        if (a.q_type != KT) {           // the other 16-bit type
-            const int qt = a.q_type;
-#pragma unroll
-            for (int cb = 0; cb < 2; ++cb)
+            for (int ds = 0; ds < DS; ++ds) qraw[ds] = *(const u32x4*)(qrow + (ds * 16 + half * 8) * 2);
+            if (a.q_type != KT) {           // the other 16-bit type
+                const int qt = a.q_type;
 #pragma unroll
                 for (int ds = 0; ds < DS; ++ds) {
-                    const u32x4 r = qraw[cb][ds];
+                    const u32x4 r = qraw[ds];
                     const uint32_t rw[4] = {r.x, r.y, r.z, r.w};
                     uint32_t cw[4];
 #pragma unroll
                     for (int k = 0; k < 4; ++k)
                         cw[k] = F::cvt(bits16_to_f32(rw[k] & 0xffffu, qt)) |
                                 ((uint32_t)F::cvt(bits16_to_f32(rw[k] >> 16, qt)) << 16);
-                    qraw[cb][ds] = u32x4{cw[0], cw[1], cw[2], cw[3]};
+                    qraw[ds] = u32x4{cw[0], cw[1], cw[2], cw[3]};
                 }
+            }
         }
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds) qf[ds] = as_vec<QF>(qok ? qraw[ds] : u32x4{0u, 0u, 0u, 0u});
     }
-#pragma unroll
-    for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-        for (int ds = 0; ds < DS; ++ds) qf[cb][ds] = as_vec<QF>(qok[cb] ? qraw[cb][ds] : u32x4{0u, 0u, 0u, 0u});
+    issue(1);
+    issue(2);
 
-    float m[2] = {-INFINITY, -INFINITY};
-    float lsum[2] = {0.0f, 0.0f};
-    f32x16 o[DT][2];
+    // Running max m (log2 domain) of the lane's row, raised lazily: only when
+    // a tile's row max passes it by more than kLazy, so p <= 2^kLazy in f16
+    // and O / the row sum are rescaled rarely.
+    float m = -INFINITY, lsum = 0.0f;
+    f32x16 o[DT];
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb) o[dt][cb] = f32x16{};
-
+    for (int dt = 0; dt < DT; ++dt) o[dt] = f32x16{};
     const float sl2 = a.scale * kLog2e;
     // per-lane LDS offsets of the operand reads within a stage
     const int k_rd = l32 * KP + half * 16;                                   // K: key l32, dims 8 half ..
     const int v_rd = ((lane & 15) >> 2) * VP + (16 * ((lane >> 4) & 1) + 4 * (lane & 3)) * 2 +
                      4 * half * VP;                                          // V^T, see v_frag
+    const char* mrow = EXPL ? a.mask + b * a.mask_nb_b + tcol * a.mask_nb_row : nullptr;
 
-    // S^T of one 32-key half of the tile; ka = stage K base + k_rd, so
-    // every read is at an immediate offset
-    auto s_half = [&](const lds_char* ka, int kt, f32x16 (&s)[2]) {
+    // S^T of the tile's two 32-key halves: key 8 (r / 4) + 4 half + r % 4
+    // of half kt in register r, for the lane's row
+    // (the two halves' MFMA chains interleaved, every K fragment of the tile
+    // read up front)
+    auto scores = [&](const lds_char* ka, f32x16 (&s)[2]) {
+        u32x4 kraw[2][DS];
 #pragma unroll
-        for (int ds = 0; ds < DS; ++ds) {
-            const u32x4 kraw = *(const __attribute__((address_space(3))) u32x4*)(ka + kt * 32 * KP + ds * 32);
-            const QF kf = as_vec<QF>(kraw);
+        for (int ds = 0; ds < DS; ++ds)
 #pragma unroll
-            for (int cb = 0; cb < 2; ++cb) s[cb] = ds == 0 ? F::mma(kf, qf[cb][0], f32x16{}) : F::mma(kf, qf[cb][ds], s[cb]);
-        }
+            for (int kt = 0; kt < 2; ++kt)
+                kraw[kt][ds] = *(const __attribute__((address_space(3))) u32x4*)(ka + kt * 32 * KP + ds * 32);
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds)
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+                s[kt] = F::mma(as_vec<QF>(kraw[kt][ds]), qf[ds], ds == 0 ? f32x16{} : s[kt]);
     };
-    // p = 2^(x * mul - m) as f16 in the order of the second product's k
-    // steps, row sums from the f16 values
-    auto probs = [&](const f32x16 (&s)[2], float mul, h8 (&pf)[2][2]) {
+    // Masked keys to -inf and explicit mask values added in score units
+    // (mask / scale, so that 2^(s * scale * log2 e) carries e^mask).  MASKED:
+    // the tile may hold keys past the row's last visible one (causal or
+    // length) or the caller passed a mask.
+    const float inv_scale = 1.0f / a.scale;
+    auto apply_mask = [&](f32x16 (&s)[2], int k0) {
+        const int lim = causal ? min(L - 1, past + tcol) : L - 1;
 #pragma unroll
-        for (int cb = 0; cb < 2; ++cb) {
-            const float nb = m[cb] == -INFINITY ? 0.0f : -m[cb];
-            float ps = lsum[cb];
+        for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
+            for (int r = 0; r < 16; ++r) {
+                const int key = k0 + kt * 32 + 8 * (r / 4) + 4 * half + (r % 4);
+                float x = s[kt][r];
+                if constexpr (EXPL)
+                    x = fmaf(f16_to_f32(*(const uint16_t*)(mrow + 2 * min(key, L - 1))), inv_scale, x);
+                s[kt][r] = key > lim ? -INFINITY : x;
+            }
+    };
+    // online softmax of the tile's raw scores s, then O^T += V^T P^T: P^T is
+    // converted in place from the S^T registers (the key order of each
+    // 16-key MFMA step is the accumulator's own order).  p = 2^(s * scale *
+    // log2 e - m), one fma and one exp2 per score.
+    auto softmax_pv = [&](const lds_char* va, f32x16 (&s)[2]) {
+        float mr = fmaxf(fmaxf(s[0][0], s[0][1]), s[0][2]);
+#pragma unroll
+        for (int r = 3; r < 15; r += 2) mr = fmaxf(fmaxf(mr, s[0][r]), s[0][r + 1]);
+        mr = fmaxf(mr, s[0][15]);
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) mr = fmaxf(fmaxf(mr, s[1][r]), s[1][r + 1]);
+        const float mx = max_swap32(mr) * sl2;                   // with the row's other 32 keys
+        if (__any(mx > m + kLazy)) {
+            if (mx > m + kLazy) {
+                const float alpha = __builtin_amdgcn_exp2f(m - mx);   // 0 while m = -inf
+                lsum *= alpha;
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+                m = mx;
+            }
+        }
+        const float nb = m == -INFINITY ? 0.0f : -m;            // no visible key yet: every s is -inf
+        h8 pf[2][2];
+        float ps = lsum;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int k2 = 0; k2 < 2; ++k2) {
                 h8 pv;
 #pragma unroll
                 for (int e = 0; e < 8; e += 2) {
-                    const float p0 = __builtin_amdgcn_exp2f(fmaf(s[cb][ks * 8 + e], mul, nb));
-                    const float p1 = __builtin_amdgcn_exp2f(fmaf(s[cb][ks * 8 + e + 1], mul, nb));
-                    h2 pp = {(_Float16)p0, (_Float16)p1};
+                    const float p0 = __builtin_amdgcn_exp2f(fmaf(s[kt][k2 * 8 + e], sl2, nb));
+                    const float p1 = __builtin_amdgcn_exp2f(fmaf(s[kt][k2 * 8 + e + 1], sl2, nb));
+                    const h2 pp = {(_Float16)p0, (_Float16)p1};
                     pv[e] = pp.x;
                     pv[e + 1] = pp.y;
                     ps = __builtin_amdgcn_fdot2(pp, h2{(_Float16)1.0f, (_Float16)1.0f}, ps, false);
                 }
-                pf[cb][ks] = pv;
+                pf[kt][k2] = pv;
             }
-            lsum[cb] = ps;
-        }
-    };
-    // O^T += V^T P^T for the two 16-key steps of half kt; va = stage V base
-    // + v_rd
-    auto pv_half = [&](const lds_char* va, int kt, const h8 (&pf)[2][2]) {
+        lsum = ps;
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
+        for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                const int kk = (kt * 2 + ks) * 16;
-                const lds_char* base = va + dt * 64;
-                const h8 vf = v_frag<KT>(base + kk * VP, base + (kk + 8) * VP);
+            for (int k2 = 0; k2 < 2; ++k2) {
+                const int kk = (kt * 2 + k2) * 16;
 #pragma unroll
-                for (int cb = 0; cb < 2; ++cb)
-                    o[dt][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[cb][ks], o[dt][cb], 0, 0, 0);
-            }
-    };
-    // max over the 32 keys of half s of each row, in the exp2 domain
-    auto half_max = [&](const f32x16 (&s)[2], float mul, float (&mx)[2]) {
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb) {
-            float x = fmaxf(fmaxf(s[cb][0], s[cb][1]), s[cb][2]);
-#pragma unroll
-            for (int r = 3; r < 15; r += 2) x = fmaxf(fmaxf(x, s[cb][r]), s[cb][r + 1]);
-            mx[cb] = max_swap32(fmaxf(x, s[cb][15])) * mul;
-        }
-    };
-    // implicit masks on half kt of the tile at key k0: keys past L, and past
-    // the row's own position when causal
-    auto mask_half = [&](f32x16 (&s)[2], int k0, int kt) {
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb) {
-            const int lim = causal ? min(L - 1, past + tcol[cb]) : L - 1;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int key = k0 + kt * 32 + 8 * (r / 4) + 4 * half + (r % 4);
-                s[cb][r] = key > lim ? -INFINITY : s[cb][r];
-            }
-        }
-    };
-
-    // stage bases of tile j, through an empty asm so that each read keeps
-    // one base register and a constant offset
-    auto bases = [&](int j, const lds_char*& ka, const lds_char*& va) {
-        uint32_t kaddr = lds0 + (j % kStages) * STAGE + k_rd;
-        uint32_t vaddr = lds0 + (j % kStages) * STAGE + KREG + v_rd;
-        asm volatile("" : "+v"(kaddr), "+v"(vaddr));
-        ka = lds_at(kaddr);
-        va = lds_at(vaddr);
-    };
-    // operand fragments of half kt, read ahead of their MFMAs into
-    // registers of their own
-    auto load_k = [&](const lds_char* ka, int kt, QF (&kf)[DS]) {
-#pragma unroll
-        for (int ds = 0; ds < DS; ++ds) {
-            const u32x4 kraw = *(const __attribute__((address_space(3))) u32x4*)(ka + kt * 32 * KP + ds * 32);
-            kf[ds] = as_vec<QF>(kraw);
-        }
-    };
-    auto mma_k = [&](const QF (&kf)[DS], f32x16 (&s)[2]) {
-#pragma unroll
-        for (int ds = 0; ds < DS; ++ds)
-#pragma unroll
-            for (int cb = 0; cb < 2; ++cb) s[cb] = ds == 0 ? F::mma(kf[0], qf[cb][0], f32x16{}) : F::mma(kf[ds], qf[cb][ds], s[cb]);
-    };
-    auto load_v = [&](const lds_char* va, int kt, h8 (&vf)[DT][2]) {
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-                const int kk = (kt * 2 + ks) * 16;
-                vf[dt][ks] = v_frag<KT>(va + dt * 64 + kk * VP, va + dt * 64 + (kk + 8) * VP);
-            }
-    };
-    auto mma_v = [&](const h8 (&vf)[DT][2], const h8 (&pf)[2][2]) {
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-                for (int cb = 0; cb < 2; ++cb)
-                    o[dt][cb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[dt][ks], pf[cb][ks], o[dt][cb], 0, 0, 0);
-    };
-    // softmax of k step ks (16 keys) of a half for both column blocks, with
-    // the fixed exponent offsets of the loop
-    float nbf[2];
-    auto probs_ks = [&](const f32x16 (&s)[2], int ks, h8 (&pf)[2][2]) {
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb) {
-            float ps = lsum[cb];
-            h8 pv;
-#pragma unroll
-            for (int e = 0; e < 8; e += 2) {
-                const float p0 = __builtin_amdgcn_exp2f(fmaf(s[cb][ks * 8 + e], sl2, nbf[cb]));
-                const float p1 = __builtin_amdgcn_exp2f(fmaf(s[cb][ks * 8 + e + 1], sl2, nbf[cb]));
-                h2 pp = {(_Float16)p0, (_Float16)p1};
-                pv[e] = pp.x;
-                pv[e + 1] = pp.y;
-                ps = __builtin_amdgcn_fdot2(pp, h2{(_Float16)1.0f, (_Float16)1.0f}, ps, false);
-            }
-            pf[cb][ks] = pv;
-            lsum[cb] = ps;
-        }
-    };
-    // a tile with masks: the implicit ones, or the explicit mask (scores
-    // then carried in the exp2 domain, the row max tracked per tile: the
-    // first visible tile sets m, a later one beyond m + 15 raises it)
-    auto slow_tile = [&](const lds_char* ka, const lds_char* va, int k0, int restarts) -> bool {
-        f32x16 s[2][2];
-        s_half(ka, 0, s[0]);
-        s_half(ka, 1, s[1]);
-        float mul = sl2;
-        bool raise = false;
-        if constexpr (EXPL) {
-            mul = 1.0f;
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-                for (int cb = 0; cb < 2; ++cb) {
-                    const char* mrow = a.mask + b * a.mask_nb_b + tcol[cb] * a.mask_nb_row;
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int key = k0 + kt * 32 + 8 * (r / 4) + 4 * half + (r % 4);
-                        const float x = fmaf(s[kt][cb][r], sl2,
-                                             f16_to_f32(*(const uint16_t*)(mrow + 2 * min(key, L - 1))) * kLog2e);
-                        s[kt][cb][r] = key > L - 1 ? -INFINITY : x;
-                    }
-                }
-            float mx0[2], mx1[2];
-            half_max(s[0], 1.0f, mx0);
-            half_max(s[1], 1.0f, mx1);
-#pragma unroll
-            for (int cb = 0; cb < 2; ++cb) {
-                const float mx = fmaxf(mx0[cb], mx1[cb]);
-                if (m[cb] == -INFINITY) m[cb] = mx;            // O and the row sum are still 0
-                if (mx > m[cb] + kLazy && restarts < kMaxRestarts) {
-                    raise = true;
-                    m[cb] = mx;
+                for (int dt = 0; dt < DT; ++dt) {
+                    const h8 vf = v_frag<KT>(va + dt * 64 + kk * VP, va + dt * 64 + (kk + 8) * VP);
+                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[kt][k2], o[dt], 0, 0, 0);
                 }
             }
-            if (__any(raise)) return true;
-        } else {
-            mask_half(s[0], k0, 0);
-            mask_half(s[1], k0, 1);
-        }
-        h8 pf0[2][2], pf1[2][2];
-        probs(s[0], mul, pf0);
-        pv_half(va, 0, pf0);
-        probs(s[1], mul, pf1);
-        pv_half(va, 1, pf1);
-        return false;
     };
-    // a p of the last tile overflowed f16 (its score passed m + 16), seen as
-    // an inf or nan row sum
-    auto overflow = [&](int restarts) -> bool {
-        return !EXPL && restarts < kMaxRestarts && (!(lsum[0] <= 3.0e38f) || !(lsum[1] <= 3.0e38f));
-    };
-    // all tiles before j_fast are seen whole by every row of the workgroup
-    const int t_lo_wg = min(a.T - 1, R0 / g);
-    const int j_fast = EXPL ? 0 : max(0, min(n_tiles, (causal ? min(L, past + t_lo_wg + 1) : L) / kBN - j_lo));
 
-    for (int restarts = 0;; ++restarts) {
-        issue(0);
-        issue(1);
-        issue(2);
-        wait_vm_barrier<2 * NLD>();                             // tile 0 is in LDS
-        if (!EXPL && restarts == 0 && n_tiles > 0) {
-            // m from half 0 of the first tile: visible to every row when it
-            // lies in the fully visible range (the single-split case: key 0);
-            // a row that cannot see it keeps m = -inf (exponent offset 0)
-            // and a restart raises m should a later p overflow f16
-            const lds_char *ka, *va;
-            bases(0, ka, va);
-            f32x16 s0[2];
-            s_half(ka, 0, s0);
-            mask_half(s0, kb0, 0);
-            half_max(s0, sl2, m);
+    for (int j = 0; j < n_tiles; ++j) {
+        // tile j has landed (tiles j + 1, j + 2 may still fly) and every wave
+        // is done with tile j - 1, whose stage tile j + 3 now takes
+        wait_vm_barrier<2 * NLD>();
+        issue(j + 3);
+        const int k0 = kb0 + j * kBN;
+        if (k0 < kend_w) {                                       // wave-uniform
+            uint32_t kaddr = lds0 + (j % kStages) * STAGE + k_rd;
+            uint32_t vaddr = lds0 + (j % kStages) * STAGE + KREG + v_rd;
+            asm volatile("" : "+v"(kaddr), "+v"(vaddr));         // one base register, constant offsets
+            f32x16 s[2];
+            scores(lds_at(kaddr), s);
+            if (EXPL || k0 + kBN - 1 > lim_w) apply_mask(s, k0);
+            softmax_pv(lds_at(vaddr), s);
         }
-        int j = 0;
-        bool restart = false;
-        // (the loops leave through their conditions only: an exit from the
-        // middle makes the compiler copy O through VGPRs on every tile)
-        int jb = 0;                                             // the tile that asked for the restart
-        int bar = 0;                                            // barriers passed (flag slot parity)
-        nbf[0] = m[0] == -INFINITY ? 0.0f : -m[0];
-        nbf[1] = m[1] == -INFINITY ? 0.0f : -m[1];
-        // ---- tiles every row of the workgroup sees whole: no masks, no
-        // branches, pipelined across tiles.  Iteration j, in four scheduling
-        // regions (sched_barrier) of 16 MFMAs, each beside a quarter of a
-        // softmax that reads scores finished at least one region earlier:
-        //   1  S of half 1 of tile j         | softmax, 2nd k step of half 0
-        //      barrier: tile j + 1 in LDS, every wave done with tile j - 1
-        //   2  S of half 0 of tile j + 1     | softmax, 1st k step of half 1
-        //   3  P.V of half 0 of tile j       | softmax, 2nd k step of half 1
-        //   4  P.V of half 1 of tile j       | softmax, 1st k step of half 0
-        //                                      of tile j + 1
-        // The loads of tile j + 3 go, after the barrier, into the stage tile
-        // j - 1 used; a tile past the last, or any tile once a restart is
-        // decided (the restart re-reads the stage of the tile that asked for
-        // it), loads nothing.  A tile's overflow verdict is complete after
-        // region 3 and published at the next barrier.
-        f32x16 sc[2];                                           // S of half 0 of the current tile
-        h8 pc[2][2];                                            // its p, first k step filled
-        QF kf1[DS];                                             // K of half 1 of the current tile
-        bool verdict = false;                                   // overflow up to the previous tile
-        auto barrier_flags = [&](bool flag, bool two_ahead) -> bool {
-            if (lane == 0) any_flag[bar & 1][w] = flag;
-            if (two_ahead) wait_vm_barrier<2 * NLD>(); else wait_vm_barrier<NLD>();
-            int any = 0;
-#pragma unroll
-            for (int i = 0; i < kWaves; ++i) any |= any_flag[bar & 1][i];
-            ++bar;
-            return any != 0;                                    // workgroup-uniform
-        };
-        if (j_fast > 0) {
-            const lds_char *ka, *va;
-            bases(0, ka, va);
-            QF kf0[DS];
-            load_k(ka, 0, kf0);
-            mma_k(kf0, sc);
-            probs_ks(sc, 0, pc);
-            load_k(ka, 1, kf1);
-        }
-        // region 1 of tile j (shared by the loop and its last tile)
-        auto region1 = [&](const lds_char* va, f32x16 (&s1)[2], h8 (&vf0)[DT][2]) {
-            load_v(va, 0, vf0);
-            mma_k(kf1, s1);
-            probs_ks(sc, 1, pc);
-            __builtin_amdgcn_sched_barrier(0);
-        };
-        for (; j + 1 < j_fast && !restart; ++j) {
-            // O stays in AGPRs across the back-edge (without the hint the
-            // compiler moves part of it through VGPRs on every tile)
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-                for (int cb = 0; cb < 2; ++cb) asm volatile("" : "+a"(o[dt][cb]));
-            const lds_char *ka, *va, *kn, *vn;
-            bases(j, ka, va);
-            bases(j + 1, kn, vn);
-            f32x16 s1[2], sn[2];
-            h8 p1[2][2], pn[2][2], vf0[DT][2], vf1[DT][2];
-            QF kf0[DS];
-            region1(va, s1, vf0);
-            if (barrier_flags(verdict, false)) {
-                restart = true;
-                jb = j - 1;
-            }
-            const bool live = !restart && j + 3 < n_tiles;
-            // region 2
-            load_k(kn, 0, kf0);
-            issue_range(j + 3, 0, NLD / 2, live);
-            mma_k(kf0, sn);
-            probs_ks(s1, 0, p1);
-            __builtin_amdgcn_sched_barrier(0);
-            // region 3
-            load_v(va, 1, vf1);
-            issue_range(j + 3, NLD / 2, NLD, live);
-            mma_v(vf0, pc);
-            probs_ks(s1, 1, p1);
-            __builtin_amdgcn_sched_barrier(0);
-            verdict = __any(overflow(restarts));
-            // region 4
-            load_k(kn, 1, kf1);
-            mma_v(vf1, p1);
-            probs_ks(sn, 0, pn);
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int cb = 0; cb < 2; ++cb) {
-                sc[cb] = sn[cb];
-                pc[cb][0] = pn[cb][0];
-            }
-        }
-        if (j_fast > 0 && !restart) {
-            // the last of these tiles, j = j_fast - 1: no next tile to start;
-            // the barrier at its end makes its stage free for the masked loop
-            const lds_char *ka, *va;
-            bases(j, ka, va);
-            f32x16 s1[2];
-            h8 p1[2][2], vf0[DT][2], vf1[DT][2];
-            region1(va, s1, vf0);
-            if (barrier_flags(verdict, false)) {
-                restart = true;
-                jb = j - 1;
-            }
-            issue_range(j + 3, 0, NLD, !restart && j + 3 < n_tiles);
-            load_v(va, 1, vf1);
-            probs_ks(s1, 0, p1);
-            mma_v(vf0, pc);
-            probs_ks(s1, 1, p1);
-            mma_v(vf1, p1);
-            if (barrier_flags(__any(overflow(restarts)), true) && !restart) {
-                restart = true;
-                jb = j;
-            }
-            ++j;
-        }
-        for (; j < n_tiles && !restart; ++j) {
-            issue(j + 3);
-            const lds_char *ka, *va;
-            bases(j, ka, va);
-            bool flag = false;
-            if (kb0 + j * kBN < kend_w) flag = slow_tile(ka, va, kb0 + j * kBN, restarts) || overflow(restarts);
-            // end of tile j: publish the restart flags, wait for tile j + 1
-            // (the loads of tiles j + 2 and j + 3 may still fly)
-            if (barrier_flags(__any(flag), true)) {
-                restart = true;
-                jb = j;
-            }
-        }
-        if (!restart) {
-            wait_vm_barrier<0>();                               // loads past the last tile
-            break;
-        }
-        j = jb;
-        wait_vm_barrier<0>();                                   // no load may land in a stage after the restart
-        if (!EXPL && kb0 + j * kBN < kend_w) {
-            // raise m for the rows whose scores on tile j passed m + 15 (tile j
-            // is still in its stage: tile j + 4 was never issued)
-            const lds_char *ka, *va;
-            bases(j, ka, va);
-            f32x16 s[2][2];
-            s_half(ka, 0, s[0]);
-            s_half(ka, 1, s[1]);
-            mask_half(s[0], kb0 + j * kBN, 0);
-            mask_half(s[1], kb0 + j * kBN, 1);
-            float mx0[2], mx1[2];
-            half_max(s[0], sl2, mx0);
-            half_max(s[1], sl2, mx1);
-#pragma unroll
-            for (int cb = 0; cb < 2; ++cb) {
-                const float mx = fmaxf(mx0[cb], mx1[cb]);
-                if (mx > m[cb] + kLazy) m[cb] = mx;
-            }
-        }
-        __syncthreads();                                        // every wave is done with the stages
-        lsum[0] = lsum[1] = 0.0f;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-            for (int cb = 0; cb < 2; ++cb) o[dt][cb] = f32x16{};
     }
+    wait_vm_barrier<0>();                                       // the padding tiles' loads
 
-    // ---- normalize and write (each lane owns one row per column block);
-    // with several key splits, write the split's partial instead: O
-    // unnormalized, and (exponent base, row sum) of the row
+    // ---- normalize and write (each lane owns its row; lanes l and l ^ 32
+    // summed different keys); with several key splits, write the split's
+    // partial instead: O unnormalized, and (exponent base, row sum)
     const int64_t nr_all = (int64_t)a.B * a.T * a.Hq;
-#pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
-        const int row = wr0 + cb * 32 + l32;
-        const float lt = lsum[cb] + __shfl_xor(lsum[cb], 32, 64);
-        if (row >= nrows) continue;
-        const int t = row / g, h = kvh * g + row % g;
-        float* orow;
-        float inv = 1.0f;
-        if (n_ks == 1) {
-            inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-            orow = (float*)((char*)a.out + b * a.o_nb_b + t * a.o_nb_t + h * a.o_nb_h);
-        } else {
-            const int64_t rg = ((int64_t)b * a.T + t) * a.Hq + h;
-            orow = ws + ((int64_t)ks * nr_all + rg) * D;
-            if (half == 0) {
-                // p = 2^(s - base): base = m, or 0 while m = -inf; an empty row is -inf
-                const float base = m[cb] != -INFINITY ? m[cb] : (lt > 0.0f ? 0.0f : -INFINITY);
-                *(float2*)(ws + nr_all * D * n_ks + ((int64_t)ks * nr_all + rg) * 2) = make_float2(base, lt);
-            }
+    const float lt = lsum + __shfl_xor(lsum, 32, 64);
+    if (!qok) return;
+    const int t = row / g, h = kvh * g + row % g;
+    float* orow;
+    float inv = 1.0f;
+    if (n_ks == 1) {
+        inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+        orow = (float*)((char*)a.out + b * a.o_nb_b + t * a.o_nb_t + h * a.o_nb_h);
+    } else {
+        const int64_t rg = ((int64_t)b * a.T + t) * a.Hq + h;
+        orow = ws + ((int64_t)ks * nr_all + rg) * D;
+        if (half == 0) {
+            // p = 2^(x - base): base = m, or 0 while m = -inf; an empty row is -inf
+            const float base = m != -INFINITY ? m : (lt > 0.0f ? 0.0f : -INFINITY);
+            *(float2*)(ws + nr_all * D * plan.max_ks + ((int64_t)ks * nr_all + rg) * 2) = make_float2(base, lt);
         }
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-            for (int q4 = 0; q4 < 4; ++q4) {
-                const int d = dt * 32 + 8 * q4 + 4 * half;
-                float4 v = make_float4(o[dt][cb][4 * q4] * inv, o[dt][cb][4 * q4 + 1] * inv,
-                                       o[dt][cb][4 * q4 + 2] * inv, o[dt][cb][4 * q4 + 3] * inv);
-                *(float4*)(orow + d) = v;
-            }
     }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+            const int d = dt * 32 + 8 * q4 + 4 * half;
+            *(float4*)(orow + d) = make_float4(o[dt][4 * q4] * inv, o[dt][4 * q4 + 1] * inv,
+                                               o[dt][4 * q4 + 2] * inv, o[dt][4 * q4 + 3] * inv);
+        }
 }
 
-// Combines the key splits of every query row: one thread per (row, 4 dims),
-// log-sum-exp over the n_ks partials (exp2 domain), normalized into out.
+// Combines the key splits of every split query row: one thread per (row,
+// 4 dims), log-sum-exp over the row tile's partials (exp2 domain),
+// normalized into out.  Rows of unsplit row tiles were written directly.
 template <int D>
-__global__ void __launch_bounds__(256) prefill_merge_kernel(AttnArgs a, const float* __restrict__ ws, int n_ks) {
+__global__ void __launch_bounds__(256) prefill_merge_kernel(AttnArgs a, const float* __restrict__ ws, PrefillPlan plan) {
     const int64_t nr_all = (int64_t)a.B * a.T * a.Hq;
     const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int64_t rg = idx / (D / 4);
     const int d4 = (int)(idx % (D / 4));
     if (rg >= nr_all) return;
-    const float* ml = ws + nr_all * D * n_ks;
+    const int h = (int)(rg % a.Hq), t = (int)((rg / a.Hq) % a.T), b = (int)(rg / ((int64_t)a.Hq * a.T));
+    const int g = a.Hq / a.Hkv, kvh = h / g;
+    const int rt = (t * g + (h - kvh * g)) / kRowsWG;
+    const int n_ks = rt_splits(plan, rt);
+    if (n_ks == 1) return;
+    const float* ml = ws + nr_all * D * plan.max_ks;
     float M = -INFINITY;
     for (int k = 0; k < n_ks; ++k) M = fmaxf(M, ml[((int64_t)k * nr_all + rg) * 2]);
     float den = 0.0f;
@@ -785,24 +534,22 @@ __global__ void __launch_bounds__(256) prefill_merge_kernel(AttnArgs a, const fl
         }
     }
     const float inv = den > 0.0f ? 1.0f / den : 0.0f;
-    const int h = (int)(rg % a.Hq), t = (int)((rg / a.Hq) % a.T), b = (int)(rg / ((int64_t)a.Hq * a.T));
     float* orow = (float*)((char*)a.out + b * a.o_nb_b + t * a.o_nb_t + h * a.o_nb_h);
     *(float4*)(orow + 4 * d4) = make_float4(num.x * inv, num.y * inv, num.z * inv, num.w * inv);
 }
 
 template <int D, int KT>
-hipError_t launch_pf(const AttnArgs& a, float* ws, int n_ks, hipStream_t s) {
-    const int g = a.Hq / a.Hkv;
-    const int nrows = a.T * g;
-    dim3 grid((nrows + kRowsWG - 1) / kRowsWG * n_ks, a.Hkv, a.B);
+hipError_t launch_pf(const AttnArgs& a, float* ws, const PrefillPlan& p, hipStream_t s) {
+    const int n_rt = (a.T * (a.Hq / a.Hkv) + kRowsWG - 1) / kRowsWG;
+    dim3 grid(plan_pieces(p, n_rt) * a.Hkv, 1, a.B);
     if (a.mask_mode == kMaskExplicit)
-        hipLaunchKernelGGL((prefill_kernel<D, KT, true>), grid, dim3(256), 0, s, a, ws, n_ks);
+        hipLaunchKernelGGL((prefill_kernel<D, KT, true>), grid, dim3(kWaves * 64), 0, s, a, ws, p);
     else
-        hipLaunchKernelGGL((prefill_kernel<D, KT, false>), grid, dim3(256), 0, s, a, ws, n_ks);
+        hipLaunchKernelGGL((prefill_kernel<D, KT, false>), grid, dim3(kWaves * 64), 0, s, a, ws, p);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || n_ks == 1) return e;
+    if (e != hipSuccess || p.max_ks == 1) return e;
     const int64_t threads = (int64_t)a.B * a.T * a.Hq * (D / 4);
-    hipLaunchKernelGGL(prefill_merge_kernel<D>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, a, ws, n_ks);
+    hipLaunchKernelGGL(prefill_merge_kernel<D>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, a, ws, p);
     return hipGetLastError();
 }
 
@@ -829,35 +576,63 @@ bool prefill_supported(const AttnArgs& a) {
     return true;
 }
 
-int prefill_plan(const AttnArgs& a, int n_cu) {
-    // Key splits per row tile: only when the row tiles alone leave CUs idle
-    // (a short chunk over a long past); as many as keep every workgroup in
-    // one round on the CUs (a partial second round costs more than the
-    // idle CUs it fills), each split at least 4 key tiles of the longest row
-    // tile.
-    const int g = a.Hq / a.Hkv;
-    const int64_t base = (int64_t)((a.T * g + kRowsWG - 1) / kRowsWG) * a.Hkv * a.B;
-    if (base >= n_cu) return 1;
-    int Lmax = 1;
-    for (int b = 0; b < a.B; ++b) Lmax = a.L[b] > Lmax ? a.L[b] : Lmax;
-    const int max_ks = ((Lmax + kBN - 1) / kBN) / 4;
-    int n_ks = (int)(n_cu / base);
-    if (n_ks > max_ks) n_ks = max_ks;
-    if (n_ks > kMaxKeySplits) n_ks = kMaxKeySplits;
-    return n_ks < 1 ? 1 : n_ks;
-}
-
-size_t prefill_ws_bytes(const AttnArgs& a, int n_ks) {
-    return n_ks <= 1 ? 0 : (size_t)n_ks * a.B * a.T * a.Hq * (a.d + 2) * sizeof(float);
-}
-
-hipError_t launch_prefill(const AttnArgs& a, float* ws, int n_ks, hipStream_t s) {
-    if (a.d == 64) {
-        return a.k_type == VVA_TYPE_F16 ? launch_pf<64, VVA_TYPE_F16>(a, ws, n_ks, s)
-                                        : launch_pf<64, VVA_TYPE_BF16>(a, ws, n_ks, s);
+// Split plan: every workgroup in one round on the CUs (a second, partial
+// round costs more than it balances), and within that budget the shortest
+// critical path, i.e. the fewest key tiles in the largest piece: the
+// heaviest row tiles (the last ones, under a causal mask) split n ways,
+// the rest whole, with the partials' round trip and the merge launch
+// counted against a split and the partials within ws_cap bytes.  Calls with
+// more row tiles than CUs need no split: launched heaviest first they
+// balance already.
+PrefillPlan prefill_plan(const AttnArgs& a, int n_cu, int forced, size_t ws_cap) {
+    const int n_rt = (a.T * (a.Hq / a.Hkv) + kRowsWG - 1) / kRowsWG;
+    const bool causal = a.mask_mode == kMaskCausal;
+    if (forced > 0) return PrefillPlan{forced, 0, forced, forced};
+    const PrefillPlan none{1, 0, 0, 1};
+    const int per = a.Hkv * a.B;                 // workgroups per piece index
+    const int budget = n_cu / per;               // pieces per (kv head, sequence) in one round
+    if (n_rt >= budget) return none;
+    // key tiles of the largest piece, over the batch, for row tiles [lo, hi) split n ways
+    auto max_piece = [&](int lo, int hi, int n) {
+        int m = 0;
+        for (int b = 0; b < a.B; ++b)
+            for (int rt = lo; rt < hi; ++rt) m = max(m, (rt_key_tiles(a, b, rt, causal) + n - 1) / n);
+        return m;
+    };
+    // time in key-tile units (one tile of 64 keys x 256 rows for one workgroup)
+    const double unit_us = 64.0 * kRowsWG * a.d * 4.0 / 4.0e6;
+    const double bytes_per_unit = 4.0e6 * unit_us;
+    const double merge_launch = 5.0 / unit_us;
+    PrefillPlan best = none;
+    double best_t = max_piece(0, n_rt, 1);
+    for (int n = 2; n <= kMaxKeySplits; ++n) {
+        // smallest R with (n_rt - R) n + R <= budget
+        const int R = max(0, (n_rt * n - budget + n - 2) / (n - 1));
+        if (R >= n_rt) break;
+        const PrefillPlan p{n, R, 0, n};
+        if (prefill_ws_bytes(a, p) > ws_cap) continue;
+        const double split_rows = (double)(n_rt - R) * kRowsWG * per;
+        const double t = max(max_piece(R, n_rt, n), max_piece(0, R, 1)) + merge_launch +
+                         split_rows * (n + 1) * (a.d + 2) * 4.0 * 2.0 / bytes_per_unit;
+        if (t < best_t * 0.95) {                 // a split must pay for itself
+            best_t = t;
+            best = p;
+        }
     }
-    return a.k_type == VVA_TYPE_F16 ? launch_pf<128, VVA_TYPE_F16>(a, ws, n_ks, s)
-                                    : launch_pf<128, VVA_TYPE_BF16>(a, ws, n_ks, s);
+    return best;
+}
+
+size_t prefill_ws_bytes(const AttnArgs& a, const PrefillPlan& p) {
+    return p.max_ks <= 1 ? 0 : (size_t)p.max_ks * a.B * a.T * a.Hq * (a.d + 2) * sizeof(float);
+}
+
+hipError_t launch_prefill(const AttnArgs& a, float* ws, const PrefillPlan& p, hipStream_t s) {
+    if (a.d == 64) {
+        return a.k_type == VVA_TYPE_F16 ? launch_pf<64, VVA_TYPE_F16>(a, ws, p, s)
+                                        : launch_pf<64, VVA_TYPE_BF16>(a, ws, p, s);
+    }
+    return a.k_type == VVA_TYPE_F16 ? launch_pf<128, VVA_TYPE_F16>(a, ws, p, s)
+                                    : launch_pf<128, VVA_TYPE_BF16>(a, ws, p, s);
 }
 
 }  // namespace vva

@@ -51,11 +51,12 @@ struct vva_kv {
 };
 
 // Split-partial scratch of vva_attn_noalloc, one copy per GPU, held until
-// the process ends.  Its size covers every split count the planners choose
-// at head_dim <= 128 on a 256-CU device (at most 32.5 MiB: key-split
-// prefill partials n_ks * B * T * Hq * (d + 2) floats with n_ks * row tiles
-// <= 256).  In host code `scratch` only names the symbol: its device address
-// comes from hipGetSymbolAddress (scratch_addr below).
+// the process ends.  The decode planners stay far below it (3.6 MiB at the
+// 7B CFG shape on 256 CUs) and the prefill planner is given its size as a
+// cap (it picks fewer key splits when the partials would not fit), so only
+// split counts forced by vva_set_schedule can exceed it.  In host code
+// `scratch` only names the symbol: its device address comes from
+// hipGetSymbolAddress (g_scratch below).
 constexpr size_t kScratchBytes = (size_t)36 << 20;
 static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
 
@@ -213,15 +214,15 @@ vva_status run_attention(vva_context* ctx, AttnArgs& a, bool fixed = false) {
         return VVA_OK;
     }
     if (ctx->attn_path != 1 && a.T > 1 && prefill_supported(a)) {
-        int n_ks = prefill_plan(a, ctx->n_cu);
-        if (ctx->sched_prefill_splits > 0) n_ks = ctx->sched_prefill_splits;
-        if (n_ks > 1) {
-            vva_status st = get_ws(ctx, fixed, prefill_ws_bytes(a, n_ks), &ws);
+        const PrefillPlan plan = prefill_plan(a, ctx->n_cu, ctx->sched_prefill_splits,
+                                              fixed ? kScratchBytes : ((size_t)1 << 34));
+        if (plan.max_ks > 1) {
+            vva_status st = get_ws(ctx, fixed, prefill_ws_bytes(a, plan), &ws);
             if (st != VVA_OK) return st;
         }
-        e = launch_prefill(a, ws, n_ks, ctx->stream);
+        e = launch_prefill(a, ws, plan, ctx->stream);
         if (e != hipSuccess) return hip_fail(ctx, e, "prefill launch");
-        ctx->last_splits = n_ks;
+        ctx->last_splits = plan.max_ks;
         return VVA_OK;
     }
     e = launch_attn_rows(a, ctx->stream);

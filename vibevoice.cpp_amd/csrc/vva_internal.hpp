@@ -129,13 +129,20 @@ bool decode_stream_supported(const AttnArgs& a);
 // takes the sequence's tiles s, s + n_splits, s + 2 n_splits, ...
 int decode_stream_plan(const AttnArgs& a, int n_cu);
 hipError_t launch_decode_stream(const AttnArgs& a, float* ws, int n_splits, hipStream_t s);
-// MFMA flash prefill (F16 / BF16 caches).  n_ks > 1 splits each row
-// tile's keys over n_ks workgroups, with partials in ws
-// (prefill_ws_bytes) merged by a second kernel.
-hipError_t launch_prefill(const AttnArgs& a, float* ws, int n_ks, hipStream_t s);
+// MFMA flash prefill (F16 / BF16 caches).  Row tiles (256 query rows of
+// one kv group) rt >= R have their key range split over n workgroups (all
+// row tiles over `forced` when forced > 0); split rows leave partials in ws
+// (prefill_ws_bytes) that a second kernel merges.
+struct PrefillPlan {
+    int n;             // splits of a heavy row tile (1: none)
+    int R;             // first heavy row tile
+    int forced;        // > 0: this many splits for every row tile
+    int max_ks;        // largest split count of the call (1: no partials)
+};
+hipError_t launch_prefill(const AttnArgs& a, float* ws, const PrefillPlan& p, hipStream_t s);
 bool prefill_supported(const AttnArgs& a);
-int prefill_plan(const AttnArgs& a, int n_cu);
-size_t prefill_ws_bytes(const AttnArgs& a, int n_ks);
+PrefillPlan prefill_plan(const AttnArgs& a, int n_cu, int forced, size_t ws_cap);
+size_t prefill_ws_bytes(const AttnArgs& a, const PrefillPlan& p);
 // Prep + GEMM of a linear layer; ws holds proj_ws_bytes(N, K, P) bytes.
 size_t proj_ws_bytes(int N, int K, int P);
 hipError_t launch_proj(ProjPrepArgs& p, ProjArgs& a, void* ws, hipStream_t s);
