@@ -79,10 +79,16 @@ def decode_append_bytes(B: int) -> float:
     return B * ((HQ + 2 * HKV) * D * 4 + HQ * D * 4 + 2 * HKV * (D // 32) * 34)
 
 
-def run_prefill(torch, vva, ctx, steps: int, warmup: int):
+def run_prefill(torch, vva, ctx, steps: int, warmup: int, heavy: bool = False):
     rng = torch.Generator(device="cuda").manual_seed(1234)
     q = torch.randn((1, T_PREFILL, HQ, D), generator=rng, device="cuda").to(torch.bfloat16)
-    k = torch.randn((1, T_PREFILL, HKV, D), generator=rng, device="cuda").to(torch.bfloat16)
+    k = torch.randn((1, T_PREFILL, HKV, D), generator=rng, device="cuda")
+    if heavy:
+        # heavy-tailed logits: K of tokens [1024 i, 1024 (i + 1)) scaled by 1 + 3.5 i, so each
+        # row's running max rises by > 10 nats every 16 key tiles (up to 31 rescales per row)
+        k = k * (1.0 + 3.5 * torch.div(torch.arange(T_PREFILL, device="cuda"), 1024,
+                                       rounding_mode="floor")).view(1, -1, 1, 1)
+    k = k.to(torch.bfloat16)
     v = torch.randn((1, T_PREFILL, HKV, D), generator=rng, device="cuda").to(torch.bfloat16)
     pos = torch.arange(T_PREFILL, dtype=torch.int32, device="cuda")
     qr = torch.empty((1, T_PREFILL, HQ, D), dtype=torch.float16, device="cuda")
@@ -528,6 +534,15 @@ def main() -> int:
             line["cpu_baseline"] = cpu_baseline_prefill(torch, vva, vvo, kv, qr)
         kv.free()
         torch.cuda.empty_cache()
+        if not args.no_extra:
+            hv, kvh_, _, _ = run_prefill(torch, vva, ctx, 1, 0, heavy=True)
+            line["prefill_heavy_logits"] = {
+                "workload": "as the prefill line, K of every 1024-token block scaled by 1 + 3.5 i: the running "
+                            "max of a row rises by > 10 nats every 16 key tiles",
+                "attn_ms": round(hv["attn_ms"], 4), "tflops": round(hv["attn_tflops"], 2),
+                "frac_of_mfma_peak": round(hv["attn_tflops"] / PEAK_F16_TFLOPS, 4)}
+            kvh_.free()
+            torch.cuda.empty_cache()
     if args.only in ("decode", "both"):
         globals()["L_DECODE"] = args.decode_len      # read by run_decode
         dec, kvd = run_decode(torch, vva, ctx, args.decode_steps, max(1, args.warmup))

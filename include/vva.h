@@ -173,9 +173,11 @@ VVA_API vva_status vva_rope_append(vva_context* ctx, vva_kv* kv, int layer,
  *         0 / -inf entries as built at src/vibevoice_asr.cpp:616-627;
  *   out:  F32 ne = [d, Hq, T, B], the FA output layout (src/qwen2.cpp:156-159).
  * Q is rounded to the dot type of K as ggml's CPU FA does (F16 -> f16,
- * BF16 -> bf16, Q8_0 -> Q8_0 blocks, F32 -> f32).  T == 1 runs the split-K
- * decode kernel; larger T runs the MFMA prefill kernel (F16 / BF16 caches)
- * or the VALU kernel (F32 / Q8_0 caches). */
+ * BF16 -> bf16, Q8_0 -> Q8_0 blocks, F32 -> f32, or f16 under
+ * vva_set_flash_attn(1)).  T == 1 runs the split-K decode kernels; larger T
+ * runs the MFMA prefill kernel (F16 / BF16 caches directly, Q8_0 and F32
+ * windows after an on-device conversion to F16), or the fp32 VALU kernel
+ * (F32 caches with vva_set_flash_attn(0)). */
 VVA_API vva_status vva_attn(vva_context* ctx, const vva_kv* kv, int layer,
                             const vva_tensor* q, const int32_t* seq_ids,
                             const vva_tensor* mask, float scale, const vva_tensor* out);
@@ -248,6 +250,17 @@ VVA_API vva_status vva_out_proj_residual(vva_context* ctx, const vva_tensor* o, 
  * run this combination on the context's device, 0 otherwise. */
 VVA_API int vva_supports(const vva_context* ctx, int head_dim, int n_q_heads, int n_kv_heads,
                          int q_type, int kv_type);
+
+/* Attention branch, as Qwen2Hparams::use_flash_attn selects it in the
+ * reference (src/qwen2.hpp:38, src/qwen2.cpp:327-344).  It matters for F32
+ * caches only:
+ *   1 (default): the flash-attention branch, which casts the F32 window to
+ *      F16 before ggml_flash_attn_ext (src/qwen2.cpp:328-331): the library
+ *      does the same cast on the device and runs the MFMA prefill;
+ *   0: the eager branch (mul_mat with F32 precision, soft_max_ext, mul_mat):
+ *      fp32 throughout.
+ * F16 / BF16 / Q8_0 caches are read in their own type either way. */
+VVA_API vva_status vva_set_flash_attn(vva_context* ctx, int use_flash_attn);
 
 /* ------------------------------------------------------------ debugging */
 

@@ -102,22 +102,69 @@ def test_decode_explicit_mask(ctx, torch_gpu):
 ROWS = [
     # d, Hq, Hkv, type, T, past  — VALU row kernel cases
     (64, 14, 2, vva.F32, 256, 0),        # 0.5B prefill (fp32 eager-equivalent)
-    (128, 28, 4, vva.Q8_0, 64, 500),     # chunk into a Q8_0 cache
+    (128, 28, 4, vva.Q8_0, 64, 500),     # chunk into a Q8_0 cache (forced onto the row kernel)
     (128, 12, 2, vva.F32, 33, 7),
 ]
 
 
 @pytest.mark.parametrize("d,Hq,Hkv,t,T,past", ROWS)
 def test_row_kernel_prefill_matches_oracle(ctx, torch_gpu, d, Hq, Hkv, t, T, past):
+    """F32 caches under the eager branch (vva_set_flash_attn(0): fp32
+    throughout, 1e-4) and a Q8_0 chunk forced onto the row kernel."""
     torch = torch_gpu
     print(f"rows d={d} Hq={Hq} Hkv={Hkv} type={t} T={T} past={past}", flush=True)
     L = past + T
     kv = vva.KVCache(ctx, 1, Hkv, d, L, 1, t)
     fill_cache(kv, [L], seed=11, scale=1.0 if t != vva.F32 else 0.125)
     kv.set_len(0, past)
-    q, out = run_attn(ctx, torch, kv, 0, T, 1, Hq, vva.F32, seed=12)
+    ctx.set_flash_attn(False)
+    if t == vva.Q8_0:
+        ctx.set_attn_path(1)
+    try:
+        q, out = run_attn(ctx, torch, kv, 0, T, 1, Hq, vva.F32, seed=12)
+    finally:
+        ctx.set_flash_attn(True)
+        ctx.set_attn_path(0)
     ref = oracle_attn(q, kv, 0, [0], [L], T, d ** -0.5)
     assert_close(out, ref, *TOL[t], what="row kernel")
+    kv.free()
+
+
+@pytest.mark.parametrize("t", [vva.Q8_0, vva.F32])
+def test_converted_window_prefill_matches_oracle(ctx, torch_gpu, t):
+    """A 512-token ASR chunk over a 32k past, 7B heads, on Q8_0 and F32
+    caches: the window is converted to f16 on the device and prefilled on
+    the MFMA kernel.  Q8_0: Q goes through a Q8_0 round trip (ggml's dot type
+    for Q8_0 K), checked against both oracle orders on the cache bytes.  F32
+    under the flash branch: the reference casts K/V to F16 first
+    (src/qwen2.cpp:328-331), so the oracle sees the f16-rounded window.
+    Rows: the chunk's first and last 16 and 32 spread between."""
+    torch = torch_gpu
+    d, Hq, Hkv, T, past = 128, 28, 4, 512, 32256
+    L = past + T
+    print(f"converted window type={t} T={T} past={past}", flush=True)
+    kv = vva.KVCache(ctx, 1, Hkv, d, L, 1, t)
+    fill_cache(kv, [L], seed=1717)
+    kv.set_len(0, past)
+    q, out = run_attn(ctx, torch, kv, 0, T, 1, Hq, vva.BF16, seed=1718)
+    splits = ctx.last_decode_splits()
+    rows = np.unique(np.concatenate([np.arange(16), np.arange(T - 16, T),
+                                     np.linspace(16, T - 17, 32).astype(np.int64)])).astype(np.int32)
+    if t == vva.Q8_0:
+        ref = oracle_attn(q, kv, 0, [0], [L], T, d ** -0.5, rows=rows)
+        mx, mn = assert_close(out[0, rows], ref[0, rows], *TOL[t], what="Q8_0 window vs exact")
+        (gmx, gmn), _ = check_ggml_order(out, q, kv, 0, [0], [L], T, d ** -0.5, *TOL[t], rows=rows,
+                                         what="Q8_0 window")
+    else:
+        kraw, vraw = kv.download(0, 0, L)
+        k16 = vvo.from_f32(vvo.to_f32(kraw.reshape(-1), vvo.F32, L * Hkv * d), vvo.F16)
+        v16 = vvo.from_f32(vvo.to_f32(vraw.reshape(-1), vvo.F32, L * Hkv * d), vvo.F16)
+        args = dict(n_kv_heads=Hkv, scale=d ** -0.5, past=[past], rows=rows)
+        ref = vvo.attn(q, [k16], [v16], vvo.F16, vvo.F16, [L], **args)
+        mx, mn = assert_close(out[0, rows], ref[0, rows], *TOL[vva.F16], what="F32 window (F16 cast) vs exact")
+        gg = vvo.attn(q, [k16], [v16], vvo.F16, vvo.F16, [L], mode=vvo.GGML_F32ACC, **args)
+        gmx, gmn = assert_close(out[0, rows], gg[0, rows], *TOL[vva.F16], what="F32 window vs ggml order")
+    print(f"  key splits {splits}: vs exact max {mx:.2e} mean {mn:.2e}; vs ggml order max {gmx:.2e} mean {gmn:.2e}")
     kv.free()
 
 

@@ -212,10 +212,49 @@ def test_full_size_1p5b_voice_clone_prefill(ctx, torch_gpu, t):
     kv.free()
 
 
-def test_prefill_score_jump_restarts_key_loop(ctx, torch_gpu):
-    """Scores of later keys exceed the first tile's by far more than 2^15 in
-    the exp2 domain: the kernel's reference max must be raised (key loop
-    restarted) without overflowing the f16 probabilities."""
+@pytest.mark.parametrize("t", [vva.F16, vva.BF16])
+def test_prefill_repeated_score_jumps(ctx, torch_gpu, t):
+    """Heavy-tailed logits: every query has 8 in dim 0 and the keys of 64-key
+    tile j carry 2 sqrt(d) (j + 1) there, so each tile adds 16 nats to every
+    row's scores and a row's running max jumps at every tile boundary it
+    crosses (31 jumps for the last rows of a 2048-token prefill).  Every jump
+    rescales O and the row sum; the result must match the exact oracle and
+    stay finite."""
+    torch = torch_gpu
+    d, Hq, Hkv, T = 128, 28, 4, 2048
+    rng = np.random.default_rng(21 + t)
+    k = rng.standard_normal((T, Hkv, d)).astype(np.float32)
+    k[:, :, 0] = (2.0 * d ** 0.5 * (np.arange(T) // 64 + 1))[:, None]
+    v = rng.standard_normal((T, Hkv, d)).astype(np.float32)
+    qn = rng.standard_normal((1, T, Hq, d))
+    qn[..., 0] = 8.0
+    kv = vva.KVCache(ctx, 1, Hkv, d, T, 1, t)
+    kv.upload(0, 0, 0, k, v)
+    kv.set_len(0, 0)
+    q = to_gpu(torch, qn, t)
+    out = torch.full((1, T, Hq, d), float("nan"), dtype=torch.float32, device="cuda")
+    ctx.attn(kv, 0, q, out, d ** -0.5)
+    torch.cuda.synchronize()
+    o = as_f32(torch, out)
+    assert np.isfinite(o).all()
+    rows = np.unique(np.concatenate([np.arange(T - 256, T), np.arange(0, T, 37)])).astype(np.int32)
+    q32 = as_f32(torch, q)
+    ref = oracle_attn(q32, kv, 0, [0], [T], T, d ** -0.5, rows=rows)
+    # jumps seen by the last row: tiles whose max score passes the running max by 10 nats
+    kd = vvo.to_f32(kv.download(0, 0, T)[0].reshape(-1), t, T * Hkv * d).reshape(T, Hkv, d)
+    s = (kd[:, 0] @ q32[0, T - 1, 0]) * d ** -0.5
+    tile_max = s.reshape(-1, 64).max(axis=1)
+    jumps = int(np.sum(tile_max[1:] > np.maximum.accumulate(tile_max)[:-1] + 10.0))
+    mx, mn = assert_close(o[0, rows], ref[0, rows], *TOL, what="repeated score jumps")
+    print(f"score jumps > 10 nats (last row, head 0): {jumps}; max {mx:.2e} mean {mn:.2e}")
+    assert jumps >= 20
+    kv.free()
+
+
+def test_prefill_single_large_score_jump(ctx, torch_gpu):
+    """Scores of later keys exceed the first tiles' by far more than 2^15 in
+    the exp2 domain: the running max must be raised (O rescaled) without
+    overflowing the f16 probabilities."""
     torch = torch_gpu
     d, Hq, Hkv, T = 128, 28, 4, 400
     rng = np.random.default_rng(11)

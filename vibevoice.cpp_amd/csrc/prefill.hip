@@ -310,41 +310,56 @@ __global__ void __launch_bounds__(kWaves * 64) prefill_kernel(AttnArgs a, float*
                        (int64_t)(kvh * g + (qok ? row % g : 0)) * a.q_nb_h;
     QF qf[DS];
     {
-        u32x4 qraw[DS];
+        // the lane's 8 dims ds * 16 + 8 half .. of each 16-dim step, as fp32
+        float x[DS][8];
         if (a.q_type == VVA_TYPE_F32) {
-            float4 x[DS][2];
 #pragma unroll
             for (int ds = 0; ds < DS; ++ds) {
-                const int d0 = ds * 16 + half * 8;
-                x[ds][0] = *(const float4*)(qrow + d0 * 4);
-                x[ds][1] = *(const float4*)(qrow + d0 * 4 + 16);
-            }
-#pragma unroll
-            for (int ds = 0; ds < DS; ++ds) {
-                const float4 x0 = x[ds][0], x1 = x[ds][1];
-                qraw[ds] = u32x4{F::cvt(x0.x) | ((uint32_t)F::cvt(x0.y) << 16), F::cvt(x0.z) | ((uint32_t)F::cvt(x0.w) << 16),
-                                 F::cvt(x1.x) | ((uint32_t)F::cvt(x1.y) << 16), F::cvt(x1.z) | ((uint32_t)F::cvt(x1.w) << 16)};
+                const float4 x0 = *(const float4*)(qrow + (ds * 16 + half * 8) * 4);
+                const float4 x1 = *(const float4*)(qrow + (ds * 16 + half * 8) * 4 + 16);
+                x[ds][0] = x0.x; x[ds][1] = x0.y; x[ds][2] = x0.z; x[ds][3] = x0.w;
+                x[ds][4] = x1.x; x[ds][5] = x1.y; x[ds][6] = x1.z; x[ds][7] = x1.w;
             }
         } else {
+            const int qt = a.q_type;
 #pragma unroll
-            for (int ds = 0; ds < DS; ++ds) qraw[ds] = *(const u32x4*)(qrow + (ds * 16 + half * 8) * 2);
-            if (a.q_type != KT) {           // the other 16-bit type
-                const int qt = a.q_type;
+            for (int ds = 0; ds < DS; ++ds) {
+                const u32x4 r = *(const u32x4*)(qrow + (ds * 16 + half * 8) * 2);
+                const uint32_t rw[4] = {r.x, r.y, r.z, r.w};
 #pragma unroll
-                for (int ds = 0; ds < DS; ++ds) {
-                    const u32x4 r = qraw[ds];
-                    const uint32_t rw[4] = {r.x, r.y, r.z, r.w};
-                    uint32_t cw[4];
+                for (int k = 0; k < 4; ++k) {
+                    x[ds][2 * k] = bits16_to_f32(rw[k] & 0xffffu, qt);
+                    x[ds][2 * k + 1] = bits16_to_f32(rw[k] >> 16, qt);
+                }
+            }
+        }
+        if (a.q_round_q8) {
+            // Q8_0 round trip per 32-dim block (steps 2 bb, 2 bb + 1; the
+            // other 16 values of the block sit in lane l ^ 32): ggml's dot
+            // type for Q8_0 K, as fp16 d times the integer code
 #pragma unroll
-                    for (int k = 0; k < 4; ++k)
-                        cw[k] = F::cvt(bits16_to_f32(rw[k] & 0xffffu, qt)) |
-                                ((uint32_t)F::cvt(bits16_to_f32(rw[k] >> 16, qt)) << 16);
-                    qraw[ds] = u32x4{cw[0], cw[1], cw[2], cw[3]};
+            for (int bb = 0; bb < DS / 2; ++bb) {
+                float am = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) am = fmaxf(am, fmaxf(fabsf(x[2 * bb][e]), fabsf(x[2 * bb + 1][e])));
+                am = max_swap32(am);
+                const float dq = am / 127.0f;
+                const float id = dq != 0.0f ? 1.0f / dq : 0.0f;
+                const float dh = bits16_to_f32(f32_to_f16(dq), VVA_TYPE_F16);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    x[2 * bb][e] = dh * roundf(x[2 * bb][e] * id);
+                    x[2 * bb + 1][e] = dh * roundf(x[2 * bb + 1][e] * id);
                 }
             }
         }
 #pragma unroll
-        for (int ds = 0; ds < DS; ++ds) qf[ds] = as_vec<QF>(qok ? qraw[ds] : u32x4{0u, 0u, 0u, 0u});
+        for (int ds = 0; ds < DS; ++ds) {
+            uint32_t cw[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) cw[k] = F::cvt(x[ds][2 * k]) | ((uint32_t)F::cvt(x[ds][2 * k + 1]) << 16);
+            qf[ds] = as_vec<QF>(qok ? u32x4{cw[0], cw[1], cw[2], cw[3]} : u32x4{0u, 0u, 0u, 0u});
+        }
     }
     issue(1);
     issue(2);
@@ -553,7 +568,55 @@ hipError_t launch_pf(const AttnArgs& a, float* ws, const PrefillPlan& p, hipStre
     return hipGetLastError();
 }
 
+// One thread per 32-element block of a K or V head row of one sequence:
+// grid (blocks of the longest window / 256, 2 B: K and V of each sequence).
+__global__ void __launch_bounds__(256) window_to_f16_kernel(AttnArgs a, uint16_t* __restrict__ dst) {
+    const int b = blockIdx.y >> 1, which = blockIdx.y & 1;
+    const int nblk = a.d / 32;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;       // (row, head, block)
+    const int L = a.L[b];
+    if (i >= (int64_t)L * a.Hkv * nblk) return;
+    const int bk = (int)(i % nblk), h = (int)((i / nblk) % a.Hkv);
+    const int64_t row = i / ((int64_t)nblk * a.Hkv);
+    const int type = which ? a.v_type : a.k_type;
+    const char* src = (which ? a.v[b] : a.k[b]) + row * (which ? a.v_nb_tok : a.k_nb_tok) +
+                      h * (which ? a.v_nb_head : a.k_nb_head);
+    size_t off = 0;                                                   // this sequence's K, then V
+    for (int b2 = 0; b2 < b; ++b2) off += (size_t)2 * a.L[b2] * a.Hkv * a.d;
+    uint16_t* o = dst + off + (size_t)which * L * a.Hkv * a.d + ((size_t)row * a.Hkv + h) * a.d + bk * 32;
+    uint32_t w[16];
+    if (type == VVA_TYPE_Q8_0) {
+        const char* blk = src + bk * kQ8Bytes;
+        const float d = f16_to_f32(*(const uint16_t*)blk);
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+            w[e] = (uint32_t)f32_to_f16(d * (float)(int8_t)blk[2 + 2 * e]) |
+                   ((uint32_t)f32_to_f16(d * (float)(int8_t)blk[3 + 2 * e]) << 16);
+    } else {
+        const float* f = (const float*)src + bk * 32;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) w[e] = (uint32_t)f32_to_f16(f[2 * e]) | ((uint32_t)f32_to_f16(f[2 * e + 1]) << 16);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ((uint4*)o)[e] = make_uint4(w[4 * e], w[4 * e + 1], w[4 * e + 2], w[4 * e + 3]);
+}
+
 }  // namespace
+
+size_t window_f16_bytes(const AttnArgs& a) {
+    size_t n = 0;
+    for (int b = 0; b < a.B; ++b) n += (size_t)2 * a.L[b] * a.Hkv * a.d * 2;
+    return (n + 255) / 256 * 256;
+}
+
+hipError_t launch_window_to_f16(const AttnArgs& a, void* dst, hipStream_t s) {
+    int Lmax = 1;
+    for (int b = 0; b < a.B; ++b) Lmax = max(Lmax, a.L[b]);
+    const int64_t n = (int64_t)Lmax * a.Hkv * (a.d / 32);
+    hipLaunchKernelGGL(window_to_f16_kernel, dim3((unsigned)((n + 255) / 256), 2 * a.B), dim3(256), 0, s, a,
+                       (uint16_t*)dst);
+    return hipGetLastError();
+}
 
 bool prefill_supported(const AttnArgs& a) {
     if (a.T < 2) return false;

@@ -27,6 +27,7 @@ struct vva_context {
     std::string err;
     int n_cu = 256;
     int attn_path = 0;
+    int use_flash_attn = 1;              // F32 caches: 1 = F16 cast + MFMA prefill, 0 = fp32 throughout
     int last_splits = 0;
     // scheduling overrides (vva_set_schedule); 0 = automatic
     int sched_decode_wgs = 0, sched_decode_splits = 0, sched_prefill_splits = 0;
@@ -213,6 +214,41 @@ vva_status run_attention(vva_context* ctx, AttnArgs& a, bool fixed = false) {
         ctx->last_splits = n_splits;
         return VVA_OK;
     }
+    // Q8_0 windows, and F32 windows under flash-attention semantics (the
+    // reference casts them to F16 before ggml_flash_attn_ext,
+    // src/qwen2.cpp:328-331): converted to f16 on the device, then the MFMA
+    // prefill (Q through a Q8_0 round trip for Q8_0 K, ggml's dot type).
+    // Not on the no-allocation path, whose scratch cannot hold a window.
+    const bool convert = a.k_type == a.v_type &&
+                         (a.k_type == VVA_TYPE_Q8_0 || (a.k_type == VVA_TYPE_F32 && ctx->use_flash_attn));
+    if (ctx->attn_path != 1 && a.T > 1 && convert && !fixed && (a.d == 64 || a.d == 128)) {
+        AttnArgs c = a;
+        const size_t wb = window_f16_bytes(a);
+        c.k_type = c.v_type = VVA_TYPE_F16;
+        c.k_nb_tok = c.v_nb_tok = (int64_t)a.Hkv * a.d * 2;
+        c.k_nb_head = c.v_nb_head = (int64_t)a.d * 2;
+        c.q_round_q8 = a.k_type == VVA_TYPE_Q8_0;
+        // pointers into the workspace only after it is sized: placeholders
+        // with the final alignment for the support check
+        for (int b = 0; b < a.B; ++b) c.k[b] = c.v[b] = (const char*)(uintptr_t)256;
+        if (prefill_supported(c)) {
+            const PrefillPlan plan = prefill_plan(c, ctx->n_cu, ctx->sched_prefill_splits, (size_t)1 << 34);
+            vva_status st = ensure_ws(ctx, wb + prefill_ws_bytes(c, plan));
+            if (st != VVA_OK) return st;
+            char* wbase = (char*)ctx->ws;
+            size_t off = 0;
+            for (int b = 0; b < a.B; ++b) {
+                c.k[b] = wbase + off;
+                c.v[b] = wbase + off + (size_t)a.L[b] * a.Hkv * a.d * 2;
+                off += (size_t)2 * a.L[b] * a.Hkv * a.d * 2;
+            }
+            e = launch_window_to_f16(a, wbase, ctx->stream);
+            if (e == hipSuccess) e = launch_prefill(c, (float*)(wbase + wb), plan, ctx->stream);
+            if (e != hipSuccess) return hip_fail(ctx, e, "prefill launch");
+            ctx->last_splits = plan.max_ks;
+            return VVA_OK;
+        }
+    }
     if (ctx->attn_path != 1 && a.T > 1 && prefill_supported(a)) {
         const PrefillPlan plan = prefill_plan(a, ctx->n_cu, ctx->sched_prefill_splits,
                                               fixed ? kScratchBytes : ((size_t)1 << 34));
@@ -336,6 +372,12 @@ extern "C" vva_status vva_set_attn_path(vva_context* ctx, int path) {
 }
 
 extern "C" int vva_last_decode_splits(const vva_context* ctx) { return ctx ? ctx->last_splits : 0; }
+
+extern "C" vva_status vva_set_flash_attn(vva_context* ctx, int use_flash_attn) {
+    if (!ctx || (use_flash_attn != 0 && use_flash_attn != 1)) return VVA_ERR_INVALID_ARG;
+    ctx->use_flash_attn = use_flash_attn;
+    return VVA_OK;
+}
 
 extern "C" vva_status vva_set_schedule(vva_context* ctx, int decode_wgs, int decode_splits, int prefill_splits) {
     if (!ctx) return VVA_ERR_INVALID_ARG;

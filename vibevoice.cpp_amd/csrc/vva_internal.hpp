@@ -73,9 +73,17 @@ struct AttnArgs {
     float* out;
     int64_t o_nb_t, o_nb_h, o_nb_b;   // in bytes
     int d, Hq, Hkv, T, B;
+    int q_round_q8;                   // prefill: Q through a Q8_0 round trip first (window of Q8_0 K)
 };
 
 enum { kMaskNone = 0, kMaskExplicit = 1, kMaskCausal = 2 };
+
+// K / V rows [0, L_b) of each sequence converted to f16 for the MFMA
+// prefill: Q8_0 blocks dequantized, F32 rounded (the reference's ggml_cast
+// to F16 before flash attention, src/qwen2.cpp:328-331).  dst holds, per
+// sequence, K then V as [L_b][Hkv][d] f16; window_f16_bytes sizes it.
+size_t window_f16_bytes(const AttnArgs& a);
+hipError_t launch_window_to_f16(const AttnArgs& a, void* dst, hipStream_t s);
 
 // Linear layers around the attention (proj.hip).  Token row n = b * T + t.
 enum { kProjQKV = 0, kProjResidual = 1 };

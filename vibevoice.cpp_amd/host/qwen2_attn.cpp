@@ -75,6 +75,10 @@ int qwen2_attention_resident(ResidentKV& kvs, int layer_idx, const vva_tensor& q
         const int st = vva_kv_set_len(kvs.kv, s, kvs.past_len[s]);
         if (st != VVA_OK) return st;
     }
+    // the branch of src/qwen2.cpp:327-344 (for F32 caches: F16 cast + flash
+    // attention, or fp32 eager)
+    int fa = vva_set_flash_attn(kvs.ctx, hp.use_flash_attn ? 1 : 0);
+    if (fa != VVA_OK) return fa;
     // rope(q), rope(k), cpy(k -> window at past_len), cpy(v -> ...)  src/qwen2.cpp:282-306
     int st = vva_rope_append(kvs.ctx, kvs.kv, layer_idx, &q, &k, &v, &pos, seq_ids, hp.rope_theta, &q);
     if (st != VVA_OK) return st;

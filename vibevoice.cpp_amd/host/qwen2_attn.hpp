@@ -27,10 +27,11 @@
 
 namespace vva {
 
-// Attention fields of vv::Qwen2Hparams (src/qwen2.hpp:24-39).  Both values
-// of use_flash_attn run the same kernels: the flash and the eager branch of
-// the reference (src/qwen2.cpp:327-344) compute the same function, and the
-// kernels never materialise the score matrix.
+// Attention fields of vv::Qwen2Hparams (src/qwen2.hpp:24-39).
+// use_flash_attn picks the branch of src/qwen2.cpp:327-344 for F32 caches:
+// the flash branch casts the window to F16 (and runs the MFMA prefill), the
+// eager branch stays fp32; other cache types are read in their own type
+// either way, and no branch materialises the score matrix.
 struct Qwen2Hparams {
     int   hidden_size    = 0;
     int   n_heads        = 0;

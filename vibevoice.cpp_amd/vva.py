@@ -32,6 +32,7 @@ EXPORTS = [
     "vva_kv_view", "vva_kv_upload", "vva_rope_ext", "vva_rope_append", "vva_attn",
     "vva_flash_attn_ext", "vva_supports", "vva_set_attn_path", "vva_last_decode_splits",
     "vva_set_schedule", "vva_attn_noalloc", "vva_qkv_rope_append", "vva_out_proj_residual",
+    "vva_set_flash_attn",
 ]
 
 
@@ -103,6 +104,7 @@ def load_library(path: str = LIB_PATH):
         "vva_set_attn_path": (I, [P, I]),
         "vva_last_decode_splits": (I, [P]),
         "vva_set_schedule": (I, [P, I, I, I]),
+        "vva_set_flash_attn": (I, [P, I]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -190,6 +192,10 @@ class Context:
 
     def set_attn_path(self, path: int):
         self.check(self.lib.vva_set_attn_path(self.h, path))
+
+    def set_flash_attn(self, use_flash_attn: bool):
+        """F32 caches: True = F16 cast + MFMA prefill (the flash branch), False = fp32 eager branch."""
+        self.check(self.lib.vva_set_flash_attn(self.h, int(bool(use_flash_attn))))
 
     def last_decode_splits(self) -> int:
         return int(self.lib.vva_last_decode_splits(self.h))
