@@ -208,7 +208,7 @@ def run_decode(torch, vva, ctx, steps: int, warmup: int):
     return res, kv
 
 
-def run_prefill_chunked(torch, vva, ctx, layers: int):
+def run_prefill_chunked(torch, vva, ctx, layers: int, cache_type: int = None):
     """The ASR prefill as the reference runs it: 64 chunks of 512 tokens per
     layer, chunk c attending to its 512 rows plus the 512 c rows before it
     (same total FLOPs as the single-shot prefill).  HIP events around each
@@ -219,7 +219,8 @@ def run_prefill_chunked(torch, vva, ctx, layers: int):
     v = torch.randn((1, CHUNK, HKV, D), generator=rng, device="cuda").to(torch.bfloat16)
     qr = torch.empty((1, CHUNK, HQ, D), dtype=torch.float16, device="cuda")
     out = torch.empty((1, CHUNK, HQ, D), dtype=torch.float32, device="cuda")
-    kv = vva.KVCache(ctx, layers + 1, HKV, D, T_PREFILL, 1, vva.F16)
+    ct = vva.F16 if cache_type is None else cache_type
+    kv = vva.KVCache(ctx, layers + 1, HKV, D, T_PREFILL, 1, ct)
     n_chunks = T_PREFILL // CHUNK
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
           for _ in range(layers * n_chunks)]
@@ -239,8 +240,9 @@ def run_prefill_chunked(torch, vva, ctx, layers: int):
     attn_ms = float(np.sum(ms)) / layers
     flops = sum(4.0 * HQ * D * (CHUNK * c * CHUNK + CHUNK * (CHUNK + 1) / 2) for c in range(n_chunks))
     kv.free()
+    tname = {vva.F16: "F16", vva.Q8_0: "Q8_0 (window converted to f16 per call)"}[ct]
     return {"workload": f"Qwen2.5-7B-shaped ASR prefill: {n_chunks} chunks of {CHUNK} tokens, past 0..{T_PREFILL - CHUNK}, "
-                        f"F16 cache, {layers} layers",
+                        f"{tname} cache, {layers} layers",
             "value": round(flops / (attn_ms * 1e-3) / 1e12, 1), "unit": "TFLOP/s",
             "frac_of_mfma_peak": round(flops / (attn_ms * 1e-3) / 1e12 / PEAK_F16_TFLOPS, 4),
             "attn_ms_per_layer": round(attn_ms, 3), "flop_per_layer": flops,
@@ -250,7 +252,7 @@ def run_prefill_chunked(torch, vva, ctx, layers: int):
             "timing": "HIP events around each chunk's attention launch"}
 
 
-def run_decode_small(torch, vva, ctx, steps: int):
+def run_decode_small(torch, vva, ctx, steps: int, vvo=None):
     """The 0.5B TTS CFG decode step (B = 2, 14 q / 2 kv heads, d = 64, F16
     caches at 1024, 24 layers of RoPE + append + attention), timed as eager
     launches from prebuilt descriptors and as one captured HIP graph per
@@ -280,22 +282,33 @@ def run_decode_small(torch, vva, ctx, steps: int):
     byref = ctypes.byref
     qv, kv_, vv_, pv, qrv, ov = (vva.view(t) for t in (q, k, v, pos, qr, out))
 
-    def step():
+    def step_unfused():
         for layer in range(S_LAYERS):
             ctx.check(lib.vva_rope_append(h, kvh, layer, byref(qv), byref(kv_), byref(vv_), byref(pv), None, THETA,
                                           byref(qrv)))
             ctx.check(lib.vva_attn(h, kvh, layer, byref(qrv), None, None, scale, byref(ov)))
 
-    for _ in range(3):
-        step()
-    torch.cuda.synchronize()
+    def step():
+        # vva_decode_step: RoPE + append + attention + split merge in one launch per layer
+        for layer in range(S_LAYERS):
+            ctx.check(lib.vva_decode_step(h, kvh, layer, byref(qv), byref(kv_), byref(vv_), byref(pv), None, THETA,
+                                          scale, byref(qrv), byref(ov)))
+
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(steps):
-        step()
-    e1.record()
-    torch.cuda.synchronize()
-    eager_us = e0.elapsed_time(e1) * 1e3 / steps
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / steps
+
+    unfused_us = timed(step_unfused)
+    eager_us = timed(step)
     g = torch.cuda.CUDAGraph()
     default = torch.cuda.current_stream()
     try:
@@ -314,13 +327,37 @@ def run_decode_small(torch, vva, ctx, steps: int):
     graph_us = e0.elapsed_time(e1) * 1e3 / steps
     del g
     L = S_L + 1
+    # bytes per layer of the step: the K/V window read, f32 q/k/v in, rotated q and output out,
+    # the appended K/V row
     attn_bytes = B * L * S_HKV * 2 * S_D * 2 + 2 * B * S_HQ * S_D * 4
+    step_bytes = attn_bytes + B * ((S_HQ + 2 * S_HKV) * S_D * 4 + S_HQ * S_D * 4 + 2 * S_HKV * S_D * 2)
+    cpu = None
+    if vvo is not None:
+        kraw = [kv.download(0, s_, L)[0].reshape(-1) for s_ in range(B)]
+        vraw = [kv.download(0, s_, L)[1].reshape(-1) for s_ in range(B)]
+        qn = qr.float().cpu().numpy()
+        calls, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < 5.0:
+            vvo.attn(qn, kraw, vraw, vvo.F16, vvo.F16, [L] * B, n_kv_heads=S_HKV, scale=scale, mode=vvo.GGML)
+            calls += 1
+        dt = time.perf_counter() - t0
+        cpu = {"value": round(calls * attn_bytes / dt / 1e9, 2), "unit": "GB/s", "cores": vvo.n_cores(),
+               "kind": "port", "us_per_layer": round(dt / calls * 1e6, 2),
+               "sample": f"{calls} attention calls of one layer (B=2, L={L}, F16 cache), ggml-order oracle, {dt:.1f} s"}
     kv.free()
+    eager_layer, graph_layer = eager_us / S_LAYERS, graph_us / S_LAYERS
     return {"workload": f"Qwen2.5-0.5B-shaped TTS CFG decode: B=2, {S_HQ}q/{S_HKV}kv d={S_D}, F16 cache at {S_L}, "
-                        f"{S_LAYERS} layers of RoPE + append + attention",
+                        f"{S_LAYERS} layers of RoPE + append + attention (vva_decode_step: one launch per layer; "
+                        f"the rope_append + attn pair beside it)",
             "eager_us_per_step": round(eager_us, 2), "graph_us_per_step": round(graph_us, 2),
-            "eager_us_per_layer": round(eager_us / S_LAYERS, 3), "graph_us_per_layer": round(graph_us / S_LAYERS, 3),
-            "attn_bytes_per_layer": attn_bytes, "steps": steps,
+            "eager_us_per_layer": round(eager_layer, 3), "graph_us_per_layer": round(graph_layer, 3),
+            "unfused_eager_us_per_layer": round(unfused_us / S_LAYERS, 3),
+            "kernels_per_layer": 1,
+            "attn_bytes_per_layer": attn_bytes, "step_bytes_per_layer": step_bytes, "steps": steps,
+            "roofline": {"bound": "hbm", "achieved": round(step_bytes / eager_layer / 1e3, 1), "peak": PEAK_HBM_GBS,
+                         "unit": "GB/s", "frac": round(step_bytes / eager_layer / 1e3 / PEAK_HBM_GBS, 4),
+                         "note": "a 1 MB window per layer is L2/MALL-resident: launch latency, not bandwidth, bounds it"},
+            "cpu_baseline": cpu,
             "timing": "HIP events around `steps` back-to-back steps; graph: one captured step replayed"}
 
 
@@ -568,7 +605,9 @@ def main() -> int:
     if not args.no_extra and args.only in ("prefill", "decode", "both"):
         line["prefill_chunked"] = run_prefill_chunked(torch, vva, ctx, layers=2)
         torch.cuda.empty_cache()
-        line["decode_small"] = run_decode_small(torch, vva, ctx, steps=200)
+        line["prefill_chunked_q8_0"] = run_prefill_chunked(torch, vva, ctx, layers=2, cache_type=vva.Q8_0)
+        torch.cuda.empty_cache()
+        line["decode_small"] = run_decode_small(torch, vva, ctx, steps=200, vvo=None if args.no_cpu else vvo)
         line["prefill_small"] = run_small_prefills(torch, vva)
         torch.cuda.empty_cache()
         line["proj"] = run_proj(torch, vva, vvo)

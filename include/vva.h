@@ -182,6 +182,22 @@ VVA_API vva_status vva_attn(vva_context* ctx, const vva_kv* kv, int layer,
                             const vva_tensor* q, const int32_t* seq_ids,
                             const vva_tensor* mask, float scale, const vva_tensor* out);
 
+/* Single-token decode step: vva_rope_append with T = 1 followed by vva_attn
+ * over the len(seq_b) + 1 keys with the implicit causal mask, i.e. the
+ * attention section of src/qwen2.cpp:282-335 for one new token per
+ * sequence (the decode loops, src/vibevoice_tts.cpp:862-880,
+ * src/vibevoice_asr.cpp:760-800), with the same arguments and results:
+ * q, k, v ne = [d, H, 1, B]; pos I32 ne = [1] or [1, B]; q_out receives
+ * RoPE(q); out F32 ne = [d, Hq, 1, B].  F16 / BF16 caches with windows up
+ * to 8192 keys run as one kernel (RoPE, append, split attention and the
+ * merge of its splits) unless q_out aliases q; other cases run the two
+ * calls.  Does not advance len.  No counterpart of its own in the reference: it fuses three of its
+ * ops for the latency-bound short windows. */
+VVA_API vva_status vva_decode_step(vva_context* ctx, vva_kv* kv, int layer,
+                                   const vva_tensor* q, const vva_tensor* k, const vva_tensor* v,
+                                   const vva_tensor* pos, const int32_t* seq_ids, float freq_base,
+                                   float scale, const vva_tensor* q_out, const vva_tensor* out);
+
 /* vva_attn without any allocation, for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc).  No counterpart in the reference.  Same arguments,

@@ -38,6 +38,7 @@ struct vva_context {
     // allocated until vva_destroy.
     std::vector<float*> ws_retired;
     float* scratch = nullptr;            // this device's `scratch` (vva_attn_noalloc)
+    unsigned* tickets = nullptr;         // vva_decode_step's merge tickets, zeroed once
     std::set<vva_kv*> caches;            // released by vva_destroy if still alive
 };
 
@@ -320,6 +321,14 @@ extern "C" vva_status vva_create(int device, void* stream, vva_context** out) {
     ctx->stream = (hipStream_t)stream;
     ctx->scratch = scr;
     ctx->err.reserve(512);               // error messages (< 512 bytes) then never allocate
+    e = hipMalloc(&ctx->tickets, sizeof(unsigned) * kMaxStepTickets);
+    if (e == hipSuccess) e = hipMemset(ctx->tickets, 0, sizeof(unsigned) * kMaxStepTickets);
+    if (e != hipSuccess) {
+        if (ctx->tickets) (void)hipFree(ctx->tickets);
+        delete ctx;
+        *out = nullptr;
+        return fail(nullptr, VVA_ERR_DEVICE, "vva_create: ticket buffer: %s", hipGetErrorString(e));
+    }
     *out = ctx;
     return VVA_OK;
 }
@@ -339,6 +348,7 @@ extern "C" void vva_destroy(vva_context* ctx) {
     ctx->caches.clear();
     if (ctx->ws) (void)hipFree(ctx->ws);
     for (float* p : ctx->ws_retired) (void)hipFree(p);
+    if (ctx->tickets) (void)hipFree(ctx->tickets);
     delete ctx;
 }
 
@@ -935,4 +945,72 @@ extern "C" vva_status vva_out_proj_residual(vva_context* ctx, const vva_tensor* 
     if ((st = ensure_ws(ctx, proj_ws_bytes((int)N, (int)K, 0))) != VVA_OK) return st;
     hipError_t e = launch_proj(p, a, ctx->ws, ctx->stream);
     return e == hipSuccess ? VVA_OK : hip_fail(ctx, e, "out_proj_residual launch");
+}
+
+// --------------------------------------------------------- decode step
+
+extern "C" vva_status vva_decode_step(vva_context* ctx, vva_kv* kv, int layer, const vva_tensor* q,
+                                      const vva_tensor* k, const vva_tensor* v, const vva_tensor* pos,
+                                      const int32_t* seq_ids, float freq_base, float scale, const vva_tensor* q_out,
+                                      const vva_tensor* out) {
+    if (!ctx) return VVA_ERR_INVALID_ARG;
+    if (!kv || !kv_live(kv) || kv->ctx != ctx)
+        return fail(ctx, VVA_ERR_INVALID_ARG, "decode_step: cache is null, released or of another context");
+    if (layer < 0 || layer >= kv->desc.n_layers) return fail(ctx, VVA_ERR_INVALID_ARG, "decode_step: layer %d", layer);
+    vva_status st = check_tensor(ctx, q, "q");
+    if (st != VVA_OK) return st;
+    const int64_t d = kv->desc.head_dim, Hkv = kv->desc.n_kv_heads;
+    const int64_t Hq = q->ne[1], T = q->ne[2], B = q->ne[3];
+    if (T != 1) return fail(ctx, VVA_ERR_INVALID_ARG, "decode_step: one new token per sequence (T = %lld)", (long long)T);
+    if (Hq % Hkv) return fail(ctx, VVA_ERR_INVALID_ARG, "decode_step: Hq %% Hkv != 0");
+    if (B > VVA_MAX_BATCH) return fail(ctx, VVA_ERR_INVALID_ARG, "decode_step: B > %d", VVA_MAX_BATCH);
+    if ((st = check_rows(ctx, q, "q", d, Hq, 1, B)) != VVA_OK) return st;
+    if ((st = check_rows(ctx, k, "k", d, Hkv, 1, B)) != VVA_OK) return st;
+    if ((st = check_rows(ctx, v, "v", d, Hkv, 1, B)) != VVA_OK) return st;
+    if ((st = check_rows(ctx, q_out, "q_out", d, Hq, 1, B)) != VVA_OK) return st;
+    if ((st = check_rows(ctx, out, "out", d, Hq, 1, B)) != VVA_OK) return st;
+    if (out->type != VVA_TYPE_F32) return fail(ctx, VVA_ERR_INVALID_ARG, "decode_step: out must be F32");
+    int64_t ps = 0;
+    if ((st = check_pos(ctx, pos, 1, B, &ps)) != VVA_OK) return st;
+    StepArgs a{};
+    for (int b = 0; b < B; ++b) {
+        const int seq = seq_ids ? seq_ids[b] : b;
+        if (seq < 0 || seq >= kv->desc.n_seq) return fail(ctx, VVA_ERR_INVALID_ARG, "decode_step: seq %d", seq);
+        for (int b2 = 0; b2 < b; ++b2)
+            if ((seq_ids ? seq_ids[b2] : b2) == seq)
+                return fail(ctx, VVA_ERR_INVALID_ARG, "decode_step: sequence %d appears twice", seq);
+        if (kv->len[seq] + 1 > kv->desc.max_seq)
+            return fail(ctx, VVA_ERR_INVALID_ARG, "decode_step: seq %d is full (max_seq %d)", seq, kv->desc.max_seq);
+        a.kc[b] = kv_tensor(kv, layer, seq, 0);
+        a.vc[b] = kv_tensor(kv, layer, seq, 1);
+        a.past[b] = kv->len[seq];
+    }
+    a.q = (const char*)q->data; a.q_type = q->type; a.q_nb_h = q->nb[1]; a.q_nb_b = q->nb[3];
+    a.k = (const char*)k->data; a.k_type = k->type; a.k_nb_h = k->nb[1]; a.k_nb_b = k->nb[3];
+    a.v = (const char*)v->data; a.v_type = v->type; a.v_nb_h = v->nb[1]; a.v_nb_b = v->nb[3];
+    a.pos = (const int32_t*)pos->data; a.pos_stride_b = ps;
+    a.q_out = (char*)q_out->data; a.q_out_type = q_out->type; a.qo_nb_h = q_out->nb[1]; a.qo_nb_b = q_out->nb[3];
+    a.cache_row_bytes = kv->row_bytes; a.cache_head_bytes = kv->head_bytes; a.cache_type = kv->desc.type;
+    a.theta_scale = powf(freq_base, -2.0f / (float)d);
+    a.scale = scale;
+    a.out = (float*)out->data; a.o_nb_h = out->nb[1]; a.o_nb_b = out->nb[3];
+    a.tickets = ctx->tickets;
+    a.d = (int)d; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.B = (int)B;
+    DeviceGuard g(ctx->device);
+    // q_out aliasing q: every split reads q while split 0 writes q_out
+    const bool alias = q_out->data == q->data;
+    if (alias || !decode_step_supported(a)) {
+        // the unfused path: RoPE + append, then attention (other cache types, longer windows)
+        if ((st = vva_rope_append(ctx, kv, layer, q, k, v, pos, seq_ids, freq_base, q_out)) != VVA_OK) return st;
+        return vva_attn(ctx, kv, layer, q_out, seq_ids, nullptr, scale, out);
+    }
+    const int n_splits = decode_step_splits(a);
+    if (n_splits > 1) {
+        if ((st = ensure_ws(ctx, (size_t)n_splits * B * Hq * (d + 2) * sizeof(float))) != VVA_OK) return st;
+    }
+    a.ws = ctx->ws;
+    hipError_t e = launch_decode_step(a, n_splits, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "decode_step launch");
+    ctx->last_splits = n_splits;
+    return VVA_OK;
 }

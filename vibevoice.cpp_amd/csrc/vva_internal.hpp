@@ -85,6 +85,30 @@ enum { kMaskNone = 0, kMaskExplicit = 1, kMaskCausal = 2 };
 size_t window_f16_bytes(const AttnArgs& a);
 hipError_t launch_window_to_f16(const AttnArgs& a, void* dst, hipStream_t s);
 
+// Single-token decode step in one launch (decode_step.hip): RoPE + append +
+// split attention + in-kernel merge.  F16 / BF16 caches, len + 1 <=
+// kMaxStepSplits * 128 keys, B * Hkv <= kMaxStepTickets.
+constexpr int kMaxStepSplits = 64;
+constexpr int kMaxStepTickets = 256;
+struct StepArgs {
+    const char* q; int q_type; int64_t q_nb_h, q_nb_b;    // ne = [d, Hq, 1, B]
+    const char* k; int k_type; int64_t k_nb_h, k_nb_b;    // ne = [d, Hkv, 1, B]
+    const char* v; int v_type; int64_t v_nb_h, v_nb_b;
+    const int32_t* pos; int64_t pos_stride_b;
+    char* q_out; int q_out_type; int64_t qo_nb_h, qo_nb_b;
+    char* kc[kMaxBatch]; char* vc[kMaxBatch];              // row 0 of each sequence's K / V of the layer
+    int64_t cache_row_bytes, cache_head_bytes; int cache_type;
+    int past[kMaxBatch];                                   // the new row's index = len(seq_b)
+    float theta_scale, scale;
+    float* out; int64_t o_nb_h, o_nb_b;
+    float* ws;                                             // split partials
+    unsigned* tickets;                                     // [B * Hkv], zero between calls
+    int d, Hq, Hkv, B;
+};
+bool decode_step_supported(const StepArgs& a);
+int decode_step_splits(const StepArgs& a);
+hipError_t launch_decode_step(const StepArgs& a, int n_splits, hipStream_t s);
+
 // Linear layers around the attention (proj.hip).  Token row n = b * T + t.
 enum { kProjQKV = 0, kProjResidual = 1 };
 struct ProjPrepArgs {

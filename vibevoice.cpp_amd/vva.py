@@ -32,7 +32,7 @@ EXPORTS = [
     "vva_kv_view", "vva_kv_upload", "vva_rope_ext", "vva_rope_append", "vva_attn",
     "vva_flash_attn_ext", "vva_supports", "vva_set_attn_path", "vva_last_decode_splits",
     "vva_set_schedule", "vva_attn_noalloc", "vva_qkv_rope_append", "vva_out_proj_residual",
-    "vva_set_flash_attn",
+    "vva_set_flash_attn", "vva_decode_step",
 ]
 
 
@@ -105,6 +105,7 @@ def load_library(path: str = LIB_PATH):
         "vva_last_decode_splits": (I, [P]),
         "vva_set_schedule": (I, [P, I, I, I]),
         "vva_set_flash_attn": (I, [P, I]),
+        "vva_decode_step": (I, [P, P, I, TP, TP, TP, TP, P, F, F, TP, TP]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -238,6 +239,14 @@ class Context:
         mp = ctypes.byref(_mask_view(mask)) if mask is not None else None
         self.check(self.lib.vva_attn(self.h, kv.h, layer, ctypes.byref(view(q)), ids, mp, scale,
                                      ctypes.byref(view(out))))
+
+    def decode_step(self, kv: "KVCache", layer: int, q, k, v, pos, q_out, out, scale: float, seq_ids=None,
+                    freq_base: float = 1.0e6):
+        """One new token per sequence: RoPE + append + attention (q/k/v [B, 1, H, d], pos int32 [1] or [B, 1])."""
+        ids = _ids(seq_ids)
+        self.check(self.lib.vva_decode_step(self.h, kv.h, layer, ctypes.byref(view(q)), ctypes.byref(view(k)),
+                                            ctypes.byref(view(v)), ctypes.byref(view(pos)), ids, freq_base, scale,
+                                            ctypes.byref(view(q_out)), ctypes.byref(view(out))))
 
     def attn_noalloc(self, kv: "KVCache", layer: int, q, out, scale: float, seq_ids=None, mask=None):
         """vva_attn_noalloc: as attn, with the split partials in the device's
