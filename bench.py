@@ -544,8 +544,13 @@ def main() -> int:
             c = vva.Context(0)
             r = run_prefill_chunked(torch, vva, c, layers=2)
             c.close()
+        elif args.only == "proj":
+            r = run_proj(torch, vva, vvo)
         else:
-            r = run_proj(torch, vva, vvo) if args.only == "proj" else run_small_prefills(torch, vva)
+            r = run_small_prefills(torch, vva)
+            c = vva.Context(0)
+            r["c2_decode_small"] = run_decode_small(torch, vva, c, steps=200)
+            c.close()
         print(json.dumps({args.only: r}), flush=True)
         return 0
     ctx = vva.Context(0)

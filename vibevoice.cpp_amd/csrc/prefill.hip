@@ -59,16 +59,11 @@ namespace vva {
 
 namespace {
 
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-typedef __bf16 b8 __attribute__((ext_vector_type(8)));
-typedef short s4 __attribute__((ext_vector_type(4)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-typedef __attribute__((address_space(3))) char lds_char;
+
+#include "mfma_ops.hpp"
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazy = 8.0f;      // running-max slack in log2 units: p <= 2^8 (f16-safe, rare rescales)
@@ -132,58 +127,8 @@ __device__ __forceinline__ float max_swap32(float x) {
     return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-template <int KT> struct Frag;
-template <> struct Frag<VVA_TYPE_F16> {
-    typedef h8 type;
-    static __device__ __forceinline__ f32x16 mma(const h8& a, const h8& b, const f32x16& c) {
-        return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-    }
-    static __device__ __forceinline__ uint16_t cvt(float x) { return f32_to_f16(x); }
-};
-template <> struct Frag<VVA_TYPE_BF16> {
-    typedef b8 type;
-    static __device__ __forceinline__ f32x16 mma(const b8& a, const b8& b, const f32x16& c) {
-        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-    }
-    static __device__ __forceinline__ uint16_t cvt(float x) { return f32_to_bf16(x); }
-};
-
 __device__ __forceinline__ float bits16_to_f32(uint32_t v, int type) {
     return type == VVA_TYPE_BF16 ? bf16_to_f32((uint16_t)v) : f16_to_f32((uint16_t)v);
-}
-
-template <typename V>
-__device__ __forceinline__ V as_vec(const u32x4& u) {
-    V v;
-    __builtin_memcpy(&v, &u, 16);
-    return v;
-}
-
-// V^T fragment of the second product: dims dt*32 + l%32, keys k0 + (0..3)
-// and k1 + (0..3), from the row-major V tile.  In each 16-lane group, lane i
-// points at row k + i/4, dims d0 + 4 (i%4) .. +3; the transposing read then
-// gives lane i the 4 keys of dim d0 + i.
-template <int KT>
-__device__ __forceinline__ h8 v_frag(const lds_char* vrow0, const lds_char* vrow1) {
-    const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)vrow0);
-    const s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s4*)vrow1);
-    h8 v;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const uint16_t x = (uint16_t)lo[e], y = (uint16_t)hi[e];
-        if constexpr (KT == VVA_TYPE_BF16) {
-            // the 16-bit patterns are bf16: widen to f32 and round to f16
-            v[e] = (_Float16)bf16_to_f32(x);
-            v[e + 4] = (_Float16)bf16_to_f32(y);
-        } else {
-            _Float16 fx, fy;
-            __builtin_memcpy(&fx, &x, 2);
-            __builtin_memcpy(&fy, &y, 2);
-            v[e] = fx;
-            v[e + 4] = fy;
-        }
-    }
-    return v;
 }
 
 __device__ __forceinline__ const lds_char* lds_at(uint32_t addr) { return (const lds_char*)(uintptr_t)addr; }
@@ -374,8 +319,7 @@ __global__ void __launch_bounds__(kWaves * 64) prefill_kernel(AttnArgs a, float*
     const float sl2 = a.scale * kLog2e;
     // per-lane LDS offsets of the operand reads within a stage
     const int k_rd = l32 * KP + half * 16;                                   // K: key l32, dims 8 half ..
-    const int v_rd = ((lane & 15) >> 2) * VP + (16 * ((lane >> 4) & 1) + 4 * (lane & 3)) * 2 +
-                     4 * half * VP;                                          // V^T, see v_frag
+    const int v_rd = v_frag_offset(lane, VP);                                // V^T, see v_frag
     const char* mrow = EXPL ? a.mask + b * a.mask_nb_b + tcol * a.mask_nb_row : nullptr;
 
     // S^T of the tile's two 32-key halves: key 8 (r / 4) + 4 half + r % 4

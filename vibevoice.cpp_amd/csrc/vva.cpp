@@ -995,7 +995,7 @@ extern "C" vva_status vva_decode_step(vva_context* ctx, vva_kv* kv, int layer, c
     a.scale = scale;
     a.out = (float*)out->data; a.o_nb_h = out->nb[1]; a.o_nb_b = out->nb[3];
     a.tickets = ctx->tickets;
-    a.d = (int)d; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.B = (int)B;
+    a.d = (int)d; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.B = (int)B; a.G = (int)(Hq / Hkv);
     DeviceGuard g(ctx->device);
     // q_out aliasing q: every split reads q while split 0 writes q_out
     const bool alias = q_out->data == q->data;

@@ -104,6 +104,7 @@ struct StepArgs {
     float* ws;                                             // split partials
     unsigned* tickets;                                     // [B * Hkv], zero between calls
     int d, Hq, Hkv, B;
+    int G;                                                 // Hq / Hkv
 };
 bool decode_step_supported(const StepArgs& a);
 int decode_step_splits(const StepArgs& a);
