@@ -24,6 +24,7 @@ constexpr int kRowsPerBlock = 4;   // one row per wave
 
 template <int DPL>
 __global__ void __launch_bounds__(256) attn_rows_kernel(AttnArgs a) {
+    prefetch_kernargs<sizeof(AttnArgs)>();
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
     if (row >= a.B * a.T * a.Hq) return;        // whole wave leaves together

@@ -82,6 +82,7 @@ struct Cfg {
 template <int D, int G, int KT>
 __global__ void __launch_bounds__(kWaves * 64)
 decode_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split_len) {
+    prefetch_kernargs<sizeof(AttnArgs)>();
     using C = Cfg<D, G, KT>;
     constexpr bool Q8 = C::Q8;
     constexpr int NW = kWaves, LPT = C::LPT, TPS = C::TPS, TPI = C::TPI, SPI = C::SPI;
@@ -503,6 +504,7 @@ constexpr int kDppRowRor8 = 0x128;
 template <int D>
 __global__ void __launch_bounds__(kMergeThreads) decode_merge_kernel(AttnArgs a, const float* __restrict__ ws,
                                                                      int n_splits) {
+    prefetch_kernargs<sizeof(AttnArgs)>();
     constexpr int TPR = kMergeDims / 4;         // threads per partial row quarter
     constexpr int NG = kMergeThreads / TPR;     // row groups
     constexpr int NW = kMergeThreads / 64;

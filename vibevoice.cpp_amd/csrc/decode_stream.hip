@@ -145,6 +145,7 @@ __device__ __forceinline__ h4 cat_h4(h2 lo, h2 hi) { return h4{lo[0], lo[1], hi[
 template <int D, int HKV, int NHG>
 __global__ void __launch_bounds__(kW * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
 decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits) {
+    prefetch_kernargs<sizeof(AttnArgs)>();
     constexpr int NB = D / 32;                // Q8_0 blocks per head row
     constexpr int HB = NB * kQ8Bytes;         // bytes per head row
     constexpr int RB = HKV * HB;              // bytes per token row in LDS (the group's kv heads)

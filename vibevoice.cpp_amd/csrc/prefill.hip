@@ -136,6 +136,7 @@ __device__ __forceinline__ const lds_char* lds_at(uint32_t addr) { return (const
 // EXPL: explicit F16 mask (otherwise implicit causal / length masking only).
 template <int D, int KT, bool EXPL>
 __global__ void __launch_bounds__(kWaves * 64) prefill_kernel(AttnArgs a, float* __restrict__ ws, PrefillPlan plan) {
+    prefetch_kernargs<sizeof(AttnArgs)>();
     using F = Frag<KT>;
     using QF = typename F::type;
     constexpr int DS = D / 16;                     // 16-dim MFMA steps of Q.K
@@ -465,6 +466,7 @@ __global__ void __launch_bounds__(kWaves * 64) prefill_kernel(AttnArgs a, float*
 // normalized into out.  Rows of unsplit row tiles were written directly.
 template <int D>
 __global__ void __launch_bounds__(256) prefill_merge_kernel(AttnArgs a, const float* __restrict__ ws, PrefillPlan plan) {
+    prefetch_kernargs<sizeof(AttnArgs)>();
     const int64_t nr_all = (int64_t)a.B * a.T * a.Hq;
     const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int64_t rg = idx / (D / 4);
@@ -515,6 +517,7 @@ hipError_t launch_pf(const AttnArgs& a, float* ws, const PrefillPlan& p, hipStre
 // One thread per 32-element block of a K or V head row of one sequence:
 // grid (blocks of the longest window / 256, 2 B: K and V of each sequence).
 __global__ void __launch_bounds__(256) window_to_f16_kernel(AttnArgs a, uint16_t* __restrict__ dst) {
+    prefetch_kernargs<sizeof(AttnArgs)>();
     const int b = blockIdx.y >> 1, which = blockIdx.y & 1;
     const int nblk = a.d / 32;
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;       // (row, head, block)

@@ -62,6 +62,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_
 // round trip, d * q with the fp16 d), and, for the q/k/v projections, the
 // row's RoPE (cos, sin) pairs with the fp32 theta recurrence.
 __global__ void __launch_bounds__(256) proj_prep_kernel(ProjPrepArgs a) {
+    prefetch_kernargs<sizeof(ProjPrepArgs)>();
     const int n = blockIdx.x;
     const int b = n / a.T, t = n - b * a.T;
     const char* src = a.x + b * a.x_nb_b + t * a.x_nb_t;
@@ -110,6 +111,7 @@ __global__ void __launch_bounds__(256) proj_prep_kernel(ProjPrepArgs a) {
 // WQ8: Q8_0 weights (else F16).  MODE: kProjQKV or kProjResidual.
 template <bool WQ8, int MODE>
 __global__ void __launch_bounds__(256) proj_gemm_kernel(ProjArgs a) {
+    prefetch_kernargs<sizeof(ProjArgs)>();
     __shared__ __attribute__((aligned(16))) char lds[2 * kStage];
 
     const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5, l32 = lane & 31;

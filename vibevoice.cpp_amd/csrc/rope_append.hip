@@ -24,6 +24,7 @@ namespace vva {
 namespace {
 
 __global__ void __launch_bounds__(256) rope_append_kernel(RopeAppendArgs a, int items_per_block) {
+    prefetch_kernargs<sizeof(RopeAppendArgs)>();
     const int t = blockIdx.x, b = blockIdx.y;
     const int P = a.d >> 1;
     __shared__ float cs[128], sn[128];
@@ -126,6 +127,7 @@ constexpr int kRopeTokens = 8;         // tokens per workgroup of the vector pat
 // kernel's bit for bit.
 template <int P>
 __global__ void __launch_bounds__(256) rope_append_vec_kernel(RopeAppendArgs a) {
+    prefetch_kernargs<sizeof(RopeAppendArgs)>();
     constexpr int C = P / 8;                          // 8-pair chunks per row
     const int t0 = blockIdx.x * kRopeTokens, b = blockIdx.y;
     const int nt = min(kRopeTokens, a.T - t0);

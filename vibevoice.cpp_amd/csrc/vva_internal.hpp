@@ -186,6 +186,28 @@ hipError_t launch_proj(ProjPrepArgs& p, ProjArgs& a, void* ws, hipStream_t s);
 #if defined(__HIPCC__)
 namespace vva {
 
+// Loads one dword of every 64-byte line of the first BYTES bytes of the
+// kernel-argument segment (BYTES = the explicit arguments' size, so every
+// load is inside the segment), then waits once.  The scalar data cache starts
+// cold at each launch, and the compiler reads argument fields where they are
+// first needed, several dependent round trips apart; after this they hit.
+// One asm block (loads, then the wait), so the scratch register it writes is
+// the block's own until every load has returned.
+template <int BYTES>
+__device__ __forceinline__ void prefetch_kernargs() {
+    const char* p = (const char*)__builtin_amdgcn_kernarg_segment_ptr();
+    uint32_t x;
+    asm volatile(".set .Lvva_ka_off, 0\n\t"
+                 ".rept %2\n\t"
+                 "s_load_dword %0, %1, .Lvva_ka_off\n\t"
+                 ".set .Lvva_ka_off, .Lvva_ka_off + 64\n\t"
+                 ".endr\n\t"
+                 "s_waitcnt lgkmcnt(0)"
+                 : "=&s"(x)
+                 : "s"(p), "n"((BYTES + 63) / 64)
+                 : "memory");
+}
+
 __device__ __forceinline__ float f16_to_f32(uint16_t h) {
     _Float16 v; __builtin_memcpy(&v, &h, 2); return (float)v;
 }
