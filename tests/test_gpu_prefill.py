@@ -350,3 +350,39 @@ def test_prefill_key_splits_score_jump(ctx, torch_gpu):
     ref = oracle_attn(as_f32(torch, q), kv, 0, [0], [L], T, d ** -0.5)
     assert_close(o, ref, *TOL, what="score jump, 6 key splits")
     kv.free()
+
+
+@pytest.mark.parametrize("t", [vva.BF16, vva.F32])
+def test_prefill_v_at_the_f16_range_edge(ctx, torch_gpu, t):
+    """P.V takes V as f16 for BF16 caches and, through the window's F16 cast
+    (the reference's own cast before flash attention, src/qwen2.cpp:328-331),
+    for F32 caches: V up to the f16 maximum 65504 must come through exactly.
+    V * 2^14 with |V| < 4 reaches 65372; every product and sum then scales by
+    the power of two, so the output must be exactly 2^14 times the unscaled
+    one, and the unscaled one must match the oracle."""
+    torch = torch_gpu
+    d, Hq, Hkv, T = 128, 28, 4, 320
+    rng = np.random.default_rng(31)
+    k = rng.standard_normal((T, Hkv, d)).astype(np.float32)
+    v = rng.standard_normal((T, Hkv, d))
+    v = np.sign(v) * np.clip(np.abs(v), 2.0 ** -6, 3.99)          # no f16 subnormals at either scale
+    v = v.astype(np.float32)
+    q = to_gpu(torch, rng.standard_normal((1, T, Hq, d)), vva.F32)
+    outs = []
+    for scale in (1.0, 2.0 ** 14):
+        kv = vva.KVCache(ctx, 1, Hkv, d, T, 1, t)
+        kv.upload(0, 0, 0, k, (v * scale).astype(np.float32))
+        kv.set_len(0, 0)
+        out = torch.full((1, T, Hq, d), float("nan"), dtype=torch.float32, device="cuda")
+        ctx.attn(kv, 0, q, out, d ** -0.5)
+        torch.cuda.synchronize()
+        outs.append(as_f32(torch, out))
+        if scale == 1.0:
+            ref = oracle_attn(as_f32(torch, q), kv, 0, [0], [T], T, d ** -0.5)
+            assert_close(outs[0], ref, *TOL, what="unscaled V")
+        else:
+            vmax = np.abs(vvo.to_f32(kv.download(0, 0, T)[1].reshape(-1), t, T * Hkv * d)).max()
+            assert 6e4 < vmax <= 65504.0
+        kv.free()
+    assert np.isfinite(outs[1]).all()
+    np.testing.assert_array_equal(outs[1], outs[0] * 2.0 ** 14)
