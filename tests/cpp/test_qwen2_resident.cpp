@@ -22,6 +22,14 @@
 //              per-sequence positions pos ne=[1, 2], against the oracle.
 //   q8         the ASR CFG decode on Q8_0 caches at the 7B shapes, ragged
 //              lengths, against the oracle.
+//   block      the attention half of the layer through
+//              qwen2_attention_block_resident (fused Q/K/V projection + bias +
+//              RoPE + append, attention, output projection + residual) at the
+//              0.5B shapes, F16 and Q8_0 weights: a 96-token chunk over a
+//              40-token past, then a B = 2 CFG decode step over ragged pasts;
+//              q, the appended rows, o and h against the oracle (ggml-order
+//              linear layers, RoPE recurrence, attention on the device's own
+//              operands).
 //   errors     past_len + T > max_seq, a bad layer and a bad sequence id come
 //              back as VVA_ERR_INVALID_ARG (the reference's GGML_ASSERTs,
 //              src/qwen2.cpp:269-270).
@@ -409,6 +417,158 @@ int test_q8(vva_context* ctx) {
     return decode_steps(ctx, 128, 28, 4, VVA_TYPE_Q8_0, prompt, 3, 41, 40);
 }
 
+// ------------------------------------------------------------ the attention block
+
+int64_t weight_row_bytes(int64_t K, int type) { return type == VVA_TYPE_F16 ? K * 2 : K / 32 * 34; }
+
+// M rows of K weights, N(0,1) / sqrt(K), stored as `type` (ggml layout)
+std::vector<uint8_t> make_weight(Rng& r, int64_t M, int64_t K, int type) {
+    std::vector<float> w = r.normal((size_t)(M * K));
+    const float s = 1.0f / sqrtf((float)K);
+    for (float& x : w) x *= s;
+    std::vector<uint8_t> raw((size_t)(M * weight_row_bytes(K, type)));
+    if (type == VVA_TYPE_F16) vvo_from_f32(w.data(), raw.data(), type, M * K);
+    else vvo_quantize_q8_0(w.data(), raw.data(), M * K);
+    return raw;
+}
+
+vva_tensor weight_view(void* p, int type, int64_t K, int64_t M) {
+    vva_tensor t = {};
+    t.data = p;
+    t.type = type;
+    const int64_t rb = weight_row_bytes(K, type);
+    t.ne[0] = K; t.ne[1] = M; t.ne[2] = 1; t.ne[3] = 1;
+    t.nb[0] = type == VVA_TYPE_F16 ? 2 : 34;
+    t.nb[1] = rb; t.nb[2] = rb * M; t.nb[3] = rb * M;
+    return t;
+}
+
+// |got - ref| <= tol + (rounding of ref to `type`), and the mean excess <= mean_tol
+bool within_rounded(const char* what, const std::vector<float>& got, const std::vector<float>& ref, int type,
+                    double tol, double mean_tol) {
+    const double ulp = type == VVA_TYPE_F16 ? 1.0 / 2048.0 : 0.0;
+    double worst = 0.0, max_err = 0.0, sum = 0.0;
+    bool finite = true;
+    for (size_t i = 0; i < got.size(); ++i) {
+        if (!std::isfinite(got[i])) finite = false;
+        const double e = fabs((double)got[i] - (double)ref[i]), r = fabs((double)ref[i]) * ulp;
+        max_err = e > max_err ? e : max_err;
+        worst = e - r - tol > worst ? e - r - tol : worst;
+        sum += e - r > 0.0 ? e - r : 0.0;
+    }
+    const double mean = sum / (double)got.size();
+    const bool ok = finite && worst <= 0.0 && mean <= mean_tol;
+    printf("  %-44s max %.3e (tol %.0e + rounding)  mean %.3e  %s\n", what, max_err, tol, mean, ok ? "ok" : "FAIL");
+    return ok;
+}
+
+int block_case(vva_context* ctx, int wt) {
+    const int hidden = 896, Hq = 14, Hkv = 2, d = 64, qd = Hq * d, kd = Hkv * d;
+    Rng r(900 + (uint64_t)wt);
+    const std::vector<uint8_t> wq = make_weight(r, qd, hidden, wt), wk = make_weight(r, kd, hidden, wt),
+                               wv = make_weight(r, kd, hidden, wt), wo = make_weight(r, hidden, qd, wt);
+    std::vector<float> bq = r.normal(qd), bk = r.normal(kd), bv = r.normal(kd);
+    Dev dwq(wq.size()), dwk(wk.size()), dwv(wv.size()), dwo(wo.size()), dbq(4 * (size_t)qd), dbk(4 * (size_t)kd),
+        dbv(4 * (size_t)kd);
+    (void)hipMemcpy(dwq.p, wq.data(), wq.size(), hipMemcpyHostToDevice);
+    (void)hipMemcpy(dwk.p, wk.data(), wk.size(), hipMemcpyHostToDevice);
+    (void)hipMemcpy(dwv.p, wv.data(), wv.size(), hipMemcpyHostToDevice);
+    (void)hipMemcpy(dwo.p, wo.data(), wo.size(), hipMemcpyHostToDevice);
+    (void)hipMemcpy(dbq.p, bq.data(), 4 * (size_t)qd, hipMemcpyHostToDevice);
+    (void)hipMemcpy(dbk.p, bk.data(), 4 * (size_t)kd, hipMemcpyHostToDevice);
+    (void)hipMemcpy(dbv.p, bv.data(), 4 * (size_t)kd, hipMemcpyHostToDevice);
+    vva::Qwen2AttnWeights W;
+    W.q = weight_view(dwq.p, wt, hidden, qd);
+    W.k = weight_view(dwk.p, wt, hidden, kd);
+    W.v = weight_view(dwv.p, wt, hidden, kd);
+    W.o = weight_view(dwo.p, wt, qd, hidden);
+    W.q_bias = view4(dbq.p, VVA_TYPE_F32, qd, 1, 1, 1);
+    W.k_bias = view4(dbk.p, VVA_TYPE_F32, kd, 1, 1, 1);
+    W.v_bias = view4(dbv.p, VVA_TYPE_F32, kd, 1, 1, 1);
+    const int64_t rbq = weight_row_bytes(hidden, wt), rbo = weight_row_bytes(qd, wt);
+
+    vva::ResidentKV kvs;
+    if (!kvs.init(ctx, 1, d, Hkv, 256, 2, VVA_TYPE_F16)) return 80;
+    const int pasts[2] = {40, 23};
+    for (int s = 0; s < 2; ++s) {
+        const std::vector<float> k = r.normal((size_t)pasts[s] * kd), v = r.normal((size_t)pasts[s] * kd);
+        if (!status_ok("upload", kvs.upload(0, s, pasts[s], k.data(), v.data()), kvs)) return 81;
+        kvs.past_len[s] = pasts[s];
+    }
+    const vva::Qwen2Hparams hp = {hidden, Hq, Hkv, d, 1.0e6f, true};
+    struct Step {
+        int T;
+        std::vector<int32_t> seqs;
+    };
+    const Step steps[2] = {{96, {0}}, {1, {0, 1}}};
+    for (const Step& st : steps) {
+        const int T = st.T, B = (int)st.seqs.size(), N = B * T;
+        const std::vector<float> x = r.normal((size_t)N * hidden), xn = r.normal((size_t)N * hidden);
+        std::vector<int32_t> pos((size_t)N);
+        std::vector<int> L(B);
+        for (int b = 0; b < B; ++b) {
+            L[b] = kvs.past_len[st.seqs[b]] + T;
+            for (int t = 0; t < T; ++t) pos[(size_t)b * T + t] = kvs.past_len[st.seqs[b]] + t;
+        }
+        Dev dx(4 * (size_t)N * hidden), dxn(4 * (size_t)N * hidden), dh(4 * (size_t)N * hidden),
+            dq(4 * (size_t)N * qd), dout(4 * (size_t)N * qd), dpos(4 * (size_t)N);
+        (void)hipMemcpy(dx.p, x.data(), 4 * x.size(), hipMemcpyHostToDevice);
+        (void)hipMemcpy(dxn.p, xn.data(), 4 * xn.size(), hipMemcpyHostToDevice);
+        (void)hipMemcpy(dpos.p, pos.data(), 4 * pos.size(), hipMemcpyHostToDevice);
+        const vva_tensor tx = view4(dx.p, VVA_TYPE_F32, hidden, T, B, 1), txn = view4(dxn.p, VVA_TYPE_F32, hidden, T, B, 1),
+                         th = view4(dh.p, VVA_TYPE_F32, hidden, T, B, 1), tq = view4(dq.p, VVA_TYPE_F32, d, Hq, T, B),
+                         to = view4(dout.p, VVA_TYPE_F32, d, Hq, T, B), tp = view4(dpos.p, VVA_TYPE_I32, T, B, 1, 1);
+        const int32_t* ids = B > 1 ? st.seqs.data() : nullptr;
+        if (!status_ok("qwen2_attention_block_resident",
+                       vva::qwen2_attention_block_resident(kvs, 0, txn, tx, W, tp, nullptr, hp, tq, to, th, ids), kvs))
+            return 82;
+        (void)hipDeviceSynchronize();
+        printf("  %s weights, T = %d, B = %d\n", wt == VVA_TYPE_F16 ? "F16" : "Q8_0", T, B);
+        // q = RoPE(linear(xn, Wq) + bq)
+        std::vector<float> ql((size_t)N * qd), kl((size_t)N * kd), vl((size_t)N * kd);
+        vvo_linear(wq.data(), wt, rbq, bq.data(), xn.data(), ql.data(), N, hidden, qd, VVO_GGML, 0);
+        vvo_linear(wk.data(), wt, rbq, bk.data(), xn.data(), kl.data(), N, hidden, kd, VVO_GGML, 0);
+        vvo_linear(wv.data(), wt, rbq, bv.data(), xn.data(), vl.data(), N, hidden, kd, VVO_GGML, 0);
+        vvo_rope_neox(ql.data(), ql.data(), pos.data(), T, d, Hq, T, B, 1.0e6f, VVO_THETA_RECURRENCE);
+        vvo_rope_neox(kl.data(), kl.data(), pos.data(), T, d, Hkv, T, B, 1.0e6f, VVO_THETA_RECURRENCE);
+        const std::vector<float> qdev = download_f32(dq.p, (size_t)N * qd, VVA_TYPE_F32);
+        if (!within("rotated q vs oracle", compare(qdev, ql), kMaxTol, kMeanTol)) return 83;
+        // the appended rows [past, past + T) of each sequence, F16
+        for (int b = 0; b < B; ++b) {
+            const int s = st.seqs[b], p0 = L[b] - T;
+            const std::vector<uint8_t> kb = cache_bytes(kvs.k(0, s), L[b]), vb = cache_bytes(kvs.v(0, s), L[b]);
+            std::vector<float> kg((size_t)T * kd), vg((size_t)T * kd);
+            vvo_to_f32(kb.data() + (size_t)p0 * kd * 2, VVA_TYPE_F16, kg.data(), (int64_t)T * kd);
+            vvo_to_f32(vb.data() + (size_t)p0 * kd * 2, VVA_TYPE_F16, vg.data(), (int64_t)T * kd);
+            const std::vector<float> kr(kl.begin() + (size_t)b * T * kd, kl.begin() + (size_t)(b + 1) * T * kd),
+                vr(vl.begin() + (size_t)b * T * kd, vl.begin() + (size_t)(b + 1) * T * kd);
+            if (!within_rounded("appended K rows vs oracle", kg, kr, VVA_TYPE_F16, kMaxTol, kMeanTol)) return 84;
+            if (!within_rounded("appended V rows vs oracle", vg, vr, VVA_TYPE_F16, kMaxTol, kMeanTol)) return 85;
+        }
+        // o over the window, on the device's own q and cache rows
+        const std::vector<float> odev = download_f32(dout.p, (size_t)N * qd, VVA_TYPE_F32);
+        const std::vector<float> oref = oracle_out(qdev, kvs, 0, std::vector<int>(st.seqs.begin(), st.seqs.end()), L,
+                                                   T, Hq, Hkv, d, VVA_TYPE_F16);
+        if (!within("attention output vs oracle", compare(odev, oref), kMaxTol, kMeanTol)) return 86;
+        // h = x + o Wo^T, on the device's own o
+        std::vector<float> href((size_t)N * hidden);
+        vvo_linear(wo.data(), wt, rbo, nullptr, odev.data(), href.data(), N, qd, hidden, VVO_GGML, 0);
+        for (size_t i = 0; i < href.size(); ++i) href[i] += x[i];
+        const std::vector<float> hdev = download_f32(dh.p, (size_t)N * hidden, VVA_TYPE_F32);
+        if (!within("h = x + attn_o(o) vs oracle", compare(hdev, href), kMaxTol, kMeanTol)) return 87;
+        for (int b = 0; b < B; ++b) kvs.past_len[st.seqs[b]] += T;
+    }
+    return 0;
+}
+
+int test_block(vva_context* ctx) {
+    for (const int wt : {VVA_TYPE_F16, VVA_TYPE_Q8_0}) {
+        const int rc = block_case(ctx, wt);
+        if (rc) return rc;
+    }
+    return 0;
+}
+
 int test_errors(vva_context* ctx) {
     const int d = 64, Hq = 14, Hkv = 2, T = 8;
     vva::ResidentKV kvs;
@@ -470,8 +630,8 @@ struct Case {
 
 int main(int argc, char** argv) {
     const std::vector<Case> cases = {{"chunks", test_chunks}, {"stack", test_stack}, {"cfg", test_cfg},
-                                     {"q8", test_q8},         {"errors", test_errors}, {"supports", test_supports},
-                                     {"order", test_order}};
+                                     {"q8", test_q8},         {"block", test_block},   {"errors", test_errors},
+                                     {"supports", test_supports}, {"order", test_order}};
     std::vector<std::string> want;
     for (int i = 1; i < argc; ++i) {
         if (!strcmp(argv[i], "--list")) {

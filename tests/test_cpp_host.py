@@ -13,7 +13,7 @@ import pytest
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 BIN = os.path.join(REPO, "tests", "cpp", "bin", "test_qwen2_resident")
 HOSTLIB = os.path.join(REPO, "vibevoice.cpp_amd", "lib", "libvva_qwen2.a")
-CASES = ["chunks", "stack", "cfg", "q8", "errors", "supports", "order"]
+CASES = ["chunks", "stack", "cfg", "q8", "block", "errors", "supports", "order"]
 
 
 def _need_built():
@@ -25,8 +25,8 @@ def test_host_archive_defines_entry_points():
     _need_built()
     syms = subprocess.run(["nm", "-C", "--defined-only", HOSTLIB], capture_output=True, text=True,
                           check=True).stdout
-    for name in ("vva::qwen2_attention_resident", "vva::ResidentKV::init", "vva::ResidentKV::free",
-                 "vva::ResidentKV::upload"):
+    for name in ("vva::qwen2_attention_resident", "vva::qwen2_attention_block_resident", "vva::ResidentKV::init",
+                 "vva::ResidentKV::free", "vva::ResidentKV::upload"):
         assert name in syms, name
 
 

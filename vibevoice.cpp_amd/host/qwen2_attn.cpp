@@ -54,30 +54,37 @@ int ResidentKV::upload(int layer, int seq, int len, const float* k_rows, const f
 
 const char* ResidentKV::last_error() const { return vva_last_error(ctx); }
 
-int qwen2_attention_resident(ResidentKV& kvs, int layer_idx, const vva_tensor& q, const vva_tensor& k,
-                             const vva_tensor& v, const vva_tensor& pos, const vva_tensor* mask,
-                             const Qwen2Hparams& hp, const vva_tensor& o, const int32_t* seq_ids) {
-    // shape checks of src/qwen2.cpp:262-270, as status codes
+namespace {
+
+// The shape checks of src/qwen2.cpp:262-270 as status codes, then the
+// caller's past_len made the library's (src/qwen2.cpp:266: past_len is the
+// source of truth) and the attention branch of src/qwen2.cpp:327-344 chosen
+// (for F32 caches: F16 cast + flash attention, or fp32 eager).
+int prepare(ResidentKV& kvs, int layer_idx, int64_t n_tokens, int64_t n_batch, const Qwen2Hparams& hp,
+            const int32_t* seq_ids) {
     if (!kvs.kv || layer_idx < 0 || layer_idx >= kvs.n_layers) return VVA_ERR_INVALID_ARG;
-    const int hd = hp.head_dim;
-    const int64_t n_tokens = q.ne[2];
-    const int64_t n_batch = q.ne[3] > 0 ? q.ne[3] : 1;
-    if (q.ne[0] != hd || q.ne[1] != hp.n_heads || k.ne[1] != hp.n_kv_heads || v.ne[1] != hp.n_kv_heads)
-        return VVA_ERR_INVALID_ARG;
     if (n_batch > VVA_MAX_BATCH) return VVA_ERR_INVALID_ARG;
     for (int64_t b = 0; b < n_batch; ++b) {
         const int s = seq_ids ? seq_ids[b] : (int)b;
         if (s < 0 || s >= kvs.n_seq) return VVA_ERR_INVALID_ARG;
         if (kvs.past_len[s] + n_tokens > kvs.max_seq) return VVA_ERR_INVALID_ARG;   // full_len <= max_seq
     }
-    // the caller's past_len is the source of truth (src/qwen2.cpp:266)
     for (int s = 0; s < kvs.n_seq; ++s) {
         const int st = vva_kv_set_len(kvs.kv, s, kvs.past_len[s]);
         if (st != VVA_OK) return st;
     }
-    // the branch of src/qwen2.cpp:327-344 (for F32 caches: F16 cast + flash
-    // attention, or fp32 eager)
-    int fa = vva_set_flash_attn(kvs.ctx, hp.use_flash_attn ? 1 : 0);
+    return vva_set_flash_attn(kvs.ctx, hp.use_flash_attn ? 1 : 0);
+}
+
+}  // namespace
+
+int qwen2_attention_resident(ResidentKV& kvs, int layer_idx, const vva_tensor& q, const vva_tensor& k,
+                             const vva_tensor& v, const vva_tensor& pos, const vva_tensor* mask,
+                             const Qwen2Hparams& hp, const vva_tensor& o, const int32_t* seq_ids) {
+    const int hd = hp.head_dim;
+    if (q.ne[0] != hd || q.ne[1] != hp.n_heads || k.ne[1] != hp.n_kv_heads || v.ne[1] != hp.n_kv_heads)
+        return VVA_ERR_INVALID_ARG;
+    int fa = prepare(kvs, layer_idx, q.ne[2], q.ne[3] > 0 ? q.ne[3] : 1, hp, seq_ids);
     if (fa != VVA_OK) return fa;
     // rope(q), rope(k), cpy(k -> window at past_len), cpy(v -> ...)  src/qwen2.cpp:282-306
     int st = vva_rope_append(kvs.ctx, kvs.kv, layer_idx, &q, &k, &v, &pos, seq_ids, hp.rope_theta, &q);
@@ -85,6 +92,36 @@ int qwen2_attention_resident(ResidentKV& kvs, int layer_idx, const vva_tensor& q
     // views of the window + flash_attn_ext(scale 1/sqrt(hd)), prec F32  src/qwen2.cpp:312-335
     const float scale = 1.0f / sqrtf((float)hd);
     return vva_attn(kvs.ctx, kvs.kv, layer_idx, &q, seq_ids, mask, scale, &o);
+}
+
+int qwen2_attention_block_resident(ResidentKV& kvs, int layer_idx, const vva_tensor& xn, const vva_tensor& x,
+                                   const Qwen2AttnWeights& w, const vva_tensor& pos, const vva_tensor* mask,
+                                   const Qwen2Hparams& hp, const vva_tensor& q_ws, const vva_tensor& o_ws,
+                                   const vva_tensor& h, const int32_t* seq_ids) {
+    const int hd = hp.head_dim;
+    const int64_t n_tokens = xn.ne[1], n_batch = xn.ne[2] > 0 ? xn.ne[2] : 1;
+    if (xn.ne[0] != hp.hidden_size || q_ws.ne[0] != hd || q_ws.ne[1] != hp.n_heads || q_ws.ne[2] != n_tokens ||
+        o_ws.ne[0] != hd || o_ws.ne[1] != hp.n_heads || o_ws.ne[2] != n_tokens)
+        return VVA_ERR_INVALID_ARG;
+    // o_ws is read back as rows of n_heads * hd (the cont_2d of src/qwen2.cpp:335)
+    if (o_ws.type != VVA_TYPE_F32 || o_ws.nb[0] != 4 || o_ws.nb[1] != (size_t)4 * hd) return VVA_ERR_INVALID_ARG;
+    int st = prepare(kvs, layer_idx, n_tokens, n_batch, hp, seq_ids);
+    if (st != VVA_OK) return st;
+    // q, k, v = linear(xn) + bias; rope(q), rope(k); k, v -> window  src/qwen2.cpp:273-306
+    const vva_tensor* bq = w.q_bias.data ? &w.q_bias : nullptr;
+    const vva_tensor* bk = w.k_bias.data ? &w.k_bias : nullptr;
+    const vva_tensor* bv = w.v_bias.data ? &w.v_bias : nullptr;
+    st = vva_qkv_rope_append(kvs.ctx, kvs.kv, layer_idx, &xn, &w.q, &w.k, &w.v, bq, bk, bv, &pos, seq_ids,
+                             hp.rope_theta, &q_ws);
+    if (st != VVA_OK) return st;
+    // flash_attn_ext over the window  src/qwen2.cpp:312-335
+    st = vva_attn(kvs.ctx, kvs.kv, layer_idx, &q_ws, seq_ids, mask, 1.0f / sqrtf((float)hd), &o_ws);
+    if (st != VVA_OK) return st;
+    // h = x + attn_o(o)  src/qwen2.cpp:349-350
+    vva_tensor rows = o_ws;
+    rows.ne[0] = (int64_t)hp.n_heads * hd; rows.ne[1] = n_tokens; rows.ne[2] = n_batch; rows.ne[3] = 1;
+    rows.nb[1] = o_ws.nb[2]; rows.nb[2] = o_ws.nb[3]; rows.nb[3] = o_ws.nb[3] * n_batch;
+    return vva_out_proj_residual(kvs.ctx, &rows, &w.o, &x, &h);
 }
 
 }  // namespace vva

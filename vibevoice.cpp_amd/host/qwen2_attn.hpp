@@ -102,4 +102,31 @@ int qwen2_attention_resident(ResidentKV& kvs, int layer_idx, const vva_tensor& q
                              const vva_tensor& v, const vva_tensor& pos, const vva_tensor* mask,
                              const Qwen2Hparams& hp, const vva_tensor& o, const int32_t* seq_ids = nullptr);
 
+// Device views of the attention weights of a layer (the attn_q / attn_k /
+// attn_v / attn_o fields of vv::Qwen2LayerWeights, src/qwen2.hpp:41-54):
+// ggml layout ne=[in, out] (rows of `in` contiguous), all F16 or all Q8_0;
+// biases F32 ne=[out], or data == nullptr for none.
+struct Qwen2AttnWeights {
+    vva_tensor q, k, v, o;
+    vva_tensor q_bias, k_bias, v_bias;
+};
+
+// The attention half of qwen2_layer_forward_resident from the normed input
+// to the residual sum (src/qwen2.cpp:273-350): q/k/v = linear(xn) with
+// bias, RoPE of q and k and the k/v rows into the resident window at each
+// sequence's past_len (one fused GEMM, vva_qkv_rope_append), attention over
+// the window (vva_attn), then h = x + o w_o^T (vva_out_proj_residual).
+//   xn:    F32/F16/BF16 ne=[hidden, T, B], rms_norm(x) (src/qwen2.cpp:274);
+//   x:     F32 ne=[hidden, T, B], the layer input;
+//   q_ws:  F32 ne=[hd, n_heads, T, B], contiguous: receives the rotated q;
+//   o_ws:  F32 ne=[hd, n_heads, T, B], contiguous: the attention output;
+//   h:     F32 ne=[hidden, T, B], x + attn_o(o) (src/qwen2.cpp:349-350),
+//          may alias x.
+// pos, mask, seq_ids, hp and the past_len contract are as for
+// qwen2_attention_resident.  Returns a vva_status.
+int qwen2_attention_block_resident(ResidentKV& kvs, int layer_idx, const vva_tensor& xn, const vva_tensor& x,
+                                   const Qwen2AttnWeights& w, const vva_tensor& pos, const vva_tensor* mask,
+                                   const Qwen2Hparams& hp, const vva_tensor& q_ws, const vva_tensor& o_ws,
+                                   const vva_tensor& h, const int32_t* seq_ids = nullptr);
+
 }  // namespace vva
