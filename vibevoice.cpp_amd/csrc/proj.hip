@@ -26,6 +26,17 @@
 // contiguous run of tiles: the 36 weight tiles of one token tile share its
 // X tile in that XCD's L2.
 //
+// Few token rows (a decode step: B * T <= 8).  The GEMM's 128-row token tile
+// would be almost empty and its 36 workgroups too few to stream the weights,
+// so proj_gemv_kernel reads each weight row once, one wave of 4 rows per
+// workgroup (1152 workgroups for the 7B q/k/v stack, evenly spread over the
+// CUs), all of a lane's weight loads in flight before any is used: F16
+// weights with v_dot2 on the f16-rounded x, Q8_0 weights with integer
+// v_dot4 block sums times d_w * d_x (ggml's Q8_0 x Q8_0 block dot, x
+// quantized by the lane that uses the block).  The token rows are read from
+// the layer input directly (L2-resident).  The q/k/v variant writes the F32
+// projections, which the RoPE + append kernel then rotates and stores.
+//
 // Epilogue.  The accumulators go through LDS as a [token][feature] tile, so
 // the epilogue threads see whole head rows: bias, then the NeoX rotation of
 // pair (i, i + d/2) with the token's (cos, sin) row written by the prep
@@ -37,10 +48,10 @@ namespace vva {
 
 namespace {
 
+#include "wave_ops.hpp"
+
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kTM = 128;                    // output features per tile
 constexpr int kTN = 128;                    // token rows per tile
@@ -311,7 +322,206 @@ __global__ void __launch_bounds__(256) proj_gemm_kernel(ProjArgs a) {
     }
 }
 
+// ------------------------------------------------------------ GEMV
+
+constexpr int kGvRows = 4;                       // output rows per workgroup (one wave)
+constexpr int kGvMaxN = 8;                       // token rows
+constexpr int kGvMaxK = 4096;                    // inputs
+constexpr int kGvF16It = kGvMaxK / 8 / 64;       // 8-element chunks per lane and row
+constexpr int kGvQ8It = kGvMaxK / 32 / 64;       // Q8_0 blocks per lane and row
+
+// Elements k0 .. k0 + 7 of token row n = b * T + t of the layer input.
+__device__ __forceinline__ void load_x8(const ProjArgs& a, int n, int k0, float (&x)[8]) {
+    const int b = n / a.T, t = n - b * a.T;
+    const char* src = a.x + b * a.x_nb_b + t * a.x_nb_t;
+    if (a.x_type == VVA_TYPE_F32) {
+        const float4 u0 = *(const float4*)(src + k0 * 4), u1 = *(const float4*)(src + k0 * 4 + 16);
+        x[0] = u0.x; x[1] = u0.y; x[2] = u0.z; x[3] = u0.w;
+        x[4] = u1.x; x[5] = u1.y; x[6] = u1.z; x[7] = u1.w;
+    } else {
+        const uint4 u = *(const uint4*)(src + k0 * 2);
+        const uint32_t wv[4] = {u.x, u.y, u.z, u.w};
+        const bool bf = a.x_type == VVA_TYPE_BF16;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint16_t lo = (uint16_t)(wv[e] & 0xffffu), hi = (uint16_t)(wv[e] >> 16);
+            x[2 * e] = bf ? bf16_to_f32(lo) : f16_to_f32(lo);
+            x[2 * e + 1] = bf ? bf16_to_f32(hi) : f16_to_f32(hi);
+        }
+    }
+}
+__device__ __forceinline__ uint32_t pack_f16(float lo, float hi) {
+    return (uint32_t)f32_to_f16(lo) | ((uint32_t)f32_to_f16(hi) << 16);
+}
+
+// One wave: rows m0 .. m0 + 3 over every token row.  Lane l takes the
+// 8-element chunks (F16) or Q8_0 blocks l, l + 64, ... of the rows: all its
+// weight loads go out first, then it converts (F16: rounds to f16) or
+// quantizes (Q8_0: ggml's quantize_row_q8_0, d = amax / 127 kept as fp16,
+// codes round(x / d)) the matching elements of each token row once and uses
+// them for all four rows.  The sums over lanes end in DPP reductions.
+template <bool WQ8, int MODE>
+__global__ void __launch_bounds__(64) proj_gemv_kernel(ProjArgs a) {
+    prefetch_kernargs<sizeof(ProjArgs)>();
+    const int lane = threadIdx.x;
+    const int N = a.N, K = a.K;
+    const int m0 = blockIdx.x * kGvRows;           // matrix boundaries are multiples of 128
+    const int mat = m0 < a.m_end[0] ? 0 : (m0 < a.m_end[1] ? 1 : 2);
+    const int mrow0 = m0 - (mat ? a.m_end[mat - 1] : 0);
+    const char* wb = a.w[mat] + (int64_t)mrow0 * a.w_nb[mat];
+    const int64_t wnb = a.w_nb[mat];
+    float acc[kGvRows][kGvMaxN];
+#pragma unroll
+    for (int r = 0; r < kGvRows; ++r)
+#pragma unroll
+        for (int n = 0; n < kGvMaxN; ++n) acc[r][n] = 0.0f;
+
+    if constexpr (!WQ8) {
+        const int nch = K / 8;
+        u32x4 wv[kGvF16It][kGvRows];
+#pragma unroll
+        for (int it = 0; it < kGvF16It; ++it) {
+            const int c = lane + 64 * it;
+            const int cc = c < nch ? c : 0;
+#pragma unroll
+            for (int r = 0; r < kGvRows; ++r) wv[it][r] = *(const u32x4*)(wb + r * wnb + (int64_t)cc * 16);
+        }
+#pragma unroll
+        for (int it = 0; it < kGvF16It; ++it) {
+            if (64 * it >= nch) break;                               // uniform
+            const int c = lane + 64 * it;
+            const bool live = c < nch;
+#pragma unroll
+            for (int n = 0; n < kGvMaxN; ++n) {
+                if (n >= N) break;                                   // uniform
+                float x[8];
+                load_x8(a, n, (live ? c : 0) * 8, x);
+                const uint32_t x0 = live ? pack_f16(x[0], x[1]) : 0u, x1 = live ? pack_f16(x[2], x[3]) : 0u;
+                const uint32_t x2 = live ? pack_f16(x[4], x[5]) : 0u, x3 = live ? pack_f16(x[6], x[7]) : 0u;
+#pragma unroll
+                for (int r = 0; r < kGvRows; ++r) {
+                    float s = acc[r][n];
+                    s = dot2_f16(wv[it][r].x, x0, s);
+                    s = dot2_f16(wv[it][r].y, x1, s);
+                    s = dot2_f16(wv[it][r].z, x2, s);
+                    s = dot2_f16(wv[it][r].w, x3, s);
+                    acc[r][n] = s;
+                }
+            }
+        }
+    } else {
+        // Q8_0 weight block j: 34 bytes from the 4-byte boundary at or below
+        // it (rows are 4-byte aligned: K is a multiple of 64, so a row holds
+        // an even number of blocks)
+        const int nbk = K / 32;
+        uint32_t qw[kGvQ8It][kGvRows][9];
+#pragma unroll
+        for (int it = 0; it < kGvQ8It; ++it) {
+            const int j = lane + 64 * it;
+            const int jj = j < nbk ? j : 0;
+#pragma unroll
+            for (int r = 0; r < kGvRows; ++r) {
+                const uint32_t* p = (const uint32_t*)(wb + r * wnb + (((int64_t)jj * kQ8Bytes) & ~(int64_t)3));
+#pragma unroll
+                for (int i = 0; i < 9; ++i) qw[it][r][i] = p[i];
+            }
+        }
+#pragma unroll
+        for (int it = 0; it < kGvQ8It; ++it) {
+            if (64 * it >= nbk) break;                               // uniform
+            const int j = lane + 64 * it;
+            const bool live = j < nbk;
+            const int jj = live ? j : 0;
+            const bool odd = jj & 1;                                 // the block starts 2 bytes into dword 0
+            float dw[kGvRows];
+            uint32_t codes[kGvRows][8];
+#pragma unroll
+            for (int r = 0; r < kGvRows; ++r) {
+                const uint32_t* q = qw[it][r];
+                dw[r] = live ? f16_to_f32((uint16_t)(odd ? q[0] >> 16 : q[0] & 0xffffu)) : 0.0f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) codes[r][i] = odd ? q[i + 1] : __builtin_amdgcn_alignbyte(q[i + 1], q[i], 2);
+            }
+#pragma unroll
+            for (int n = 0; n < kGvMaxN; ++n) {
+                if (n >= N) break;                                   // uniform
+                float x[32];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    float xs[8];
+                    load_x8(a, n, jj * 32 + 8 * q, xs);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) x[8 * q + e] = xs[e];
+                }
+                float am = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 32; ++e) am = fmaxf(am, fabsf(x[e]));
+                const float d = am / 127.0f;
+                const float id = d != 0.0f ? 1.0f / d : 0.0f;
+                const float dx = f16_to_f32(f32_to_f16(d));
+                uint32_t xc[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    uint32_t c = 0u;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        c |= ((uint32_t)(uint8_t)(int8_t)roundf(x[4 * i + e] * id)) << (8 * e);
+                    xc[i] = c;
+                }
+#pragma unroll
+                for (int r = 0; r < kGvRows; ++r) {
+                    int s = 0;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) s = __builtin_amdgcn_sdot4((int)codes[r][i], (int)xc[i], s, false);
+                    acc[r][n] = fmaf((float)s, dw[r] * dx, acc[r][n]);
+                }
+            }
+        }
+    }
+
+    // sums over the lanes; lane r * N + n keeps (row r, token n)
+    float outv = 0.0f;
+#pragma unroll
+    for (int r = 0; r < kGvRows; ++r)
+#pragma unroll
+        for (int n = 0; n < kGvMaxN; ++n) {
+            if (n >= N) break;                                       // uniform
+            const float s = wave_sum(acc[r][n]);
+            if (lane == r * N + n) outv = s;
+        }
+    if (lane < kGvRows * N) {
+        const int r = lane / N, n = lane - r * N;
+        const int m = m0 + r;
+        if constexpr (MODE == kProjQKV) {
+            const float* bias = a.bias[mat];
+            a.y[(int64_t)n * a.M + m] = outv + (bias ? bias[mrow0 + r] : 0.0f);
+        } else {
+            const int b = n / a.T, t = n - b * a.T;
+            const float xr = *(const float*)(a.res + b * a.res_nb_b + t * a.res_nb_t + (int64_t)m * 4);
+            *(float*)(a.h + b * a.h_nb_b + t * a.h_nb_t + (int64_t)m * 4) = outv + xr;
+        }
+    }
+}
+
 }  // namespace
+
+bool proj_gemv_supported(int N, int K, int M) {
+    return N >= 1 && N <= kGvMaxN && K <= kGvMaxK && K % 64 == 0 && M % kGvRows == 0;
+}
+
+hipError_t launch_proj_gemv(ProjArgs& a, float* y_ws, hipStream_t s) {
+    const bool q8 = a.w_type == VVA_TYPE_Q8_0;
+    a.y = y_ws;
+    const dim3 grid(a.M / kGvRows), block(64);
+    if (a.mode == kProjQKV) {
+        if (q8) hipLaunchKernelGGL((proj_gemv_kernel<true, kProjQKV>), grid, block, 0, s, a);
+        else    hipLaunchKernelGGL((proj_gemv_kernel<false, kProjQKV>), grid, block, 0, s, a);
+    } else {
+        if (q8) hipLaunchKernelGGL((proj_gemv_kernel<true, kProjResidual>), grid, block, 0, s, a);
+        else    hipLaunchKernelGGL((proj_gemv_kernel<false, kProjResidual>), grid, block, 0, s, a);
+    }
+    return hipGetLastError();
+}
 
 size_t proj_ws_bytes(int N, int K, int P) {
     const size_t xh = ((size_t)N * K * 2 + 255) / 256 * 256;

@@ -810,6 +810,12 @@ vva_status check_act(vva_context* ctx, const vva_tensor* x, const char* name, in
     return VVA_OK;
 }
 
+// Rows that start on 16-byte boundaries (the few-row projection reads them
+// 16 bytes at a time).
+bool rows16(const vva_tensor* x) {
+    return (uintptr_t)x->data % 16 == 0 && x->nb[1] % 16 == 0 && x->nb[2] % 16 == 0;
+}
+
 }  // namespace
 
 extern "C" vva_status vva_qkv_rope_append(vva_context* ctx, vva_kv* kv, int layer, const vva_tensor* x,
@@ -893,6 +899,25 @@ extern "C" vva_status vva_qkv_rope_append(vva_context* ctx, vva_kv* kv, int laye
     p.P = (int)(d / 2);
     p.theta_scale = powf(freq_base, -2.0f / (float)d);
     DeviceGuard g(ctx->device);
+    if (proj_gemv_supported((int)N, (int)K, a.M) && rows16(x)) {
+        // a decode step: the weight-streaming GEMV writes the F32 projections,
+        // then the RoPE + append kernel rotates q and k and stores the rows
+        if ((st = ensure_ws(ctx, (size_t)N * a.M * sizeof(float))) != VVA_OK) return st;
+        a.x = p.x; a.x_type = p.x_type; a.x_nb_t = p.x_nb_t; a.x_nb_b = p.x_nb_b;
+        float* y = ctx->ws;
+        hipError_t e = launch_proj_gemv(a, y, ctx->stream);
+        if (e != hipSuccess) return hip_fail(ctx, e, "qkv_rope_append launch");
+        auto proj_view = [&](int64_t first_row, int64_t heads) {
+            vva_tensor t{};
+            t.data = y + first_row;
+            t.type = VVA_TYPE_F32;
+            t.ne[0] = d; t.ne[1] = heads; t.ne[2] = T; t.ne[3] = B;
+            t.nb[0] = 4; t.nb[1] = 4 * d; t.nb[2] = 4 * (size_t)a.M; t.nb[3] = 4 * (size_t)a.M * T;
+            return t;
+        };
+        const vva_tensor tq = proj_view(0, Hq), tk = proj_view(Hq * d, Hkv), tv = proj_view((Hq + Hkv) * d, Hkv);
+        return vva_rope_append(ctx, kv, layer, &tq, &tk, &tv, pos, seq_ids, freq_base, q_out);
+    }
     if ((st = ensure_ws(ctx, proj_ws_bytes((int)N, (int)K, p.P))) != VVA_OK) return st;
     hipError_t e = launch_proj(p, a, ctx->ws, ctx->stream);
     return e == hipSuccess ? VVA_OK : hip_fail(ctx, e, "qkv_rope_append launch");
@@ -942,8 +967,14 @@ extern "C" vva_status vva_out_proj_residual(vva_context* ctx, const vva_tensor* 
     p.q8 = wt == VVA_TYPE_Q8_0;
     p.P = 0;
     DeviceGuard g(ctx->device);
-    if ((st = ensure_ws(ctx, proj_ws_bytes((int)N, (int)K, 0))) != VVA_OK) return st;
-    hipError_t e = launch_proj(p, a, ctx->ws, ctx->stream);
+    hipError_t e;
+    if (proj_gemv_supported((int)N, (int)K, (int)M) && rows16(o)) {
+        a.x = p.x; a.x_type = p.x_type; a.x_nb_t = p.x_nb_t; a.x_nb_b = p.x_nb_b;
+        e = launch_proj_gemv(a, nullptr, ctx->stream);
+    } else {
+        if ((st = ensure_ws(ctx, proj_ws_bytes((int)N, (int)K, 0))) != VVA_OK) return st;
+        e = launch_proj(p, a, ctx->ws, ctx->stream);
+    }
     return e == hipSuccess ? VVA_OK : hip_fail(ctx, e, "out_proj_residual launch");
 }
 

@@ -139,6 +139,10 @@ struct ProjArgs {
     // kProjResidual: h = y + res (F32 rows; may alias)
     const char* res; int64_t res_nb_t, res_nb_b;
     char* h; int64_t h_nb_t, h_nb_b;
+    // few-row path: the token rows themselves (converted in each workgroup),
+    // and, for kProjQKV, the projections y = x w^T + bias as F32 [N][M]
+    const char* x; int x_type; int64_t x_nb_t, x_nb_b;
+    float* y;
 };
 
 // --------------------------------------------------------- host launchers
@@ -179,6 +183,11 @@ size_t prefill_ws_bytes(const AttnArgs& a, const PrefillPlan& p);
 // Prep + GEMM of a linear layer; ws holds proj_ws_bytes(N, K, P) bytes.
 size_t proj_ws_bytes(int N, int K, int P);
 hipError_t launch_proj(ProjPrepArgs& p, ProjArgs& a, void* ws, hipStream_t s);
+// Few token rows (decode steps): one weight-streaming GEMV launch that
+// converts the rows itself.  kProjQKV writes y = x w^T + bias (F32 [N][M],
+// at `ws`) for the caller's RoPE + append; kProjResidual writes h.
+bool proj_gemv_supported(int N, int K, int M);
+hipError_t launch_proj_gemv(ProjArgs& a, float* y_ws, hipStream_t s);
 
 }  // namespace vva
 
