@@ -59,8 +59,8 @@ S_D, S_HQ, S_HKV, S_LAYERS, S_L = 64, 14, 2, 24, 1024
 # 1 GiB device-to-device copy (`--only copy`): FETCH_SIZE read 512 MiB for 1 GiB (x 2.0),
 # WRITE_SIZE 1 GiB (x 1.0).  Counters and commands: profiles/prefill_kernel_7b_32k.md,
 # profiles/decode_stream_q8_0_7b_32k.md.
-TRAFFIC_PREFILL = (972114.1 * 2.0 + 458752.5 * 1.0) * 1024          # prefill_kernel<128,F16>
-TRAFFIC_DECODE = ((35102.9 + 933.5) * 2.0 + (1904.0 + 28.0) * 1.0) * 1024    # stream + merge
+TRAFFIC_PREFILL = (605956.9 * 2.0 + 459122.8 * 1.0) * 1024          # prefill_kernel<128,F16>
+TRAFFIC_DECODE = ((35116.1 + 937.5) * 2.0 + (1904.0 + 28.0) * 1.0) * 1024    # stream + merge
 
 
 def prefill_flops_per_layer(T: int, past: int = 0) -> float:
@@ -425,14 +425,18 @@ def run_small_prefills(torch, vva, reps: int = 20):
     RoPE + append), HIP events around `reps` launches per layer of a 28- (or
     24-) layer stack:
       C1  0.5B heads (14 q / 2 kv, d = 64), 256 tokens, F32 Q/K/V and F32
-          cache: the fp32 path (eager semantics, 1e-4 tolerance);
+          cache: the fp32 eager branch (src/qwen2.cpp:336-344; the 1e-4
+          tolerance), and beside it the flash branch, which casts the F32
+          window to F16 (src/qwen2.cpp:328-331) and runs the MFMA prefill;
       C3  1.5B heads (12 q / 2 kv, d = 128), 4096 tokens, bf16 Q/K/V, F16
           cache: the MFMA flash prefill."""
     ctx = vva.Context(0)
     res = {}
-    for name, (d, hq, hkv, T, layers, qt, ct) in {
-            "c1_0p5b_fp32_T256": (64, 14, 2, 256, 24, torch.float32, vva.F32),
-            "c3_1p5b_T4096": (128, 12, 2, 4096, 28, torch.bfloat16, vva.F16)}.items():
+    for name, (d, hq, hkv, T, layers, qt, ct, fa) in {
+            "c1_0p5b_fp32_T256": (64, 14, 2, 256, 24, torch.float32, vva.F32, False),
+            "c1_0p5b_f32cache_flash_T256": (64, 14, 2, 256, 24, torch.float32, vva.F32, True),
+            "c3_1p5b_T4096": (128, 12, 2, 4096, 28, torch.bfloat16, vva.F16, True)}.items():
+        ctx.set_flash_attn(fa)
         kv = vva.KVCache(ctx, layers, hkv, d, T, 1, ct)
         q = torch.randn((1, T, hq, d), device="cuda").to(qt)
         k = torch.randn((1, T, hkv, d), device="cuda").to(qt)
@@ -455,7 +459,7 @@ def run_small_prefills(torch, vva, reps: int = 20):
         torch.cuda.synchronize()
         ms = float(np.mean([a.elapsed_time(b) for a, b in ev]))
         flops = 4.0 * hq * d * T * (T + 1) / 2
-        peak = 157.3 if ct == vva.F32 else PEAK_F16_TFLOPS
+        peak = 157.3 if not fa else PEAK_F16_TFLOPS
         res[name] = {"attn_ms_per_layer": round(ms, 4), "tflops": round(flops / ms / 1e9, 2),
                      "peak_tflops": peak, "frac": round(flops / ms / 1e9 / peak, 4), "layers": layers,
                      "flop_per_layer": flops}

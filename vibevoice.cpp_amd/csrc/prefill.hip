@@ -8,19 +8,23 @@
 // Work decomposition.  Query rows are the (token, head) pairs of one KV
 // group flattened as r = t * g + (h - kvh * g), so the g = Hq / Hkv heads of
 // a group share every K/V tile a workgroup stages in LDS (GQA sharing) and no
-// padding is wasted for g = 7 or 6.  Grid = (row tiles of 256, Hkv, B); a
-// workgroup is 4 waves x 64 rows and walks the key tiles (64 keys) its rows
-// can see; row tiles are issued heaviest-first for the causal imbalance.
+// padding is wasted for g = 7 or 6.  A workgroup is 8 waves (two per SIMD) x
+// 32 rows = a 256-row tile and walks the key tiles (64 keys) its rows can
+// see.  Workgroups go out heaviest row tile first, with the kv heads
+// innermost so that the heads of one row tile run side by side (their K/V
+// tiles stay in the XCD's L2).  When the row tiles alone would leave CUs
+// idle (short chunks over a long past), a row tile's key tiles are split
+// over several workgroups (PrefillPlan) whose partials prefill_merge_kernel
+// combines by log-sum-exp.
 //
 // Staging.  K and V tiles go from HBM straight into LDS with buffer loads
 // that write LDS (no registers, no VALU), into a ring of four stages: the
-// loads of tile j + 3 are issued, spread over the work of tile j, while
-// tile j is computed.  Both tiles are kept row-major ([key][dim]); K rows
-// are padded to 16 mod 256 bytes and V rows to 64 mod 256 bytes, which
-// keeps both operand reads free of bank conflicts.  The V^T operand of the
-// second product is read with ds_read_b64_tr_b16, whose 16-lane transpose
-// hands each lane 4 consecutive keys of one dim.  Keys past L read as 0
-// through the buffer range check.
+// loads of tile j + 3 go out at the start of tile j.  Both tiles are kept
+// row-major ([key][dim]); K rows are padded to 16 mod 256 bytes and V rows
+// to 64 mod 256 bytes, which keeps both operand reads free of bank
+// conflicts.  The V^T operand of the second product is read with
+// ds_read_b64_tr_b16, whose 16-lane transpose hands each lane 4 consecutive
+// keys of one dim.  Keys past L read as 0 through the buffer range check.
 //
 // Per wave and key tile, with v_mfma_f32_32x32x16_{f16,bf16}:
 //   S^T[key][row] = K . Q^T  A = K rows from LDS (16 B per lane), B = Q^T
@@ -28,27 +32,24 @@
 //                            lane owns one query row (column) of S^T and the
 //                            softmax row reductions are in-register plus one
 //                            cross-half exchange;
-//   softmax                  fp32, exp2 domain;
+//   softmax                  fp32, exp2 domain, on the raw scores (the scale
+//                            folded into the exp's fma); the running max m of
+//                            a row is raised lazily, only when a tile's row
+//                            max passes it by more than 2^8, so p <= 256 fits
+//                            f16 and O and the row sum are rescaled rarely;
 //   O^T[d][row] += V^T . P^T B = P^T converted in place from the S^T
 //                            accumulators: the key order of an MFMA step is
 //                            chosen to be the one the accumulator layout
 //                            already has, so no shuffle is needed.
-// Tiles every row of the workgroup sees whole run a branch-free loop that is
-// pipelined across tiles: the scores of half 0 of tile j + 1 are computed
-// while P.V of tile j still runs, so that each group of 16 MFMAs has a
-// quarter of a softmax to overlap.  The diagonal and length-boundary tiles
-// at the end of a workgroup's range run a second loop with masks.
-// The reference max m of a row is taken from half 0 of the first tile (key 0
-// is visible to every row) and never moves inside the tile loop, so O stays
-// in MFMA accumulators with no rescale and no max is tracked per tile.  A
-// later score beyond m + 16 turns its f16 p into inf; the row sum shows it,
-// and the workgroup restarts its key loop with m raised to that tile's row
-// max (rare: logits rarely grow by 2^16 after the first tile).  With an
-// explicit mask the row max is tracked per tile instead (masked loop only).
+// Tiles whose last key some row of the wave must not see (the diagonal, the
+// length boundary, or an explicit mask) set those scores to -inf first.
 // P and V enter the second product as f16 (BF16 V is converted after the
 // transposing read): an 8-bit-mantissa P would cost up to ~4e-3 on short
 // rows, f16 P stays below 4e-4.  Q is rounded to K's type, as ggml's CPU
-// flash attention does.
+// flash attention does.  Q8_0 and F32 windows are converted to f16 first by
+// window_to_f16_kernel (the reference casts F32 windows the same way before
+// flash attention, src/qwen2.cpp:328-331; for Q8_0 K, Q takes the Q8_0
+// round trip ggml's vec-dot type implies).
 #include "vva_internal.hpp"
 
 #include <algorithm>
