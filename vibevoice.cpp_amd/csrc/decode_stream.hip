@@ -62,18 +62,20 @@ typedef __attribute__((address_space(3))) char lds_char;
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kW = 4;                        // waves per workgroup (one per SIMD)
+constexpr int kW = 4;                        // compute waves per workgroup (one per SIMD)
+constexpr int kP = 2;                        // producer waves: they only issue the tile loads and wait
 constexpr int kStages = 4;                   // LDS ring depth (power of 2)
 constexpr int kTileOpBytes = 17408;          // one operand of a tile: 512 Q8_0 blocks
 constexpr int kOpChunks = 18;                // 1 KB chunks per operand: 17 KB + alignment slack
 constexpr int kOpBytes = kOpChunks * 1024;
 constexpr int kStage = 2 * kOpBytes;         // K, then V
-constexpr int kJunk = kStages * kStage;      // 1 KB target of the padding loads
-constexpr int kLdsBytes = kJunk + 1024;
-constexpr int kOpLoads = (kOpChunks + kW - 1) / kW;     // DMA loads per wave, operand and tile
-constexpr int kLoads = 2 * kOpLoads;         // DMA loads per wave per tile
-constexpr int kQLoads = 6;                   // DMA loads per wave for the raw Q rows
-constexpr int kQRawBytes = kQLoads * kW * 1024;   // raw Q area: up to 24 KB
+constexpr int kLdsBytes = kStages * kStage;
+constexpr int kOpLoads = kOpChunks / kP;     // DMA loads per producer, operand and tile
+constexpr int kLoads = 2 * kOpLoads;         // DMA loads per producer per tile
+constexpr int kQLoads = 12;                  // DMA loads per producer for the raw Q rows
+constexpr int kQRawBytes = kQLoads * kP * 1024;   // raw Q area: up to 24 KB
+static_assert(kOpChunks % kP == 0, "chunks split evenly over the producers");
+static_assert(3 * kLoads <= 63, "three tiles of a producer's loads fit its 6-bit vmcnt");
 constexpr int kDead = 0x40000000;            // buffer offset past every range
 constexpr float kLazy = 8.0f;                // running-max slack in log2 units: p <= 256
 static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
@@ -106,6 +108,12 @@ __device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t lds_addr, int voffset
 template <int N>
 __device__ __forceinline__ void wait_vm_barrier() {
     asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(N) : "memory");
+}
+
+// meet the workgroup at a barrier once this wave's LDS operations are done
+// (its memory loads, if any, stay in flight)
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory");
 }
 
 // f16 half HI of dword `h` times f32 `x` (v_fma_mix_f32 reads the half in
@@ -143,7 +151,7 @@ __device__ __forceinline__ h4 cat_h4(h2 lo, h2 hi) { return h4{lo[0], lo[1], hi[
 // group * RB in a row of NHG * RB bytes): the split partials then cover HKV
 // kv heads over NHG times the keys, NHG times fewer of them.
 template <int D, int HKV, int NHG>
-__global__ void __launch_bounds__(kW * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ void __launch_bounds__((kW + kP) * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits) {
     prefetch_kernargs<sizeof(AttnArgs)>();
     constexpr int NB = D / 32;                // Q8_0 blocks per head row
@@ -208,58 +216,76 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits) {
     const i32x4 vrs = make_rsrc_sgpr(vfirst - dv, dv + span);
     const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_char*)lds;
 
+    // ---- Loads.  Only the kP producer waves (w >= kW) issue memory loads:
+    // a load instruction stalls its wave while the CU's queue of outstanding
+    // loads is full, and a compute wave stalled there leaves the matrix and
+    // vector units idle and the queue unrefilled while it computes.  The
+    // producers meet the compute waves at every barrier: A (raw Q landed),
+    // B (Q quantized), one per tile t (tile t landed, every compute wave done
+    // with tile t - 1, so its stage takes tile t + 3), then the two barriers
+    // of the epilogue.
     // Tile t of an operand is bytes [t * 17408, t * 17408 + 18 KB) of its
-    // buffer: 18 chunks of 1 KB, chunk c loaded by wave c % kW.  Every wave
-    // issues kOpLoads loads per operand and tile; a chunk index past 17 is a
-    // padding load (from past the range: zeros, no memory access) into the
-    // junk kilobyte.  A tile past the last one loads nothing but zeros; the
-    // 18th chunk of an operand is needed only when delta > 0.
-    // Byte offset, in the split's buffer, of this lane's 16 bytes of chunk c
-    // of tile 0: the tile is contiguous in the cache (NHG = 1), or the group's
-    // RB-byte slice of each of its rows (NHG > 1).  Tile t is t * TT rows on.
-    int loff[kOpLoads];
-#pragma unroll
-    for (int i = 0; i < kOpLoads; ++i) {
-        const int bt = (w + kW * i) * 1024 + lane * 16;
-        loff[i] = NHG == 1 ? bt : (bt / RB) * RBM + hgrp * RB + bt % RB;
-    }
-    auto issue = [&](int t) {
-        const bool live = t < n_tiles;
-        const uint32_t st = lds0 + (uint32_t)(t & (kStages - 1)) * kStage;
-        const int tb = tile_key(t) * RBM;
-#pragma unroll
-        for (int op = 0; op < 2; ++op)
-#pragma unroll
-            for (int i = 0; i < kOpLoads; ++i) {
-                const int c = w + kW * i;
-                const bool have = c < kOpChunks;
-                const bool need = live && have && (c < kOpChunks - 1 || (op ? dv : dk) > 0);
-                const uint32_t dst = have ? st + op * kOpBytes + c * 1024 : lds0 + kJunk;
-                dma16<true>(op ? vrs : krs, dst, need ? tb + loff[i] : kDead);
-            }
-    };
-
-    // ---- Q: its rows (contiguous, at most 24 KB) are DMA'd first into the
-    // ring's last stage, which the loop does not load before its first
-    // barrier, then tile 0 goes out.  Once the wave's own Q loads have landed
-    // (they were issued first) and the workgroup has met, Q is quantized to
-    // Q8_0 blocks (codes + fp16-rounded scale) next to the raw rows, and
-    // tiles 1 and 2 go out.  Four adjacent lanes share a block (8 values
-    // each; the block max over the quad by DPP); a thread takes every
-    // (kW * 64)-th quarter block.
+    // buffer: 18 chunks of 1 KB, chunk c loaded by producer c % kP.  A tile
+    // past the last one loads nothing but zeros (offsets past the range: no
+    // memory access); the 18th chunk of an operand is needed only when
+    // delta > 0.
     const int eb = (int)type_elem_bytes(a.q_type);
-    {
-        const i32x4 qrs = make_rsrc_sgpr(a.q + b * a.q_nb_b + (int64_t)hq0 * D * eb, (uint32_t)(HQL * D * eb));
+    if (w >= kW) {
+        const int pw = w - kW;
+        // Byte offset, in the split's buffer, of this lane's 16 bytes of chunk
+        // c of tile 0: the tile is contiguous in the cache (NHG = 1), or the
+        // group's RB-byte slice of each of its rows (NHG > 1).  Tile t is
+        // t * TT rows on.
+        int loff[kOpLoads];
 #pragma unroll
-        for (int i = 0; i < kQLoads; ++i) {
-            const int c = i * kW + w;
-            dma16(qrs, lds0 + (kStages - 1) * kStage + c * 1024, c * 1024 + lane * 16);
+        for (int i = 0; i < kOpLoads; ++i) {
+            const int bt = (pw + kP * i) * 1024 + lane * 16;
+            loff[i] = NHG == 1 ? bt : (bt / RB) * RBM + hgrp * RB + bt % RB;
         }
+        auto issue = [&](int t) {
+            const bool live = t < n_tiles;
+            const uint32_t st = lds0 + (uint32_t)(t & (kStages - 1)) * kStage;
+            const int tb = tile_key(t) * RBM;
+#pragma unroll
+            for (int op = 0; op < 2; ++op)
+#pragma unroll
+                for (int i = 0; i < kOpLoads; ++i) {
+                    const int c = pw + kP * i;
+                    const bool need = live && (c < kOpChunks - 1 || (op ? dv : dk) > 0);
+                    dma16<true>(op ? vrs : krs, st + op * kOpBytes + c * 1024, need ? tb + loff[i] : kDead);
+                }
+        };
+        // Q's rows (contiguous, at most 24 KB) go to the ring's last stage,
+        // which takes no tile before barrier T_0, then tile 0
+        {
+            const i32x4 qrs = make_rsrc_sgpr(a.q + b * a.q_nb_b + (int64_t)hq0 * D * eb, (uint32_t)(HQL * D * eb));
+#pragma unroll
+            for (int i = 0; i < kQLoads; ++i) {
+                const int c = i * kP + pw;
+                dma16(qrs, lds0 + (kStages - 1) * kStage + c * 1024, c * 1024 + lane * 16);
+            }
+        }
+        issue(0);
+        wait_vm_barrier<kLoads>();                   // A: Q landed
+        wait_vm_barrier<kLoads>();                   // B
+        issue(1);
+        issue(2);
+        for (int t = 0; t < n_tiles; ++t) {
+            wait_vm_barrier<2 * kLoads>();           // T_t: tile t landed
+            issue(t + kStages - 1);
+        }
+        // the padding tiles' loads land before the ring is reused
+        asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+        __syncthreads();                             // epilogue: records written
+        __syncthreads();                             // epilogue: records read
+        return;
     }
-    // only tile 0 goes out with Q: the fewer requests ahead of Q's, the
-    // sooner the quantization starts
-    issue(0);
-    wait_vm_barrier<kLoads>();
+
+    // ---- Q is quantized to Q8_0 blocks (codes + fp16-rounded scale) next
+    // to the raw rows.  Four adjacent lanes share a block (8 values each; the
+    // block max over the quad by DPP); a thread takes every (kW * 64)-th
+    // quarter block.
+    lds_barrier();                                   // A
 
     const char* qraw = lds + (kStages - 1) * kStage;
     uint32_t* qlds = (uint32_t*)(lds + (kStages - 1) * kStage + kQRawBytes);
@@ -306,10 +332,7 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits) {
             if ((t & 3) == 0) dst[8] = __float_as_uint(f16_to_f32(f32_to_f16(dq)));
         }
     }
-#pragma unroll
-    for (int t = 1; t < kStages - 1; ++t) issue(t);
-    // LDS only: the tile loads stay in flight
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory");
+    lds_barrier();                                   // B
 
     // B operands of the score MFMAs, block-diagonal over k: per block and
     // 16-dim half j, lane (g, n) holds codes 16 j + 8 (g & 1) .. + 7 of row
@@ -519,14 +542,13 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits) {
         }
     }
     auto tile = [&](int t, auto check, const PendingPV (&prev)[NSUB], PendingPV (&cur)[NSUB]) {
-        wait_vm_barrier<(kStages - 2) * kLoads>();
+        lds_barrier();                               // T_t
         const char* kt = lds + (t & (kStages - 1)) * kStage + dk;
         const char* vt = lds + (t & (kStages - 1)) * kStage + kOpBytes + dv;
         const int jt = tile_key(t);
         PairOps ops[NSUB];
 #pragma unroll
         for (int u = 0; u < NSUB; ++u) read_pair(kt, vt, pair_key(u), ops[u]);
-        issue(t + kStages - 1);
         // every pending P.V into acc and every score of the tile first, then
         // one rescale decision, then the tile's P' on the final base: with
         // NSUB > 1 (d = 64) a raise decided per slot pair would leave P'
@@ -563,9 +585,7 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits) {
 #pragma unroll
         for (int u = 0; u < NSUB; ++u) pv(pz[u]);
     }
-    // the padding tiles' loads land before the ring is reused
-    asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
-    __syncthreads();
+    __syncthreads();                                 // the producers' last loads have landed
 
     // row n's sum over the four lane groups
     l = add_swap32(add_swap16(l));
@@ -653,7 +673,7 @@ int stream_groups(const AttnArgs& a) {
 template <int D>
 hipError_t launch_ds(const AttnArgs& a, float* ws, int n_splits, hipStream_t s) {
     const int ng = stream_groups(a);
-    const dim3 grid(n_splits, a.B * ng), block(kW * 64);
+    const dim3 grid(n_splits, a.B * ng), block((kW + kP) * 64);
     auto finish = [&]() -> hipError_t {
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess || n_splits == 1) return e;
