@@ -65,6 +65,7 @@ QKV_CASES = [
     (3584, 28, 4, 128, vva.Q8_0, vva.Q8_0, 1, 2, vva.F32),     # 7B CFG decode step
     (3584, 28, 4, 128, vva.F16, vva.F16, 512, 1, vva.F16),     # 7B ASR chunk, f16 Q
     (3584, 28, 4, 128, vva.Q8_0, vva.F32, 129, 2, vva.BF16),   # Q8_0 weights, two sequences
+    (3584, 28, 4, 128, vva.F16, vva.Q8_0, 200, 2, vva.F32),    # F16 weights into a Q8_0 cache, two sequences
 ]
 
 

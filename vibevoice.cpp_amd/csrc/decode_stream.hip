@@ -63,7 +63,7 @@ typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kW = 4;                        // compute waves per workgroup (one per SIMD)
-constexpr int kP = 2;                        // producer waves: they only issue the tile loads and wait
+constexpr int kP = 3;                        // producer waves: they only issue the tile loads and wait
 constexpr int kStages = 4;                   // LDS ring depth (power of 2)
 constexpr int kTileOpBytes = 17408;          // one operand of a tile: 512 Q8_0 blocks
 constexpr int kOpChunks = 18;                // 1 KB chunks per operand: 17 KB + alignment slack
@@ -72,7 +72,7 @@ constexpr int kStage = 2 * kOpBytes;         // K, then V
 constexpr int kLdsBytes = kStages * kStage;
 constexpr int kOpLoads = kOpChunks / kP;     // DMA loads per producer, operand and tile
 constexpr int kLoads = 2 * kOpLoads;         // DMA loads per producer per tile
-constexpr int kQLoads = 12;                  // DMA loads per producer for the raw Q rows
+constexpr int kQLoads = 8;                   // DMA loads per producer for the raw Q rows
 constexpr int kQRawBytes = kQLoads * kP * 1024;   // raw Q area: up to 24 KB
 static_assert(kOpChunks % kP == 0, "chunks split evenly over the producers");
 static_assert(3 * kLoads <= 63, "three tiles of a producer's loads fit its 6-bit vmcnt");

@@ -322,6 +322,223 @@ __global__ void __launch_bounds__(256) proj_gemm_kernel(ProjArgs a) {
     }
 }
 
+// ------------------------------------------------------------ wide GEMM (F16 weights)
+
+// 256 output features x 128 token rows per workgroup, k in steps of 64.
+// Eight producer waves DMA the tiles straight into a 3-stage LDS ring
+// (buffer_load_dwordx4 ... lds).  From L2 one wave's LDS loads stream at
+// ~20 GB/s whatever their number in flight, so eight issuing waves are what
+// a CU needs to feed its matrix cores (~110 GB/s at this tile shape); the
+// compute waves issue none, so they never wait behind a full load queue.
+// Eight compute waves, two per SIMD, each own a 64 x 64 quadrant of 2 x 2
+// v_mfma_f32_32x32x16_f16 blocks.  Rows are 128 bytes (64 f16 of k) in LDS;
+// a DMA instruction fills 8 rows, and its lane l writes LDS 16-byte slot
+// l % 8 of row l / 8 with the row's 16-byte k chunk (l % 8) ^ sw(row),
+// sw(row) = (row / 2) % 8: a fragment read (16 lanes x 16 bytes per LDS
+// cycle, rows r .. r + 15 at one k chunk) then touches every bank once.
+constexpr int kWM = 256, kWN = 128, kWK = 64;
+constexpr int kWStages = 3;
+constexpr int kWA = kWM * kWK * 2;             // 32 KB of weights per stage
+constexpr int kWB = kWN * kWK * 2;             // 16 KB of token rows per stage
+constexpr int kWStage = kWA + kWB;
+constexpr int kWCompute = 8, kWProd = 8;
+constexpr int kWLoadsA = kWA / 1024 / kWProd;  // DMA loads per producer and stage
+constexpr int kWLoadsB = kWB / 1024 / kWProd;
+constexpr int kWLoads = kWLoadsA + kWLoadsB;
+constexpr int kWCPitch = kWM + 4;              // floats per token row of the epilogue tile
+static_assert(2 * kWLoads <= 63, "two stages of a producer's loads fit its 6-bit vmcnt");
+static_assert(kWN * kWCPitch * 4 <= kWStages * kWStage, "the epilogue tile reuses the ring");
+
+__device__ __forceinline__ void wdma16(i32x4 rsrc, uint32_t lds_addr, int voffset) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voffset), "s"(rsrc)
+                 : "m0");
+}
+template <int N>
+__device__ __forceinline__ void wwait_barrier() {
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(N) : "memory");
+}
+__device__ __forceinline__ void wlds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory");
+}
+
+template <int MODE>
+__global__ void __launch_bounds__((kWCompute + kWProd) * 64) proj_gemm_wide_kernel(ProjArgs a) {
+    prefetch_kernargs<sizeof(ProjArgs)>();
+    __shared__ __attribute__((aligned(16))) char lds[kWStages * kWStage];
+    const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5, l32 = lane & 31;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+    // Workgroup i runs on XCD i % 8; XCD x takes the contiguous run of tiles
+    // [x * q + min(x, r), ...) of an order that walks groups of 4 token
+    // tiles, the 4 token tiles of every weight tile in turn: the tiles an
+    // XCD runs at one time share few weight and token rows in its L2.
+    const int n_mt = (a.M + kWM - 1) / kWM, n_nt = (a.N + kWN - 1) / kWN;
+    const int tiles = gridDim.x;
+    const int q = tiles / 8, r = tiles % 8, x = blockIdx.x % 8;
+    const int tile = x * q + min(x, r) + (int)blockIdx.x / 8;
+    const int grp = tile / (n_mt * 4), gn = min(4, n_nt - grp * 4), j = tile - grp * n_mt * 4;
+    const int mt = j / gn, nt = grp * 4 + j % gn;
+    const int m0 = mt * kWM, n0 = nt * kWN;
+    const int nk = a.K / kWK;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
+
+    if (w >= kWCompute) {
+        // ---- producers: chunks p, p + 2, ... of each operand's stage
+        const int pw = w - kWCompute;
+        const int sub = lane >> 3, slot = lane & 7;
+        int aoff[kWLoadsA], boff[kWLoadsB];
+        i32x4 ars[kWLoadsA];
+#pragma unroll
+        for (int i = 0; i < kWLoadsA; ++i) {
+            const int row = (pw + kWProd * i) * 8 + sub;            // tile row of this lane
+            const int g = m0 + (pw + kWProd * i) * 8;               // its 8-row group (one matrix)
+            const int mat = g < a.m_end[0] ? 0 : (g < a.m_end[1] ? 1 : (g < a.m_end[2] ? 2 : 3));
+            const int mbeg = mat == 0 ? 0 : a.m_end[mat - 1];
+            const int mrows = mat < 3 ? a.m_end[mat] - mbeg : 0;
+            ars[i] = make_rsrc_sgpr(mat < 3 ? a.w[mat] : a.w[0], (uint32_t)(mrows * a.w_nb[mat < 3 ? mat : 0]));
+            const int mr = m0 + row - mbeg;
+            aoff[i] = mr * (int)a.w_nb[mat < 3 ? mat : 0] + (((slot ^ ((row >> 1) & 7))) << 4);
+        }
+        const int nrows = min(a.N - n0, kWN);
+        const i32x4 brs = make_rsrc_sgpr((const char*)(a.xh + (int64_t)n0 * a.K), (uint32_t)(nrows * a.K * 2));
+#pragma unroll
+        for (int i = 0; i < kWLoadsB; ++i) {
+            const int row = (pw + kWProd * i) * 8 + sub;
+            boff[i] = row * a.K * 2 + (((slot ^ ((row >> 1) & 7))) << 4);
+        }
+        // a stage past the last loads zeros (offsets past every range)
+        auto issue = [&](int kt) {
+            const uint32_t st = lds0 + (uint32_t)(kt % kWStages) * kWStage;
+            const bool live = kt < nk;
+            const int ko = kt * kWK * 2;
+#pragma unroll
+            for (int i = 0; i < kWLoadsA; ++i)
+                wdma16(ars[i], st + (pw + kWProd * i) * 1024, live ? aoff[i] + ko : 0x40000000);
+#pragma unroll
+            for (int i = 0; i < kWLoadsB; ++i)
+                wdma16(brs, st + kWA + (pw + kWProd * i) * 1024, live ? boff[i] + ko : 0x40000000);
+        };
+        issue(0);
+        issue(1);
+        for (int kt = 0; kt < nk; ++kt) {
+            wwait_barrier<kWLoads>();                      // T_kt: stage kt landed
+            issue(kt + 2);                                 // into the stage of kt - 1
+        }
+        asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+        __syncthreads();                                   // accumulators written
+        __syncthreads();                                   // epilogue tile read
+        return;
+    }
+
+    // ---- compute waves: quadrant (wm, wn) of 64 features x 64 tokens
+    const int wm = w & 3, wn = w >> 2;
+    const int sw = (l32 >> 1) & 7;
+    const int a_rd = (wm * 64 + l32) * 128;
+    const int b_rd = kWA + (wn * 64 + l32) * 128;
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+    for (int kt = 0; kt < nk; ++kt) {
+        wlds_barrier();                                    // T_kt
+        const char* st = lds + (kt % kWStages) * kWStage;
+#pragma unroll
+        for (int ks = 0; ks < kWK / 16; ++ks) {
+            const int ch = ((2 * ks + half) ^ sw) << 4;
+            h8 af[2], bf[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const u32x4 ua = *(const u32x4*)(st + a_rd + i * 32 * 128 + ch);
+                const u32x4 ub = *(const u32x4*)(st + b_rd + i * 32 * 128 + ch);
+                __builtin_memcpy(&af[i], &ua, 16);
+                __builtin_memcpy(&bf[i], &ub, 16);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+    }
+    __syncthreads();                                       // every wave is done with the ring
+
+    // ---- accumulators to LDS as C[token][feature]: lane (half, l32) of
+    // block (i, j) holds features 8 (r / 4) + 4 half + r % 4 of token l32
+    float* C = (float*)lds;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            float* crow = C + (wn * 64 + 32 * j + l32) * kWCPitch + wm * 64 + 32 * i + 4 * half;
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                *(float4*)(crow + 8 * g) = make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                                                       acc[i][j][4 * g + 3]);
+        }
+    __syncthreads();
+
+    if constexpr (MODE == kProjQKV) {
+        // 128 rotation pairs per token (two heads of d = 128, four of d = 64):
+        // thread (token tid / 128 + 4 pass, pair tid % 128)
+        const int d = a.d, P = d >> 1;
+        const int pi = tid & 127, hl = pi / P, i = pi - hl * P;
+        const int f0 = m0 + hl * d;                        // first feature of the head
+        if (f0 >= a.M) return;                             // past the last matrix (uniform per half-wave)
+        const int mat = f0 < a.m_end[0] ? 0 : (f0 < a.m_end[1] ? 1 : 2);
+        const int mrow = f0 - (mat ? a.m_end[mat - 1] : 0);
+        const int head = mrow / d;
+        const float* bias = a.bias[mat];
+        const float b0 = bias ? bias[mrow + i] : 0.0f;
+        const float b1 = bias ? bias[mrow + i + P] : 0.0f;
+        for (int nl = tid >> 7; nl < kWN; nl += kWCompute * 64 / 128) {
+            const int n = n0 + nl;
+            if (n >= a.N) break;                           // uniform per wave
+            float y0 = C[nl * kWCPitch + hl * d + i] + b0;
+            float y1 = C[nl * kWCPitch + hl * d + i + P] + b1;
+            if (mat < 2) {
+                const float2 cs = a.rope[(int64_t)n * P + i];
+                const float r0 = fmaf(y0, cs.x, -(y1 * cs.y));
+                const float r1 = fmaf(y0, cs.y, y1 * cs.x);
+                y0 = r0;
+                y1 = r1;
+            }
+            const int b = n / a.T, t = n - b * a.T;
+            if (mat == 0) {
+                const int64_t eo = type_elem_bytes(a.q_out_type);
+                char* dst = a.q_out + b * a.qo_nb_b + t * a.qo_nb_t + head * a.qo_nb_h;
+                store_elem(dst + i * eo, a.q_out_type, y0);
+                store_elem(dst + (i + P) * eo, a.q_out_type, y1);
+            } else {
+                char* row = (mat == 1 ? a.k_dst[b] : a.v_dst[b]) + t * a.cache_row_bytes + head * a.cache_head_bytes;
+                if (a.cache_type == VVA_TYPE_Q8_0) {
+                    store_q8_pair(row, i, P, y0, y1);
+                } else {
+                    const int64_t ec = type_elem_bytes(a.cache_type);
+                    store_elem(row + i * ec, a.cache_type, y0);
+                    store_elem(row + (i + P) * ec, a.cache_type, y1);
+                }
+            }
+        }
+    } else {
+        // h = y + x, 4 features per thread: thread (token tid / 64 + 8 pass,
+        // features 4 (tid % 64) ..)
+        const int c4 = (tid & 63) * 4;
+        if (m0 + c4 >= a.M) return;
+        for (int nl = tid >> 6; nl < kWN; nl += kWCompute) {
+            const int n = n0 + nl;
+            if (n >= a.N) break;
+            const int b = n / a.T, t = n - b * a.T;
+            const float4 xr = *(const float4*)(a.res + b * a.res_nb_b + t * a.res_nb_t + (int64_t)(m0 + c4) * 4);
+            const float* cr = C + nl * kWCPitch + c4;
+            *(float4*)(a.h + b * a.h_nb_b + t * a.h_nb_t + (int64_t)(m0 + c4) * 4) =
+                make_float4(cr[0] + xr.x, cr[1] + xr.y, cr[2] + xr.z, cr[3] + xr.w);
+        }
+    }
+}
+
 // ------------------------------------------------------------ GEMV
 
 constexpr int kGvRows = 4;                       // output rows per workgroup (one wave)
@@ -536,8 +753,15 @@ hipError_t launch_proj(ProjPrepArgs& p, ProjArgs& a, void* ws, hipStream_t s) {
     hipLaunchKernelGGL(proj_prep_kernel, dim3(p.N), dim3(256), 0, s, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const int tiles = (a.M / kTM) * ((a.N + kTN - 1) / kTN);
     const bool q8 = a.w_type == VVA_TYPE_Q8_0;
+    if (!q8) {
+        const int wtiles = ((a.M + kWM - 1) / kWM) * ((a.N + kWN - 1) / kWN);
+        const dim3 block((kWCompute + kWProd) * 64);
+        if (a.mode == kProjQKV) hipLaunchKernelGGL((proj_gemm_wide_kernel<kProjQKV>), dim3(wtiles), block, 0, s, a);
+        else                    hipLaunchKernelGGL((proj_gemm_wide_kernel<kProjResidual>), dim3(wtiles), block, 0, s, a);
+        return hipGetLastError();
+    }
+    const int tiles = (a.M / kTM) * ((a.N + kTN - 1) / kTN);
     if (a.mode == kProjQKV) {
         if (q8) hipLaunchKernelGGL((proj_gemm_kernel<true, kProjQKV>), dim3(tiles), dim3(256), 0, s, a);
         else    hipLaunchKernelGGL((proj_gemm_kernel<false, kProjQKV>), dim3(tiles), dim3(256), 0, s, a);
