@@ -104,6 +104,7 @@ ROWS = [
     (64, 14, 2, vva.F32, 256, 0),        # 0.5B prefill (fp32 eager-equivalent)
     (128, 28, 4, vva.Q8_0, 64, 500),     # chunk into a Q8_0 cache (forced onto the row kernel)
     (128, 12, 2, vva.F32, 33, 7),
+    (64, 14, 2, vva.F32, 100, 900),      # 0.5B TTS window past 1k: 16 key steps, the last partial
 ]
 
 
@@ -127,6 +128,37 @@ def test_row_kernel_prefill_matches_oracle(ctx, torch_gpu, d, Hq, Hkv, t, T, pas
         ctx.set_attn_path(0)
     ref = oracle_attn(q, kv, 0, [0], [L], T, d ** -0.5)
     assert_close(out, ref, *TOL[t], what="row kernel")
+    kv.free()
+
+
+def test_row_kernel_f32_explicit_mask_ragged(ctx, torch_gpu):
+    """The fp32 eager branch on F32 caches (the lane-per-key row kernel) over
+    windows of several 64-key steps: two ragged sequences, an explicit F16
+    mask with a hole covering one whole 64-key step and scattered holes, and
+    a row with every key masked (its output is 0).  Tolerance 1e-4 (fp32)."""
+    torch = torch_gpu
+    d, Hq, Hkv, T = 128, 12, 2, 9
+    lens = [700, 300]
+    kv = vva.KVCache(ctx, 1, Hkv, d, max(lens), 2, vva.F32)
+    fill_cache(kv, lens, seed=41, scale=0.125)
+    for s_, L in enumerate(lens):
+        kv.set_len(s_, L - T)
+    rng = np.random.default_rng(42)
+    m = np.where(rng.random((2, T, max(lens))) < 0.2, -np.inf, 0.0).astype(np.float32)
+    m[0, :, 64:128] = -np.inf                               # one whole 64-key step
+    m[1, 3, :] = -np.inf                                    # a row with nothing visible
+    m[:, :, 5] = 0.0                                        # every other row sees key 5
+    m[1, 3, 5] = -np.inf
+    mbits = vvo.f16_bits(m)
+    ctx.set_flash_attn(False)
+    try:
+        q, out = run_attn(ctx, torch, kv, 0, T, 2, Hq, vva.F32, seed=43, mask=mbits)
+    finally:
+        ctx.set_flash_attn(True)
+    ref = oracle_attn(q, kv, 0, [0, 1], lens, T, d ** -0.5, mask=mbits)
+    assert np.all(out[1, 3] == 0.0)
+    mx, mn = assert_close(out, ref, *TOL[vva.F32], what="f32 rows, explicit mask")
+    print(f"  f32 rows with mask: max {mx:.2e} mean {mn:.2e}")
     kv.free()
 
 

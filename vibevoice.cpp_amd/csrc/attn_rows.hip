@@ -20,6 +20,8 @@ namespace vva {
 
 namespace {
 
+#include "wave_ops.hpp"
+
 constexpr int kRowsPerBlock = 4;   // one row per wave
 
 template <int DPL>
@@ -146,6 +148,141 @@ __global__ void __launch_bounds__(256) attn_rows_kernel(AttnArgs a) {
     }
 }
 
+// Max over all 64 lanes (every lane gets it).
+__device__ __forceinline__ float wave_max(float x) {
+    x = fmaxf(x, dpp<kDppXor1>(x));
+    x = fmaxf(x, dpp<kDppXor2>(x));
+    x = fmaxf(x, dpp<kDppHalfMirror>(x));
+    x = fmaxf(x, dpp<kDppMirror>(x));
+    x = max_swap16(x);
+    return max_swap32(x);
+}
+
+// F32 K and V (the eager branch, src/qwen2.cpp:337-343, in fp32): one wave
+// per query row, keys 64 at a time.  Lane l computes the whole dot product
+// of key j0 + l (16-byte loads of its K row against Q broadcast from LDS),
+// so no cross-lane sum per key; the 64 scores then take one online-softmax
+// step (max and sum over the wave), and P.V runs with lane l owning dims
+// l, l + 64, ... over the 64 keys (V rows read whole by the wave, p
+// broadcast from LDS).  Same semantics as attn_rows_kernel: scores scaled
+// then masked, keys at -inf skipped, a row with no visible key gives 0.
+template <int DPL>
+__global__ void __launch_bounds__(256) attn_rows_f32_kernel(AttnArgs a) {
+    prefetch_kernargs<sizeof(AttnArgs)>();
+    __shared__ __attribute__((aligned(16))) float qsh[kRowsPerBlock][256];
+    __shared__ __attribute__((aligned(16))) float psh[kRowsPerBlock][64];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int row = blockIdx.x * kRowsPerBlock + wv;
+    if (row >= a.B * a.T * a.Hq) return;        // whole wave leaves together
+    const int h = row % a.Hq;
+    const int bt = row / a.Hq;
+    const int t = bt % a.T;
+    const int b = bt / a.T;
+    const int kvh = h / (a.Hq / a.Hkv);
+    const int d = a.d;
+
+    const int64_t qes = type_elem_bytes(a.q_type);
+    const char* qrow = a.q + b * a.q_nb_b + t * a.q_nb_t + h * a.q_nb_h;
+#pragma unroll
+    for (int r = 0; r < DPL; ++r) {
+        const int i = lane + 64 * r;
+        if (i < d) qsh[wv][i] = load_elem(qrow + i * qes, a.q_type);
+    }
+    wave_lds_sync();
+
+    const int L = a.L[b];
+    int jend = L;
+    if (a.mask_mode == kMaskCausal) jend = min(L, a.past[b] + t + 1);
+    const char* kbase = a.k[b] + kvh * a.k_nb_head;
+    const char* vbase = a.v[b] + kvh * a.v_nb_head;
+    const char* mrow = a.mask ? a.mask + b * a.mask_nb_b + t * a.mask_nb_row : nullptr;
+
+    float M = -INFINITY, S = 0.0f;
+    float acc[DPL];
+#pragma unroll
+    for (int r = 0; r < DPL; ++r) acc[r] = 0.0f;
+
+    for (int j0 = 0; j0 < jend; j0 += 64) {
+        const int j = j0 + lane;
+        const bool live = j < jend;
+        const float4* kr = (const float4*)(kbase + (int64_t)(live ? j : j0) * a.k_nb_tok);
+        float dot0 = 0.0f, dot1 = 0.0f;
+        for (int i4 = 0; i4 < d / 4; i4 += 2) {
+            const float4 k0 = kr[i4], q0 = *(const float4*)&qsh[wv][4 * i4];
+            dot0 = fmaf(q0.x, k0.x, dot0); dot0 = fmaf(q0.y, k0.y, dot0);
+            dot0 = fmaf(q0.z, k0.z, dot0); dot0 = fmaf(q0.w, k0.w, dot0);
+            if (i4 + 1 < d / 4) {
+                const float4 k1 = kr[i4 + 1], q1 = *(const float4*)&qsh[wv][4 * i4 + 4];
+                dot1 = fmaf(q1.x, k1.x, dot1); dot1 = fmaf(q1.y, k1.y, dot1);
+                dot1 = fmaf(q1.z, k1.z, dot1); dot1 = fmaf(q1.w, k1.w, dot1);
+            }
+        }
+        float sc = -INFINITY;
+        if (live) {
+            const float mv = (a.mask_mode == kMaskExplicit) ? f16_to_f32(*(const uint16_t*)(mrow + 2 * (int64_t)j)) : 0.0f;
+            sc = mv == -INFINITY ? -INFINITY : (dot0 + dot1) * a.scale + mv;
+        }
+        const float mx = wave_max(sc);
+        if (mx == -INFINITY) continue;              // nothing visible in these 64 keys (uniform)
+        const float Mn = fmaxf(M, mx);
+        const float alpha = __expf(M - Mn);         // 0 while M = -inf
+        const float p = sc == -INFINITY ? 0.0f : __expf(sc - Mn);
+        S = fmaf(S, alpha, wave_sum(p));
+#pragma unroll
+        for (int r = 0; r < DPL; ++r) acc[r] *= alpha;
+        M = Mn;
+        psh[wv][lane] = p;
+        wave_lds_sync();
+        const int nk = min(64, jend - j0);
+        const char* vr = vbase + (int64_t)j0 * a.v_nb_tok;
+        int u = 0;
+        for (; u + 4 <= nk; u += 4) {
+            const float4 pu = *(const float4*)&psh[wv][u];
+#pragma unroll
+            for (int r = 0; r < DPL; ++r) {
+                const int i = lane + 64 * r;
+                if (i < d) {
+                    const float* vc = (const float*)(vr + (int64_t)u * a.v_nb_tok) + i;
+                    const float v0 = vc[0];
+                    const float v1 = *(const float*)((const char*)vc + a.v_nb_tok);
+                    const float v2 = *(const float*)((const char*)vc + 2 * a.v_nb_tok);
+                    const float v3 = *(const float*)((const char*)vc + 3 * a.v_nb_tok);
+                    acc[r] = fmaf(pu.x, v0, acc[r]);
+                    acc[r] = fmaf(pu.y, v1, acc[r]);
+                    acc[r] = fmaf(pu.z, v2, acc[r]);
+                    acc[r] = fmaf(pu.w, v3, acc[r]);
+                }
+            }
+        }
+        for (; u < nk; ++u) {
+            const float pu = psh[wv][u];
+#pragma unroll
+            for (int r = 0; r < DPL; ++r) {
+                const int i = lane + 64 * r;
+                if (i < d) acc[r] = fmaf(pu, *((const float*)(vr + (int64_t)u * a.v_nb_tok) + i), acc[r]);
+            }
+        }
+        wave_lds_sync();                            // psh is rewritten by the next step
+    }
+    const float inv = S == 0.0f ? 0.0f : 1.0f / S;
+    float* orow = (float*)((char*)a.out + b * a.o_nb_b + t * a.o_nb_t + h * a.o_nb_h);
+#pragma unroll
+    for (int r = 0; r < DPL; ++r) {
+        const int i = lane + 64 * r;
+        if (i < d) orow[i] = acc[r] * inv;
+    }
+}
+
+// F32 K and V with 16-byte aligned rows take attn_rows_f32_kernel.
+bool rows_f32_ok(const AttnArgs& a) {
+    if (a.k_type != VVA_TYPE_F32 || a.v_type != VVA_TYPE_F32) return false;
+    if (a.d % 8 != 0 || a.d > 256) return false;
+    if (a.k_nb_tok % 16 || a.k_nb_head % 16) return false;
+    for (int b = 0; b < a.B; ++b)
+        if ((uintptr_t)a.k[b] % 16) return false;
+    return true;
+}
+
 }  // namespace
 
 hipError_t launch_attn_rows(const AttnArgs& a, hipStream_t s) {
@@ -153,6 +290,16 @@ hipError_t launch_attn_rows(const AttnArgs& a, hipStream_t s) {
     if (rows == 0) return hipSuccess;
     dim3 grid((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock));
     const int dpl = (a.d + 63) / 64;
+    if (rows_f32_ok(a)) {
+        switch (dpl) {
+            case 1: hipLaunchKernelGGL(attn_rows_f32_kernel<1>, grid, dim3(256), 0, s, a); break;
+            case 2: hipLaunchKernelGGL(attn_rows_f32_kernel<2>, grid, dim3(256), 0, s, a); break;
+            case 3: hipLaunchKernelGGL(attn_rows_f32_kernel<3>, grid, dim3(256), 0, s, a); break;
+            case 4: hipLaunchKernelGGL(attn_rows_f32_kernel<4>, grid, dim3(256), 0, s, a); break;
+            default: return hipErrorInvalidValue;
+        }
+        return hipGetLastError();
+    }
     switch (dpl) {
         case 1: hipLaunchKernelGGL(attn_rows_kernel<1>, grid, dim3(256), 0, s, a); break;
         case 2: hipLaunchKernelGGL(attn_rows_kernel<2>, grid, dim3(256), 0, s, a); break;
