@@ -85,3 +85,57 @@ def test_decode_step_graph_replays(ctx, torch_gpu, d, Hq, Hkv, kt, past, layers)
         print(f"  replay {r}: outputs and appended rows equal the eager step", flush=True)
     del g
     kv.free()
+
+
+def test_graph_replay_after_workspace_growth(torch_gpu):
+    """A graph captured while the split workspace is small keeps working
+    after a later eager call grows it: the outgrown workspace is retired,
+    not freed, so the replays still write into live memory and reproduce
+    the eager step bit for bit.  A fresh context, so the workspace starts
+    at the small call's size."""
+    torch = torch_gpu
+    c = vva.Context(0)
+    small = big = None
+    try:
+        d, Hq, Hkv, B, past = 64, 14, 2, 2, 1024
+        small = vva.KVCache(c, 1, Hkv, d, past + 8, B, vva.F16)
+        fill_cache(small, [past] * B, seed=77)
+        rng = np.random.default_rng(78)
+        q = to_gpu(torch, rng.standard_normal((B, 1, Hq, d)), vva.F32)
+        out = torch.empty((B, 1, Hq, d), dtype=torch.float32, device="cuda")
+        c.attn(small, 0, q, out, d ** -0.5)                # eager: sizes the workspace
+        torch.cuda.synchronize()
+        assert c.last_decode_splits() > 1
+        ref = out.cpu().numpy().copy()
+
+        g = torch.cuda.CUDAGraph()
+        default = torch.cuda.current_stream()
+        try:
+            with torch.cuda.graph(g):
+                c.set_stream(torch.cuda.current_stream())
+                c.attn(small, 0, q, out, d ** -0.5)
+        finally:
+            c.set_stream(default)
+
+        # a 7B-shaped Q8_0 decode over 4096 keys: many more split partials
+        big = vva.KVCache(c, 1, 4, 128, 4104, B, vva.Q8_0)
+        fill_cache(big, [4096] * B, seed=79)
+        qb = to_gpu(torch, rng.standard_normal((B, 1, 28, 128)), vva.F32)
+        ob = torch.empty((B, 1, 28, 128), dtype=torch.float32, device="cuda")
+        c.attn(big, 0, qb, ob, 128 ** -0.5)
+        torch.cuda.synchronize()
+        assert c.last_decode_splits() > 9 and np.isfinite(ob.cpu().numpy()).all()
+
+        for r in range(3):
+            out.fill_(float("nan"))
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            assert np.array_equal(out.cpu().numpy(), ref), f"replay {r} after the workspace grew"
+        print("  3 replays after the workspace grew equal the eager step", flush=True)
+        del g
+    finally:
+        for kv in (small, big):
+            if kv is not None:
+                kv.free()
+        c.close()
