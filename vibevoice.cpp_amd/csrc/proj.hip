@@ -720,6 +720,126 @@ __global__ void __launch_bounds__(64) proj_gemv_kernel(ProjArgs a) {
     }
 }
 
+// Q8_0 weights, 16 rows per workgroup (4 waves of 4): every weight load of
+// the workgroup goes out first, then its 256 threads quantize the token rows
+// once into LDS (ggml's quantize_row_q8_0, as proj_gemv_kernel does per
+// lane: the same codes and fp16-rounded scales), and each wave takes its 4
+// rows' integer block dots against them.
+constexpr int kGv8Waves = 4;
+constexpr int kGv8Rows = kGvRows * kGv8Waves;
+template <int MODE>
+__global__ void __launch_bounds__(64 * kGv8Waves) proj_gemv_q8_kernel(ProjArgs a) {
+    prefetch_kernargs<sizeof(ProjArgs)>();
+    __shared__ __attribute__((aligned(16))) uint32_t xq[kGvMaxN][kGvMaxK / 32][8];   // codes of row n, block j
+    __shared__ float xd[kGvMaxN][kGvMaxK / 32];         // their fp16-rounded scales
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int N = a.N, K = a.K, nbk = K / 32;
+    const int m0 = blockIdx.x * kGv8Rows + wv * kGvRows; // matrix boundaries are multiples of 16
+    const int mat = m0 < a.m_end[0] ? 0 : (m0 < a.m_end[1] ? 1 : 2);
+    const int mrow0 = m0 - (mat ? a.m_end[mat - 1] : 0);
+    const char* wb = a.w[mat] + (int64_t)mrow0 * a.w_nb[mat];
+    const int64_t wnb = a.w_nb[mat];
+    // weight block j of each row: 34 bytes from the 4-byte boundary at or
+    // below it (rows are 4-byte aligned: K is a multiple of 64)
+    uint32_t qw[kGvQ8It][kGvRows][9];
+#pragma unroll
+    for (int it = 0; it < kGvQ8It; ++it) {
+        const int j = lane + 64 * it;
+        const int jj = j < nbk ? j : 0;
+#pragma unroll
+        for (int r = 0; r < kGvRows; ++r) {
+            const uint32_t* p = (const uint32_t*)(wb + r * wnb + (((int64_t)jj * kQ8Bytes) & ~(int64_t)3));
+#pragma unroll
+            for (int i = 0; i < 9; ++i) qw[it][r][i] = p[i];
+        }
+    }
+    for (int task = threadIdx.x; task < N * nbk; task += 64 * kGv8Waves) {
+        const int n = task / nbk, j = task - n * nbk;
+        float x[32];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            float xs[8];
+            load_x8(a, n, j * 32 + 8 * q, xs);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[8 * q + e] = xs[e];
+        }
+        float am = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 32; ++e) am = fmaxf(am, fabsf(x[e]));
+        const float d = am / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            uint32_t c = 0u;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) c |= ((uint32_t)(uint8_t)(int8_t)roundf(x[4 * i + e] * id)) << (8 * e);
+            xq[n][j][i] = c;
+        }
+        xd[n][j] = f16_to_f32(f32_to_f16(d));
+    }
+    __syncthreads();
+
+    float acc[kGvRows][kGvMaxN];
+#pragma unroll
+    for (int r = 0; r < kGvRows; ++r)
+#pragma unroll
+        for (int n = 0; n < kGvMaxN; ++n) acc[r][n] = 0.0f;
+#pragma unroll
+    for (int it = 0; it < kGvQ8It; ++it) {
+        if (64 * it >= nbk) break;                                   // uniform
+        const int j = lane + 64 * it;
+        const bool live = j < nbk;
+        const int jj = live ? j : 0;
+        const bool odd = jj & 1;                                     // the block starts 2 bytes into dword 0
+        float dw[kGvRows];
+        uint32_t codes[kGvRows][8];
+#pragma unroll
+        for (int r = 0; r < kGvRows; ++r) {
+            const uint32_t* q = qw[it][r];
+            dw[r] = live ? f16_to_f32((uint16_t)(odd ? q[0] >> 16 : q[0] & 0xffffu)) : 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) codes[r][i] = odd ? q[i + 1] : __builtin_amdgcn_alignbyte(q[i + 1], q[i], 2);
+        }
+#pragma unroll
+        for (int n = 0; n < kGvMaxN; ++n) {
+            if (n >= N) break;                                       // uniform
+            const u32x4 c0 = *(const u32x4*)&xq[n][jj][0], c1 = *(const u32x4*)&xq[n][jj][4];
+            const uint32_t xc[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+            const float dx = xd[n][jj];
+#pragma unroll
+            for (int r = 0; r < kGvRows; ++r) {
+                int s = 0;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) s = __builtin_amdgcn_sdot4((int)codes[r][i], (int)xc[i], s, false);
+                acc[r][n] = fmaf((float)s, dw[r] * dx, acc[r][n]);
+            }
+        }
+    }
+
+    // sums over the lanes; lane r * N + n keeps (row r, token n)
+    float outv = 0.0f;
+#pragma unroll
+    for (int r = 0; r < kGvRows; ++r)
+#pragma unroll
+        for (int n = 0; n < kGvMaxN; ++n) {
+            if (n >= N) break;                                       // uniform
+            const float sum = wave_sum(acc[r][n]);
+            if (lane == r * N + n) outv = sum;
+        }
+    if (lane < kGvRows * N) {
+        const int r = lane / N, n = lane - r * N;
+        const int m = m0 + r;
+        if constexpr (MODE == kProjQKV) {
+            const float* bias = a.bias[mat];
+            a.y[(int64_t)n * a.M + m] = outv + (bias ? bias[mrow0 + r] : 0.0f);
+        } else {
+            const int b = n / a.T, t = n - b * a.T;
+            const float xr = *(const float*)(a.res + b * a.res_nb_b + t * a.res_nb_t + (int64_t)m * 4);
+            *(float*)(a.h + b * a.h_nb_b + t * a.h_nb_t + (int64_t)m * 4) = outv + xr;
+        }
+    }
+}
+
 }  // namespace
 
 bool proj_gemv_supported(int N, int K, int M) {
@@ -729,6 +849,12 @@ bool proj_gemv_supported(int N, int K, int M) {
 hipError_t launch_proj_gemv(ProjArgs& a, float* y_ws, hipStream_t s) {
     const bool q8 = a.w_type == VVA_TYPE_Q8_0;
     a.y = y_ws;
+    if (q8 && a.M % kGv8Rows == 0 && a.m_end[0] % kGv8Rows == 0 && a.m_end[1] % kGv8Rows == 0) {
+        const dim3 g8(a.M / kGv8Rows), b8(64 * kGv8Waves);
+        if (a.mode == kProjQKV) hipLaunchKernelGGL((proj_gemv_q8_kernel<kProjQKV>), g8, b8, 0, s, a);
+        else                    hipLaunchKernelGGL((proj_gemv_q8_kernel<kProjResidual>), g8, b8, 0, s, a);
+        return hipGetLastError();
+    }
     const dim3 grid(a.M / kGvRows), block(64);
     if (a.mode == kProjQKV) {
         if (q8) hipLaunchKernelGGL((proj_gemv_kernel<true, kProjQKV>), grid, block, 0, s, a);
