@@ -53,6 +53,7 @@
 #include "vva_internal.hpp"
 
 #include <algorithm>
+#include <type_traits>
 #include <functional>
 #include <vector>
 
@@ -359,18 +360,20 @@ __global__ void __launch_bounds__(kWaves * 64) prefill_kernel(AttnArgs a, float*
                 s[kt][r] = key > lim ? -INFINITY : x;
             }
     };
-    // online softmax of the tile's raw scores s, then O^T += V^T P^T: P^T is
-    // converted in place from the S^T registers (the key order of each
-    // 16-key MFMA step is the accumulator's own order).  p = 2^(s * scale *
-    // log2 e - m), one fma and one exp2 per score.
-    auto softmax_pv = [&](const lds_char* va, f32x16 (&s)[2]) {
+    // The row max of a tile's raw scores, in the exp2 domain (with the row's
+    // other 32 keys in lane l ^ 32).
+    auto rowmax = [&](const f32x16 (&s)[2]) {
         float mr = fmaxf(fmaxf(s[0][0], s[0][1]), s[0][2]);
 #pragma unroll
         for (int r = 3; r < 15; r += 2) mr = fmaxf(fmaxf(mr, s[0][r]), s[0][r + 1]);
         mr = fmaxf(mr, s[0][15]);
 #pragma unroll
         for (int r = 0; r < 16; r += 2) mr = fmaxf(fmaxf(mr, s[1][r]), s[1][r + 1]);
-        const float mx = max_swap32(mr) * sl2;                   // with the row's other 32 keys
+        return max_swap32(mr) * sl2;
+    };
+    // Raise the running max lazily to a tile's row max mx: O and the row sum
+    // are rescaled only when mx passes m by more than kLazy.
+    auto rescale = [&](float mx) {
         if (__any(mx > m + kLazy)) {
             if (mx > m + kLazy) {
                 const float alpha = __builtin_amdgcn_exp2f(m - mx);   // 0 while m = -inf
@@ -380,55 +383,123 @@ __global__ void __launch_bounds__(kWaves * 64) prefill_kernel(AttnArgs a, float*
                 m = mx;
             }
         }
+    };
+    // Software pipeline over the key tiles.  Step j first raises the running
+    // max to tile j's row max (found by the previous step), then runs one
+    // straight-line block of 2 DS + 4 DT matrix-core slots: the score MFMAs of
+    // tile j + 1, then the P.V MFMAs of tile j.  Between them go the VALU
+    // work of tile j's softmax (one fma and one exp2 per score, the f16
+    // packing and the row sum) and the LDS operand reads, each placed a few
+    // slots before its MFMA, so that the VALU issues while the matrix cores
+    // run.  Tile j + 1's mask (on the tiles that need one) and row max follow
+    // the block.  Scheduling fences between the slots keep this order.  The wave's live tiles are its first n_live (the tiles
+    // are in key order and the wave sees keys below kend_w only).
+    const int n_live = wave_live ? max(0, min(n_tiles, (kend_w - kb0 + kBN - 1) / kBN)) : 0;
+    auto k_addr = [&](int j) {
+        uint32_t x = lds0 + (j % kStages) * STAGE + k_rd;
+        asm volatile("" : "+v"(x));                              // one base register, constant offsets
+        return lds_at(x);
+    };
+    auto needs_mask = [&](int j) { return EXPL || kb0 + j * kBN + kBN - 1 > lim_w; };
+    constexpr int NQ = 2 * DS;                                   // score MFMAs per tile
+    constexpr int NP = 4 * DT;                                   // P.V MFMAs per tile
+    constexpr int KAHEAD = 2;                                    // K fragment reads ahead of their MFMA
+    constexpr int VAHEAD = 2;                                    // V^T fragment reads ahead of their MFMA
+    auto block = [&](const f32x16 (&cur)[2], f32x16 (&nxt)[2], const lds_char* ka, const lds_char* va) {
         const float nb = m == -INFINITY ? 0.0f : -m;            // no visible key yet: every s is -inf
-        h8 pf[2][2];
+        u32x4 kf[NQ];
+        h8 vf[NP];
+        float pe[32];
+        h8 pf[4];
         float ps = lsum;
+        auto read_k = [&](int i) {
+            kf[i] = *(const __attribute__((address_space(3))) u32x4*)(ka + (i & 1) * 32 * KP + (i >> 1) * 32);
+        };
+        auto read_v = [&](int p) {
+            const int kk = (p / DT) * 16, dt = p % DT;
+            vf[p] = v_frag<KT>(va + dt * 64 + kk * VP, va + dt * 64 + (kk + 8) * VP);
+        };
+        // The softmax of score v (p = 2^(s * scale * log2 e - m), then f16
+        // pairs packed into chunk v / 8 = one 16-key MFMA step's P^T, and
+        // the row sum) is itself pipelined over the slots, so that no VALU
+        // instruction waits on the one before it: the fma of v in slot
+        // fslot(v), its exp2 one slot later, the f16 pack of pair (2i, 2i + 1)
+        // three slots after the fma of 2i + 1, its row-sum term one slot
+        // after that.  The fmas are spread over the first NS - 8 slots, which
+        // completes chunk c before its first P.V MFMA (slot NQ + c DT).
+        constexpr int NS = NQ + NP;
+        auto fslot = [](int v) { return v * (NS - 8) / 32; };
+        auto pair_slot = [&](int i) { return fslot(2 * i + 1) + 3; };
+        static_assert(((31 * (NQ + NP - 8)) / 32) + 3 < NQ + 3 * DT, "chunk 3 packed before its P.V");
+        auto valu_slot = [&](int sl) {
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
+            for (int v = 0; v < 32; ++v) {
+                if (fslot(v) == sl) pe[v] = fmaf(cur[v >> 4][v & 15], sl2, nb);
+                if (fslot(v) + 1 == sl) pe[v] = __builtin_amdgcn_exp2f(pe[v]);
+            }
 #pragma unroll
-            for (int k2 = 0; k2 < 2; ++k2) {
-                h8 pv;
-#pragma unroll
-                for (int e = 0; e < 8; e += 2) {
-                    const float p0 = __builtin_amdgcn_exp2f(fmaf(s[kt][k2 * 8 + e], sl2, nb));
-                    const float p1 = __builtin_amdgcn_exp2f(fmaf(s[kt][k2 * 8 + e + 1], sl2, nb));
-                    const h2 pp = {(_Float16)p0, (_Float16)p1};
-                    pv[e] = pp.x;
-                    pv[e + 1] = pp.y;
+            for (int i = 0; i < 16; ++i) {
+                if (pair_slot(i) == sl) {
+                    const h2 pp = {(_Float16)pe[2 * i], (_Float16)pe[2 * i + 1]};
+                    pf[i >> 2][2 * (i & 3)] = pp.x;
+                    pf[i >> 2][2 * (i & 3) + 1] = pp.y;
+                }
+                if (pair_slot(i) + 1 == sl) {
+                    const h2 pp = {pf[i >> 2][2 * (i & 3)], pf[i >> 2][2 * (i & 3) + 1]};
                     ps = __builtin_amdgcn_fdot2(pp, h2{(_Float16)1.0f, (_Float16)1.0f}, ps, false);
                 }
-                pf[kt][k2] = pv;
             }
-        lsum = ps;
+        };
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
+        for (int i = 0; i < KAHEAD; ++i) read_k(i);
 #pragma unroll
-            for (int k2 = 0; k2 < 2; ++k2) {
-                const int kk = (kt * 2 + k2) * 16;
-#pragma unroll
-                for (int dt = 0; dt < DT; ++dt) {
-                    const h8 vf = v_frag<KT>(va + dt * 64 + kk * VP, va + dt * 64 + (kk + 8) * VP);
-                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[kt][k2], o[dt], 0, 0, 0);
-                }
+        for (int sl = 0; sl < NS; ++sl) {
+            if (sl < NQ) {
+                const int ds = sl >> 1, kt = sl & 1;
+                nxt[kt] = F::mma(as_vec<QF>(kf[sl]), qf[ds], ds == 0 ? f32x16{} : nxt[kt]);
+                if (sl + KAHEAD < NQ) read_k(sl + KAHEAD);
+            } else if (sl < NS) {
+                const int p = sl - NQ;
+                o[p % DT] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[p], pf[p / DT], o[p % DT], 0, 0, 0);
             }
-    };
-
-    for (int j = 0; j < n_tiles; ++j) {
-        // tile j has landed (tiles j + 1, j + 2 may still fly) and every wave
-        // is done with tile j - 1, whose stage tile j + 3 now takes
-        wait_vm_barrier<2 * NLD>();
-        issue(j + 3);
-        const int k0 = kb0 + j * kBN;
-        if (k0 < kend_w) {                                       // wave-uniform
-            uint32_t kaddr = lds0 + (j % kStages) * STAGE + k_rd;
-            uint32_t vaddr = lds0 + (j % kStages) * STAGE + KREG + v_rd;
-            asm volatile("" : "+v"(kaddr), "+v"(vaddr));         // one base register, constant offsets
-            f32x16 s[2];
-            scores(lds_at(kaddr), s);
-            if (EXPL || k0 + kBN - 1 > lim_w) apply_mask(s, k0);
-            softmax_pv(lds_at(vaddr), s);
+            if (sl - NQ + VAHEAD >= 0 && sl - NQ + VAHEAD < NP) read_v(sl - NQ + VAHEAD);
+            valu_slot(sl);
+            __builtin_amdgcn_sched_barrier(0);
         }
+        lsum = ps;
+    };
+    // K of tile 0 has landed (its V and tiles 1, 2 may still fly)
+    wait_vm_barrier<NIV + 2 * NLD>();
+    f32x16 sa[2], sb[2];
+    float mx = 0.0f;
+    if (n_live > 0) {
+        scores(k_addr(0), sa);
+        if (needs_mask(0)) apply_mask(sa, kb0);
+        mx = rowmax(sa);
     }
+    auto step = [&](int j, const f32x16 (&cur)[2], f32x16 (&nxt)[2]) {
+        // K of tile j + 1 and V of tile j have landed (loads complete in
+        // order; V of j + 1 and tile j + 2 may still fly), and every wave is
+        // done with tile j - 1, whose stage tile j + 3 now takes
+        wait_vm_barrier<NIV + NLD>();
+        issue(j + 3);
+        if (j < n_live) {                                        // wave-uniform
+            rescale(mx);
+            uint32_t vaddr = lds0 + (j % kStages) * STAGE + KREG + v_rd;
+            asm volatile("" : "+v"(vaddr));
+            // tile j + 1's scores are computed whether or not the wave sees
+            // it: past the wave's last live tile no step reads them
+            block(cur, nxt, k_addr(j + 1), lds_at(vaddr));
+            if (needs_mask(j + 1)) apply_mask(nxt, kb0 + (j + 1) * kBN);
+            mx = rowmax(nxt);
+        }
+    };
+    int j = 0;
+    for (; j + 1 < n_tiles; j += 2) {
+        step(j, sa, sb);
+        step(j + 1, sb, sa);
+    }
+    if (j < n_tiles) step(j, sa, sb);
     wait_vm_barrier<0>();                                       // the padding tiles' loads
 
     // ---- normalize and write (each lane owns its row; lanes l and l ^ 32
