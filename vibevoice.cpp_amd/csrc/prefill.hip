@@ -658,14 +658,16 @@ bool prefill_supported(const AttnArgs& a) {
     return true;
 }
 
-// Split plan: every workgroup in one round on the CUs (a second, partial
-// round costs more than it balances), and within that budget the shortest
-// critical path, i.e. the fewest key tiles in the largest piece: the
-// heaviest row tiles (the last ones, under a causal mask) split n ways,
-// the rest whole, with the partials' round trip and the merge launch
-// counted against a split and the partials within ws_cap bytes.  Calls with
-// more row tiles than CUs need no split: launched heaviest first they
-// balance already.
+// Split plan.  The candidates split the key tiles of the row tiles rt >= R
+// n ways (R = 0: every row tile; or the smallest R that keeps the whole
+// grid in one round on the CUs).  Each is scored by replaying the
+// hardware's dispatch: workgroups go out in launch order (heaviest row tile
+// first, kv heads innermost), each to the CU that frees first, costing its
+// key tiles plus a fixed prologue (Q rows loaded, the first tiles staged);
+// a split plan adds the partials' round trip and the merge launch.  Causal
+// row tiles differ in length, so a plan with more, smaller pieces over
+// several rounds can finish sooner than one round of equal-count splits.
+// Calls with many more row tiles than CUs balance unsplit.
 PrefillPlan prefill_plan(const AttnArgs& a, int n_cu, int forced, size_t ws_cap) {
     const int n_rt = (a.T * (a.Hq / a.Hkv) + kRowsWG - 1) / kRowsWG;
     const bool causal = a.mask_mode == kMaskCausal;
@@ -673,32 +675,67 @@ PrefillPlan prefill_plan(const AttnArgs& a, int n_cu, int forced, size_t ws_cap)
     const PrefillPlan none{1, 0, 0, 1};
     const int per = a.Hkv * a.B;                 // workgroups per piece index
     const int budget = n_cu / per;               // pieces per (kv head, sequence) in one round
-    if (n_rt >= budget) return none;
-    // key tiles of the largest piece, over the batch, for row tiles [lo, hi) split n ways
-    auto max_piece = [&](int lo, int hi, int n) {
-        int m = 0;
-        for (int b = 0; b < a.B; ++b)
-            for (int rt = lo; rt < hi; ++rt) m = max(m, (rt_key_tiles(a, b, rt, causal) + n - 1) / n);
-        return m;
-    };
+    if (n_rt >= 4 * budget) return none;
     // time in key-tile units (one tile of 64 keys x 256 rows for one workgroup)
     const double unit_us = 64.0 * kRowsWG * a.d * 4.0 / 4.0e6;
-    const double bytes_per_unit = 4.0e6 * unit_us;
+    const double bytes_per_unit = 5.0e6 * unit_us;   // 5 TB/s
     const double merge_launch = 5.0 / unit_us;
+    const double prologue = 3.0;                 // ~6 us per workgroup, measured at the 7B shape
+    std::vector<int> nt((size_t)a.B * n_rt);
+    for (int b = 0; b < a.B; ++b)
+        for (int rt = 0; rt < n_rt; ++rt) nt[(size_t)b * n_rt + rt] = rt_key_tiles(a, b, rt, causal);
+    // cost of piece x of sequence b under plan p (key tiles + prologue)
+    auto piece_cost = [&](const PrefillPlan& p, int b, int x) {
+        const int nh = p.forced > 0 ? p.forced : p.n, R = p.forced > 0 ? 0 : p.R;
+        const int heavy = (n_rt - R) * nh;
+        const int rt = x < heavy ? n_rt - 1 - x / nh : R - 1 - (x - heavy);
+        const int ks = x < heavy ? x % nh : 0, n_ks = x < heavy ? nh : 1;
+        const int n_all = nt[(size_t)b * n_rt + rt];
+        return (double)((int64_t)(ks + 1) * n_all / n_ks - (int64_t)ks * n_all / n_ks) + prologue;
+    };
+    // finish time of plan p: the kv heads of one piece index cost the same,
+    // so the CUs are taken in groups of Hkv; pieces go out in the kernel's
+    // order (sequence-major, heaviest row tile first) to the group that frees
+    // first.  One round (every piece has a group): the largest piece.
+    const int groups = max(1, n_cu / a.Hkv);
+    std::vector<double> cu;
+    auto makespan = [&](const PrefillPlan& p) {
+        const int pieces = plan_pieces(p, n_rt);
+        double m = 0.0;
+        if ((int64_t)pieces * a.B <= groups) {
+            for (int b = 0; b < a.B; ++b)
+                for (int x = 0; x < pieces; ++x) m = max(m, piece_cost(p, b, x));
+            return m;
+        }
+        cu.assign((size_t)groups, 0.0);
+        for (int b = 0; b < a.B; ++b)
+            for (int x = 0; x < pieces; ++x) {
+                std::pop_heap(cu.begin(), cu.end(), std::greater<double>());
+                cu.back() += piece_cost(p, b, x);
+                std::push_heap(cu.begin(), cu.end(), std::greater<double>());
+            }
+        for (double c : cu) m = max(m, c);
+        return m;
+    };
     PrefillPlan best = none;
-    double best_t = max_piece(0, n_rt, 1);
+    double best_t = makespan(none);
     for (int n = 2; n <= kMaxKeySplits; ++n) {
-        // smallest R with (n_rt - R) n + R <= budget
-        const int R = max(0, (n_rt * n - budget + n - 2) / (n - 1));
-        if (R >= n_rt) break;
-        const PrefillPlan p{n, R, 0, n};
-        if (prefill_ws_bytes(a, p) > ws_cap) continue;
-        const double split_rows = (double)(n_rt - R) * kRowsWG * per;
-        const double t = max(max_piece(R, n_rt, n), max_piece(0, R, 1)) + merge_launch +
-                         split_rows * (n + 1) * (a.d + 2) * 4.0 * 2.0 / bytes_per_unit;
-        if (t < best_t * 0.95) {                 // a split must pay for itself
-            best_t = t;
-            best = p;
+        // the smallest R with (n_rt - R) n + R <= budget (one round), and for
+        // a few split counts R = 0 (every row tile split, several rounds)
+        const int R_fit = max(0, (n_rt * n - budget + n - 2) / (n - 1));
+        for (int R : {R_fit, 0}) {
+            if (R >= n_rt || (R == 0 && R_fit > 0 && n > 8)) continue;
+            const PrefillPlan p{n, R, 0, n};
+            if (prefill_ws_bytes(a, p) > ws_cap) continue;
+            const double split_rows = (double)(n_rt - R) * kRowsWG * per;
+            // the partials are written while other workgroups compute; the merge
+            // kernel's reads of the n partials and its output write are not hidden
+            const double t = makespan(p) + merge_launch + split_rows * (n + 1) * (a.d + 2) * 4.0 / bytes_per_unit;
+            if (t < best_t * 0.95) {             // a split must pay for itself
+                best_t = t;
+                best = p;
+            }
+            if (R_fit == 0) break;
         }
     }
     return best;

@@ -40,6 +40,10 @@ struct vva_context {
     float* scratch = nullptr;            // this device's `scratch` (vva_attn_noalloc)
     unsigned* tickets = nullptr;         // vva_decode_step's merge tickets, zeroed once
     std::set<vva_kv*> caches;            // released by vva_destroy if still alive
+    // the last prefill plan and the call shape it was made for: a layer stack
+    // repeats one shape layer after layer
+    std::vector<int64_t> plan_key;
+    PrefillPlan plan{1, 0, 0, 1};
 };
 
 struct vva_kv {
@@ -222,6 +226,20 @@ vva_status run_attention(vva_context* ctx, AttnArgs& a, bool fixed = false) {
     // Not on the no-allocation path, whose scratch cannot hold a window.
     const bool convert = a.k_type == a.v_type &&
                          (a.k_type == VVA_TYPE_Q8_0 || (a.k_type == VVA_TYPE_F32 && ctx->use_flash_attn));
+    // prefill plan of call shape c, reused while the shape repeats
+    auto plan_for = [&](const AttnArgs& c, size_t cap) {
+        std::vector<int64_t> key = {c.d, c.Hq, c.Hkv, c.T, c.B, c.mask_mode, ctx->n_cu, ctx->sched_prefill_splits,
+                                    (int64_t)cap};
+        for (int b = 0; b < c.B; ++b) {
+            key.push_back(c.L[b]);
+            key.push_back(c.past[b]);
+        }
+        if (key != ctx->plan_key) {
+            ctx->plan = prefill_plan(c, ctx->n_cu, ctx->sched_prefill_splits, cap);
+            ctx->plan_key = std::move(key);
+        }
+        return ctx->plan;
+    };
     if (ctx->attn_path != 1 && a.T > 1 && convert && !fixed && (a.d == 64 || a.d == 128)) {
         AttnArgs c = a;
         const size_t wb = window_f16_bytes(a);
@@ -233,7 +251,7 @@ vva_status run_attention(vva_context* ctx, AttnArgs& a, bool fixed = false) {
         // with the final alignment for the support check
         for (int b = 0; b < a.B; ++b) c.k[b] = c.v[b] = (const char*)(uintptr_t)256;
         if (prefill_supported(c)) {
-            const PrefillPlan plan = prefill_plan(c, ctx->n_cu, ctx->sched_prefill_splits, (size_t)1 << 34);
+            const PrefillPlan plan = plan_for(c, (size_t)1 << 34);
             vva_status st = ensure_ws(ctx, wb + prefill_ws_bytes(c, plan));
             if (st != VVA_OK) return st;
             char* wbase = (char*)ctx->ws;
@@ -251,8 +269,7 @@ vva_status run_attention(vva_context* ctx, AttnArgs& a, bool fixed = false) {
         }
     }
     if (ctx->attn_path != 1 && a.T > 1 && prefill_supported(a)) {
-        const PrefillPlan plan = prefill_plan(a, ctx->n_cu, ctx->sched_prefill_splits,
-                                              fixed ? kScratchBytes : ((size_t)1 << 34));
+        const PrefillPlan plan = plan_for(a, fixed ? kScratchBytes : ((size_t)1 << 34));
         if (plan.max_ks > 1) {
             vva_status st = get_ws(ctx, fixed, prefill_ws_bytes(a, plan), &ws);
             if (st != VVA_OK) return st;
