@@ -130,7 +130,8 @@ def run_prefill(torch, vva, ctx, steps: int, warmup: int, heavy: bool = False):
 
 def run_decode(torch, vva, ctx, steps: int, warmup: int):
     rng = torch.Generator(device="cuda").manual_seed(4321)
-    kv = vva.KVCache(ctx, LAYERS, HKV, D, L_DECODE + steps + warmup + 8, B_DECODE, vva.Q8_0)
+    n_layer_steps = 32                  # per form, in the decode-step comparison below
+    kv = vva.KVCache(ctx, LAYERS, HKV, D, L_DECODE + steps + warmup + 2 * n_layer_steps + 16, B_DECODE, vva.Q8_0)
     # fill every layer's caches by appending L_DECODE random rows (RoPE'd K, raw V)
     chunk = 8192
     for layer in range(LAYERS):
@@ -190,6 +191,38 @@ def run_decode(torch, vva, ctx, steps: int, warmup: int):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     attn_us = float(np.mean([a.elapsed_time(b) for a, b in ev])) * 1e3 / LAYERS
+
+    # The decode step as the ASR loop runs it, layer after layer (RoPE +
+    # append + attention of one new token per stream): vva_decode_step (the
+    # streamed kernel in step mode, then its merge) against the
+    # vva_rope_append + vva_attn pair, alternating, n_layer_steps steps each.
+    def layer_step(fused, events):
+        cur = kv.get_len(0)
+        pos.fill_(cur)
+        events[0].record()
+        for layer in range(LAYERS):
+            if fused:
+                ctx.check(lib.vva_decode_step(h, kvh, layer, qv_r, kv_r, vv_r, pv_r, None, THETA, scale, qrv_r, ov_r))
+            else:
+                ctx.check(lib.vva_rope_append(h, kvh, layer, qv_r, kv_r, vv_r, pv_r, None, THETA, qrv_r))
+                ctx.check(lib.vva_attn(h, kvh, layer, qrv_r, None, None, scale, ov_r))
+        events[1].record()
+        for s in range(B_DECODE):
+            kv.set_len(s, cur + 1)
+        return cur + 1
+
+    layer_step(True, ev[0])
+    layer_step(False, ev[0])
+    torch.cuda.synchronize()
+    ev_f = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n_layer_steps)]
+    ev_u = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n_layer_steps)]
+    lens_fused = []
+    for i in range(n_layer_steps):
+        lens_fused.append(layer_step(True, ev_f[i]))
+        layer_step(False, ev_u[i])
+    torch.cuda.synchronize()
+    step_fused_us = float(np.mean([a.elapsed_time(b) for a, b in ev_f])) * 1e3 / LAYERS
+    step_pair_us = float(np.mean([a.elapsed_time(b) for a, b in ev_u])) * 1e3 / LAYERS
     bytes_total = sum(decode_attn_bytes([L] * B_DECODE) + decode_append_bytes(B_DECODE)
                       for L in lens_timed) * LAYERS
     mean_L = float(np.mean(lens_timed))
@@ -204,6 +237,9 @@ def run_decode(torch, vva, ctx, steps: int, warmup: int):
         "kv_bytes_per_layer": kv_bytes_layer,
         "splits": ctx.last_decode_splits(),
         "mean_L": mean_L,
+        "step_fused_us": step_fused_us,
+        "step_pair_us": step_pair_us,
+        "step_bytes": decode_attn_bytes([float(np.mean(lens_fused))] * B_DECODE) + decode_append_bytes(B_DECODE),
     }
     return res, kv
 
@@ -602,6 +638,13 @@ def main() -> int:
                          "avg_launch_us": round(dec["attn_us"], 3), "bytes_per_launch": dec["bytes_per_layer"],
                          "timing": "HIP events around each step's 28 back-to-back attention calls",
                          "splits": dec["splits"]},
+            "step": {"workload": "the decode step as the ASR loop runs it: per layer RoPE + append + attention of "
+                                 "one new token per stream, layer after layer",
+                     "fused_us_per_layer": round(dec["step_fused_us"], 3),
+                     "rope_append_plus_attn_us_per_layer": round(dec["step_pair_us"], 3),
+                     "fused_gbs": round(dec["step_bytes"] / (dec["step_fused_us"] * 1e-6) / 1e9, 1),
+                     "fused_frac_of_hbm_peak": round(dec["step_bytes"] / (dec["step_fused_us"] * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+                     "timing": "HIP events around each step's 28 layers, 32 steps per form, alternating"},
         }
         if not args.no_cpu:
             line["decode"]["cpu_baseline"] = cpu_baseline_decode(torch, vva, vvo, kvd)

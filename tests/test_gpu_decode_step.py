@@ -1,5 +1,7 @@
-"""GPU parity of vva_decode_step (decode_step.hip): RoPE + append + split
-attention + in-kernel merge of the splits in one launch.
+"""GPU parity of vva_decode_step: on F16 / BF16 caches decode_step.hip (RoPE +
+append + split attention + in-kernel merge of the splits in one launch), on
+Q8_0 caches the streamed decode kernel in step mode (RoPE + append +
+attention, then its merge kernel).
 
 Each step is checked three ways on the same inputs: the appended cache rows
 must equal those of vva_rope_append bit for bit (same rotation, same
@@ -26,7 +28,11 @@ CASES = [
     (128, 12, 2, vva.BF16, [3999], vva.BF16),        # 1.5B heads
     (128, 28, 4, vva.F16, [90, 2000], vva.F16),      # one split for the first stream
     (128, 28, 4, vva.F16, [9000], vva.F32),          # past the fused kernel's window: the unfused path
-    (64, 14, 2, vva.Q8_0, [700, 700], vva.F32),      # Q8_0 cache: the unfused path
+    (64, 14, 2, vva.Q8_0, [700, 700], vva.F32),      # Q8_0 caches: the streamed kernel in step mode
+    (128, 28, 4, vva.Q8_0, [3000, 2500], vva.F32),   # 7B heads (kv-head pairs), ragged CFG streams
+    (128, 28, 4, vva.Q8_0, [32768, 32768], vva.F16), # the ASR transcript decode at full length
+    (128, 12, 2, vva.Q8_0, [4100], vva.BF16),        # 1.5B heads, whole rows
+    (64, 8, 1, vva.Q8_0, [500], vva.F32),            # one kv head
 ]
 
 
@@ -57,6 +63,10 @@ def test_decode_step_matches_unfused_and_oracle(ctx, torch_gpu, d, Hq, Hkv, t, l
         ctx.attn(u, 0, qu, ou, d ** -0.5)
         torch.cuda.synchronize()
         assert torch.equal(qa, qu), "rotated q differs"
+        if t == vva.Q8_0:
+            # the same streamed kernel on the same bytes: the new row patched
+            # into its tile equals the row rope_append wrote
+            assert torch.equal(oa, ou), "fused Q8_0 step differs from the unfused pair"
         for s in range(B):
             ka, va_ = a.download(0, s, L[s] + 1)
             ku, vu = u.download(0, s, L[s] + 1)

@@ -152,8 +152,7 @@ __global__ void __launch_bounds__(64 * kStepWaves) decode_step_kernel(StepArgs a
 
     // ---- 1. angle table; the raw q / k / v words to LDS
     if (tid < P) {
-        float th = (float)pos_i;
-        for (int k = 0; k < tid; ++k) th *= theta_scale;
+        const float th = rope_theta((float)pos_i, theta_scale, tid, P);
         cs[tid] = cosf(th);
         sn[tid] = sinf(th);
     }

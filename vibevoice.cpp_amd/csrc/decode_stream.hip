@@ -48,6 +48,14 @@
 // query head; the workgroup writes (m, l, acc[d]) per query head, or the
 // output when there is one split, and decode_merge_kernel (decode.hip)
 // combines the splits.
+//
+// Step mode (STEP; vva_decode_step on Q8_0 caches, the ASR decode loop of
+// src/vibevoice_asr.cpp:760-800 with src/qwen2.cpp:282-306 fused in): q
+// arrives raw and is RoPE'd while it is quantized (split 0 writes q_out),
+// and the split that holds key len(seq_b) computes the new row itself
+// (RoPE(k), v, both quantized to Q8_0 blocks exactly as rope_append.hip
+// does), writes it to the cache and copies it into its own tile once that
+// tile has landed; its DMA copy of the row, older or newer, is overwritten.
 #include "vva_internal.hpp"
 
 #include <type_traits>
@@ -78,7 +86,8 @@ static_assert(kOpChunks % kP == 0, "chunks split evenly over the producers");
 static_assert(3 * kLoads <= 63, "three tiles of a producer's loads fit its 6-bit vmcnt");
 constexpr int kDead = 0x40000000;            // buffer offset past every range
 constexpr float kLazy = 8.0f;                // running-max slack in log2 units: p <= 256
-static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
+constexpr int kStepLds = 2048;               // step mode: angle table + the new K / V rows
+static_assert(kLdsBytes + kStepLds <= 160 * 1024, "LDS budget");
 
 // buffer_load_dwordx4 ... lds: each lane's 16 bytes land at LDS address
 // m0 + 16 * lane.  Inline asm, so the compiler neither fences LDS reads on it
@@ -150,10 +159,10 @@ __device__ __forceinline__ h4 cat_h4(h2 lo, h2 hi) { return h4{lo[0], lo[1], hi[
 // its group's slice of every cache row (RB bytes, a multiple of 16, at
 // group * RB in a row of NHG * RB bytes): the split partials then cover HKV
 // kv heads over NHG times the keys, NHG times fewer of them.
-template <int D, int HKV, int NHG>
+template <int D, int HKV, int NHG, bool STEP>
 __global__ void __launch_bounds__((kW + kP) * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
-decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits) {
-    prefetch_kernargs<sizeof(AttnArgs)>();
+decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, StreamStep st) {
+    prefetch_kernargs<sizeof(AttnArgs) + 16 + (STEP ? sizeof(StreamStep) : 0)>();
     constexpr int NB = D / 32;                // Q8_0 blocks per head row
     constexpr int HB = NB * kQ8Bytes;         // bytes per head row
     constexpr int RB = HKV * HB;              // bytes per token row in LDS (the group's kv heads)
@@ -167,7 +176,8 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits) {
     static_assert(TT * RB == kTileOpBytes && NSUB * kW == NPAIR && NSUB >= 1, "tile size");
     static_assert(kW % HP == 0, "a wave keeps its head pair across its slot pairs");
 
-    __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
+    // step mode: the RoPE angle table and the new K and V rows after the ring
+    __shared__ __attribute__((aligned(16))) char lds[kLdsBytes + (STEP ? kStepLds : 0)];
 
     const int lane = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -202,6 +212,12 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits) {
     const int n_full = L / TT;                // tiles without keys past L
     const int n_whole = split < n_full ? (n_full - split + n_splits - 1) / n_splits : 0;
     auto tile_key = [&](int t) { return (split + t * n_splits) * TT; };   // first key of tile t
+    // step mode: the split holding key L - 1 (the new row) and its tile index
+    const bool owns_new = STEP && (all_tiles - 1) % n_splits == split;
+    const int new_t = owns_new ? n_tiles - 1 : -1;
+    float* const rope_cs = (float*)(lds + kLdsBytes);                  // [D / 2]
+    float* const rope_sn = rope_cs + D / 2;
+    char* const new_rows = (char*)(rope_sn + D / 2);                   // K slice, then V slice (RB each)
 
     // One raw buffer per operand: from the 16-byte boundary at or below the
     // sequence's row 0 to its row L - 1.  delta = row 0's offset from that
@@ -267,11 +283,20 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits) {
         }
         issue(0);
         wait_vm_barrier<kLoads>();                   // A: Q landed
-        wait_vm_barrier<kLoads>();                   // B
-        issue(1);
-        issue(2);
+        if constexpr (STEP) {
+            // step mode: the RoPE of q lengthens A -> B, so tiles 1 and 2 go
+            // out at A
+            issue(1);
+            issue(2);
+            wait_vm_barrier<3 * kLoads>();           // B
+        } else {
+            wait_vm_barrier<kLoads>();               // B
+            issue(1);
+            issue(2);
+        }
         for (int t = 0; t < n_tiles; ++t) {
             wait_vm_barrier<2 * kLoads>();           // T_t: tile t landed
+            if (STEP && t == new_t) lds_barrier();   // N: the new row is in tile t's stage
             issue(t + kStages - 1);
         }
         // the padding tiles' loads land before the ring is reused
@@ -281,11 +306,83 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits) {
         return;
     }
 
+    // ---- step mode, while q flies: the raw new k / v pair of this lane
+    // (the split holding key L - 1; waves 0, 1: k of the group's kv heads,
+    // waves 2, 3: v) and the angle table of the new token's position (the
+    // fp32 theta recurrence of rope_append.hip)
+    float nx0 = 0.0f, nx1 = 0.0f;
+    if constexpr (STEP) {
+        constexpr int P = D / 2;
+        const int kind = w >> 1, hh = w & 1;
+        if (owns_new && hh < HKV) {                  // wave-uniform
+            const int head = hgrp * HKV + hh;
+            const int typ = kind ? st.v_type : st.k_type;
+            const int64_t es = type_elem_bytes(typ);
+            const char* src = (kind ? st.v + b * st.v_nb_b + head * st.v_nb_h : st.k + b * st.k_nb_b + head * st.k_nb_h);
+            const int ii = lane < P ? lane : 0;
+            nx0 = load_elem(src + ii * es, typ);
+            nx1 = load_elem(src + (ii + P) * es, typ);
+        }
+        if (threadIdx.x < D / 2) {
+            const int i = threadIdx.x;
+            const float th = rope_theta((float)st.pos[b * st.pos_stride_b], st.theta_scale, i, D / 2);
+            rope_cs[i] = cosf(th);
+            rope_sn[i] = sinf(th);
+        }
+    }
+
     // ---- Q is quantized to Q8_0 blocks (codes + fp16-rounded scale) next
     // to the raw rows.  Four adjacent lanes share a block (8 values each; the
     // block max over the quad by DPP); a thread takes every (kW * 64)-th
     // quarter block.
     lds_barrier();                                   // A
+
+    // ---- step mode, the split holding key L - 1: the new K row (waves 0,
+    // 1: RoPE'd) and V row (waves 2, 3) of the group's kv heads, one
+    // rotation pair (i, i + D / 2) per lane, quantized per 32-dim block
+    // (block max over a half-wave) like rope_append.hip's Q8_0 append; to the
+    // cache row and to new_rows
+    if constexpr (STEP) {
+        const int kind = w >> 1, hh = w & 1, i = lane;
+        if (owns_new && hh < HKV) {                  // wave-uniform
+            constexpr int P = D / 2;
+            const int head = hgrp * HKV + hh;
+            const int ii = i < P ? i : 0;
+            const float x0 = nx0, x1 = nx1;
+            float y0 = x0, y1 = x1;
+            if (kind == 0) {
+                const float c = rope_cs[ii], sn = rope_sn[ii];
+                y0 = fmaf(x0, c, -(x1 * sn));
+                y1 = fmaf(x0, sn, x1 * c);
+            }
+            float a0 = fabsf(y0), a1 = fabsf(y1);
+#pragma unroll
+            for (int m = 16; m >= 1; m >>= 1) {
+                a0 = fmaxf(a0, __shfl_xor(a0, m, 32));
+                a1 = fmaxf(a1, __shfl_xor(a1, m, 32));
+            }
+            const float d0 = a0 / 127.0f, d1 = a1 / 127.0f;
+            const float id0 = d0 != 0.0f ? 1.0f / d0 : 0.0f;
+            const float id1 = d1 != 0.0f ? 1.0f / d1 : 0.0f;
+            if (i < P) {
+                char* crow = (char*)(kind ? a.v[b] : a.k[b]) + (int64_t)(L - 1) * RBM + (int64_t)head * HB;
+                char* lrow = new_rows + kind * RB + hh * HB;
+                const int j0 = i, j1 = i + P;
+                const char c0 = (char)(int8_t)roundf(y0 * id0), c1 = (char)(int8_t)roundf(y1 * id1);
+                if ((j0 & 31) == 0) {
+                    const uint16_t h0 = f32_to_f16(d0), h1 = f32_to_f16(d1);
+                    *(uint16_t*)(crow + (j0 / 32) * kQ8Bytes) = h0;
+                    *(uint16_t*)(crow + (j1 / 32) * kQ8Bytes) = h1;
+                    *(uint16_t*)(lrow + (j0 / 32) * kQ8Bytes) = h0;
+                    *(uint16_t*)(lrow + (j1 / 32) * kQ8Bytes) = h1;
+                }
+                crow[(j0 / 32) * kQ8Bytes + 2 + (j0 & 31)] = c0;
+                crow[(j1 / 32) * kQ8Bytes + 2 + (j1 & 31)] = c1;
+                lrow[(j0 / 32) * kQ8Bytes + 2 + (j0 & 31)] = c0;
+                lrow[(j1 / 32) * kQ8Bytes + 2 + (j1 & 31)] = c1;
+            }
+        }
+    }
 
     const char* qraw = lds + (kStages - 1) * kStage;
     uint32_t* qlds = (uint32_t*)(lds + (kStages - 1) * kStage + kQRawBytes);
@@ -313,6 +410,66 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits) {
                 const uint16_t lo = (uint16_t)(wv[e] & 0xffffu), hi = (uint16_t)(wv[e] >> 16);
                 x[2 * e] = bf ? bf16_to_f32(lo) : f16_to_f32(lo);
                 x[2 * e + 1] = bf ? bf16_to_f32(hi) : f16_to_f32(hi);
+            }
+        }
+        if constexpr (STEP) {
+            // RoPE (pairs i, i + D / 2 of the head row; the partners of this
+            // quarter block's 8 dims sit D / 2 further or nearer in qraw),
+            // rounded to q_out's type as the unfused path stores it; split 0
+            // writes q_out
+            constexpr int P = D / 2;
+            const int hr = (tt >> 2) / NB, dim0 = ((tt >> 2) % NB) * 32 + (tt & 3) * 8;
+            const bool lo = dim0 < P;
+            const char* prow = qraw + (int64_t)((tt >> 2) * 32 + (tt & 3) * 8 + (lo ? P : -P)) * eb;
+            float xp[8];
+            if (a.q_type == VVA_TYPE_F32) {
+                const uint4 u0 = ((const uint4*)prow)[0], u1 = ((const uint4*)prow)[1];
+                xp[0] = __uint_as_float(u0.x); xp[1] = __uint_as_float(u0.y);
+                xp[2] = __uint_as_float(u0.z); xp[3] = __uint_as_float(u0.w);
+                xp[4] = __uint_as_float(u1.x); xp[5] = __uint_as_float(u1.y);
+                xp[6] = __uint_as_float(u1.z); xp[7] = __uint_as_float(u1.w);
+            } else {
+                const bool bf = a.q_type == VVA_TYPE_BF16;
+                const uint4 u0 = ((const uint4*)prow)[0];
+                const uint32_t wv[4] = {u0.x, u0.y, u0.z, u0.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint16_t l16 = (uint16_t)(wv[e] & 0xffffu), h16 = (uint16_t)(wv[e] >> 16);
+                    xp[2 * e] = bf ? bf16_to_f32(l16) : f16_to_f32(l16);
+                    xp[2 * e + 1] = bf ? bf16_to_f32(h16) : f16_to_f32(h16);
+                }
+            }
+            const float4 c0 = *(const float4*)(rope_cs + (dim0 & (P - 1))), c1 = *(const float4*)(rope_cs + (dim0 & (P - 1)) + 4);
+            const float4 s0 = *(const float4*)(rope_sn + (dim0 & (P - 1))), s1 = *(const float4*)(rope_sn + (dim0 & (P - 1)) + 4);
+            const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+            const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+            float y[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) y[e] = lo ? fmaf(x[e], cv[e], -(xp[e] * sv[e])) : fmaf(xp[e], sv[e], x[e] * cv[e]);
+            // rounded to q_out's type, as the unfused path reads it back; split
+            // 0 writes q_out
+            const int qot = st.q_out_type;
+            const bool wq = split == 0 && t < nqi;
+            char* qo = st.q_out + b * st.qo_nb_b + (int64_t)(hq0 + hr) * st.qo_nb_h;
+            if (qot == VVA_TYPE_F32) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) x[e] = y[e];
+                if (wq) {
+                    ((float4*)(qo + dim0 * 4))[0] = make_float4(y[0], y[1], y[2], y[3]);
+                    ((float4*)(qo + dim0 * 4))[1] = make_float4(y[4], y[5], y[6], y[7]);
+                }
+            } else {
+                const bool bf = qot == VVA_TYPE_BF16;
+                uint32_t hw[4];
+#pragma unroll
+                for (int e = 0; e < 8; e += 2) {
+                    const uint16_t h0 = bf ? f32_to_bf16(y[e]) : f32_to_f16(y[e]);
+                    const uint16_t h1 = bf ? f32_to_bf16(y[e + 1]) : f32_to_f16(y[e + 1]);
+                    x[e] = bf ? bf16_to_f32(h0) : f16_to_f32(h0);
+                    x[e + 1] = bf ? bf16_to_f32(h1) : f16_to_f32(h1);
+                    hw[e / 2] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+                }
+                if (wq) *(uint4*)(qo + dim0 * 2) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
             }
         }
         float am = 0.0f;
@@ -546,6 +703,16 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits) {
         const char* kt = lds + (t & (kStages - 1)) * kStage + dk;
         const char* vt = lds + (t & (kStages - 1)) * kStage + kOpBytes + dv;
         const int jt = tile_key(t);
+        if constexpr (STEP) {
+            if (t == new_t) {                        // wave-uniform: the new row into the tile
+                const int r = L - 1 - jt;
+                for (int x = threadIdx.x; x < 2 * RB / 4; x += kW * 64) {
+                    const int op = x / (RB / 4), wd = x % (RB / 4);
+                    ((uint32_t*)((op ? vt : kt) + r * RB))[wd] = ((const uint32_t*)(new_rows + op * RB))[wd];
+                }
+                lds_barrier();                       // N
+            }
+        }
         PairOps ops[NSUB];
 #pragma unroll
         for (int u = 0; u < NSUB; ++u) read_pair(kt, vt, pair_key(u), ops[u]);
@@ -670,8 +837,8 @@ int stream_groups(const AttnArgs& a) {
     return a.Hkv / 2;
 }
 
-template <int D>
-hipError_t launch_ds(const AttnArgs& a, float* ws, int n_splits, hipStream_t s) {
+template <int D, bool STEP>
+hipError_t launch_ds(const AttnArgs& a, const StreamStep& st, float* ws, int n_splits, hipStream_t s) {
     const int ng = stream_groups(a);
     const dim3 grid(n_splits, a.B * ng), block((kW + kP) * 64);
     auto finish = [&]() -> hipError_t {
@@ -679,15 +846,15 @@ hipError_t launch_ds(const AttnArgs& a, float* ws, int n_splits, hipStream_t s) 
         if (e != hipSuccess || n_splits == 1) return e;
         return launch_decode_merge(a, ws, n_splits, s);
     };
-#define VVA_DS(H, NG) hipLaunchKernelGGL((decode_stream_kernel<D, H, NG>), grid, block, 0, s, a, ws, n_splits)
+#define VVA_DS(H, NG) hipLaunchKernelGGL((decode_stream_kernel<D, H, NG, STEP>), grid, block, 0, s, a, ws, n_splits, st)
     if constexpr (D == 128) {
         if (ng == 2) { VVA_DS(2, 2); return finish(); }
         if (ng == 4) { VVA_DS(2, 4); return finish(); }
     }
     if (a.Hkv == 1) VVA_DS(1, 1);
     else if (a.Hkv == 2) VVA_DS(2, 1);
-    else if (a.Hkv == 4) VVA_DS(4, 1);
-    else if (a.Hkv == 8) VVA_DS(8, 1);
+    else if (!STEP && a.Hkv == 4) VVA_DS(4, 1);
+    else if (!STEP && a.Hkv == 8) VVA_DS(8, 1);
     else return hipErrorInvalidValue;
 #undef VVA_DS
     return finish();
@@ -735,8 +902,22 @@ int decode_stream_plan(const AttnArgs& a, int n_cu) {
 }
 
 hipError_t launch_decode_stream(const AttnArgs& a, float* ws, int n_splits, hipStream_t s) {
-    if (a.d == 64) return launch_ds<64>(a, ws, n_splits, s);
-    if (a.d == 128) return launch_ds<128>(a, ws, n_splits, s);
+    const StreamStep none{};
+    if (a.d == 64) return launch_ds<64, false>(a, none, ws, n_splits, s);
+    if (a.d == 128) return launch_ds<128, false>(a, none, ws, n_splits, s);
+    return hipErrorInvalidValue;
+}
+
+// Step mode: the kv heads of a workgroup (a head pair, or one or two heads
+// without head groups) are one wave's rotation pairs each, for K and for V.
+bool decode_stream_step_supported(const AttnArgs& a) {
+    if (!decode_stream_supported(a)) return false;
+    return a.Hkv / stream_groups(a) <= 2;
+}
+
+hipError_t launch_decode_stream_step(const AttnArgs& a, const StreamStep& st, float* ws, int n_splits, hipStream_t s) {
+    if (a.d == 64) return launch_ds<64, true>(a, st, ws, n_splits, s);
+    if (a.d == 128) return launch_ds<128, true>(a, st, ws, n_splits, s);
     return hipErrorInvalidValue;
 }
 

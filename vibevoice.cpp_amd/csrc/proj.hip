@@ -110,8 +110,7 @@ __global__ void __launch_bounds__(256) proj_prep_kernel(ProjPrepArgs a) {
     if (a.rope) {
         const float p = (float)a.pos[b * a.pos_stride_b + t];
         for (int i = threadIdx.x; i < a.P; i += 256) {
-            float th = p;
-            for (int k = 0; k < i; ++k) th *= a.theta_scale;
+            const float th = rope_theta(p, a.theta_scale, i, a.P);
             a.rope[(int64_t)n * a.P + i] = make_float2(cosf(th), sinf(th));
         }
     }

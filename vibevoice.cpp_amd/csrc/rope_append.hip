@@ -30,8 +30,7 @@ __global__ void __launch_bounds__(256) rope_append_kernel(RopeAppendArgs a, int 
     __shared__ float cs[128], sn[128];
     const float p = (float)a.pos[b * a.pos_stride_b + t];
     for (int i = threadIdx.x; i < P; i += blockDim.x) {
-        float th = p;
-        for (int k = 0; k < i; ++k) th *= a.theta_scale;
+        const float th = rope_theta(p, a.theta_scale, i, P);
         cs[i] = cosf(th);
         sn[i] = sinf(th);
     }
@@ -134,8 +133,7 @@ __global__ void __launch_bounds__(256) rope_append_vec_kernel(RopeAppendArgs a) 
     __shared__ float cs[kRopeTokens][P], sn[kRopeTokens][P];
     for (int k = threadIdx.x; k < nt * P; k += blockDim.x) {
         const int tl = k / P, i = k - tl * P;
-        float th = (float)a.pos[b * a.pos_stride_b + t0 + tl];
-        for (int j = 0; j < i; ++j) th *= a.theta_scale;
+        const float th = rope_theta((float)a.pos[b * a.pos_stride_b + t0 + tl], a.theta_scale, i, P);
         cs[tl][i] = cosf(th);
         sn[tl][i] = sinf(th);
     }

@@ -1047,6 +1047,49 @@ extern "C" vva_status vva_decode_step(vva_context* ctx, vva_kv* kv, int layer, c
     DeviceGuard g(ctx->device);
     // q_out aliasing q: every split reads q while split 0 writes q_out
     const bool alias = q_out->data == q->data;
+    if (!alias && kv->desc.type == VVA_TYPE_Q8_0 && ctx->attn_path == 0) {
+        // dense Q8_0 caches: the streamed decode kernel in step mode (RoPE of q,
+        // the new row appended by the split that holds it), then its merge
+        AttnArgs c{};
+        for (int b = 0; b < B; ++b) {
+            c.k[b] = a.kc[b];
+            c.v[b] = a.vc[b];
+            c.past[b] = a.past[b];
+            c.L[b] = a.past[b] + 1;
+        }
+        c.q = a.q; c.q_type = a.q_type;
+        c.q_nb_h = q->nb[1]; c.q_nb_t = q->nb[2]; c.q_nb_b = q->nb[3];
+        c.k_nb_tok = c.v_nb_tok = kv->row_bytes;
+        c.k_nb_head = c.v_nb_head = kv->head_bytes;
+        c.k_type = c.v_type = VVA_TYPE_Q8_0;
+        c.mask_mode = kMaskCausal;
+        c.scale = scale;
+        c.out = a.out; c.o_nb_h = out->nb[1]; c.o_nb_t = out->nb[2]; c.o_nb_b = out->nb[3];
+        c.d = (int)d; c.Hq = (int)Hq; c.Hkv = (int)Hkv; c.T = 1; c.B = (int)B;
+        // q_out rows are written 16 bytes at a time
+        const bool qo_aligned = (uintptr_t)q_out->data % 16 == 0 && q_out->nb[1] % 16 == 0 && q_out->nb[3] % 16 == 0 &&
+                                (int64_t)q_out->nb[0] == type_elem_bytes(q_out->type);
+        if (qo_aligned && decode_stream_step_supported(c) && float_type(k->type) && float_type(v->type)) {
+            StreamStep sp{};
+            sp.k = a.k; sp.v = a.v; sp.k_type = a.k_type; sp.v_type = a.v_type;
+            sp.k_nb_h = a.k_nb_h; sp.k_nb_b = a.k_nb_b; sp.v_nb_h = a.v_nb_h; sp.v_nb_b = a.v_nb_b;
+            sp.pos = a.pos; sp.pos_stride_b = a.pos_stride_b;
+            sp.theta_scale = a.theta_scale;
+            sp.q_out = a.q_out; sp.q_out_type = a.q_out_type; sp.qo_nb_h = a.qo_nb_h; sp.qo_nb_b = a.qo_nb_b;
+            const int wgs = ctx->sched_decode_wgs > 0 ? ctx->sched_decode_wgs : ctx->n_cu;
+            int n_splits = decode_stream_plan(c, wgs);
+            if (ctx->sched_decode_splits > 0) n_splits = ctx->sched_decode_splits;
+            float* ws = nullptr;
+            if (n_splits > 1) {
+                if ((st = ensure_ws(ctx, (size_t)n_splits * B * Hq * (d + 2) * sizeof(float))) != VVA_OK) return st;
+                ws = ctx->ws;
+            }
+            hipError_t e = launch_decode_stream_step(c, sp, ws, n_splits, ctx->stream);
+            if (e != hipSuccess) return hip_fail(ctx, e, "decode_step launch");
+            ctx->last_splits = n_splits;
+            return VVA_OK;
+        }
+    }
     if (alias || !decode_step_supported(a)) {
         // the unfused path: RoPE + append, then attention (other cache types, longer windows)
         if ((st = vva_rope_append(ctx, kv, layer, q, k, v, pos, seq_ids, freq_base, q_out)) != VVA_OK) return st;

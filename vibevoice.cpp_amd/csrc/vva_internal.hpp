@@ -162,6 +162,21 @@ hipError_t launch_decode_merge(const AttnArgs& a, const float* ws, int n_splits,
 // tiles of each split are DMA'd into a 4-stage LDS ring.  Partials use the
 // layout of launch_decode and are combined by launch_decode_merge.
 bool decode_stream_supported(const AttnArgs& a);
+// vva_decode_step on dense Q8_0 caches: AttnArgs::q is the raw q (not yet
+// RoPE'd) and L_b = len(seq_b) + 1; the streamed decode kernel applies the
+// RoPE to q itself (writing q_out), and the split that holds key len(seq_b)
+// appends the new row: RoPE(k) and v quantized to Q8_0 blocks, to the cache
+// and into its own tile.
+struct StreamStep {
+    const char* k; const char* v;
+    int k_type, v_type;
+    int64_t k_nb_h, k_nb_b, v_nb_h, v_nb_b;
+    const int32_t* pos; int64_t pos_stride_b;
+    float theta_scale;
+    char* q_out; int q_out_type; int64_t qo_nb_h, qo_nb_b;
+};
+bool decode_stream_step_supported(const AttnArgs& a);
+hipError_t launch_decode_stream_step(const AttnArgs& a, const StreamStep& st, float* ws, int n_splits, hipStream_t s);
 // Key splits for one call (workgroups per sequence and head group); split s
 // takes the sequence's tiles s, s + n_splits, s + 2 n_splits, ...
 int decode_stream_plan(const AttnArgs& a, int n_cu);
@@ -215,6 +230,17 @@ __device__ __forceinline__ void prefetch_kernargs() {
                  : "=&s"(x)
                  : "s"(p), "n"((BYTES + 63) / 64)
                  : "memory");
+}
+
+// Angle of rotation pair i at position p: p * ts * ts * ... with i products,
+// each rounded to fp32 (ggml's rope-cache recurrence).  Every lane runs the
+// same n - 1 steps and keeps its i-th product, so a wave does not run its
+// lanes' different trip counts one after another; the products, and so the
+// result, are those of the plain loop.
+__device__ __forceinline__ float rope_theta(float p, float ts, int i, int n) {
+    float th = p;
+    for (int k = 0; k < n - 1; ++k) th = k < i ? th * ts : th;
+    return th;
 }
 
 __device__ __forceinline__ float f16_to_f32(uint16_t h) {
