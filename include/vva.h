@@ -188,11 +188,14 @@ VVA_API vva_status vva_attn(vva_context* ctx, const vva_kv* kv, int layer,
  * sequence (the decode loops, src/vibevoice_tts.cpp:862-880,
  * src/vibevoice_asr.cpp:760-800), with the same arguments and results:
  * q, k, v ne = [d, H, 1, B]; pos I32 ne = [1] or [1, B]; q_out receives
- * RoPE(q); out F32 ne = [d, Hq, 1, B].  F16 / BF16 caches with windows up
- * to 8192 keys run as one kernel (RoPE, append, split attention and the
- * merge of its splits) unless q_out aliases q; other cases run the two
- * calls.  Does not advance len.  No counterpart of its own in the reference: it fuses three of its
- * ops for the latency-bound short windows. */
+ * RoPE(q); out F32 ne = [d, Hq, 1, B].  Unless q_out aliases q: F16 / BF16
+ * caches with windows up to 8192 keys run as one kernel (RoPE, append,
+ * split attention and the merge of its splits); dense Q8_0 caches run the
+ * streamed decode kernel in step mode (RoPE of q, the new row appended by
+ * the split that holds it) and its merge kernel, with q_out rows 16-byte
+ * aligned.  Other cases run the two calls.  Results equal the two calls'
+ * (bit for bit on Q8_0 caches).  Does not advance len.  No counterpart of
+ * its own in the reference: it fuses three of its ops per decode step. */
 VVA_API vva_status vva_decode_step(vva_context* ctx, vva_kv* kv, int layer,
                                    const vva_tensor* q, const vva_tensor* k, const vva_tensor* v,
                                    const vva_tensor* pos, const int32_t* seq_ids, float freq_base,
