@@ -30,7 +30,8 @@ def fill_cache(kv: vva.KVCache, lens, seed: int, layers=None, scale: float = 1.0
         for s, n in enumerate(lens):
             k = (rng.standard_normal((n, kv.n_kv_heads, kv.head_dim)) * scale).astype(np.float32)
             v = (rng.standard_normal((n, kv.n_kv_heads, kv.head_dim)) * scale).astype(np.float32)
-            kv.upload(layer, s, 0, k, v)
+            if n > 0:                                     # an empty upload is an argument error
+                kv.upload(layer, s, 0, k, v)
     for s, n in enumerate(lens):
         kv.set_len(s, n)
 

@@ -89,6 +89,49 @@ def test_decode_step_matches_unfused_and_oracle(ctx, torch_gpu, d, Hq, Hkv, t, l
     u.free()
 
 
+@pytest.mark.parametrize("lens,seq_ids", [([0, 17], None), ([0], None), ([5000, 33], [1, 0])])
+def test_decode_step_q8_0_first_token_and_seq_ids(ctx, torch_gpu, lens, seq_ids):
+    """Q8_0 step mode at its edges: an empty cache (the first token is the
+    whole window), ragged streams, and sequences addressed through seq_ids
+    in another order.  Bit for bit against the unfused pair."""
+    torch = torch_gpu
+    d, Hq, Hkv = 128, 28, 4
+    B = len(lens)
+    n_seq = max(B, 2)
+    ids = seq_ids if seq_ids is not None else list(range(B))
+    store = [0] * n_seq
+    for b, s_ in enumerate(ids):
+        store[s_] = lens[b]
+    a = vva.KVCache(ctx, 1, Hkv, d, max(lens) + 4, n_seq, vva.Q8_0)
+    u = vva.KVCache(ctx, 1, Hkv, d, max(lens) + 4, n_seq, vva.Q8_0)
+    fill_cache(a, store, seed=77)
+    fill_cache(u, store, seed=77)
+    rng = np.random.default_rng(78)
+    q = to_gpu(torch, rng.standard_normal((B, 1, Hq, d)), vva.F32)
+    k = to_gpu(torch, rng.standard_normal((B, 1, Hkv, d)), vva.F32)
+    v = to_gpu(torch, rng.standard_normal((B, 1, Hkv, d)), vva.F32)
+    pos = torch.tensor([[n] for n in lens], dtype=torch.int32, device="cuda")
+    qa = torch.empty((B, 1, Hq, d), dtype=torch.float32, device="cuda")
+    qu = torch.empty_like(qa)
+    oa = torch.full((B, 1, Hq, d), float("nan"), dtype=torch.float32, device="cuda")
+    ou = torch.full_like(oa, float("nan"))
+    ctx.decode_step(a, 0, q, k, v, pos, qa, oa, d ** -0.5, seq_ids=seq_ids)
+    ctx.rope_append(u, 0, q, k, v, pos, qu, seq_ids=seq_ids)
+    ctx.attn(u, 0, qu, ou, d ** -0.5, seq_ids=seq_ids)
+    torch.cuda.synchronize()
+    assert torch.equal(qa, qu)
+    assert torch.equal(oa, ou)
+    for b, s_ in enumerate(ids):
+        ka, va_ = a.download(0, s_, lens[b] + 1)
+        ku, vu = u.download(0, s_, lens[b] + 1)
+        np.testing.assert_array_equal(ka, ku)
+        np.testing.assert_array_equal(va_, vu)
+    ref = oracle_attn(as_f32(torch, qa), a, 0, ids, [n + 1 for n in lens], 1, d ** -0.5)
+    assert_close(as_f32(torch, oa), ref, *TOL, what="Q8_0 step edges")
+    a.free()
+    u.free()
+
+
 def test_decode_step_graph_replays_match_eager(ctx, torch_gpu):
     """One captured step replayed three times, with eager work and
     synchronizations between the replays: every replay's output equals the
