@@ -308,6 +308,51 @@ def test_prefill_key_splits_do_not_change_result(ctx, torch_gpu):
     kv.free()
 
 
+@pytest.mark.parametrize("splits,masked", [(2, False), (3, False), (4, False), (4, True)])
+def test_prefill_in_launch_merge_equals_merge_kernel(ctx, torch_gpu, splits, masked):
+    """With at most four key splits per row tile, the last split of a row
+    tile to finish merges the partials inside the prefill launch (a ticket
+    per row tile); vva_attn_noalloc keeps the separate merge kernel.  Both
+    combine the same partials in split order with the same arithmetic, so the
+    outputs are equal bit for bit: two sequences of different lengths, causal
+    or with an explicit mask that hides whole splits and whole rows.  Two
+    calls in a row check that the tickets are back at zero after each."""
+    torch = torch_gpu
+    d, Hq, Hkv, T = 128, 28, 4, 256
+    pasts = [3000, 1700]
+    L = [p + T for p in pasts]
+    print(f"in-launch merge splits={splits} masked={masked}", flush=True)
+    kv = vva.KVCache(ctx, 1, Hkv, d, max(L), 2, vva.F16)
+    fill_cache(kv, L, seed=40 + splits)
+    for s, p in enumerate(pasts):
+        kv.set_len(s, p)
+    q = to_gpu(torch, np.random.default_rng(41).standard_normal((2, T, Hq, d)), vva.F16)
+    mt = None
+    if masked:
+        Lm = max(L)
+        m = np.where(np.arange(Lm)[None, :] > pasts[0] + np.arange(T)[:, None], -np.inf, 0.0).astype(np.float32)
+        m[:, 200:2400] = -np.inf                      # whole splits with nothing visible
+        m[7, :] = -np.inf                             # a row with no visible key -> 0
+        mt = torch.from_numpy(vvo.f16_bits(m)[None].view(np.float16)).cuda()
+    outs = []
+    with ctx.schedule(prefill_splits=splits):
+        for fn in (ctx.attn, ctx.attn, ctx.attn_noalloc):
+            out = torch.full((2, T, Hq, d), float("nan"), dtype=torch.float32, device="cuda")
+            fn(kv, 0, q, out, d ** -0.5, mask=mt)
+            torch.cuda.synchronize()
+            assert ctx.last_decode_splits() == splits
+            outs.append(as_f32(torch, out))
+    assert np.isfinite(outs[0]).all()
+    assert np.array_equal(outs[0], outs[1]), "second in-launch call differs"
+    assert np.array_equal(outs[0], outs[2]), np.abs(outs[0] - outs[2]).max()
+    if masked:
+        assert not outs[0][:, 7].any()
+    elif splits == 2:
+        ref = oracle_attn(as_f32(torch, q), kv, 0, [0, 1], L, T, d ** -0.5)
+        assert_close(outs[0], ref, *TOL, what=f"{splits} key splits, merged in the launch")
+    kv.free()
+
+
 def test_prefill_key_splits_explicit_mask(ctx, torch_gpu):
     torch = torch_gpu
     d, Hq, Hkv, T, past = 64, 14, 2, 40, 3000

@@ -43,16 +43,6 @@ constexpr int kStepWaves = 4;
 constexpr int kKPW = 32 * kStepWaves;    // keys per workgroup
 constexpr int kMaxG = 8;                 // query heads per kv head
 
-// 64-bit agent-scope stores and loads of float pairs
-__device__ __forceinline__ void store_coherent2(float* p, float x, float y) {
-    const uint64_t v = (uint64_t)__float_as_uint(x) | ((uint64_t)__float_as_uint(y) << 32);
-    __hip_atomic_store((uint64_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float2 load_coherent2(const float* p) {
-    const uint64_t v = __hip_atomic_load((uint64_t*)const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return make_float2(__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32)));
-}
-
 // Barrier for LDS hand-offs only: unlike __syncthreads it does not wait for
 // the wave's outstanding global loads and stores.
 __device__ __forceinline__ void lds_barrier() {

@@ -137,7 +137,8 @@ __device__ __forceinline__ const lds_char* lds_at(uint32_t addr) { return (const
 
 // EXPL: explicit F16 mask (otherwise implicit causal / length masking only).
 template <int D, int KT, bool EXPL>
-__global__ void __launch_bounds__(kWaves * 64) prefill_kernel(AttnArgs a, float* __restrict__ ws, PrefillPlan plan) {
+__global__ void __launch_bounds__(kWaves * 64) prefill_kernel(AttnArgs a, float* __restrict__ ws, unsigned* tickets,
+                                                               PrefillPlan plan) {
     prefetch_kernargs<sizeof(AttnArgs)>();
     using F = Frag<KT>;
     using QF = typename F::type;
@@ -507,31 +508,152 @@ __global__ void __launch_bounds__(kWaves * 64) prefill_kernel(AttnArgs a, float*
     // partial instead: O unnormalized, and (exponent base, row sum)
     const int64_t nr_all = (int64_t)a.B * a.T * a.Hq;
     const float lt = lsum + __shfl_xor(lsum, 32, 64);
-    if (!qok) return;
     const int t = row / g, h = kvh * g + row % g;
-    float* orow;
-    float inv = 1.0f;
+    float* const orow = (float*)((char*)a.out + b * a.o_nb_b + (int64_t)t * a.o_nb_t + (int64_t)h * a.o_nb_h);
     if (n_ks == 1) {
-        inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-        orow = (float*)((char*)a.out + b * a.o_nb_b + t * a.o_nb_t + h * a.o_nb_h);
-    } else {
-        const int64_t rg = ((int64_t)b * a.T + t) * a.Hq + h;
-        orow = ws + ((int64_t)ks * nr_all + rg) * D;
-        if (half == 0) {
-            // p = 2^(x - base): base = m, or 0 while m = -inf; an empty row is -inf
-            const float base = m != -INFINITY ? m : (lt > 0.0f ? 0.0f : -INFINITY);
-            *(float2*)(ws + nr_all * D * plan.max_ks + ((int64_t)ks * nr_all + rg) * 2) = make_float2(base, lt);
+        if (!qok) return;
+        const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const int d = dt * 32 + 8 * q4 + 4 * half;
+                *(float4*)(orow + d) = make_float4(o[dt][4 * q4] * inv, o[dt][4 * q4 + 1] * inv,
+                                                   o[dt][4 * q4 + 2] * inv, o[dt][4 * q4 + 3] * inv);
+            }
+        return;
+    }
+    // p = 2^(x - base): base = m, or 0 while m = -inf; an empty row is -inf
+    const float base = m != -INFINITY ? m : (lt > 0.0f ? 0.0f : -INFINITY);
+    const int64_t rg = ((int64_t)b * a.T + t) * a.Hq + h;
+    float* const wml = ws + nr_all * D * plan.max_ks;            // (base, row sum) of [split][row]
+    if (!plan.in_launch) {
+        // prefill_merge_kernel combines the partials
+        if (!qok) return;
+        float* prow = ws + ((int64_t)ks * nr_all + rg) * D;
+        if (half == 0) *(float2*)(wml + ((int64_t)ks * nr_all + rg) * 2) = make_float2(base, lt);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const int d = dt * 32 + 8 * q4 + 4 * half;
+                *(float4*)(prow + d) = make_float4(o[dt][4 * q4], o[dt][4 * q4 + 1], o[dt][4 * q4 + 2], o[dt][4 * q4 + 3]);
+            }
+        return;
+    }
+    // In-launch merge (n_ks <= kMaxInLaunchSplits).  Each split's partial is
+    // one block of the workspace, [wave][16-dim group][lane] float4s then
+    // [wave][lane] (base, row sum), so that every store and load instruction
+    // moves whole contiguous lines; they go out with agent-scope (sc1)
+    // buffer stores, coherent across the XCDs without an L2 write-back.  The
+    // workgroup then takes its row tile's ticket; the last of the n_ks splits
+    // combines every partial with its own registers, in split order and with
+    // the arithmetic of prefill_merge_kernel (the same result bit for bit),
+    // and resets the ticket for the next call.
+    constexpr int kSc1 = 16;                                     // cache policy: agent scope
+    constexpr int WAVE_O = DT * 16 * 64 * 4;                     // bytes of a wave's O block
+    constexpr int PIECE = kWaves * (WAVE_O + 64 * 8);            // bytes of one split's partial
+    const int64_t tile_piece = (((int64_t)b * a.Hkv + kvh) * n_rt + rt) * plan.max_ks;
+    auto piece_rsrc = [&](int k) {
+        return __builtin_amdgcn_make_buffer_rsrc((char*)ws + (tile_piece + k) * PIECE, 0, PIECE, 0x00020000);
+    };
+    const int o_off = w * WAVE_O + lane * 16;                   // + 1024 per 16-dim group
+    const int ml_off = kWaves * WAVE_O + w * 512 + lane * 8;
+    {
+        const __amdgpu_buffer_rsrc_t rs = piece_rsrc(ks);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const u32x4 v = {__float_as_uint(o[dt][4 * q4]), __float_as_uint(o[dt][4 * q4 + 1]),
+                                 __float_as_uint(o[dt][4 * q4 + 2]), __float_as_uint(o[dt][4 * q4 + 3])};
+                __builtin_amdgcn_raw_buffer_store_b128(v, rs, o_off + (dt * 4 + q4) * 1024, 0, kSc1);
+            }
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2{__float_as_uint(base), __float_as_uint(lt)}, rs, ml_off, 0, kSc1);
+    }
+    // every partial store of the workgroup has completed before its ticket;
+    // the ring's LDS is idle (every wave passed the last tile barrier)
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    int* const last = (int*)lds;
+    if (tid == 0) {
+        unsigned* tk = tickets + ((int64_t)b * a.Hkv + kvh) * n_rt + rt;
+        const unsigned old = __hip_atomic_fetch_add(tk, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *last = old == (unsigned)(n_ks - 1);
+        if (*last) __hip_atomic_store(tk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!*last || !qok) return;
+    // every other split's (base, row sum) and the first other split's O go
+    // out in one batch (one memory round trip at two splits)
+    const int k0 = ks == 0 ? 1 : 0;
+    float2 mlk[kMaxInLaunchSplits];
+#pragma unroll
+    for (int k = 0; k < kMaxInLaunchSplits; ++k) {
+        if (k >= n_ks) continue;
+        if (k == ks) {
+            mlk[k] = make_float2(base, lt);
+        } else {
+            const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(piece_rsrc(k), ml_off, 0, kSc1);
+            mlk[k] = make_float2(__uint_as_float(v.x), __uint_as_float(v.y));
         }
     }
+    u32x4 ov[DT * 4];
+    {
+        const __amdgpu_buffer_rsrc_t rs = piece_rsrc(k0);
+#pragma unroll
+        for (int i = 0; i < DT * 4; ++i) ov[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, o_off + i * 1024, 0, kSc1);
+        // keep the loads here, in the batch (not sunk into the branch below)
+#pragma unroll
+        for (int i = 0; i < DT * 4; ++i) asm volatile("" : "+v"(ov[i]));
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < kMaxInLaunchSplits; ++k)
+        if (k < n_ks) M = fmaxf(M, mlk[k].x);
+    float num[DT][16];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) num[dt][r] = 0.0f;
+    float den = 0.0f;
+    if (M != -INFINITY) {
+#pragma unroll
+        for (int k = 0; k < kMaxInLaunchSplits; ++k) {
+            if (k >= n_ks) continue;
+            const float f = __builtin_amdgcn_exp2f(mlk[k].x - M);       // 0 for an empty split
+            if (k == ks) {
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) num[dt][r] = fmaf(o[dt][r], f, num[dt][r]);
+            } else {
+                if (k != k0) {
+                    const __amdgpu_buffer_rsrc_t rs = piece_rsrc(k);
+#pragma unroll
+                    for (int i = 0; i < DT * 4; ++i)
+                        ov[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, o_off + i * 1024, 0, kSc1);
+                }
+#pragma unroll
+                for (int i = 0; i < DT * 4; ++i)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        num[i / 4][4 * (i % 4) + e] = fmaf(__uint_as_float(ov[i][e]), f, num[i / 4][4 * (i % 4) + e]);
+            }
+            den = fmaf(mlk[k].y, f, den);
+        }
+    }
+    const float inv = den > 0.0f ? 1.0f / den : 0.0f;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4) {
             const int d = dt * 32 + 8 * q4 + 4 * half;
-            *(float4*)(orow + d) = make_float4(o[dt][4 * q4] * inv, o[dt][4 * q4 + 1] * inv,
-                                               o[dt][4 * q4 + 2] * inv, o[dt][4 * q4 + 3] * inv);
+            *(float4*)(orow + d) = make_float4(num[dt][4 * q4] * inv, num[dt][4 * q4 + 1] * inv,
+                                               num[dt][4 * q4 + 2] * inv, num[dt][4 * q4 + 3] * inv);
         }
 }
+
 
 // Combines the key splits of every split query row: one thread per (row,
 // 4 dims), log-sum-exp over the row tile's partials (exp2 domain),
@@ -572,15 +694,15 @@ __global__ void __launch_bounds__(256) prefill_merge_kernel(AttnArgs a, const fl
 }
 
 template <int D, int KT>
-hipError_t launch_pf(const AttnArgs& a, float* ws, const PrefillPlan& p, hipStream_t s) {
+hipError_t launch_pf(const AttnArgs& a, float* ws, unsigned* tickets, const PrefillPlan& p, hipStream_t s) {
     const int n_rt = (a.T * (a.Hq / a.Hkv) + kRowsWG - 1) / kRowsWG;
     dim3 grid(plan_pieces(p, n_rt) * a.Hkv, 1, a.B);
     if (a.mask_mode == kMaskExplicit)
-        hipLaunchKernelGGL((prefill_kernel<D, KT, true>), grid, dim3(kWaves * 64), 0, s, a, ws, p);
+        hipLaunchKernelGGL((prefill_kernel<D, KT, true>), grid, dim3(kWaves * 64), 0, s, a, ws, tickets, p);
     else
-        hipLaunchKernelGGL((prefill_kernel<D, KT, false>), grid, dim3(kWaves * 64), 0, s, a, ws, p);
+        hipLaunchKernelGGL((prefill_kernel<D, KT, false>), grid, dim3(kWaves * 64), 0, s, a, ws, tickets, p);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || p.max_ks == 1) return e;
+    if (e != hipSuccess || p.max_ks == 1 || p.in_launch) return e;
     const int64_t threads = (int64_t)a.B * a.T * a.Hq * (D / 4);
     hipLaunchKernelGGL(prefill_merge_kernel<D>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, a, ws, p);
     return hipGetLastError();
@@ -664,15 +786,23 @@ bool prefill_supported(const AttnArgs& a) {
 // hardware's dispatch: workgroups go out in launch order (heaviest row tile
 // first, kv heads innermost), each to the CU that frees first, costing its
 // key tiles plus a fixed prologue (Q rows loaded, the first tiles staged);
-// a split plan adds the partials' round trip and the merge launch.  Causal
+// a split plan adds its merge: in the launch (up to kMaxInLaunchSplits
+// splits), the last split's epilogue (partial stores completed, ticket, the
+// other partials loaded: ~4.7 us at two splits, ~1.5 us more per further
+// split, measured at the 1.5B and 7B shapes); otherwise the merge kernel's
+// launch and its exposed traffic.  Causal
 // row tiles differ in length, so a plan with more, smaller pieces over
 // several rounds can finish sooner than one round of equal-count splits.
 // Calls with many more row tiles than CUs balance unsplit.
-PrefillPlan prefill_plan(const AttnArgs& a, int n_cu, int forced, size_t ws_cap) {
+PrefillPlan prefill_plan(const AttnArgs& a, int n_cu, int forced, size_t ws_cap, bool allow_in_launch) {
     const int n_rt = (a.T * (a.Hq / a.Hkv) + kRowsWG - 1) / kRowsWG;
     const bool causal = a.mask_mode == kMaskCausal;
-    if (forced > 0) return PrefillPlan{forced, 0, forced, forced};
-    const PrefillPlan none{1, 0, 0, 1};
+    auto with_merge = [&](PrefillPlan p) {
+        p.in_launch = allow_in_launch && prefill_in_launch_ok(a, p);
+        return p;
+    };
+    if (forced > 0) return with_merge(PrefillPlan{forced, 0, forced, forced, 0});
+    const PrefillPlan none{1, 0, 0, 1, 0};
     const int per = a.Hkv * a.B;                 // workgroups per piece index
     const int budget = n_cu / per;               // pieces per (kv head, sequence) in one round
     if (n_rt >= 4 * budget) return none;
@@ -725,12 +855,15 @@ PrefillPlan prefill_plan(const AttnArgs& a, int n_cu, int forced, size_t ws_cap)
         const int R_fit = max(0, (n_rt * n - budget + n - 2) / (n - 1));
         for (int R : {R_fit, 0}) {
             if (R >= n_rt || (R == 0 && R_fit > 0 && n > 8)) continue;
-            const PrefillPlan p{n, R, 0, n};
+            const PrefillPlan p = with_merge(PrefillPlan{n, R, 0, n, 0});
             if (prefill_ws_bytes(a, p) > ws_cap) continue;
             const double split_rows = (double)(n_rt - R) * kRowsWG * per;
-            // the partials are written while other workgroups compute; the merge
-            // kernel's reads of the n partials and its output write are not hidden
-            const double t = makespan(p) + merge_launch + split_rows * (n + 1) * (a.d + 2) * 4.0 / bytes_per_unit;
+            // merge kernel: the partials are written while other workgroups
+            // compute; its reads of the n partials and its output write are not
+            // hidden
+            const double merge = p.in_launch ? (4.7 + 1.5 * (n - 2)) / unit_us
+                                             : merge_launch + split_rows * (n + 1) * (a.d + 2) * 4.0 / bytes_per_unit;
+            const double t = makespan(p) + merge;
             if (t < best_t * 0.95) {             // a split must pay for itself
                 best_t = t;
                 best = p;
@@ -742,16 +875,26 @@ PrefillPlan prefill_plan(const AttnArgs& a, int n_cu, int forced, size_t ws_cap)
 }
 
 size_t prefill_ws_bytes(const AttnArgs& a, const PrefillPlan& p) {
-    return p.max_ks <= 1 ? 0 : (size_t)p.max_ks * a.B * a.T * a.Hq * (a.d + 2) * sizeof(float);
+    if (p.max_ks <= 1) return 0;
+    if (!p.in_launch) return (size_t)p.max_ks * a.B * a.T * a.Hq * (a.d + 2) * sizeof(float);
+    // the in-launch layout: one block of kRowsWG rows x (d + 4) floats per piece
+    const int n_rt = (a.T * (a.Hq / a.Hkv) + kRowsWG - 1) / kRowsWG;
+    return (size_t)p.max_ks * a.B * a.Hkv * n_rt * kRowsWG * (a.d + 4) * sizeof(float);
 }
 
-hipError_t launch_prefill(const AttnArgs& a, float* ws, const PrefillPlan& p, hipStream_t s) {
+bool prefill_in_launch_ok(const AttnArgs& a, const PrefillPlan& p) {
+    const int n_rt = (a.T * (a.Hq / a.Hkv) + kRowsWG - 1) / kRowsWG;
+    return p.max_ks > 1 && p.max_ks <= kMaxInLaunchSplits && (int64_t)a.B * a.Hkv * n_rt <= kMaxPrefillTickets;
+}
+
+hipError_t launch_prefill(const AttnArgs& a, float* ws, unsigned* tickets, const PrefillPlan& p, hipStream_t s) {
+    if (p.in_launch && (!tickets || !prefill_in_launch_ok(a, p))) return hipErrorInvalidValue;
     if (a.d == 64) {
-        return a.k_type == VVA_TYPE_F16 ? launch_pf<64, VVA_TYPE_F16>(a, ws, p, s)
-                                        : launch_pf<64, VVA_TYPE_BF16>(a, ws, p, s);
+        return a.k_type == VVA_TYPE_F16 ? launch_pf<64, VVA_TYPE_F16>(a, ws, tickets, p, s)
+                                        : launch_pf<64, VVA_TYPE_BF16>(a, ws, tickets, p, s);
     }
-    return a.k_type == VVA_TYPE_F16 ? launch_pf<128, VVA_TYPE_F16>(a, ws, p, s)
-                                    : launch_pf<128, VVA_TYPE_BF16>(a, ws, p, s);
+    return a.k_type == VVA_TYPE_F16 ? launch_pf<128, VVA_TYPE_F16>(a, ws, tickets, p, s)
+                                    : launch_pf<128, VVA_TYPE_BF16>(a, ws, tickets, p, s);
 }
 
 }  // namespace vva

@@ -38,7 +38,9 @@ struct vva_context {
     // allocated until vva_destroy.
     std::vector<float*> ws_retired;
     float* scratch = nullptr;            // this device's `scratch` (vva_attn_noalloc)
-    unsigned* tickets = nullptr;         // vva_decode_step's merge tickets, zeroed once
+    // merge tickets, zeroed once: vva_decode_step's [kMaxStepTickets], then the
+    // prefill's in-launch merge [kMaxPrefillTickets]
+    unsigned* tickets = nullptr;
     std::set<vva_kv*> caches;            // released by vva_destroy if still alive
     // the last prefill plan and the call shape it was made for: a layer stack
     // repeats one shape layer after layer
@@ -227,15 +229,16 @@ vva_status run_attention(vva_context* ctx, AttnArgs& a, bool fixed = false) {
     const bool convert = a.k_type == a.v_type &&
                          (a.k_type == VVA_TYPE_Q8_0 || (a.k_type == VVA_TYPE_F32 && ctx->use_flash_attn));
     // prefill plan of call shape c, reused while the shape repeats
+    // (the merge in the launch needs the context's tickets: not vva_attn_noalloc)
     auto plan_for = [&](const AttnArgs& c, size_t cap) {
         std::vector<int64_t> key = {c.d, c.Hq, c.Hkv, c.T, c.B, c.mask_mode, ctx->n_cu, ctx->sched_prefill_splits,
-                                    (int64_t)cap};
+                                    (int64_t)cap, (int64_t)fixed};
         for (int b = 0; b < c.B; ++b) {
             key.push_back(c.L[b]);
             key.push_back(c.past[b]);
         }
         if (key != ctx->plan_key) {
-            ctx->plan = prefill_plan(c, ctx->n_cu, ctx->sched_prefill_splits, cap);
+            ctx->plan = prefill_plan(c, ctx->n_cu, ctx->sched_prefill_splits, cap, !fixed);
             ctx->plan_key = std::move(key);
         }
         return ctx->plan;
@@ -262,7 +265,8 @@ vva_status run_attention(vva_context* ctx, AttnArgs& a, bool fixed = false) {
                 off += (size_t)2 * a.L[b] * a.Hkv * a.d * 2;
             }
             e = launch_window_to_f16(a, wbase, ctx->stream);
-            if (e == hipSuccess) e = launch_prefill(c, (float*)(wbase + wb), plan, ctx->stream);
+            if (e == hipSuccess)
+                e = launch_prefill(c, (float*)(wbase + wb), ctx->tickets + kMaxStepTickets, plan, ctx->stream);
             if (e != hipSuccess) return hip_fail(ctx, e, "prefill launch");
             ctx->last_splits = plan.max_ks;
             return VVA_OK;
@@ -274,7 +278,7 @@ vva_status run_attention(vva_context* ctx, AttnArgs& a, bool fixed = false) {
             vva_status st = get_ws(ctx, fixed, prefill_ws_bytes(a, plan), &ws);
             if (st != VVA_OK) return st;
         }
-        e = launch_prefill(a, ws, plan, ctx->stream);
+        e = launch_prefill(a, ws, ctx->tickets + kMaxStepTickets, plan, ctx->stream);
         if (e != hipSuccess) return hip_fail(ctx, e, "prefill launch");
         ctx->last_splits = plan.max_ks;
         return VVA_OK;
@@ -338,8 +342,9 @@ extern "C" vva_status vva_create(int device, void* stream, vva_context** out) {
     ctx->stream = (hipStream_t)stream;
     ctx->scratch = scr;
     ctx->err.reserve(512);               // error messages (< 512 bytes) then never allocate
-    e = hipMalloc(&ctx->tickets, sizeof(unsigned) * kMaxStepTickets);
-    if (e == hipSuccess) e = hipMemset(ctx->tickets, 0, sizeof(unsigned) * kMaxStepTickets);
+    constexpr size_t ticket_bytes = sizeof(unsigned) * (kMaxStepTickets + kMaxPrefillTickets);
+    e = hipMalloc(&ctx->tickets, ticket_bytes);
+    if (e == hipSuccess) e = hipMemset(ctx->tickets, 0, ticket_bytes);
     if (e != hipSuccess) {
         if (ctx->tickets) (void)hipFree(ctx->tickets);
         delete ctx;

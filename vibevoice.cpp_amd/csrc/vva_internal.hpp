@@ -184,16 +184,26 @@ hipError_t launch_decode_stream(const AttnArgs& a, float* ws, int n_splits, hipS
 // MFMA flash prefill (F16 / BF16 caches).  Row tiles (256 query rows of
 // one kv group) rt >= R have their key range split over n workgroups (all
 // row tiles over `forced` when forced > 0); split rows leave partials in ws
-// (prefill_ws_bytes) that a second kernel merges.
+// (prefill_ws_bytes) that the last split of the row tile merges inside the
+// launch (in_launch, at most kMaxInLaunchSplits splits) or a second kernel
+// merges.
 struct PrefillPlan {
     int n;             // splits of a heavy row tile (1: none)
     int R;             // first heavy row tile
     int forced;        // > 0: this many splits for every row tile
     int max_ks;        // largest split count of the call (1: no partials)
+    int in_launch;     // 1: the last split of a row tile merges (tickets), no merge kernel
 };
-hipError_t launch_prefill(const AttnArgs& a, float* ws, const PrefillPlan& p, hipStream_t s);
+// Row-tile tickets of the in-launch merge: B * Hkv * row tiles of them,
+// zero between calls (the last split of a row tile resets its ticket).
+constexpr int kMaxPrefillTickets = 16384;
+constexpr int kMaxInLaunchSplits = 4;
+// whether plan p may merge in the launch (split count, ticket count)
+bool prefill_in_launch_ok(const AttnArgs& a, const PrefillPlan& p);
+hipError_t launch_prefill(const AttnArgs& a, float* ws, unsigned* tickets, const PrefillPlan& p, hipStream_t s);
 bool prefill_supported(const AttnArgs& a);
-PrefillPlan prefill_plan(const AttnArgs& a, int n_cu, int forced, size_t ws_cap);
+// allow_in_launch: the caller passes the tickets (otherwise the merge kernel)
+PrefillPlan prefill_plan(const AttnArgs& a, int n_cu, int forced, size_t ws_cap, bool allow_in_launch);
 size_t prefill_ws_bytes(const AttnArgs& a, const PrefillPlan& p);
 // Prep + GEMM of a linear layer; ws holds proj_ws_bytes(N, K, P) bytes.
 size_t proj_ws_bytes(int N, int K, int P);
@@ -241,6 +251,18 @@ __device__ __forceinline__ float rope_theta(float p, float ts, int i, int n) {
     float th = p;
     for (int k = 0; k < n - 1; ++k) th = k < i ? th * ts : th;
     return th;
+}
+
+// 64-bit agent-scope stores and loads of float pairs: coherent across the
+// XCDs' L2 caches without an L2 write-back or invalidate (split partials
+// handed from one workgroup to another within a launch)
+__device__ __forceinline__ void store_coherent2(float* p, float x, float y) {
+    const uint64_t v = (uint64_t)__float_as_uint(x) | ((uint64_t)__float_as_uint(y) << 32);
+    __hip_atomic_store((uint64_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float2 load_coherent2(const float* p) {
+    const uint64_t v = __hip_atomic_load((uint64_t*)const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return make_float2(__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32)));
 }
 
 __device__ __forceinline__ float f16_to_f32(uint16_t h) {
