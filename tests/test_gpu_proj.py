@@ -66,6 +66,8 @@ QKV_CASES = [
     (3584, 28, 4, 128, vva.F16, vva.F16, 512, 1, vva.F16),     # 7B ASR chunk, f16 Q
     (3584, 28, 4, 128, vva.Q8_0, vva.F32, 129, 2, vva.BF16),   # Q8_0 weights, two sequences
     (3584, 28, 4, 128, vva.F16, vva.Q8_0, 200, 2, vva.F32),    # F16 weights into a Q8_0 cache, two sequences
+    (3584, 28, 4, 128, vva.F16, vva.F16, 1, 2, vva.F32),       # 7B CFG decode step, F16 weights (GEMV)
+    (896, 14, 2, 64, vva.F16, vva.Q8_0, 3, 2, vva.F32),        # 6 token rows, F16 weights (GEMV)
 ]
 
 
@@ -152,6 +154,8 @@ O_CASES = [
     (1536, 1536, vva.F16, 333, 1, vva.BF16),
     (3584, 3584, vva.Q8_0, 512, 1, vva.F32),    # 7B ASR chunk
     (3584, 3584, vva.F16, 2, 2, vva.F16),
+    (1536, 1536, vva.F16, 4, 2, vva.BF16),      # 8 token rows: more row chunks than the staged batch
+    (3584, 3584, vva.F16, 1, 2, vva.F32),       # 7B CFG decode step
 ]
 
 

@@ -719,6 +719,202 @@ __global__ void __launch_bounds__(64) proj_gemv_kernel(ProjArgs a) {
     }
 }
 
+// Raw bytes of elements k0 .. k0 + 7 (F16 / BF16: r[0]) or k0 .. k0 + 31
+// (Q8_0 blocks: F32 r[0..7], 16-bit r[0..3]) of token row n, as loads the
+// caller converts later (so that they stay in flight meanwhile).
+template <int E>
+__device__ __forceinline__ void load_x_raw(const ProjArgs& a, int n, int k0, u32x4 (&r)[E / 4]) {
+    const int b = n / a.T, t = n - b * a.T;
+    const char* src = a.x + b * a.x_nb_b + t * a.x_nb_t;
+    if (a.x_type == VVA_TYPE_F32) {
+#pragma unroll
+        for (int i = 0; i < E / 4; ++i) r[i] = *(const u32x4*)(src + k0 * 4 + 16 * i);
+    } else {
+#pragma unroll
+        for (int i = 0; i < E / 8; ++i) r[i] = *(const u32x4*)(src + k0 * 2 + 16 * i);
+    }
+}
+template <int E>
+__device__ __forceinline__ void x_from_raw(const ProjArgs& a, const u32x4 (&r)[E / 4], float (&x)[E]) {
+    if (a.x_type == VVA_TYPE_F32) {
+#pragma unroll
+        for (int i = 0; i < E / 4; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[4 * i + e] = __uint_as_float(r[i][e]);
+    } else {
+        const bool bf = a.x_type == VVA_TYPE_BF16;
+#pragma unroll
+        for (int i = 0; i < E / 8; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint16_t lo = (uint16_t)(r[i][e] & 0xffffu), hi = (uint16_t)(r[i][e] >> 16);
+                x[8 * i + 2 * e] = bf ? bf16_to_f32(lo) : f16_to_f32(lo);
+                x[8 * i + 2 * e + 1] = bf ? bf16_to_f32(hi) : f16_to_f32(hi);
+            }
+    }
+}
+
+// What the output of lane (row m0 + r, token n = lane - r N) adds: its row's
+// bias (kProjQKV) or the residual (kProjResidual).  Loaded before the
+// weights, branch-free (lanes past the outputs and a missing bias read a
+// valid address and add 0), so that it is not a second round trip at the end.
+template <int MODE>
+__device__ __forceinline__ float gemv_addend(const ProjArgs& a, int lane, int N, int m0, int mat, int mrow0,
+                                             const char* any) {
+    const bool out = lane < kGvRows * N;
+    const int l = out ? lane : 0;
+    const int r = l / N, n = l - r * N;
+    if constexpr (MODE == kProjQKV) {
+        const float* bias = mat == 0 ? a.bias[0] : mat == 1 ? a.bias[1] : a.bias[2];
+        const float v = *(bias ? bias + mrow0 + r : (const float*)any);
+        return out && bias ? v : 0.0f;
+    } else {
+        const int b = n / a.T, t = n - b * a.T;
+        const float v = *(const float*)(a.res + b * a.res_nb_b + t * a.res_nb_t + (int64_t)(m0 + r) * 4);
+        return out ? v : 0.0f;
+    }
+}
+template <int MODE>
+__device__ __forceinline__ void gemv_store(const ProjArgs& a, int lane, int N, int m0, float v) {
+    if (lane < kGvRows * N) {
+        const int r = lane / N, n = lane - r * N;
+        const int m = m0 + r;
+        if constexpr (MODE == kProjQKV) {
+            a.y[(int64_t)n * a.M + m] = v;
+        } else {
+            const int b = n / a.T, t = n - b * a.T;
+            *(float*)(a.h + b * a.h_nb_b + t * a.h_nb_t + (int64_t)m * 4) = v;
+        }
+    }
+}
+
+// F16 weights, one or two token rows (the decode step), 8 weight rows per
+// workgroup (2 waves of 4), NIT = ceil(K / 512) chunks of 8 per lane and row.
+// Straight-line loads, so that every wait is exact: the token rows' chunks go
+// out first, then all of the workgroup's weight loads; the token rows are
+// rounded to f16 into LDS while the weights are in flight, and the dot loop
+// takes chunk it as soon as it has landed (loads complete in order), so the
+// arithmetic overlaps the rest of the stream.  Products and summation order
+// are those of proj_gemv_kernel.
+constexpr int kGvhWaves = 2;
+constexpr int kGvhRows = kGvRows * kGvhWaves;
+constexpr int kGvhN = 2;                                    // token rows
+__device__ __forceinline__ void lds_barrier_only() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory");
+}
+template <int MODE, int NIT>
+__global__ void __launch_bounds__(64 * kGvhWaves) proj_gemv_f16_kernel(ProjArgs a) {
+    prefetch_kernargs<sizeof(ProjArgs)>();
+    constexpr int NT = 64 * kGvhWaves;
+    constexpr int XT = kGvhN * NIT * 64 / NT;                 // token-row chunks per thread
+    __shared__ __attribute__((aligned(16))) uint32_t xh[kGvhN][NIT * 64][4];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int N = a.N, K = a.K, nch = K / 8, tasks = N * nch;
+    // the wave's weight rows (selects, not an indexed kernel-argument load,
+    // which would wait for the loads below)
+    const int m0 = blockIdx.x * kGvhRows + wv * kGvRows;     // matrix boundaries are multiples of 128
+    const int mat = m0 < a.m_end[0] ? 0 : (m0 < a.m_end[1] ? 1 : 2);
+    const int mrow0 = m0 - (mat == 0 ? 0 : mat == 1 ? a.m_end[0] : a.m_end[1]);
+    const int64_t wnb = mat == 0 ? a.w_nb[0] : mat == 1 ? a.w_nb[1] : a.w_nb[2];
+    const char* wb = (mat == 0 ? a.w[0] : mat == 1 ? a.w[1] : a.w[2]) + (int64_t)mrow0 * wnb;
+    const float addend = gemv_addend<MODE>(a, lane, N, m0, mat, mrow0, wb);
+    // token-row chunk t = (n, c): 16 bytes, and for F32 rows the next 16
+    // (16-bit rows load the same 16 bytes twice: no branch, no read past the row)
+    const bool f32 = a.x_type == VVA_TYPE_F32;
+    const int es = f32 ? 4 : 2;
+    u32x4 xr[XT][2];
+#pragma unroll
+    for (int i = 0; i < XT; ++i) {
+        // (n, c) and (b, t) without integer divisions (n < 2), which would
+        // hold back the weight loads below
+        const int t0 = tid + NT * i, t = t0 < tasks ? t0 : 0;
+        const int n = t >= nch ? 1 : 0, c = t - n * nch;
+        const int b = n >= a.T ? 1 : 0, tt = n - b * a.T;
+        const char* src = a.x + b * a.x_nb_b + tt * a.x_nb_t + (int64_t)c * 8 * es;
+        xr[i][0] = *(const u32x4*)src;
+        xr[i][1] = *(const u32x4*)(src + (f32 ? 16 : 0));
+    }
+    u32x4 wq[NIT][kGvRows];
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        const int c = lane + 64 * it;
+        const int cc = c < nch ? c : 0;
+#pragma unroll
+        for (int r = 0; r < kGvRows; ++r) wq[it][r] = *(const u32x4*)(wb + r * wnb + (int64_t)cc * 16);
+    }
+    const bool bf = a.x_type == VVA_TYPE_BF16;
+#pragma unroll
+    for (int i = 0; i < XT; ++i) {
+        const int t = tid + NT * i;
+        // 16-bit rows: elements 2e, 2e + 1 sit in dword e of the first 16 bytes
+        float y[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t h = xr[i][0][e / 2];
+            const uint16_t v16 = (uint16_t)(e & 1 ? h >> 16 : h & 0xffffu);
+            const float v = bf ? bf16_to_f32(v16) : f16_to_f32(v16);
+            y[e] = f32 ? __uint_as_float(xr[i][e / 4][e % 4]) : v;
+        }
+        if (t < tasks) {
+            const int n = t >= nch ? 1 : 0, c = t - n * nch;
+            *(u32x4*)xh[n][c] = u32x4{pack_f16(y[0], y[1]), pack_f16(y[2], y[3]), pack_f16(y[4], y[5]), pack_f16(y[6], y[7])};
+        }
+    }
+    lds_barrier_only();
+
+    float acc[kGvRows][kGvhN];
+#pragma unroll
+    for (int r = 0; r < kGvRows; ++r)
+#pragma unroll
+        for (int n = 0; n < kGvhN; ++n) acc[r][n] = 0.0f;
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        const int c = lane + 64 * it;
+        const bool live = c < nch;
+#pragma unroll
+        for (int n = 0; n < kGvhN; ++n) {
+            // row n >= N: its LDS chunks were never written; its sums are not stored
+            const u32x4 xv = *(const u32x4*)xh[n][c];
+            const uint32_t x0 = live ? xv.x : 0u, x1 = live ? xv.y : 0u, x2 = live ? xv.z : 0u, x3 = live ? xv.w : 0u;
+#pragma unroll
+            for (int r = 0; r < kGvRows; ++r) {
+                float s = acc[r][n];
+                s = dot2_f16(wq[it][r].x, x0, s);
+                s = dot2_f16(wq[it][r].y, x1, s);
+                s = dot2_f16(wq[it][r].z, x2, s);
+                s = dot2_f16(wq[it][r].w, x3, s);
+                acc[r][n] = s;
+            }
+        }
+    }
+
+    // sums over the lanes; lane r * N + n keeps (row r, token n)
+    float outv = 0.0f;
+#pragma unroll
+    for (int r = 0; r < kGvRows; ++r)
+#pragma unroll
+        for (int n = 0; n < kGvhN; ++n) {
+            const float sum = wave_sum(acc[r][n]);
+            if (n < N && lane == r * N + n) outv = sum;
+        }
+    gemv_store<MODE>(a, lane, N, m0, outv + addend);
+}
+template <int MODE>
+hipError_t launch_gemv_f16(const ProjArgs& a, hipStream_t s) {
+    const dim3 g(a.M / kGvhRows), bl(64 * kGvhWaves);
+    switch ((a.K + 511) / 512) {
+    case 1: hipLaunchKernelGGL((proj_gemv_f16_kernel<MODE, 1>), g, bl, 0, s, a); break;
+    case 2: hipLaunchKernelGGL((proj_gemv_f16_kernel<MODE, 2>), g, bl, 0, s, a); break;
+    case 3: hipLaunchKernelGGL((proj_gemv_f16_kernel<MODE, 3>), g, bl, 0, s, a); break;
+    case 4: hipLaunchKernelGGL((proj_gemv_f16_kernel<MODE, 4>), g, bl, 0, s, a); break;
+    case 5: hipLaunchKernelGGL((proj_gemv_f16_kernel<MODE, 5>), g, bl, 0, s, a); break;
+    case 6: hipLaunchKernelGGL((proj_gemv_f16_kernel<MODE, 6>), g, bl, 0, s, a); break;
+    case 7: hipLaunchKernelGGL((proj_gemv_f16_kernel<MODE, 7>), g, bl, 0, s, a); break;
+    default: hipLaunchKernelGGL((proj_gemv_f16_kernel<MODE, 8>), g, bl, 0, s, a); break;
+    }
+    return hipGetLastError();
+}
+
 // Q8_0 weights, 16 rows per workgroup (4 waves of 4): every weight load of
 // the workgroup goes out first, then its 256 threads quantize the token rows
 // once into LDS (ggml's quantize_row_q8_0, as proj_gemv_kernel does per
@@ -734,10 +930,33 @@ __global__ void __launch_bounds__(64 * kGv8Waves) proj_gemv_q8_kernel(ProjArgs a
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int N = a.N, K = a.K, nbk = K / 32;
     const int m0 = blockIdx.x * kGv8Rows + wv * kGvRows; // matrix boundaries are multiples of 16
+    // (selects, not an indexed kernel-argument load, which would wait for
+    // the token-row loads below)
     const int mat = m0 < a.m_end[0] ? 0 : (m0 < a.m_end[1] ? 1 : 2);
-    const int mrow0 = m0 - (mat ? a.m_end[mat - 1] : 0);
-    const char* wb = a.w[mat] + (int64_t)mrow0 * a.w_nb[mat];
-    const int64_t wnb = a.w_nb[mat];
+    const int mrow0 = m0 - (mat == 0 ? 0 : mat == 1 ? a.m_end[0] : a.m_end[1]);
+    const int64_t wnb = mat == 0 ? a.w_nb[0] : mat == 1 ? a.w_nb[1] : a.w_nb[2];
+    const char* wb = (mat == 0 ? a.w[0] : mat == 1 ? a.w[1] : a.w[2]) + (int64_t)mrow0 * wnb;
+    const float addend = gemv_addend<MODE>(a, lane, N, m0, mat, mrow0, wb);
+    // this thread's first token-row block goes out ahead of the weights
+    const int tasks = N * nbk;
+    u32x4 xr0[8];
+    {
+        // row n = task / nbk and its (b, t) by comparisons (n < kGvMaxN):
+        // integer divisions would hold back the weight loads below
+        const int task = threadIdx.x < tasks ? (int)threadIdx.x : 0;
+        int n = 0, b = 0;
+#pragma unroll
+        for (int k = 1; k < kGvMaxN; ++k) n += task >= k * nbk ? 1 : 0;
+#pragma unroll
+        for (int k = 1; k < kGvMaxN; ++k) b += n >= k * a.T ? 1 : 0;
+        const int t = n - b * a.T, j = task - n * nbk;
+        const char* src = a.x + b * a.x_nb_b + t * a.x_nb_t;
+        const bool f32 = a.x_type == VVA_TYPE_F32;
+        // 16-bit rows: the 64 bytes of the block, then the same 64 again
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            xr0[i] = *(const u32x4*)(src + (int64_t)j * 32 * (f32 ? 4 : 2) + 16 * (f32 ? i : i % 4));
+    }
     // weight block j of each row: 34 bytes from the 4-byte boundary at or
     // below it (rows are 4-byte aligned: K is a multiple of 64)
     uint32_t qw[kGvQ8It][kGvRows][9];
@@ -752,16 +971,17 @@ __global__ void __launch_bounds__(64 * kGv8Waves) proj_gemv_q8_kernel(ProjArgs a
             for (int i = 0; i < 9; ++i) qw[it][r][i] = p[i];
         }
     }
-    for (int task = threadIdx.x; task < N * nbk; task += 64 * kGv8Waves) {
+    for (int task = threadIdx.x; task < tasks; task += 64 * kGv8Waves) {
         const int n = task / nbk, j = task - n * nbk;
-        float x[32];
+        u32x4 raw[8];
+        if (task == (int)threadIdx.x) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            float xs[8];
-            load_x8(a, n, j * 32 + 8 * q, xs);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) x[8 * q + e] = xs[e];
+            for (int i = 0; i < 8; ++i) raw[i] = xr0[i];
+        } else {
+            load_x_raw<32>(a, n, j * 32, raw);
         }
+        float x[32];
+        x_from_raw<32>(a, raw, x);
         float am = 0.0f;
 #pragma unroll
         for (int e = 0; e < 32; ++e) am = fmaxf(am, fabsf(x[e]));
@@ -825,18 +1045,7 @@ __global__ void __launch_bounds__(64 * kGv8Waves) proj_gemv_q8_kernel(ProjArgs a
             const float sum = wave_sum(acc[r][n]);
             if (lane == r * N + n) outv = sum;
         }
-    if (lane < kGvRows * N) {
-        const int r = lane / N, n = lane - r * N;
-        const int m = m0 + r;
-        if constexpr (MODE == kProjQKV) {
-            const float* bias = a.bias[mat];
-            a.y[(int64_t)n * a.M + m] = outv + (bias ? bias[mrow0 + r] : 0.0f);
-        } else {
-            const int b = n / a.T, t = n - b * a.T;
-            const float xr = *(const float*)(a.res + b * a.res_nb_b + t * a.res_nb_t + (int64_t)m * 4);
-            *(float*)(a.h + b * a.h_nb_b + t * a.h_nb_t + (int64_t)m * 4) = outv + xr;
-        }
-    }
+    gemv_store<MODE>(a, lane, N, m0, outv + addend);
 }
 
 }  // namespace
@@ -854,6 +1063,8 @@ hipError_t launch_proj_gemv(ProjArgs& a, float* y_ws, hipStream_t s) {
         else                    hipLaunchKernelGGL((proj_gemv_q8_kernel<kProjResidual>), g8, b8, 0, s, a);
         return hipGetLastError();
     }
+    if (!q8 && a.N <= kGvhN && a.M % kGvhRows == 0 && a.m_end[0] % kGvhRows == 0 && a.m_end[1] % kGvhRows == 0)
+        return a.mode == kProjQKV ? launch_gemv_f16<kProjQKV>(a, s) : launch_gemv_f16<kProjResidual>(a, s);
     const dim3 grid(a.M / kGvRows), block(64);
     if (a.mode == kProjQKV) {
         if (q8) hipLaunchKernelGGL((proj_gemv_kernel<true, kProjQKV>), grid, block, 0, s, a);
