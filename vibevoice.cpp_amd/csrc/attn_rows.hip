@@ -366,9 +366,11 @@ __global__ void __launch_bounds__(64 * kGqaWaves) attn_gqa_f32_kernel(AttnArgs a
 
     // the G query rows of this token and kv head
     const int64_t qes = type_elem_bytes(a.q_type);
-    for (int i = threadIdx.x; i < G * D; i += 64 * kGqaWaves) {
+    for (int i = threadIdx.x; i < kGqaMaxG * D; i += 64 * kGqaWaves) {
         const int h = i / D, e = i - h * D;
-        qsh[h][e] = load_elem(a.q + b * a.q_nb_b + t * a.q_nb_t + (int64_t)(kvh * G + h) * a.q_nb_h + e * qes, a.q_type);
+        qsh[h][e] = h < G ? load_elem(a.q + b * a.q_nb_b + t * a.q_nb_t + (int64_t)(kvh * G + h) * a.q_nb_h + e * qes,
+                                      a.q_type)
+                          : 0.0f;
     }
     __syncthreads();
 
@@ -404,12 +406,11 @@ __global__ void __launch_bounds__(64 * kGqaWaves) attn_gqa_f32_kernel(AttnArgs a
             for (int r = 0; r < DPL; ++r)
                 vv[u][r] = lane + 64 * r < D ? *((const float*)(vr + (int64_t)min(u, nk - 1) * a.v_nb_tok) + lane + 64 * r) : 0.0f;
         const float mv = live && a.mask_mode == kMaskExplicit ? f16_to_f32(*(const uint16_t*)(mrow + 2 * (int64_t)j)) : 0.0f;
-        float p[kGqaMaxG], alpha[kGqaMaxG];
+        // every head slot in straight-line code (slots past G score -inf),
+        // so that the heads' dot products and wave reductions interleave
+        float sc[kGqaMaxG], p[kGqaMaxG], alpha[kGqaMaxG], mx[kGqaMaxG], ps[kGqaMaxG];
 #pragma unroll
         for (int h = 0; h < kGqaMaxG; ++h) {
-            p[h] = 0.0f;
-            alpha[h] = 1.0f;
-            if (h >= G) continue;                                // uniform
             float dot0 = 0.0f, dot1 = 0.0f;
 #pragma unroll
             for (int i4 = 0; i4 < D / 4; i4 += 2) {
@@ -422,18 +423,22 @@ __global__ void __launch_bounds__(64 * kGqaWaves) attn_gqa_f32_kernel(AttnArgs a
                     dot1 = fmaf(q1.z, kv[i4 + 1].z, dot1); dot1 = fmaf(q1.w, kv[i4 + 1].w, dot1);
                 }
             }
-            const float sc = !live || mv == -INFINITY ? -INFINITY : (dot0 + dot1) * a.scale + mv;
-            const float mx = wave_max(sc);
-            if (mx == -INFINITY) continue;                       // nothing visible for this head (uniform)
-            const float Mn = fmaxf(M[h], mx);
-            alpha[h] = __expf(M[h] - Mn);                       // 0 while M = -inf
-            p[h] = sc == -INFINITY ? 0.0f : __expf(sc - Mn);
-            S[h] = fmaf(S[h], alpha[h], wave_sum(p[h]));
+            sc[h] = !live || mv == -INFINITY || h >= G ? -INFINITY : (dot0 + dot1) * a.scale + mv;
+        }
+#pragma unroll
+        for (int h = 0; h < kGqaMaxG; ++h) mx[h] = wave_max(sc[h]);
+#pragma unroll
+        for (int h = 0; h < kGqaMaxG; ++h) {
+            const float Mn = fmaxf(M[h], mx[h]);
+            alpha[h] = Mn == -INFINITY ? 1.0f : __expf(M[h] - Mn);     // 0 while M = -inf
+            p[h] = sc[h] == -INFINITY ? 0.0f : __expf(sc[h] - Mn);
             M[h] = Mn;
         }
 #pragma unroll
+        for (int h = 0; h < kGqaMaxG; ++h) ps[h] = wave_sum(p[h]);
+#pragma unroll
         for (int h = 0; h < kGqaMaxG; ++h) {
-            if (h >= G) break;
+            S[h] = fmaf(S[h], alpha[h], ps[h]);
             psh[wv][h][lane] = p[h];
 #pragma unroll
             for (int r = 0; r < DPL; ++r) acc[h][r] *= alpha[h];
@@ -451,7 +456,6 @@ __global__ void __launch_bounds__(64 * kGqaWaves) attn_gqa_f32_kernel(AttnArgs a
             }
 #pragma unroll
             for (int h = 0; h < kGqaMaxG; ++h) {
-                if (h >= G) break;
 #pragma unroll
                 for (int u = 0; u < VB; u += 4) {
                     const float4 pu = *(const float4*)&psh[wv][h][u0 + u];
