@@ -401,8 +401,8 @@ def run_proj(torch, vva, vvo, reps: int = 10):
     """The fused projections at 7B shapes (hidden 3584, 28 q / 4 kv heads,
     d = 128), F16 and Q8_0 weights: vva_qkv_rope_append (q/k/v GEMM + bias +
     RoPE + F16 cache append) and vva_out_proj_residual.
-      4096-token prefill chunk: MFMA-bound (FLOP = 2 N K M); HIP events
-        around `reps` back-to-back calls.
+      4096-token prefill and a 512-token ASR chunk: MFMA-bound (FLOP =
+        2 N K M); HIP events around `reps` back-to-back calls.
       2-token CFG decode step: bound by streaming the weights (bytes = weight
         bytes); the calls rotate over 28 layers' weights, as a layer stack
         does (1.6 GB of F16 weights, beyond the 256 MB MALL), timed as one
@@ -428,7 +428,7 @@ def run_proj(torch, vva, vvo, reps: int = 10):
             sets.append(ws)
         wbytes_qkv = sum(sets[0][k_].raw.numel() for k_ in "qkv")
         wbytes_o = sets[0]["o"].raw.numel()
-        for T, B in ((4096, 1), (1, 2)):
+        for T, B in ((4096, 1), (512, 1), (1, 2)):
             kv = vva.KVCache(ctx, 1, HKV, D, T + 8, B, vva.F16)
             x = torch.randn((B, T, hidden), device="cuda")
             q_out = torch.empty((B, T, HQ, D), dtype=torch.float16, device="cuda")
@@ -493,8 +493,8 @@ def run_proj(torch, vva, vvo, reps: int = 10):
     ctx.close()
     return {"workload": "Qwen2.5-7B-shaped projections: q/k/v GEMM + bias + RoPE + F16 cache append "
                         "(vva_qkv_rope_append) and output projection + residual (vva_out_proj_residual), "
-                        "F16 and Q8_0 weights, 4096-token chunk and 2-token CFG decode step",
-            "timing": f"4096 tokens: HIP events around {reps} back-to-back calls (prep + GEMM kernels); "
+                        "F16 and Q8_0 weights, 4096- and 512-token chunks and 2-token CFG decode step",
+            "timing": f"4096 and 512 tokens: HIP events around {reps} back-to-back calls (prep + GEMM kernels); "
                       "2 tokens: 28 layers' weights in rotation, one captured HIP graph of the 28 calls replayed "
                       f"{reps} times (us_per_call), and the same calls launched eagerly", **out}
 

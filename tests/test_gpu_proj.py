@@ -181,6 +181,49 @@ def test_out_proj_residual_matches_oracle(ctx, torch_gpu, K, hidden, wt, T, B, o
     print(f"  max {m[0]:.2e} mean {m[1]:.2e}")
 
 
+@pytest.mark.parametrize("wt", [vva.F16, vva.Q8_0])
+def test_short_chunk_projections_repeat_bit_for_bit(ctx, torch_gpu, wt):
+    """A 512-token ASR chunk fills few GEMM tiles, so the GEMM is split along
+    K: every piece stores its partial and the tile's last piece sums them in
+    split order.  The sum must not depend on which piece finishes last, and the
+    tiles' tickets must be back at zero after each call: three calls in a row
+    give the same bytes, and the result matches the oracle."""
+    torch = torch_gpu
+    hidden, Hq, Hkv, d, T = 3584, 28, 4, 128, 512
+    print(f"split-K projections w={wt} T={T}", flush=True)
+    rng = np.random.default_rng(77 + wt)
+    x = rng.standard_normal((1, T, hidden)).astype(np.float32)
+    wo_raw, wo = _weight(torch, rng, hidden, Hq * d, wt)
+    o = rng.standard_normal((1, T, Hq * d)).astype(np.float32)
+    xg, og = torch.from_numpy(x).cuda(), torch.from_numpy(o).cuda()
+    hs = []
+    for _ in range(3):
+        h = torch.full((1, T, hidden), float("nan"), dtype=torch.float32, device="cuda")
+        ctx.out_proj_residual(og, wo, xg, h)
+        torch.cuda.synchronize()
+        hs.append(as_f32(torch, h))
+    assert np.array_equal(hs[0], hs[1]) and np.array_equal(hs[0], hs[2])
+    ref = vvo.linear(o[0], wo_raw, wt, hidden) + x[0]
+    m = _check(hs[0][0], ref, vva.F32, "h (split K)")
+    wq_raw, wq = _weight(torch, rng, Hq * d, hidden, wt)
+    wk_raw, wk = _weight(torch, rng, Hkv * d, hidden, wt)
+    wv_raw, wv = _weight(torch, rng, Hkv * d, hidden, wt)
+    pos = torch.arange(T, dtype=torch.int32, device="cuda").reshape(1, T)
+    qs = []
+    for _ in range(3):
+        kv = vva.KVCache(ctx, 1, Hkv, d, T + 8, 1, vva.F16)
+        q_out = torch.full((1, T, Hq, d), float("nan"), dtype=torch.float32, device="cuda")
+        ctx.qkv_rope_append(kv, 0, xg, wq, wk, wv, pos, q_out)
+        torch.cuda.synchronize()
+        qs.append(as_f32(torch, q_out))
+        kv.free()
+    assert np.array_equal(qs[0], qs[1]) and np.array_equal(qs[0], qs[2])
+    yq = vvo.linear(x[0], wq_raw, wt, Hq * d).reshape(1, T, Hq, d)
+    rq = vvo.rope(yq, np.arange(T, dtype=np.int32))[0]
+    mq = _check(qs[0][0], rq, vva.F32, "q (split K)")
+    print(f"  h max {m[0]:.2e}; q max {mq[0]:.2e}")
+
+
 def test_projection_argument_errors(ctx, torch_gpu):
     torch = torch_gpu
     rng = np.random.default_rng(0)

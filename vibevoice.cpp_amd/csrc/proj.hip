@@ -60,10 +60,178 @@ constexpr int kPitch = kTK * 2 + 16;        // LDS bytes per operand row
 constexpr int kOpBytes = 128 * kPitch;      // one operand tile: 18,432
 constexpr int kStage = 2 * kOpBytes;        // A (weights) then B (x)
 constexpr int kCPitch = kTM + 4;            // floats per token row of the epilogue tile
-static_assert(2 * kStage >= kTN * kCPitch * 4, "the epilogue tile reuses the two stages");
+static_assert(2 * kStage >= kTN * kCPitch * 4 + 16, "the epilogue tile (and the split ticket flag) reuse the two stages");
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// ---- q/k/v epilogue with vector stores.  The tile's C (TN tokens x TM
+// features, cpitch floats per token row): each thread keeps one 8-feature
+// chunk of the tile and walks its tokens; it adds the bias, rotates q and k
+// (NeoX pairs i, i + P, the RoPE table's (cos, sin) of the token), and
+// stores the 8 results as one 16-byte (f16 / bf16) or two (f32) stores.
+// One element per lane and store instruction would issue one lane per cycle.
+// The arithmetic per element is the pair epilogue's.
+template <int TM, int TN, int NTH>
+__device__ __forceinline__ void qkv_epilogue_vec(const ProjArgs& a, const float* C, int cpitch, int m0, int n0, int tid) {
+    constexpr int CPT = TM / 8;                        // chunks per token row of the tile
+    static_assert(NTH % CPT == 0, "a thread keeps its chunk");
+    constexpr int TPP = NTH / CPT;                     // tokens per pass
+    constexpr int EB = 4;                              // passes whose RoPE loads go out together
+    const int d = a.d, P = d >> 1;
+    const int c = tid % CPT, f = c * 8;
+    const int hl = f / d, i0 = f - hl * d;             // head within the tile, its first dim
+    const int f0 = m0 + hl * d;
+    if (f0 >= a.M) return;                             // past the last matrix
+    const int mat = f0 < a.m_end[0] ? 0 : (f0 < a.m_end[1] ? 1 : 2);
+    const int mrow = f0 - (mat == 0 ? 0 : mat == 1 ? a.m_end[0] : a.m_end[1]);
+    const int head = mrow / d;
+    const bool lo = i0 < P;                            // first halves of the rotation pairs
+    const int ip = lo ? i0 + P : i0 - P;               // the partners' first dim
+    const int j0 = lo ? i0 : ip;                       // pair index of the first dim
+    const float* bias = mat == 0 ? a.bias[0] : mat == 1 ? a.bias[1] : a.bias[2];
+    float bs[8], bp[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        bs[e] = bias ? bias[mrow + i0 + e] : 0.0f;
+        bp[e] = bias ? bias[mrow + ip + e] : 0.0f;
+    }
+    const int dt = mat == 0 ? a.q_out_type : a.cache_type;
+    const int64_t es = type_elem_bytes(dt);
+    const bool one_seq = a.N == a.T;
+    for (int nb = tid / CPT; nb < TN; nb += TPP * EB) {
+        float4 csr[EB][4];                             // (cos, sin) of pairs j0 .. j0 + 7
+#pragma unroll
+        for (int e = 0; e < EB; ++e) {
+            const float4* rp = (const float4*)(a.rope + (int64_t)min(n0 + nb + TPP * e, a.N - 1) * P + j0);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) csr[e][q] = rp[q];
+        }
+#pragma unroll
+        for (int e = 0; e < EB; ++e) {
+            const int nl = nb + TPP * e, n = n0 + nl;
+            if (nl >= TN || n >= a.N) break;
+            const float* cr = C + nl * cpitch + hl * d;
+            float out[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const float y = cr[i0 + k] + bs[k], yq = cr[ip + k] + bp[k];
+                const float cs = (k & 1) ? csr[e][k >> 1].z : csr[e][k >> 1].x;
+                const float sn = (k & 1) ? csr[e][k >> 1].w : csr[e][k >> 1].y;
+                // pair (y0, y1) = (dim j, dim j + P): lo threads hold y0
+                out[k] = mat == 2 ? y : (lo ? fmaf(y, cs, -(yq * sn)) : fmaf(yq, sn, y * cs));
+            }
+            const int b = one_seq ? 0 : n / a.T, t = n - b * a.T;
+            char* dst;
+            if (mat == 0) {
+                dst = a.q_out + b * a.qo_nb_b + t * a.qo_nb_t + head * a.qo_nb_h + i0 * es;
+            } else {
+                char* const kd = one_seq ? a.k_dst[0] : a.k_dst[b];
+                char* const vd = one_seq ? a.v_dst[0] : a.v_dst[b];
+                dst = (mat == 1 ? kd : vd) + t * a.cache_row_bytes + head * a.cache_head_bytes + i0 * es;
+            }
+            if (dt == VVA_TYPE_F32) {
+                *(float4*)dst = make_float4(out[0], out[1], out[2], out[3]);
+                *(float4*)(dst + 16) = make_float4(out[4], out[5], out[6], out[7]);
+            } else {
+                const bool bf = dt == VVA_TYPE_BF16;
+                uint32_t w4[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const uint32_t x0 = bf ? f32_to_bf16(out[2 * k]) : f32_to_f16(out[2 * k]);
+                    const uint32_t x1 = bf ? f32_to_bf16(out[2 * k + 1]) : f32_to_f16(out[2 * k + 1]);
+                    w4[k] = x0 | (x1 << 16);
+                }
+                *(u32x4*)dst = u32x4{w4[0], w4[1], w4[2], w4[3]};
+            }
+        }
+    }
+}
+
+// ---- split along K.  Each piece of a tile stores its accumulators (NW
+// compute waves x 2 x 2 blocks of v_mfma_f32_32x32x16) as one block of the
+// partial area, in the accumulators' own order [wave][block][4-register
+// group][lane] so that every store instruction writes 1 KB of whole lines,
+// with agent-scope (sc1) buffer stores: coherent across the XCDs' L2 caches
+// without an L2 write-back.  After the stores have completed, thread 0 takes
+// the tile's ticket; the last piece sums the pieces' blocks in split order
+// (deterministic whatever the arrival order) into the epilogue's LDS tile C
+// and resets the ticket for the next call.
+constexpr int kSc1 = 16;                               // buffer cache policy: agent scope
+// Epilogue passes whose loads go out together, before the batch's stores:
+// vmcnt counts stores too, so a load waited for after a store waits for
+// that store as well (a batch of 8 keeps the unrolled code small)
+constexpr int kEpiQkv = 8, kEpiRes = 8;
+template <int NW>
+__device__ __forceinline__ void splitk_store(const f32x16 (&acc)[2][2], char* piece, int w, int lane) {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(piece, (short)0, NW * 4096 * 4, 0x00020000);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const u32x4 v = {__float_as_uint(acc[i][j][4 * g]), __float_as_uint(acc[i][j][4 * g + 1]),
+                                 __float_as_uint(acc[i][j][4 * g + 2]), __float_as_uint(acc[i][j][4 * g + 3])};
+                __builtin_amdgcn_raw_buffer_store_b128(v, rs, (w * 16 + (i * 2 + j) * 4 + g) * 1024 + lane * 16, 0, kSc1);
+            }
+}
+// Thread 0 takes the ticket (after every piece store of the workgroup has
+// completed and a barrier); returns, to every thread, whether this piece is
+// the tile's last.  `flag` is an int of LDS that nothing else uses meanwhile.
+__device__ __forceinline__ bool splitk_ticket(unsigned* tk, int ksplit, int* flag) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned old = __hip_atomic_fetch_add(tk, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *flag = old == (unsigned)(ksplit - 1);
+        if (*flag) __hip_atomic_store(tk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    return *flag != 0;
+}
+// C[token][feature] (cpitch floats per token row) = sum over the pieces of
+// the tile, in split order; every thread of the workgroup (NT) takes part,
+// FB float4s at a time with all their loads in flight.  WM: compute waves
+// along the features (the wave's quadrant is wm = w % WM, wn = w / WM).
+template <int NW, int NT, int WM, int FB>
+__device__ __forceinline__ void splitk_sum(const char* piece0, int ksplit, float* C, int cpitch) {
+    constexpr int PIECE = NW * 4096 * 4;
+    constexpr int NF = NW * 1024 / NT;                 // float4s per thread
+    static_assert(NF % FB == 0, "whole batches");
+#pragma unroll
+    for (int f0 = 0; f0 < NF; f0 += FB) {
+        u32x4 v[FB][4];
+#pragma unroll
+        for (int e = 0; e < FB; ++e) {
+            const int f = (int)threadIdx.x + NT * (f0 + e);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                if (k >= ksplit) break;                // uniform
+                const __amdgpu_buffer_rsrc_t rs =
+                    __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(piece0) + (int64_t)k * PIECE, (short)0, PIECE, 0x00020000);
+                v[e][k] = __builtin_amdgcn_raw_buffer_load_b128(rs, f * 16, 0, kSc1);
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < FB; ++e) {
+            const int f = (int)threadIdx.x + NT * (f0 + e);
+            float4 s = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                if (k >= ksplit) break;
+                s.x += __uint_as_float(v[e][k].x);
+                s.y += __uint_as_float(v[e][k].y);
+                s.z += __uint_as_float(v[e][k].z);
+                s.w += __uint_as_float(v[e][k].w);
+            }
+            const int w = f >> 10, gi = (f >> 6) & 15, lane = f & 63;
+            const int i = gi >> 3, j = (gi >> 2) & 1, g = gi & 3;
+            const int wm = w % WM, wn = w / WM, l32 = lane & 31, half = lane >> 5;
+            *(float4*)(C + (wn * 64 + 32 * j + l32) * cpitch + wm * 64 + 32 * i + 4 * half + 8 * g) = s;
+        }
+    }
 }
 
 // ------------------------------------------------------------ prep
@@ -130,11 +298,18 @@ __global__ void __launch_bounds__(256) proj_gemm_kernel(ProjArgs a) {
 
     // Workgroup i runs on XCD i % 8; XCD x takes the contiguous run of tiles
     // [x * q + min(x, r), ...) of its c_x = q + (x < r) workgroups.
-    const int n_mt = a.M / kTM;
-    const int tiles = gridDim.x;
-    const int q = tiles / 8, r = tiles % 8, x = blockIdx.x % 8;
-    const int tile = x * q + min(x, r) + (int)blockIdx.x / 8;
-    const int mt = tile % n_mt, nt = tile / n_mt;
+    const int n_mt = a.M / kTM, n_nt = (a.N + kTN - 1) / kTN;
+    const int ksplit = a.ksplit;
+    const int pieces = gridDim.x;
+    const int q = pieces / 8, r = pieces % 8, x = blockIdx.x % 8;
+    const int wo = x * q + min(x, r) + (int)blockIdx.x / 8;   // the XCD's contiguous run of the order
+    // split along K: the order walks (k piece, weight tile, token tile),
+    // token tiles innermost, so that the workgroups an XCD runs together
+    // share one weight slice in its L2
+    const int ks = ksplit > 1 ? wo / (n_nt * n_mt) : 0;
+    const int mt = ksplit > 1 ? (wo / n_nt) % n_mt : wo % n_mt;
+    const int nt = ksplit > 1 ? wo % n_nt : wo / n_mt;
+    const int tile = mt * n_nt + nt;                          // ticket and partials of the tile
     const int m0 = mt * kTM, n0 = nt * kTN;
     const int mat = m0 < a.m_end[0] ? 0 : (m0 < a.m_end[1] ? 1 : 2);
     const int mrow0 = m0 - (mat ? a.m_end[mat - 1] : 0);     // first row in its matrix
@@ -144,6 +319,9 @@ __global__ void __launch_bounds__(256) proj_gemm_kernel(ProjArgs a) {
     // x rows past N read as zeros through the buffer range
     const __amdgpu_buffer_rsrc_t xrs = rsrc(a.xh + (int64_t)n0 * a.K, (uint32_t)(min(a.N - n0, kTN) * a.K * 2));
     const __amdgpu_buffer_rsrc_t wrs = rsrc(wbase, (uint32_t)(kTM * wnb));
+    const int nk_all = a.K / kTK;
+    const int k_lo = ks * nk_all / ksplit;
+    const int nk = (ks + 1) * nk_all / ksplit - k_lo;
 
     // per thread and k step: 4 x 16 bytes of B (and of an F16 A): chunk c =
     // tid + 256 i is row c / 8, 16-byte column c % 8
@@ -153,20 +331,20 @@ __global__ void __launch_bounds__(256) proj_gemm_kernel(ProjArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int c = tid + 256 * i, row = c >> 3, col = c & 7;
-            breg[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (row * a.K + kt * kTK) * 2 + col * 16, 0, 0);
+            breg[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (row * a.K + (k_lo + kt) * kTK) * 2 + col * 16, 0, 0);
         }
         if constexpr (!WQ8) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int c = tid + 256 * i, row = c >> 3, col = c & 7;
-                areg[i] = __builtin_amdgcn_raw_buffer_load_b128(wrs, (uint32_t)(row * wnb) + kt * kTK * 2 + col * 16, 0, 0);
+                areg[i] = __builtin_amdgcn_raw_buffer_load_b128(wrs, (uint32_t)(row * wnb) + (k_lo + kt) * kTK * 2 + col * 16, 0, 0);
             }
         } else {
             // block kt * 2 + (tid & 1) of row tid / 2: 34 bytes from the
             // 4-byte boundary at or below it (9 dwords; the block of an odd
             // index starts 2 bytes in, an even one's 9th dword is the next
             // block's scale, always inside the row)
-            const uint32_t off = (uint32_t)((tid >> 1) * wnb) + (uint32_t)(kt * 2 + (tid & 1)) * kQ8Bytes;
+            const uint32_t off = (uint32_t)((tid >> 1) * wnb) + (uint32_t)((k_lo + kt) * 2 + (tid & 1)) * kQ8Bytes;
 #pragma unroll
             for (int i = 0; i < 9; ++i) qreg[i] = __builtin_amdgcn_raw_buffer_load_b32(wrs, (off & ~3u) + 4 * i, 0, 0);
         }
@@ -218,7 +396,6 @@ __global__ void __launch_bounds__(256) proj_gemm_kernel(ProjArgs a) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
 
-    const int nk = a.K / kTK;
     load(0);
     store(0);
     if (nk > 1) load(1);
@@ -254,20 +431,32 @@ __global__ void __launch_bounds__(256) proj_gemm_kernel(ProjArgs a) {
 
     // ---- accumulators to LDS as C[token][feature]: lane (half, l32) of
     // block (i, j) holds features 8 (r / 4) + 4 half + r % 4 of token l32
+    // (split along K: the tile's last piece sums every piece's partial there)
     float* C = (float*)lds;
+    if (ksplit > 1) {
+        constexpr int PIECE = 4 * 4096 * 4;
+        splitk_store<4>(acc, a.part + ((int64_t)tile * ksplit + ks) * PIECE, w, lane);
+        if (!splitk_ticket(a.tickets + tile, ksplit, (int*)(lds + 2 * kStage - 16))) return;
+        splitk_sum<4, 256, 2, 8>(a.part + (int64_t)tile * ksplit * PIECE, ksplit, C, kCPitch);
+    } else {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            float* crow = C + (wn * 64 + 32 * j + l32) * kCPitch + wm * 64 + 32 * i + 4 * half;
+            for (int j = 0; j < 2; ++j) {
+                float* crow = C + (wn * 64 + 32 * j + l32) * kCPitch + wm * 64 + 32 * i + 4 * half;
 #pragma unroll
-            for (int g = 0; g < 4; ++g)
-                *(float4*)(crow + 8 * g) = make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
-                                                       acc[i][j][4 * g + 3]);
-        }
+                for (int g = 0; g < 4; ++g)
+                    *(float4*)(crow + 8 * g) = make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                                                           acc[i][j][4 * g + 3]);
+            }
+    }
     __syncthreads();
 
     if constexpr (MODE == kProjQKV) {
+        if (a.vec_store) {
+            qkv_epilogue_vec<kTM, kTN, 256>(a, C, kCPitch, m0, n0, tid);
+            return;
+        }
         // 64 rotation pairs per token (one head of d = 128, two of d = 64):
         // thread (token tid / 64 + 4 pass, pair tid % 64)
         const int d = a.d, P = d >> 1;
@@ -276,26 +465,37 @@ __global__ void __launch_bounds__(256) proj_gemm_kernel(ProjArgs a) {
         const float* bias = a.bias[mat];
         const float b0 = bias ? bias[mrow0 + hl * d + i] : 0.0f;
         const float b1 = bias ? bias[mrow0 + hl * d + i + P] : 0.0f;
-        for (int nl = tid >> 6; nl < kTN; nl += 4) {
+        // the batch's RoPE pairs loaded first (one memory round trip per batch)
+        for (int nb = tid >> 6; nb < kTN; nb += 4 * kEpiQkv) {
+            float2 csb[kEpiQkv];
+#pragma unroll
+            for (int e = 0; e < kEpiQkv; ++e)
+                csb[e] = a.rope[(int64_t)min(n0 + nb + 4 * e, a.N - 1) * P + i];      // used for q and k only
+#pragma unroll
+            for (int e = 0; e < kEpiQkv; ++e) {
+            const int nl = nb + 4 * e;
             const int n = n0 + nl;
-            if (n >= a.N) break;                       // wave-uniform
+            if (nl >= kTN || n >= a.N) break;              // wave-uniform
             float y0 = C[nl * kCPitch + hl * d + i] + b0;
             float y1 = C[nl * kCPitch + hl * d + i + P] + b1;
             if (mat < 2) {
-                const float2 cs = a.rope[(int64_t)n * P + i];
+                const float2 cs = csb[e];
                 const float r0 = fmaf(y0, cs.x, -(y1 * cs.y));
                 const float r1 = fmaf(y0, cs.y, y1 * cs.x);
                 y0 = r0;
                 y1 = r1;
             }
-            const int b = n / a.T, t = n - b * a.T;
+            const int b = a.N == a.T ? 0 : n / a.T, t = n - b * a.T;
             if (mat == 0) {
                 const int64_t eo = type_elem_bytes(a.q_out_type);
                 char* dst = a.q_out + b * a.qo_nb_b + t * a.qo_nb_t + head * a.qo_nb_h;
                 store_elem(dst + i * eo, a.q_out_type, y0);
                 store_elem(dst + (i + P) * eo, a.q_out_type, y1);
             } else {
-                char* row = (mat == 1 ? a.k_dst[b] : a.v_dst[b]) + t * a.cache_row_bytes + head * a.cache_head_bytes;
+                // (one sequence: constant indices, no indexed kernel-argument load per pass)
+                char* const kd = a.N == a.T ? a.k_dst[0] : a.k_dst[b];
+                char* const vd = a.N == a.T ? a.v_dst[0] : a.v_dst[b];
+                char* row = (mat == 1 ? kd : vd) + t * a.cache_row_bytes + head * a.cache_head_bytes;
                 if (a.cache_type == VVA_TYPE_Q8_0) {
                     store_q8_pair(row, i, P, y0, y1);
                 } else {
@@ -304,19 +504,32 @@ __global__ void __launch_bounds__(256) proj_gemm_kernel(ProjArgs a) {
                     store_elem(row + (i + P) * ec, a.cache_type, y1);
                 }
             }
+            }
         }
     } else {
         // h = y + x, 4 features per thread: thread (token tid / 32 + 8 pass,
         // features 4 (tid % 32) ..)
         const int c4 = (tid & 31) * 4;
-        for (int nl = tid >> 5; nl < kTN; nl += 8) {
-            const int n = n0 + nl;
-            if (n >= a.N) break;
-            const int b = n / a.T, t = n - b * a.T;
-            const float4 xr = *(const float4*)(a.res + b * a.res_nb_b + t * a.res_nb_t + (int64_t)(m0 + c4) * 4);
-            const float* cr = C + nl * kCPitch + c4;
-            *(float4*)(a.h + b * a.h_nb_b + t * a.h_nb_t + (int64_t)(m0 + c4) * 4) =
-                make_float4(cr[0] + xr.x, cr[1] + xr.y, cr[2] + xr.z, cr[3] + xr.w);
+        // the batch's residual rows loaded first (one memory round trip per batch)
+        for (int nb = tid >> 5; nb < kTN; nb += 8 * kEpiRes) {
+            float4 xrb[kEpiRes];
+#pragma unroll
+            for (int e = 0; e < kEpiRes; ++e) {
+                const int n = min(n0 + nb + 8 * e, a.N - 1);
+                const int b = a.N == a.T ? 0 : n / a.T, t = n - b * a.T;
+                xrb[e] = *(const float4*)(a.res + b * a.res_nb_b + t * a.res_nb_t + (int64_t)(m0 + c4) * 4);
+            }
+#pragma unroll
+            for (int e = 0; e < kEpiRes; ++e) {
+                const int nl = nb + 8 * e;
+                const int n = n0 + nl;
+                if (nl >= kTN || n >= a.N) break;
+                const int b = a.N == a.T ? 0 : n / a.T, t = n - b * a.T;
+                const float4 xr = xrb[e];
+                const float* cr = C + nl * kCPitch + c4;
+                *(float4*)(a.h + b * a.h_nb_b + t * a.h_nb_t + (int64_t)(m0 + c4) * 4) =
+                    make_float4(cr[0] + xr.x, cr[1] + xr.y, cr[2] + xr.z, cr[3] + xr.w);
+            }
         }
     }
 }
@@ -346,7 +559,7 @@ constexpr int kWLoadsB = kWB / 1024 / kWProd;
 constexpr int kWLoads = kWLoadsA + kWLoadsB;
 constexpr int kWCPitch = kWM + 4;              // floats per token row of the epilogue tile
 static_assert(2 * kWLoads <= 63, "two stages of a producer's loads fit its 6-bit vmcnt");
-static_assert(kWN * kWCPitch * 4 <= kWStages * kWStage, "the epilogue tile reuses the ring");
+static_assert(kWN * kWCPitch * 4 + 16 <= kWStages * kWStage, "the epilogue tile (and the split ticket flag) reuse the ring");
 
 __device__ __forceinline__ void wdma16(i32x4 rsrc, uint32_t lds_addr, int voffset) {
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
@@ -374,13 +587,30 @@ __global__ void __launch_bounds__((kWCompute + kWProd) * 64) proj_gemm_wide_kern
     // tiles, the 4 token tiles of every weight tile in turn: the tiles an
     // XCD runs at one time share few weight and token rows in its L2.
     const int n_mt = (a.M + kWM - 1) / kWM, n_nt = (a.N + kWN - 1) / kWN;
-    const int tiles = gridDim.x;
-    const int q = tiles / 8, r = tiles % 8, x = blockIdx.x % 8;
-    const int tile = x * q + min(x, r) + (int)blockIdx.x / 8;
-    const int grp = tile / (n_mt * 4), gn = min(4, n_nt - grp * 4), j = tile - grp * n_mt * 4;
-    const int mt = j / gn, nt = grp * 4 + j % gn;
+    const int ksplit = a.ksplit;
+    const int pieces = gridDim.x;
+    const int q = pieces / 8, r = pieces % 8, x = blockIdx.x % 8;
+    const int wo = x * q + min(x, r) + (int)blockIdx.x / 8;   // the XCD's contiguous run of the order
+    int mt, nt, ks = 0;
+    if (ksplit > 1) {
+        // split along K: the order walks (k piece, weight tile, token tile),
+        // token tiles innermost, so that the workgroups an XCD runs together
+        // share one weight slice in its L2
+        nt = wo % n_nt;
+        mt = (wo / n_nt) % n_mt;
+        ks = wo / (n_nt * n_mt);
+    } else {
+        const int grp = wo / (n_mt * 4), gn = min(4, n_nt - grp * 4), j = wo - grp * n_mt * 4;
+        mt = j / gn;
+        nt = grp * 4 + j % gn;
+    }
+    const int tile = mt * n_nt + nt;                          // ticket and partials of the tile
     const int m0 = mt * kWM, n0 = nt * kWN;
-    const int nk = a.K / kWK;
+    const int nk_all = a.K / kWK;
+    const int k_lo = ks * nk_all / ksplit;
+    const int nk = (ks + 1) * nk_all / ksplit - k_lo;
+    constexpr int PIECE = kWCompute * 4096 * 4;
+    int* const split_flag = (int*)(lds + kWStages * kWStage - 16);
     const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
 
     if (w >= kWCompute) {
@@ -411,7 +641,7 @@ __global__ void __launch_bounds__((kWCompute + kWProd) * 64) proj_gemm_wide_kern
         auto issue = [&](int kt) {
             const uint32_t st = lds0 + (uint32_t)(kt % kWStages) * kWStage;
             const bool live = kt < nk;
-            const int ko = kt * kWK * 2;
+            const int ko = (k_lo + kt) * kWK * 2;
 #pragma unroll
             for (int i = 0; i < kWLoadsA; ++i)
                 wdma16(ars[i], st + (pw + kWProd * i) * 1024, live ? aoff[i] + ko : 0x40000000);
@@ -426,8 +656,13 @@ __global__ void __launch_bounds__((kWCompute + kWProd) * 64) proj_gemm_wide_kern
             issue(kt + 2);                                 // into the stage of kt - 1
         }
         asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
-        __syncthreads();                                   // accumulators written
-        __syncthreads();                                   // epilogue tile read
+        __syncthreads();                                   // every wave is done with the ring
+        if (ksplit > 1) {
+            if (!splitk_ticket(a.tickets + tile, ksplit, split_flag)) return;
+            splitk_sum<kWCompute, (kWCompute + kWProd) * 64, 4, 4>(a.part + (int64_t)tile * ksplit * PIECE, ksplit,
+                                                                 (float*)lds, kWCPitch);
+        }
+        __syncthreads();                                   // the epilogue tile is written
         return;
     }
 
@@ -466,20 +701,33 @@ __global__ void __launch_bounds__((kWCompute + kWProd) * 64) proj_gemm_wide_kern
 
     // ---- accumulators to LDS as C[token][feature]: lane (half, l32) of
     // block (i, j) holds features 8 (r / 4) + 4 half + r % 4 of token l32
+    // (split along K: the tile's last piece sums every piece's partial there,
+    // with the producer waves)
     float* C = (float*)lds;
+    if (ksplit > 1) {
+        splitk_store<kWCompute>(acc, a.part + ((int64_t)tile * ksplit + ks) * PIECE, w, lane);
+        if (!splitk_ticket(a.tickets + tile, ksplit, split_flag)) return;
+        splitk_sum<kWCompute, (kWCompute + kWProd) * 64, 4, 4>(a.part + (int64_t)tile * ksplit * PIECE, ksplit, C,
+                                                             kWCPitch);
+    } else {
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            float* crow = C + (wn * 64 + 32 * j + l32) * kWCPitch + wm * 64 + 32 * i + 4 * half;
+            for (int j = 0; j < 2; ++j) {
+                float* crow = C + (wn * 64 + 32 * j + l32) * kWCPitch + wm * 64 + 32 * i + 4 * half;
 #pragma unroll
-            for (int g = 0; g < 4; ++g)
-                *(float4*)(crow + 8 * g) = make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
-                                                       acc[i][j][4 * g + 3]);
-        }
+                for (int g = 0; g < 4; ++g)
+                    *(float4*)(crow + 8 * g) = make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                                                           acc[i][j][4 * g + 3]);
+            }
+    }
     __syncthreads();
 
     if constexpr (MODE == kProjQKV) {
+        if (a.vec_store) {
+            if (tid < kWCompute * 64) qkv_epilogue_vec<kWM, kWN, kWCompute * 64>(a, C, kWCPitch, m0, n0, tid);
+            return;
+        }
         // 128 rotation pairs per token (two heads of d = 128, four of d = 64):
         // thread (token tid / 128 + 4 pass, pair tid % 128)
         const int d = a.d, P = d >> 1;
@@ -492,26 +740,38 @@ __global__ void __launch_bounds__((kWCompute + kWProd) * 64) proj_gemm_wide_kern
         const float* bias = a.bias[mat];
         const float b0 = bias ? bias[mrow + i] : 0.0f;
         const float b1 = bias ? bias[mrow + i + P] : 0.0f;
-        for (int nl = tid >> 7; nl < kWN; nl += kWCompute * 64 / 128) {
+        // the batch's RoPE pairs loaded first (one memory round trip per batch)
+        constexpr int PS = kWCompute * 64 / 128;          // token stride between passes
+        for (int nb = tid >> 7; nb < kWN; nb += PS * kEpiQkv) {
+            float2 csb[kEpiQkv];
+#pragma unroll
+            for (int e = 0; e < kEpiQkv; ++e)
+                csb[e] = a.rope[(int64_t)min(n0 + nb + PS * e, a.N - 1) * P + i];     // used for q and k only
+#pragma unroll
+            for (int e = 0; e < kEpiQkv; ++e) {
+            const int nl = nb + PS * e;
             const int n = n0 + nl;
-            if (n >= a.N) break;                           // uniform per wave
+            if (nl >= kWN || n >= a.N) break;              // uniform per wave
             float y0 = C[nl * kWCPitch + hl * d + i] + b0;
             float y1 = C[nl * kWCPitch + hl * d + i + P] + b1;
             if (mat < 2) {
-                const float2 cs = a.rope[(int64_t)n * P + i];
+                const float2 cs = csb[e];
                 const float r0 = fmaf(y0, cs.x, -(y1 * cs.y));
                 const float r1 = fmaf(y0, cs.y, y1 * cs.x);
                 y0 = r0;
                 y1 = r1;
             }
-            const int b = n / a.T, t = n - b * a.T;
+            const int b = a.N == a.T ? 0 : n / a.T, t = n - b * a.T;
             if (mat == 0) {
                 const int64_t eo = type_elem_bytes(a.q_out_type);
                 char* dst = a.q_out + b * a.qo_nb_b + t * a.qo_nb_t + head * a.qo_nb_h;
                 store_elem(dst + i * eo, a.q_out_type, y0);
                 store_elem(dst + (i + P) * eo, a.q_out_type, y1);
             } else {
-                char* row = (mat == 1 ? a.k_dst[b] : a.v_dst[b]) + t * a.cache_row_bytes + head * a.cache_head_bytes;
+                // (one sequence: constant indices, no indexed kernel-argument load per pass)
+                char* const kd = a.N == a.T ? a.k_dst[0] : a.k_dst[b];
+                char* const vd = a.N == a.T ? a.v_dst[0] : a.v_dst[b];
+                char* row = (mat == 1 ? kd : vd) + t * a.cache_row_bytes + head * a.cache_head_bytes;
                 if (a.cache_type == VVA_TYPE_Q8_0) {
                     store_q8_pair(row, i, P, y0, y1);
                 } else {
@@ -520,20 +780,33 @@ __global__ void __launch_bounds__((kWCompute + kWProd) * 64) proj_gemm_wide_kern
                     store_elem(row + (i + P) * ec, a.cache_type, y1);
                 }
             }
+            }
         }
     } else {
         // h = y + x, 4 features per thread: thread (token tid / 64 + 8 pass,
         // features 4 (tid % 64) ..)
         const int c4 = (tid & 63) * 4;
         if (m0 + c4 >= a.M) return;
-        for (int nl = tid >> 6; nl < kWN; nl += kWCompute) {
-            const int n = n0 + nl;
-            if (n >= a.N) break;
-            const int b = n / a.T, t = n - b * a.T;
-            const float4 xr = *(const float4*)(a.res + b * a.res_nb_b + t * a.res_nb_t + (int64_t)(m0 + c4) * 4);
-            const float* cr = C + nl * kWCPitch + c4;
-            *(float4*)(a.h + b * a.h_nb_b + t * a.h_nb_t + (int64_t)(m0 + c4) * 4) =
-                make_float4(cr[0] + xr.x, cr[1] + xr.y, cr[2] + xr.z, cr[3] + xr.w);
+        // the batch's residual rows loaded first (one memory round trip per batch)
+        for (int nb = tid >> 6; nb < kWN; nb += kWCompute * kEpiRes) {
+            float4 xrb[kEpiRes];
+#pragma unroll
+            for (int e = 0; e < kEpiRes; ++e) {
+                const int n = min(n0 + nb + kWCompute * e, a.N - 1);
+                const int b = a.N == a.T ? 0 : n / a.T, t = n - b * a.T;
+                xrb[e] = *(const float4*)(a.res + b * a.res_nb_b + t * a.res_nb_t + (int64_t)(m0 + c4) * 4);
+            }
+#pragma unroll
+            for (int e = 0; e < kEpiRes; ++e) {
+                const int nl = nb + kWCompute * e;
+                const int n = n0 + nl;
+                if (nl >= kWN || n >= a.N) break;
+                const int b = a.N == a.T ? 0 : n / a.T, t = n - b * a.T;
+                const float4 xr = xrb[e];
+                const float* cr = C + nl * kWCPitch + c4;
+                *(float4*)(a.h + b * a.h_nb_b + t * a.h_nb_t + (int64_t)(m0 + c4) * 4) =
+                    make_float4(cr[0] + xr.x, cr[1] + xr.y, cr[2] + xr.z, cr[3] + xr.w);
+            }
         }
     }
 }
@@ -1076,6 +1349,26 @@ hipError_t launch_proj_gemv(ProjArgs& a, float* y_ws, hipStream_t s) {
     return hipGetLastError();
 }
 
+// The GEMM's tiles against the workgroups resident at once (one wide F16
+// workgroup per CU, two of the 128 x 128 kernel): a call whose tiles fill
+// at most half of them (short chunks, e.g. 512 tokens) is split along K, at
+// least 4 k steps per piece, up to 4 pieces, one round.
+int proj_ksplit(const ProjArgs& a, int n_cu) {
+    const bool q8 = a.w_type == VVA_TYPE_Q8_0;
+    const int tiles = q8 ? (a.M / kTM) * ((a.N + kTN - 1) / kTN) : ((a.M + kWM - 1) / kWM) * ((a.N + kWN - 1) / kWN);
+    const int slots = q8 ? 2 * n_cu : n_cu;
+    const int nk = a.K / (q8 ? kTK : kWK);
+    if (tiles < 1 || 2 * tiles > slots || tiles > kMaxProjTickets) return 1;
+    return max(1, min(min(4, slots / tiles), nk / 4));
+}
+size_t proj_part_bytes(const ProjArgs& a) {
+    if (a.ksplit <= 1) return 0;
+    const bool q8 = a.w_type == VVA_TYPE_Q8_0;
+    const size_t tiles = q8 ? (size_t)(a.M / kTM) * ((a.N + kTN - 1) / kTN)
+                            : (size_t)((a.M + kWM - 1) / kWM) * ((a.N + kWN - 1) / kWN);
+    return tiles * a.ksplit * (q8 ? 4 : kWCompute) * 4096 * sizeof(float);
+}
+
 size_t proj_ws_bytes(int N, int K, int P) {
     const size_t xh = ((size_t)N * K * 2 + 255) / 256 * 256;
     return xh + (size_t)N * P * sizeof(float2);
@@ -1090,14 +1383,15 @@ hipError_t launch_proj(ProjPrepArgs& p, ProjArgs& a, void* ws, hipStream_t s) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const bool q8 = a.w_type == VVA_TYPE_Q8_0;
+    if (a.ksplit < 1 || !a.part || !a.tickets) a.ksplit = 1;
     if (!q8) {
-        const int wtiles = ((a.M + kWM - 1) / kWM) * ((a.N + kWN - 1) / kWN);
+        const int wtiles = ((a.M + kWM - 1) / kWM) * ((a.N + kWN - 1) / kWN) * a.ksplit;
         const dim3 block((kWCompute + kWProd) * 64);
         if (a.mode == kProjQKV) hipLaunchKernelGGL((proj_gemm_wide_kernel<kProjQKV>), dim3(wtiles), block, 0, s, a);
         else                    hipLaunchKernelGGL((proj_gemm_wide_kernel<kProjResidual>), dim3(wtiles), block, 0, s, a);
         return hipGetLastError();
     }
-    const int tiles = (a.M / kTM) * ((a.N + kTN - 1) / kTN);
+    const int tiles = (a.M / kTM) * ((a.N + kTN - 1) / kTN) * a.ksplit;
     if (a.mode == kProjQKV) {
         if (q8) hipLaunchKernelGGL((proj_gemm_kernel<true, kProjQKV>), dim3(tiles), dim3(256), 0, s, a);
         else    hipLaunchKernelGGL((proj_gemm_kernel<false, kProjQKV>), dim3(tiles), dim3(256), 0, s, a);

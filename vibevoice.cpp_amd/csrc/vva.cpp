@@ -39,7 +39,8 @@ struct vva_context {
     std::vector<float*> ws_retired;
     float* scratch = nullptr;            // this device's `scratch` (vva_attn_noalloc)
     // merge tickets, zeroed once: vva_decode_step's [kMaxStepTickets], then the
-    // prefill's in-launch merge [kMaxPrefillTickets]
+    // prefill's in-launch merge [kMaxPrefillTickets], then the projection
+    // GEMM's split along K [kMaxProjTickets]
     unsigned* tickets = nullptr;
     std::set<vva_kv*> caches;            // released by vva_destroy if still alive
     // the last prefill plan and the call shape it was made for: a layer stack
@@ -342,7 +343,7 @@ extern "C" vva_status vva_create(int device, void* stream, vva_context** out) {
     ctx->stream = (hipStream_t)stream;
     ctx->scratch = scr;
     ctx->err.reserve(512);               // error messages (< 512 bytes) then never allocate
-    constexpr size_t ticket_bytes = sizeof(unsigned) * (kMaxStepTickets + kMaxPrefillTickets);
+    constexpr size_t ticket_bytes = sizeof(unsigned) * (kMaxStepTickets + kMaxPrefillTickets + kMaxProjTickets);
     e = hipMalloc(&ctx->tickets, ticket_bytes);
     if (e == hipSuccess) e = hipMemset(ctx->tickets, 0, ticket_bytes);
     if (e != hipSuccess) {
@@ -840,6 +841,21 @@ bool rows16(const vva_tensor* x) {
 
 }  // namespace
 
+// The prep + GEMM launches of a projection with their workspace: the
+// converted token rows (and RoPE table), then, when the GEMM is split along
+// K, the pieces' partials; the split tickets follow the decode step's and the
+// prefill's in the context's ticket buffer.
+static vva_status run_proj_gemm(vva_context* ctx, ProjPrepArgs& p, ProjArgs& a, int N, int K, int P) {
+    a.ksplit = proj_ksplit(a, ctx->n_cu);
+    a.tickets = ctx->tickets + kMaxStepTickets + kMaxPrefillTickets;
+    const size_t base = (proj_ws_bytes(N, K, P) + 255) / 256 * 256;
+    vva_status st = ensure_ws(ctx, base + proj_part_bytes(a));
+    if (st != VVA_OK) return st;
+    a.part = a.ksplit > 1 ? (char*)ctx->ws + base : nullptr;
+    const hipError_t e = launch_proj(p, a, ctx->ws, ctx->stream);
+    return e == hipSuccess ? VVA_OK : hip_fail(ctx, e, "projection launch");
+}
+
 extern "C" vva_status vva_qkv_rope_append(vva_context* ctx, vva_kv* kv, int layer, const vva_tensor* x,
                                           const vva_tensor* wq, const vva_tensor* wk, const vva_tensor* wv,
                                           const vva_tensor* bq, const vva_tensor* bk, const vva_tensor* bv,
@@ -912,6 +928,19 @@ extern "C" vva_status vva_qkv_rope_append(vva_context* ctx, vva_kv* kv, int laye
     a.cache_head_bytes = kv->head_bytes;
     a.cache_type = kv->desc.type;
     a.d = (int)d; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.T = (int)T;
+    {
+        // the GEMM epilogue stores 8 elements at a time where q_out and the
+        // cache rows are of a float type and 16-byte aligned (Q8_0 caches
+        // quantize per rotation pair)
+        auto al16 = [](int64_t v) { return v % 16 == 0; };
+        bool vec = float_type(a.q_out_type) && float_type(a.cache_type) && d % 8 == 0 &&
+                   (int64_t)q_out->nb[0] == type_elem_bytes(a.q_out_type) && al16((int64_t)(uintptr_t)a.q_out) &&
+                   al16(a.qo_nb_h) && al16(a.qo_nb_t) && al16(a.qo_nb_b) && al16(a.cache_row_bytes) &&
+                   al16(a.cache_head_bytes);
+        for (int b = 0; b < (int)B; ++b)
+            vec = vec && al16((int64_t)(uintptr_t)a.k_dst[b]) && al16((int64_t)(uintptr_t)a.v_dst[b]);
+        a.vec_store = vec;
+    }
     ProjPrepArgs p{};
     p.x = (const char*)x->data; p.x_type = x->type;
     p.x_nb_t = (int64_t)x->nb[1]; p.x_nb_b = (int64_t)x->nb[2];
@@ -940,9 +969,8 @@ extern "C" vva_status vva_qkv_rope_append(vva_context* ctx, vva_kv* kv, int laye
         const vva_tensor tq = proj_view(0, Hq), tk = proj_view(Hq * d, Hkv), tv = proj_view((Hq + Hkv) * d, Hkv);
         return vva_rope_append(ctx, kv, layer, &tq, &tk, &tv, pos, seq_ids, freq_base, q_out);
     }
-    if ((st = ensure_ws(ctx, proj_ws_bytes((int)N, (int)K, p.P))) != VVA_OK) return st;
-    hipError_t e = launch_proj(p, a, ctx->ws, ctx->stream);
-    return e == hipSuccess ? VVA_OK : hip_fail(ctx, e, "qkv_rope_append launch");
+    if ((st = run_proj_gemm(ctx, p, a, (int)N, (int)K, p.P)) != VVA_OK) return st;
+    return VVA_OK;
 }
 
 extern "C" vva_status vva_out_proj_residual(vva_context* ctx, const vva_tensor* o, const vva_tensor* w_o,
@@ -993,11 +1021,9 @@ extern "C" vva_status vva_out_proj_residual(vva_context* ctx, const vva_tensor* 
     if (proj_gemv_supported((int)N, (int)K, (int)M) && rows16(o)) {
         a.x = p.x; a.x_type = p.x_type; a.x_nb_t = p.x_nb_t; a.x_nb_b = p.x_nb_b;
         e = launch_proj_gemv(a, nullptr, ctx->stream);
-    } else {
-        if ((st = ensure_ws(ctx, proj_ws_bytes((int)N, (int)K, 0))) != VVA_OK) return st;
-        e = launch_proj(p, a, ctx->ws, ctx->stream);
+        return e == hipSuccess ? VVA_OK : hip_fail(ctx, e, "out_proj_residual launch");
     }
-    return e == hipSuccess ? VVA_OK : hip_fail(ctx, e, "out_proj_residual launch");
+    return run_proj_gemm(ctx, p, a, (int)N, (int)K, 0);
 }
 
 // --------------------------------------------------------- decode step

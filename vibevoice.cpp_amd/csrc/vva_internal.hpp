@@ -143,7 +143,19 @@ struct ProjArgs {
     // and, for kProjQKV, the projections y = x w^T + bias as F32 [N][M]
     const char* x; int x_type; int64_t x_nb_t, x_nb_b;
     float* y;
+    // GEMM split along K (ksplit > 1): every piece stores its accumulators in
+    // `part`, the last piece of a tile (ticket) sums them and runs the epilogue
+    int ksplit;
+    char* part;
+    unsigned* tickets;                                     // [tiles], zero between calls
+    // kProjQKV: q_out and cache rows take 8-element vector stores (F32 / F16 /
+    // BF16 destinations, 16-byte aligned rows); else one element per lane
+    int vec_store;
 };
+constexpr int kMaxProjTickets = 1024;
+// K split of the GEMM of a call (1: none) and the bytes of its partials
+int proj_ksplit(const ProjArgs& a, int n_cu);
+size_t proj_part_bytes(const ProjArgs& a);
 
 // --------------------------------------------------------- host launchers
 
