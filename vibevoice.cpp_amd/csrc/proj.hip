@@ -247,11 +247,33 @@ __global__ void __launch_bounds__(256) proj_prep_kernel(ProjPrepArgs a) {
     const char* src = a.x + b * a.x_nb_b + t * a.x_nb_t;
     const int64_t es = type_elem_bytes(a.x_type);
     uint16_t* dst = a.xh + (int64_t)n * a.K;
-    // 8 consecutive elements per thread; four threads make one 32-block
-    for (int k0 = threadIdx.x * 8; k0 < a.K; k0 += 256 * 8) {
-        float x[8];
+    // 8 consecutive elements per thread; four threads make one 32-block.  A
+    // 16-byte aligned row is read with vector loads, two passes' loads out
+    // together (K <= 4096); otherwise element by element.
+    const bool f32 = a.x_type == VVA_TYPE_F32, bf = a.x_type == VVA_TYPE_BF16;
+    const bool vec = ((uintptr_t)src & 15) == 0;
+    u32x4 raw[2][2];
+    if (vec) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = load_elem(src + (k0 + e) * es, a.x_type);
+        for (int u = 0; u < 2; ++u) {
+            const int k0 = min((int)threadIdx.x * 8 + 2048 * u, a.K - 8);
+            raw[u][0] = *(const u32x4*)(src + k0 * es);
+            raw[u][1] = *(const u32x4*)(src + k0 * es + (f32 ? 16 : 0));
+        }
+    }
+    for (int k0 = threadIdx.x * 8, u = 0; k0 < a.K; k0 += 256 * 8, ++u) {
+        float x[8];
+        if (vec && u < 2) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t wd = raw[u][0][e / 2];
+                const uint16_t v16 = (uint16_t)(e & 1 ? wd >> 16 : wd & 0xffffu);
+                x[e] = f32 ? __uint_as_float(raw[u][e / 4][e % 4]) : (bf ? bf16_to_f32(v16) : f16_to_f32(v16));
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[e] = load_elem(src + (k0 + e) * es, a.x_type);
+        }
         uint16_t h[8];
         if (a.q8) {
             float am = 0.0f;
