@@ -224,6 +224,45 @@ def test_short_chunk_projections_repeat_bit_for_bit(ctx, torch_gpu, wt):
     print(f"  h max {m[0]:.2e}; q max {mq[0]:.2e}")
 
 
+@pytest.mark.parametrize("wt", [vva.F16, vva.Q8_0])
+def test_4096_token_projection_with_split_tail(ctx, torch_gpu, wt):
+    """At 4096 tokens the 7B q/k/v GEMM has 576 (F16) or 1152 (Q8_0) tiles:
+    two or more full rounds and a last round of a quarter of the CUs, whose
+    tiles are split along K and merged by their last piece.  The first and
+    last 256 token rows (the last ones are in the split tail) match the
+    oracle, and two calls give the same bytes."""
+    torch = torch_gpu
+    hidden, Hq, Hkv, d, T = 3584, 28, 4, 128, 4096
+    print(f"tail-split projections w={wt} T={T}", flush=True)
+    rng = np.random.default_rng(91 + wt)
+    x = rng.standard_normal((1, T, hidden)).astype(np.float32)
+    wq_raw, wq = _weight(torch, rng, Hq * d, hidden, wt)
+    wk_raw, wk = _weight(torch, rng, Hkv * d, hidden, wt)
+    wv_raw, wv = _weight(torch, rng, Hkv * d, hidden, wt)
+    xg = torch.from_numpy(x).cuda()
+    pos = torch.arange(T, dtype=torch.int32, device="cuda").reshape(1, T)
+    qs, ks = [], []
+    for _ in range(2):
+        kv = vva.KVCache(ctx, 1, Hkv, d, T + 8, 1, vva.F16)
+        q_out = torch.full((1, T, Hq, d), float("nan"), dtype=torch.float32, device="cuda")
+        ctx.qkv_rope_append(kv, 0, xg, wq, wk, wv, pos, q_out)
+        torch.cuda.synchronize()
+        qs.append(as_f32(torch, q_out))
+        kraw, _ = kv.download(0, 0, T)
+        ks.append(kraw.copy())
+        kv.free()
+    assert np.array_equal(qs[0], qs[1]) and np.array_equal(ks[0], ks[1])
+    rows = np.r_[0:256, T - 256:T]
+    yq = vvo.linear(x[0][rows], wq_raw, wt, Hq * d).reshape(1, len(rows), Hq, d)
+    rq = vvo.rope(yq, rows.astype(np.int32))[0]
+    mq = _check(qs[0][0][rows], rq, vva.F32, "q rows (split tail)")
+    yk = vvo.linear(x[0][rows], wk_raw, wt, Hkv * d).reshape(1, len(rows), Hkv, d)
+    rk = vvo.rope(yk, rows.astype(np.int32))[0]
+    kdec = vvo.to_f32(ks[0][rows].reshape(-1), vva.F16, len(rows) * Hkv * d).reshape(len(rows), Hkv, d)
+    mk = _check(kdec, rk, vva.F16, "k cache rows (split tail)")
+    print(f"  q max {mq[0]:.2e}; k max {mk[0]:.2e}")
+
+
 def test_projection_argument_errors(ctx, torch_gpu):
     torch = torch_gpu
     rng = np.random.default_rng(0)

@@ -321,17 +321,33 @@ __global__ void __launch_bounds__(256) proj_gemm_kernel(ProjArgs a) {
     // Workgroup i runs on XCD i % 8; XCD x takes the contiguous run of tiles
     // [x * q + min(x, r), ...) of its c_x = q + (x < r) workgroups.
     const int n_mt = a.M / kTM, n_nt = (a.N + kTN - 1) / kTN;
-    const int ksplit = a.ksplit;
-    const int pieces = gridDim.x;
-    const int q = pieces / 8, r = pieces % 8, x = blockIdx.x % 8;
-    const int wo = x * q + min(x, r) + (int)blockIdx.x / 8;   // the XCD's contiguous run of the order
-    // split along K: the order walks (k piece, weight tile, token tile),
-    // token tiles innermost, so that the workgroups an XCD runs together
-    // share one weight slice in its L2
-    const int ks = ksplit > 1 ? wo / (n_nt * n_mt) : 0;
-    const int mt = ksplit > 1 ? (wo / n_nt) % n_mt : wo % n_mt;
-    const int nt = ksplit > 1 ? wo % n_nt : wo / n_mt;
-    const int tile = mt * n_nt + nt;                          // ticket and partials of the tile
+    const int ksplit = a.ksplit, tail0 = a.tail0;
+    int mt, nt, ks = 0, tile = 0;                             // tile: its ticket and partials
+    if (ksplit > 1 && tail0 == 0) {
+        // every tile split along K: the order walks (k piece, weight tile,
+        // token tile), token tiles innermost, so that the workgroups an XCD
+        // runs together share one weight slice in its L2
+        const int q = gridDim.x / 8, r = gridDim.x % 8, x = blockIdx.x % 8;
+        const int wo = x * q + min(x, r) + (int)blockIdx.x / 8;
+        ks = wo / (n_nt * n_mt);
+        mt = (wo / n_nt) % n_mt;
+        nt = wo % n_nt;
+        tile = mt * n_nt + nt;
+    } else if (ksplit > 1 && (int)blockIdx.x >= tail0) {
+        // the last round's tiles, split along K (after the unsplit ones)
+        const int qq = (int)blockIdx.x - tail0, wo = tail0 + qq / ksplit;
+        ks = qq % ksplit;
+        tile = qq / ksplit;
+        mt = wo % n_mt;
+        nt = wo / n_mt;
+    } else {
+        const int hp = ksplit > 1 ? tail0 : (int)gridDim.x;
+        const int q = hp / 8, r = hp % 8, x = blockIdx.x % 8;
+        const int wo = x * q + min(x, r) + (int)blockIdx.x / 8;   // the XCD's contiguous run of the order
+        mt = wo % n_mt;
+        nt = wo / n_mt;
+    }
+    const bool split = ksplit > 1 && (tail0 == 0 || (int)blockIdx.x >= tail0);
     const int m0 = mt * kTM, n0 = nt * kTN;
     const int mat = m0 < a.m_end[0] ? 0 : (m0 < a.m_end[1] ? 1 : 2);
     const int mrow0 = m0 - (mat ? a.m_end[mat - 1] : 0);     // first row in its matrix
@@ -342,8 +358,9 @@ __global__ void __launch_bounds__(256) proj_gemm_kernel(ProjArgs a) {
     const __amdgpu_buffer_rsrc_t xrs = rsrc(a.xh + (int64_t)n0 * a.K, (uint32_t)(min(a.N - n0, kTN) * a.K * 2));
     const __amdgpu_buffer_rsrc_t wrs = rsrc(wbase, (uint32_t)(kTM * wnb));
     const int nk_all = a.K / kTK;
-    const int k_lo = ks * nk_all / ksplit;
-    const int nk = (ks + 1) * nk_all / ksplit - k_lo;
+    const int nsp = split ? ksplit : 1;
+    const int k_lo = ks * nk_all / nsp;
+    const int nk = (ks + 1) * nk_all / nsp - k_lo;
 
     // per thread and k step: 4 x 16 bytes of B (and of an F16 A): chunk c =
     // tid + 256 i is row c / 8, 16-byte column c % 8
@@ -455,7 +472,7 @@ __global__ void __launch_bounds__(256) proj_gemm_kernel(ProjArgs a) {
     // block (i, j) holds features 8 (r / 4) + 4 half + r % 4 of token l32
     // (split along K: the tile's last piece sums every piece's partial there)
     float* C = (float*)lds;
-    if (ksplit > 1) {
+    if (split) {
         constexpr int PIECE = 4 * 4096 * 4;
         splitk_store<4>(acc, a.part + ((int64_t)tile * ksplit + ks) * PIECE, w, lane);
         if (!splitk_ticket(a.tickets + tile, ksplit, (int*)(lds + 2 * kStage - 16))) return;
@@ -609,28 +626,40 @@ __global__ void __launch_bounds__((kWCompute + kWProd) * 64) proj_gemm_wide_kern
     // tiles, the 4 token tiles of every weight tile in turn: the tiles an
     // XCD runs at one time share few weight and token rows in its L2.
     const int n_mt = (a.M + kWM - 1) / kWM, n_nt = (a.N + kWN - 1) / kWN;
-    const int ksplit = a.ksplit;
-    const int pieces = gridDim.x;
-    const int q = pieces / 8, r = pieces % 8, x = blockIdx.x % 8;
-    const int wo = x * q + min(x, r) + (int)blockIdx.x / 8;   // the XCD's contiguous run of the order
-    int mt, nt, ks = 0;
-    if (ksplit > 1) {
-        // split along K: the order walks (k piece, weight tile, token tile),
-        // token tiles innermost, so that the workgroups an XCD runs together
-        // share one weight slice in its L2
-        nt = wo % n_nt;
-        mt = (wo / n_nt) % n_mt;
-        ks = wo / (n_nt * n_mt);
-    } else {
+    const int ksplit = a.ksplit, tail0 = a.tail0;
+    int mt, nt, ks = 0, tile = 0;                             // tile: its ticket and partials
+    auto order = [&](int wo) {
         const int grp = wo / (n_mt * 4), gn = min(4, n_nt - grp * 4), j = wo - grp * n_mt * 4;
         mt = j / gn;
         nt = grp * 4 + j % gn;
+    };
+    if (ksplit > 1 && tail0 == 0) {
+        // every tile split along K: the order walks (k piece, weight tile,
+        // token tile), token tiles innermost, so that the workgroups an XCD
+        // runs together share one weight slice in its L2
+        const int q = gridDim.x / 8, r = gridDim.x % 8, x = blockIdx.x % 8;
+        const int wo = x * q + min(x, r) + (int)blockIdx.x / 8;
+        nt = wo % n_nt;
+        mt = (wo / n_nt) % n_mt;
+        ks = wo / (n_nt * n_mt);
+        tile = mt * n_nt + nt;
+    } else if (ksplit > 1 && (int)blockIdx.x >= tail0) {
+        // the last round's tiles, split along K (after the unsplit ones)
+        const int qq = (int)blockIdx.x - tail0;
+        order(tail0 + qq / ksplit);
+        ks = qq % ksplit;
+        tile = qq / ksplit;
+    } else {
+        const int hp = ksplit > 1 ? tail0 : (int)gridDim.x;
+        const int q = hp / 8, r = hp % 8, x = blockIdx.x % 8;
+        order(x * q + min(x, r) + (int)blockIdx.x / 8);      // the XCD's contiguous run of the order
     }
-    const int tile = mt * n_nt + nt;                          // ticket and partials of the tile
+    const bool split = ksplit > 1 && (tail0 == 0 || (int)blockIdx.x >= tail0);
     const int m0 = mt * kWM, n0 = nt * kWN;
     const int nk_all = a.K / kWK;
-    const int k_lo = ks * nk_all / ksplit;
-    const int nk = (ks + 1) * nk_all / ksplit - k_lo;
+    const int nsp = split ? ksplit : 1;
+    const int k_lo = ks * nk_all / nsp;
+    const int nk = (ks + 1) * nk_all / nsp - k_lo;
     constexpr int PIECE = kWCompute * 4096 * 4;
     int* const split_flag = (int*)(lds + kWStages * kWStage - 16);
     const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
@@ -679,7 +708,7 @@ __global__ void __launch_bounds__((kWCompute + kWProd) * 64) proj_gemm_wide_kern
         }
         asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
         __syncthreads();                                   // every wave is done with the ring
-        if (ksplit > 1) {
+        if (split) {
             if (!splitk_ticket(a.tickets + tile, ksplit, split_flag)) return;
             splitk_sum<kWCompute, (kWCompute + kWProd) * 64, 4, 4>(a.part + (int64_t)tile * ksplit * PIECE, ksplit,
                                                                  (float*)lds, kWCPitch);
@@ -726,7 +755,7 @@ __global__ void __launch_bounds__((kWCompute + kWProd) * 64) proj_gemm_wide_kern
     // (split along K: the tile's last piece sums every piece's partial there,
     // with the producer waves)
     float* C = (float*)lds;
-    if (ksplit > 1) {
+    if (split) {
         splitk_store<kWCompute>(acc, a.part + ((int64_t)tile * ksplit + ks) * PIECE, w, lane);
         if (!splitk_ticket(a.tickets + tile, ksplit, split_flag)) return;
         splitk_sum<kWCompute, (kWCompute + kWProd) * 64, 4, 4>(a.part + (int64_t)tile * ksplit * PIECE, ksplit, C,
@@ -1375,20 +1404,30 @@ hipError_t launch_proj_gemv(ProjArgs& a, float* y_ws, hipStream_t s) {
 // workgroup per CU, two of the 128 x 128 kernel): a call whose tiles fill
 // at most half of them (short chunks, e.g. 512 tokens) is split along K, at
 // least 4 k steps per piece, up to 4 pieces, one round.
-int proj_ksplit(const ProjArgs& a, int n_cu) {
+int proj_ksplit(const ProjArgs& a, int n_cu, int* tail0) {
     const bool q8 = a.w_type == VVA_TYPE_Q8_0;
     const int tiles = q8 ? (a.M / kTM) * ((a.N + kTN - 1) / kTN) : ((a.M + kWM - 1) / kWM) * ((a.N + kWN - 1) / kWN);
     const int slots = q8 ? 2 * n_cu : n_cu;
     const int nk = a.K / (q8 ? kTK : kWK);
-    if (tiles < 1 || 2 * tiles > slots || tiles > kMaxProjTickets) return 1;
-    return max(1, min(min(4, slots / tiles), nk / 4));
+    *tail0 = 0;
+    if (tiles < 1 || nk < 8) return 1;
+    if (2 * tiles <= slots) {                          // every tile: one round
+        if (tiles > kMaxProjTickets) return 1;
+        return max(1, min(min(4, slots / tiles), nk / 4));
+    }
+    // the last round's tiles when they fill at most a quarter of the slots
+    const int r = tiles % slots;
+    if (r == 0 || 4 * r > slots || r > kMaxProjTickets) return 1;
+    *tail0 = tiles - r;
+    return max(1, min(min(4, slots / r), nk / 4));
 }
 size_t proj_part_bytes(const ProjArgs& a) {
     if (a.ksplit <= 1) return 0;
     const bool q8 = a.w_type == VVA_TYPE_Q8_0;
     const size_t tiles = q8 ? (size_t)(a.M / kTM) * ((a.N + kTN - 1) / kTN)
                             : (size_t)((a.M + kWM - 1) / kWM) * ((a.N + kWN - 1) / kWN);
-    return tiles * a.ksplit * (q8 ? 4 : kWCompute) * 4096 * sizeof(float);
+    const size_t split = a.tail0 > 0 ? tiles - a.tail0 : tiles;
+    return split * a.ksplit * (q8 ? 4 : kWCompute) * 4096 * sizeof(float);
 }
 
 size_t proj_ws_bytes(int N, int K, int P) {
@@ -1405,15 +1444,20 @@ hipError_t launch_proj(ProjPrepArgs& p, ProjArgs& a, void* ws, hipStream_t s) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const bool q8 = a.w_type == VVA_TYPE_Q8_0;
-    if (a.ksplit < 1 || !a.part || !a.tickets) a.ksplit = 1;
+    if (a.ksplit < 1 || !a.part || !a.tickets) {
+        a.ksplit = 1;
+        a.tail0 = 0;
+    }
+    // every tile's pieces, or the unsplit tiles then the split tail's pieces
+    auto grid = [&](int tiles) { return a.tail0 > 0 ? a.tail0 + (tiles - a.tail0) * a.ksplit : tiles * a.ksplit; };
     if (!q8) {
-        const int wtiles = ((a.M + kWM - 1) / kWM) * ((a.N + kWN - 1) / kWN) * a.ksplit;
+        const int wtiles = grid(((a.M + kWM - 1) / kWM) * ((a.N + kWN - 1) / kWN));
         const dim3 block((kWCompute + kWProd) * 64);
         if (a.mode == kProjQKV) hipLaunchKernelGGL((proj_gemm_wide_kernel<kProjQKV>), dim3(wtiles), block, 0, s, a);
         else                    hipLaunchKernelGGL((proj_gemm_wide_kernel<kProjResidual>), dim3(wtiles), block, 0, s, a);
         return hipGetLastError();
     }
-    const int tiles = (a.M / kTM) * ((a.N + kTN - 1) / kTN) * a.ksplit;
+    const int tiles = grid((a.M / kTM) * ((a.N + kTN - 1) / kTN));
     if (a.mode == kProjQKV) {
         if (q8) hipLaunchKernelGGL((proj_gemm_kernel<true, kProjQKV>), dim3(tiles), dim3(256), 0, s, a);
         else    hipLaunchKernelGGL((proj_gemm_kernel<false, kProjQKV>), dim3(tiles), dim3(256), 0, s, a);

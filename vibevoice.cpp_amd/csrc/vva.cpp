@@ -846,7 +846,7 @@ bool rows16(const vva_tensor* x) {
 // K, the pieces' partials; the split tickets follow the decode step's and the
 // prefill's in the context's ticket buffer.
 static vva_status run_proj_gemm(vva_context* ctx, ProjPrepArgs& p, ProjArgs& a, int N, int K, int P) {
-    a.ksplit = proj_ksplit(a, ctx->n_cu);
+    a.ksplit = proj_ksplit(a, ctx->n_cu, &a.tail0);
     a.tickets = ctx->tickets + kMaxStepTickets + kMaxPrefillTickets;
     const size_t base = (proj_ws_bytes(N, K, P) + 255) / 256 * 256;
     vva_status st = ensure_ws(ctx, base + proj_part_bytes(a));

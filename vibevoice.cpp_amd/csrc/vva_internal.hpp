@@ -146,15 +146,17 @@ struct ProjArgs {
     // GEMM split along K (ksplit > 1): every piece stores its accumulators in
     // `part`, the last piece of a tile (ticket) sums them and runs the epilogue
     int ksplit;
+    int tail0;                                             // > 0: only the tiles from this place of the order on are split
     char* part;
-    unsigned* tickets;                                     // [tiles], zero between calls
+    unsigned* tickets;                                     // [split tiles], zero between calls
     // kProjQKV: q_out and cache rows take 8-element vector stores (F32 / F16 /
     // BF16 destinations, 16-byte aligned rows); else one element per lane
     int vec_store;
 };
 constexpr int kMaxProjTickets = 1024;
-// K split of the GEMM of a call (1: none) and the bytes of its partials
-int proj_ksplit(const ProjArgs& a, int n_cu);
+// K split of the GEMM of a call (1: none; *tail0 > 0: only the last round's
+// tiles) and the bytes of its partials
+int proj_ksplit(const ProjArgs& a, int n_cu, int* tail0);
 size_t proj_part_bytes(const ProjArgs& a);
 
 // --------------------------------------------------------- host launchers
