@@ -4,11 +4,12 @@
 // ggml_flash_attn_ext with one query row per head (src/qwen2.cpp:332-334)
 // on Q8_0 K/V.
 //
-// Streaming.  Every workgroup (4 waves, one per SIMD; one workgroup per CU)
-// takes every n_splits-th tile of one sequence (split s: tiles s, s +
-// n_splits, ...) and streams them through a 4-stage LDS ring filled by
-// buffer_load_dwordx4 ... lds (non-temporal: the cache is read once), so
-// three tiles (102 KB per CU) are on their way from HBM while one is
+// Streaming.  Every workgroup (4 compute waves, one per SIMD, and 3 producer
+// waves; one workgroup per CU) takes every n_splits-th whole tile of one
+// sequence (split s: tiles s, s + n_splits, ...) plus an equal piece of the
+// keys past the last whole round, and streams them through a 4-stage LDS
+// ring filled by buffer_load_dwordx4 ... lds (non-temporal: the cache is read
+// once), so two tiles (70 KB per CU) are on their way from HBM while one is
 // computed.  A tile is 512 (key, kv head, 32-dim block) rows of the cache =
 // 17,408 B of K plus the same of V, read as the cache lays them out
 // ([token][kv head][34-byte GGUF block]): one contiguous byte range per
@@ -83,7 +84,7 @@ constexpr int kLoads = 2 * kOpLoads;         // DMA loads per producer per tile
 constexpr int kQLoads = 8;                   // DMA loads per producer for the raw Q rows
 constexpr int kQRawBytes = kQLoads * kP * 1024;   // raw Q area: up to 24 KB
 static_assert(kOpChunks % kP == 0, "chunks split evenly over the producers");
-static_assert(3 * kLoads <= 63, "three tiles of a producer's loads fit its 6-bit vmcnt");
+static_assert(kQLoads + 2 * kLoads <= 63, "Q and two tiles of a producer's loads fit its 6-bit vmcnt");
 constexpr int kDead = 0x40000000;            // buffer offset past every range
 constexpr float kLazy = 8.0f;                // running-max slack in log2 units: p <= 256
 constexpr int kStepLds = 2048;               // step mode: angle table + the new K / V rows
@@ -201,35 +202,46 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, StreamSte
     const int split = blockIdx.x, b = blockIdx.y / NHG, hgrp = blockIdx.y % NHG;
     const int hq0 = hgrp * HQL;               // first query head of the group
     const int L = a.L[b];
-    // Tiles are dealt round-robin: the split's tile t is tile split + t *
-    // n_splits of the sequence, so at any moment the workgroups of a sequence
-    // stream neighbouring tiles of the cache (measured 4 % faster than a
-    // contiguous key range per split).  Only the sequence's last tile can
-    // hold keys past L.
-    const int j1 = L;
-    const int all_tiles = (L + TT - 1) / TT;
-    const int n_tiles = split < all_tiles ? (all_tiles - split + n_splits - 1) / n_splits : 0;
-    const int n_full = L / TT;                // tiles without keys past L
-    const int n_whole = split < n_full ? (n_full - split + n_splits - 1) / n_splits : 0;
-    auto tile_key = [&](int t) { return (split + t * n_splits) * TT; };   // first key of tile t
-    // step mode: the split holding key L - 1 (the new row) and its tile index
-    const bool owns_new = STEP && (all_tiles - 1) % n_splits == split;
-    const int new_t = owns_new ? n_tiles - 1 : -1;
+    // Keys are dealt so that every split streams the same bytes (within one
+    // key).  The first RF = n_rounds * n_splits * TT keys are whole tiles
+    // dealt round-robin: the split's tile 1 + f is tile split + f * n_splits
+    // of the sequence, so at any moment the workgroups of a sequence stream
+    // neighbouring tiles of the cache (measured 4 % faster than a contiguous
+    // key range per split).  The remaining keys (fewer than n_splits tiles'
+    // worth) are cut into n_splits nearly equal pieces: the split's piece
+    // (possibly empty) is its tile 0, computed while its first whole tiles are
+    // still on their way, so no split streams an extra tile at the end.
+    const int span_keys = TT * n_splits;
+    const int n_rounds = L / span_keys;
+    const int RF = n_rounds * span_keys;
+    const int p_begin = RF + (int)(((int64_t)(L - RF) * split) / n_splits);
+    const int p_end = RF + (int)(((int64_t)(L - RF) * (split + 1)) / n_splits);
+    const int n_tiles = 1 + n_rounds;
+    // first key of tile t
+    auto tile_key = [&](int t) { return t == 0 ? p_begin : (split + (t - 1) * n_splits) * TT; };
+    // step mode: the split holding key L - 1 (the new row) is the last one:
+    // the key ends its piece, or (no remainder) its last whole tile
+    const bool owns_new = STEP && split == n_splits - 1 && L > 0;
+    const int new_t = owns_new ? (p_end > p_begin ? 0 : n_tiles - 1) : -1;
     float* const rope_cs = (float*)(lds + kLdsBytes);                  // [D / 2]
     float* const rope_sn = rope_cs + D / 2;
     char* const new_rows = (char*)(rope_sn + D / 2);                   // K slice, then V slice (RB each)
 
-    // One raw buffer per operand: from the 16-byte boundary at or below the
-    // sequence's row 0 to its row L - 1.  delta = row 0's offset from that
-    // boundary (a multiple of 4), also a tile's offset in its LDS stage
-    // (tiles start TT * RBM = 17,408 bytes apart).  (NHG > 1: the cache rows
-    // are 16-byte aligned, delta = 0)
+    // Two raw buffers per operand, both from the 16-byte boundary at or
+    // below the sequence's row 0: the whole tiles' ends at row RF - 1, the
+    // piece's at row p_end - 1, so a piece's 17 KB load fetches its own rows
+    // only.  delta = row 0's offset from that boundary (a multiple of 4),
+    // also a tile's offset in its LDS stage (a tile at key j starts j * RBM
+    // bytes into the buffer).  (NHG > 1: the cache rows are 16-byte aligned,
+    // delta = 0)
     const char* kfirst = a.k[b];
     const char* vfirst = a.v[b];
     const int dk = (int)((uintptr_t)kfirst & 15), dv = (int)((uintptr_t)vfirst & 15);
-    const uint32_t span = (uint32_t)L * (uint32_t)RBM;
+    const uint32_t span = (uint32_t)RF * (uint32_t)RBM, pspan = (uint32_t)p_end * (uint32_t)RBM;
     const i32x4 krs = make_rsrc_sgpr(kfirst - dk, dk + span);
     const i32x4 vrs = make_rsrc_sgpr(vfirst - dv, dv + span);
+    const i32x4 kprs = make_rsrc_sgpr(kfirst - dk, dk + pspan);
+    const i32x4 vprs = make_rsrc_sgpr(vfirst - dv, dv + pspan);
     const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_char*)lds;
 
     // ---- Loads.  Only the kP producer waves (w >= kW) issue memory loads:
@@ -238,8 +250,8 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, StreamSte
     // vector units idle and the queue unrefilled while it computes.  The
     // producers meet the compute waves at every barrier: A (raw Q landed),
     // B (Q quantized), one per tile t (tile t landed, every compute wave done
-    // with tile t - 1, so its stage takes tile t + 3), then the two barriers
-    // of the epilogue.
+    // with tile t - 1, so the stage of tile t - 2 takes tile t + 2), then the
+    // two barriers of the epilogue.
     // Tile t of an operand is bytes [t * 17408, t * 17408 + 18 KB) of its
     // buffer: 18 chunks of 1 KB, chunk c loaded by producer c % kP.  A tile
     // past the last one loads nothing but zeros (offsets past the range: no
@@ -262,17 +274,20 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, StreamSte
             const bool live = t < n_tiles;
             const uint32_t st = lds0 + (uint32_t)(t & (kStages - 1)) * kStage;
             const int tb = tile_key(t) * RBM;
+            const bool pc = t == 0;                  // wave-uniform
+            const i32x4 ks = pc ? kprs : krs, vs = pc ? vprs : vrs;
 #pragma unroll
             for (int op = 0; op < 2; ++op)
 #pragma unroll
                 for (int i = 0; i < kOpLoads; ++i) {
                     const int c = pw + kP * i;
                     const bool need = live && (c < kOpChunks - 1 || (op ? dv : dk) > 0);
-                    dma16<true>(op ? vrs : krs, st + op * kOpBytes + c * 1024, need ? tb + loff[i] : kDead);
+                    dma16<true>(op ? vs : ks, st + op * kOpBytes + c * 1024, need ? tb + loff[i] : kDead);
                 }
         };
         // Q's rows (contiguous, at most 24 KB) go to the ring's last stage,
-        // which takes no tile before barrier T_0, then tile 0
+        // which takes no tile before barrier T_1 (its quantized codes are in
+        // registers from barrier B on)
         {
             const i32x4 qrs = make_rsrc_sgpr(a.q + b * a.q_nb_b + (int64_t)hq0 * D * eb, (uint32_t)(HQL * D * eb));
 #pragma unroll
@@ -281,23 +296,19 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, StreamSte
                 dma16(qrs, lds0 + (kStages - 1) * kStage + c * 1024, c * 1024 + lane * 16);
             }
         }
+        // Q, tile 0 (the piece) and the first whole tile go out together;
+        // from then on tile t + 2 goes out once tile t has landed, so two
+        // tiles (70 KB per CU) are on their way while one is computed.  More
+        // at once (three tiles, or a second whole tile at the start) measured
+        // slower: Q lands later behind them and every tile waits for Q.
         issue(0);
-        wait_vm_barrier<kLoads>();                   // A: Q landed
-        if constexpr (STEP) {
-            // step mode: the RoPE of q lengthens A -> B, so tiles 1 and 2 go
-            // out at A
-            issue(1);
-            issue(2);
-            wait_vm_barrier<3 * kLoads>();           // B
-        } else {
-            wait_vm_barrier<kLoads>();               // B
-            issue(1);
-            issue(2);
-        }
+        issue(1);
+        wait_vm_barrier<2 * kLoads>();               // A: Q landed
+        wait_vm_barrier<2 * kLoads>();               // B
         for (int t = 0; t < n_tiles; ++t) {
-            wait_vm_barrier<2 * kLoads>();           // T_t: tile t landed
+            wait_vm_barrier<kLoads>();               // T_t: tile t landed
             if (STEP && t == new_t) lds_barrier();   // N: the new row is in tile t's stage
-            issue(t + kStages - 1);
+            issue(t + 2);
         }
         // the padding tiles' loads land before the ring is reused
         asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
@@ -594,8 +605,8 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, StreamSte
     // the first tile) in the same instruction stream: the two are
     // independent.  The pair's V codes go to cur.  CHECK: the group may hold
     // keys past the split or the caller passed a mask.
-    auto group_scores = [&](const PairOps& o, int kb, int jt, auto check, const PendingPV& prev, PendingPV& cur,
-                            float (&sc)[4]) {
+    auto group_scores = [&](const PairOps& o, int kb, int jt, int jend, auto check, const PendingPV& prev,
+                            PendingPV& cur, float (&sc)[4]) {
         constexpr bool CHECK = decltype(check)::value;
         pv(prev);
         // ---- scores: per block, two block-diagonal halves into one sum
@@ -633,7 +644,7 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, StreamSte
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int j = jt + kb + SK * sr + 4 * i + g;
-                bool live = j < j1;
+                bool live = j < jend;
                 if (mrow) {
                     const float mv = live ? f16_to_f32(*(const uint16_t*)(mrow + 2 * (int64_t)j)) * kLog2e : 0.0f;
                     live = live && mv != -INFINITY;
@@ -703,6 +714,7 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, StreamSte
         const char* kt = lds + (t & (kStages - 1)) * kStage + dk;
         const char* vt = lds + (t & (kStages - 1)) * kStage + kOpBytes + dv;
         const int jt = tile_key(t);
+        const int jend = t == 0 ? p_end : L;         // the piece ends early
         if constexpr (STEP) {
             if (t == new_t) {                        // wave-uniform: the new row into the tile
                 const int r = L - 1 - jt;
@@ -722,7 +734,7 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, StreamSte
         // formed on the old base unscaled
         float sc[NSUB][4];
 #pragma unroll
-        for (int u = 0; u < NSUB; ++u) group_scores(ops[u], pair_key(u), jt, check, prev[u], cur[u], sc[u]);
+        for (int u = 0; u < NSUB; ++u) group_scores(ops[u], pair_key(u), jt, jend, check, prev[u], cur[u], sc[u]);
         float smax = -INFINITY;
 #pragma unroll
         for (int u = 0; u < NSUB; ++u) smax = fmaxf(smax, fmaxf(fmaxf(sc[u][0], sc[u][1]), fmaxf(sc[u][2], sc[u][3])));
@@ -730,27 +742,30 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, StreamSte
 #pragma unroll
         for (int u = 0; u < NSUB; ++u) group_probs(ops[u], sc[u], cur[u]);
     };
-    // tiles whose keys all lie inside the split run without checks; only the
-    // last can hold keys past its end (all tiles are checked under a mask).
-    // Tiles go in pairs (pz -> pa, pa -> pz); an odd count ends with one
-    // more tile into pa, whose P.V is the last.
-    const int n_plain = mrow != nullptr ? 0 : n_whole;
-    int t = 0;
-    for (; t + 1 < n_plain; t += 2) {
-        tile(t, std::false_type{}, pz, pa);
-        tile(t + 1, std::false_type{}, pa, pz);
-    }
-    for (; t + 1 < n_tiles; t += 2) {
-        tile(t, std::true_type{}, pz, pa);
-        tile(t + 1, std::true_type{}, pa, pz);
+    // The piece (tile 0) is checked against its end; the whole tiles run
+    // without checks (all tiles are checked under a mask).  Tiles go in pairs
+    // (pa -> pz, pz -> pa) after the piece (pz -> pa); an even count ends
+    // with one more tile into pz, whose P.V is the last.
+    tile(0, std::true_type{}, pz, pa);
+    int t = 1;
+    if (mrow != nullptr) {
+        for (; t + 1 < n_tiles; t += 2) {
+            tile(t, std::true_type{}, pa, pz);
+            tile(t + 1, std::true_type{}, pz, pa);
+        }
+    } else {
+        for (; t + 1 < n_tiles; t += 2) {
+            tile(t, std::false_type{}, pa, pz);
+            tile(t + 1, std::false_type{}, pz, pa);
+        }
     }
     if (t < n_tiles) {
-        tile(t, std::true_type{}, pz, pa);
-#pragma unroll
-        for (int u = 0; u < NSUB; ++u) pv(pa[u]);
-    } else {
+        tile(t, std::true_type{}, pa, pz);
 #pragma unroll
         for (int u = 0; u < NSUB; ++u) pv(pz[u]);
+    } else {
+#pragma unroll
+        for (int u = 0; u < NSUB; ++u) pv(pa[u]);
     }
     __syncthreads();                                 // the producers' last loads have landed
 
