@@ -167,3 +167,43 @@ def test_decode_step_graph_replays_match_eager(ctx, torch_gpu):
         assert torch.equal(out, eager)
     del g
     kv.free()
+
+
+def test_decode_step_q8_v_beyond_the_f16_range(ctx, torch_gpu):
+    """A 7B Q8_0 step whose V blocks reach d_v = 2^13 (|V| near 1e6, the
+    new row's v as large): the streamed kernel raises the rows' exp2 base
+    so its f16 P' stays finite.  Fused and unfused agree bit for bit and
+    match the oracle within the tolerance scaled by the V scale."""
+    torch = torch_gpu
+    d, Hq, Hkv, lens, vs = 128, 28, 4, [3000, 2500], 2.0 ** 18
+    B = len(lens)
+    print(f"decode_step Q8_0 V scale 2^18 lens={lens}", flush=True)
+    rng = np.random.default_rng(91)
+    a = vva.KVCache(ctx, 1, Hkv, d, max(lens) + 4, B, vva.Q8_0)
+    u = vva.KVCache(ctx, 1, Hkv, d, max(lens) + 4, B, vva.Q8_0)
+    for s, n in enumerate(lens):
+        kk = rng.standard_normal((n, Hkv, d)).astype(np.float32)
+        vv = (np.clip(rng.standard_normal((n, Hkv, d)), -3.95, 3.95) * vs).astype(np.float32)
+        for c in (a, u):
+            c.upload(0, s, 0, kk, vv)
+            c.set_len(s, n)
+    q = to_gpu(torch, rng.standard_normal((B, 1, Hq, d)), vva.F32)
+    k = to_gpu(torch, rng.standard_normal((B, 1, Hkv, d)), vva.F32)
+    v = to_gpu(torch, rng.standard_normal((B, 1, Hkv, d)) * vs, vva.F32)
+    pos = torch.tensor([[n] for n in lens], dtype=torch.int32, device="cuda")
+    qa = torch.empty((B, 1, Hq, d), dtype=torch.float32, device="cuda")
+    qu = torch.empty_like(qa)
+    oa = torch.full((B, 1, Hq, d), float("nan"), dtype=torch.float32, device="cuda")
+    ou = torch.full_like(oa, float("nan"))
+    ctx.decode_step(a, 0, q, k, v, pos, qa, oa, d ** -0.5)
+    ctx.rope_append(u, 0, q, k, v, pos, qu)
+    ctx.attn(u, 0, qu, ou, d ** -0.5)
+    torch.cuda.synchronize()
+    got = as_f32(torch, oa)
+    assert np.isfinite(got).all()
+    assert torch.equal(oa, ou)
+    ref = oracle_attn(as_f32(torch, qa), a, 0, range(B), [n + 1 for n in lens], 1, d ** -0.5)
+    mx, mn = assert_close(got / vs, ref / vs, *TOL, what="Q8_0 step, V * 2^18, rescaled")
+    print(f"  |out| up to {np.abs(got).max():.3g}; rescaled vs oracle max {mx:.2e} mean {mn:.2e}")
+    a.free()
+    u.free()

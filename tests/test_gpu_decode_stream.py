@@ -282,21 +282,26 @@ def test_stream_decode_peaked_scores(ctx, torch_gpu, d, Hq, Hkv, L):
     kv.free()
 
 
-def test_stream_decode_v_at_the_q8_0_range_edge(ctx, torch_gpu):
-    """The streamed decode forms P' = p * d_v in f16 with p <= 2^8 (the lazy
-    running-max slack), so a V block's scale d_v = amax / 127 may reach 255:
-    |V| up to 256 * 127 = 32512.  V * 2^13 with |V| < 3.95 reaches 32358;
-    scaling a Q8_0 block by a power of two keeps its codes and scales d by
-    it, so the output divided by 2^13 must match the oracle of the unscaled
-    cache."""
+@pytest.mark.parametrize("vscale", [2.0 ** 13, 2.0 ** 16, 2.0 ** 20])
+def test_stream_decode_v_beyond_the_f16_range(ctx, torch_gpu, vscale):
+    """The streamed decode forms P' = p * d_v as an f16 MFMA operand with p
+    <= 2^8 (the lazy running-max slack).  V blocks with d_v = amax / 127 <
+    2^8 (|V| <= 32512) take the plain f16 product; a larger d_v raises the
+    row's exp2 base so P' stays below 2^15, so any Q8_0 cache gives a finite
+    result (ggml dequantizes Q8_0 V to fp32, src/qwen2.cpp:332-335).
+    Scaling a Q8_0 block by a power of two keeps its codes and scales d by
+    it, so the output divided by the scale must match the oracle of the
+    unscaled cache.  V * 2^13 with |V| < 3.95 reaches 32358 (the plain path,
+    at its edge); 2^16 and 2^20 reach 2.6e5 and 4.1e6 (d_v up to 32600)."""
     torch = torch_gpu
     d, Hq, Hkv, lens = 128, 28, 4, [6001, 6001]
+    print(f"stream decode V scale 2^{int(np.log2(vscale))}", flush=True)
     rng = np.random.default_rng(41)
     caches, outs = [], []
     k = [rng.standard_normal((n, Hkv, d)).astype(np.float32) for n in lens]
     v = [np.clip(rng.standard_normal((n, Hkv, d)), -3.95, 3.95).astype(np.float32) for n in lens]
     q = to_gpu(torch, rng.standard_normal((len(lens), 1, Hq, d)), vva.F32)
-    for scale in (1.0, 2.0 ** 13):
+    for scale in (1.0, vscale):
         kv = vva.KVCache(ctx, 1, Hkv, d, max(lens), len(lens), vva.Q8_0)
         for s, n in enumerate(lens):
             kv.upload(0, s, 0, k[s], (v[s] * scale).astype(np.float32))
@@ -308,11 +313,11 @@ def test_stream_decode_v_at_the_q8_0_range_edge(ctx, torch_gpu):
         caches.append(kv)
     vmax = max(np.abs(vvo.to_f32(caches[1].download(0, s, n)[1].reshape(-1), vva.Q8_0, n * Hkv * d)).max()
                for s, n in enumerate(lens))
-    assert 3.2e4 < vmax <= 32512.0
+    assert 3.2e4 * vscale / 2.0 ** 13 < vmax <= 32512.0 * vscale / 2.0 ** 13
     assert np.isfinite(outs[1]).all()
     ref = oracle_attn(as_f32(torch, q), caches[0], 0, range(len(lens)), lens, 1, d ** -0.5)
     assert_close(outs[0], ref, MAX_TOL, MEAN_TOL, what="unscaled V")
-    mx, mn = assert_close(outs[1] / 2.0 ** 13, ref, MAX_TOL, MEAN_TOL, what="V * 2^13, rescaled")
+    mx, mn = assert_close(outs[1] / vscale, ref, MAX_TOL, MEAN_TOL, what="V scaled, rescaled back")
     print(f"  V up to {vmax:.0f}: rescaled output vs oracle max {mx:.2e} mean {mn:.2e}")
     for kv in caches:
         kv.free()

@@ -273,6 +273,13 @@ def test_projection_argument_errors(ctx, torch_gpu):
     with pytest.raises(vva.VvaError) as e:
         ctx.out_proj_residual(o, w, bad, bad)          # residual of the wrong width
     assert e.value.status == vva.ERR_INVALID_ARG
+    # h may alias x (in-place residual), never o: the few-row kernel reads
+    # every row of o while other workgroups already write h
+    with pytest.raises(vva.VvaError) as e:
+        ctx.out_proj_residual(o, w, x, o)
+    assert e.value.status == vva.ERR_INVALID_ARG and "overlaps" in str(e.value)
+    ctx.out_proj_residual(o, w, x, x)                  # h == x is allowed
+    torch.cuda.synchronize()
     kv = vva.KVCache(ctx, 1, 2, 64, 8, 1, vva.F16)
     kv.set_len(0, 6)
     q = torch.zeros((1, 4, 14, 64), dtype=torch.float32, device="cuda")

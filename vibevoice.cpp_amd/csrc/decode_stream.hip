@@ -11,7 +11,7 @@
 // ring filled by buffer_load_dwordx4 ... lds (non-temporal: the cache is read
 // once), so two tiles (70 KB per CU) are on their way from HBM while one is
 // computed.  A tile is 512 (key, kv head, 32-dim block) rows of the cache =
-// 17,408 B of K plus the same of V, read as the cache lays them out
+// 17,408 B of K plus the same of V (256 rows at d = 64), read as the cache lays them out
 // ([token][kv head][34-byte GGUF block]): one contiguous byte range per
 // operand, 1 KB per wave instruction.  The buffer ranges end at the
 // sequence's last key, so chunks past it come back as zeros without a
@@ -74,7 +74,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kW = 4;                        // compute waves per workgroup (one per SIMD)
 constexpr int kP = 3;                        // producer waves: they only issue the tile loads and wait
 constexpr int kStages = 4;                   // LDS ring depth (power of 2)
-constexpr int kTileOpBytes = 17408;          // one operand of a tile: 512 Q8_0 blocks
+constexpr int kTileOpBytes = 17408;          // one operand of a tile: 512 Q8_0 blocks (d = 128; 256 at d = 64)
 constexpr int kOpChunks = 18;                // 1 KB chunks per operand: 17 KB + alignment slack
 constexpr int kOpBytes = kOpChunks * 1024;
 constexpr int kStage = 2 * kOpBytes;         // K, then V
@@ -152,6 +152,12 @@ __device__ __forceinline__ h4 as_h4(uint32_t lo, uint32_t hi) {
     return v;
 }
 __device__ __forceinline__ h4 cat_h4(h2 lo, h2 hi) { return h4{lo[0], lo[1], hi[0], hi[1]}; }
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ u16x2 as_u16x2(uint32_t w) {
+    u16x2 v;
+    __builtin_memcpy(&v, &w, 4);
+    return v;
+}
 
 // D: head dim (64 / 128); HKV: kv heads of the workgroup's tile (1, 2, 4,
 // 8), which fixes the row pitch in LDS, so every LDS offset inside a tile is
@@ -169,12 +175,19 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, StreamSte
     constexpr int RB = HKV * HB;              // bytes per token row in LDS (the group's kv heads)
     constexpr int RBM = NHG * RB;             // bytes per token row in the cache
     static_assert(NHG == 1 || RB % 16 == 0, "16-byte pieces of a row slice");
-    constexpr int TT = kTileOpBytes / RB;     // keys per tile
+    // d = 64 tiles hold half the bytes, so that every wave takes one slot
+    // pair per tile at both head dims (two pairs at d = 64 would need more
+    // than the 256 VGPRs of a wave)
+    constexpr int TB = D == 64 ? kTileOpBytes / 2 : kTileOpBytes;   // bytes per operand and tile
+    constexpr int OPL = D == 64 ? kOpLoads / 2 : kOpLoads;          // DMA loads per producer, operand and tile
+    constexpr int LD = 2 * OPL;                                     // DMA loads per producer per tile
+    static_assert(OPL * kP * 1024 >= TB + 16, "a tile's chunks cover it at any 16-byte delta");
+    constexpr int TT = TB / RB;               // keys per tile
     constexpr int NPAIR = TT * HKV / 32;      // slot pairs (2 slots of 16 keys x 1 kv head) per tile
     constexpr int NSUB = NPAIR / kW;          // slot pairs per wave per tile
     constexpr int HP = HKV >= 2 ? HKV / 2 : 1;    // kv head pairs
     constexpr int NJ = 2 * NB;                // P.V MFMAs (16 dims each) per slot
-    static_assert(TT * RB == kTileOpBytes && NSUB * kW == NPAIR && NSUB >= 1, "tile size");
+    static_assert(TT * RB == TB && NSUB * kW == NPAIR && NSUB >= 1, "tile size");
     static_assert(kW % HP == 0, "a wave keeps its head pair across its slot pairs");
 
     // step mode: the RoPE angle table and the new K and V rows after the ring
@@ -252,11 +265,11 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, StreamSte
     // B (Q quantized), one per tile t (tile t landed, every compute wave done
     // with tile t - 1, so the stage of tile t - 2 takes tile t + 2), then the
     // two barriers of the epilogue.
-    // Tile t of an operand is bytes [t * 17408, t * 17408 + 18 KB) of its
-    // buffer: 18 chunks of 1 KB, chunk c loaded by producer c % kP.  A tile
-    // past the last one loads nothing but zeros (offsets past the range: no
-    // memory access); the 18th chunk of an operand is needed only when
-    // delta > 0.
+    // A tile of an operand is TB bytes of its buffer from the tile's first
+    // key on (17,408 B, or 8,704 B at d = 64), loaded as 1 KB chunks, chunk c
+    // by producer c % kP; the chunk holding the 16-byte delta's overhang is
+    // loaded only when delta > 0.  A tile past the last one loads nothing
+    // but zeros (offsets past the range: no memory access).
     const int eb = (int)type_elem_bytes(a.q_type);
     if (w >= kW) {
         const int pw = w - kW;
@@ -264,9 +277,9 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, StreamSte
         // c of tile 0: the tile is contiguous in the cache (NHG = 1), or the
         // group's RB-byte slice of each of its rows (NHG > 1).  Tile t is
         // t * TT rows on.
-        int loff[kOpLoads];
+        int loff[OPL];
 #pragma unroll
-        for (int i = 0; i < kOpLoads; ++i) {
+        for (int i = 0; i < OPL; ++i) {
             const int bt = (pw + kP * i) * 1024 + lane * 16;
             loff[i] = NHG == 1 ? bt : (bt / RB) * RBM + hgrp * RB + bt % RB;
         }
@@ -279,9 +292,9 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, StreamSte
 #pragma unroll
             for (int op = 0; op < 2; ++op)
 #pragma unroll
-                for (int i = 0; i < kOpLoads; ++i) {
+                for (int i = 0; i < OPL; ++i) {
                     const int c = pw + kP * i;
-                    const bool need = live && (c < kOpChunks - 1 || (op ? dv : dk) > 0);
+                    const bool need = live && c * 1024 < TB + (op ? dv : dk);
                     dma16<true>(op ? vs : ks, st + op * kOpBytes + c * 1024, need ? tb + loff[i] : kDead);
                 }
         };
@@ -303,10 +316,10 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, StreamSte
         // slower: Q lands later behind them and every tile waits for Q.
         issue(0);
         issue(1);
-        wait_vm_barrier<2 * kLoads>();               // A: Q landed
-        wait_vm_barrier<2 * kLoads>();               // B
+        wait_vm_barrier<2 * LD>();                   // A: Q landed
+        wait_vm_barrier<2 * LD>();                   // B
         for (int t = 0; t < n_tiles; ++t) {
-            wait_vm_barrier<kLoads>();               // T_t: tile t landed
+            wait_vm_barrier<LD>();                   // T_t: tile t landed
             if (STEP && t == new_t) lds_barrier();   // N: the new row is in tile t's stage
             issue(t + 2);
         }
@@ -530,6 +543,17 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, StreamSte
     for (int s = 0; s < 2; ++s)
 #pragma unroll
         for (int j = 0; j < NJ; ++j) acc[s][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    // V-range exponent of row n.  P' = p * d_v is an f16 MFMA operand and p
+    // <= 2^8, so a V block scale d_v >= 2^8 could overflow it.  Once a tile
+    // of the row holds such a block, the row's exp2 base is raised by e
+    // beyond its running max (mb = m + e, so p <= 2^(8 - e)) and P' =
+    // f16(p * d_v) is formed in fp32, with e = x - 6 for the largest d_v in
+    // [2^x, 2^(x+1)) seen so far (P' < 2^15).  The row's record carries m + e
+    // as its max, so records on different bases merge exactly.  Caches whose
+    // d_v stay below 2^8 (|V| <= 32512) never take this path, so their
+    // results are those of the plain f16 P'.
+    int vexp = 0;
+    bool vscaled = false;                     // wave-uniform: some row of the wave has e > 0
     const char* mrow = a.mask_mode == kMaskExplicit ? a.mask + b * a.mask_nb_b : nullptr;   // query row 0
     // LDS offsets from a slot pair's first key.  Score A operand: key
     // sigma(n) = 4 (n % 4) + n / 4 of slot g >> 1, codes 8 (g & 1) .. of each
@@ -669,28 +693,81 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, StreamSte
 #pragma unroll
                     for (int j = 0; j < NJ; ++j) acc[s][j] *= alpha;
                 m = cm;
-                mb = cm;
+                mb = cm + (float)vexp;
             }
         }
     };
-    // p = 2^(s - mb) of one slot pair, its row sums, and its P' = p * d_v.
+    // The V block scales of keys 0, 1 (h = 0) or 2, 3 (h = 1) of a slot pair,
+    // block bb, as an f16 pair.
+    auto pair_dv = [&](const PairOps& o, int bb, int h) {
+        const uint32_t sel = (bb & 1) ? 0x07060302u : 0x05040100u;          // high or low halves
+        return __builtin_amdgcn_perm(o.vd[2 * h + 1][bb], o.vd[2 * h][bb], sel);
+    };
+    // Raises row n's V-range exponent when a block of the tile has d_v >=
+    // 2^8 (e = 0) or 2^(7 + e) (d_v >= 0, so f16 bits compare as integers).  Called after
+    // the softmax rescale, when every pending P.V is in acc, before the
+    // tile's P' is formed.  The test reads the scale dwords as they are:
+    // even blocks hold d_v in the low half, odd blocks in the high half.
+    auto vrange = [&](const PairOps (&ops)[NSUB]) {
+        u16x2 me = {0, 0}, mo = {0, 0};
+#pragma unroll
+        for (int u = 0; u < NSUB; ++u)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int bb = 0; bb < NB; ++bb) {
+                    if (bb & 1) mo = __builtin_elementwise_max(mo, as_u16x2(ops[u].vd[i][bb]));
+                    else me = __builtin_elementwise_max(me, as_u16x2(ops[u].vd[i][bb]));
+                }
+        uint32_t m16 = __builtin_elementwise_max((uint32_t)me[0], (uint32_t)mo[1]);
+        const uint32_t lim = __builtin_elementwise_max(0x5c00u, 0x5800u + ((uint32_t)vexp << 10));
+        if (__any(m16 >= lim)) {
+            // row n's max over the four lane groups
+            auto r16 = __builtin_amdgcn_permlane16_swap(m16, m16, false, false);
+            m16 = __builtin_elementwise_max(r16[0], r16[1]);
+            auto r32 = __builtin_amdgcn_permlane32_swap(m16, m16, false, false);
+            m16 = __builtin_elementwise_max(r32[0], r32[1]);
+            const int need = m16 >= lim ? (int)(m16 >> 10) - 15 - 6 : vexp;
+            const float f = __builtin_amdgcn_ldexpf(1.0f, vexp - need);
+            l *= f;
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) acc[s2][j] *= f;
+            mb += (float)(need - vexp);
+            vexp = need;
+            vscaled = true;
+        }
+    };
+    // p = 2^(s - mb) of one slot pair, its row sums, and its P' = p * d_v
+    // (formed in fp32 once the wave's V range needs it).
     auto group_probs = [&](const PairOps& o, const float (&sc)[4], PendingPV& cur) {
         float p[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(sc[i] - mb);   // 0 when masked
         l += (p[0] + p[1]) + (p[2] + p[3]);
-        const h2 p01 = h2{(_Float16)p[0], (_Float16)p[1]};
-        const h2 p23 = h2{(_Float16)p[2], (_Float16)p[3]};
-
+        if (!vscaled) {
+            const h2 p01 = h2{(_Float16)p[0], (_Float16)p[1]};
+            const h2 p23 = h2{(_Float16)p[2], (_Float16)p[3]};
 #pragma unroll
-        for (int bb = 0; bb < NB; ++bb) {
-            const uint32_t sel = (bb & 1) ? 0x07060302u : 0x05040100u;      // high or low halves
-            h2 dv01, dv23;
-            const uint32_t u01 = __builtin_amdgcn_perm(o.vd[1][bb], o.vd[0][bb], sel);
-            const uint32_t u23 = __builtin_amdgcn_perm(o.vd[3][bb], o.vd[2][bb], sel);
-            __builtin_memcpy(&dv01, &u01, 4);
-            __builtin_memcpy(&dv23, &u23, 4);
-            cur.pb[bb] = cat_h4(p01 * dv01, p23 * dv23);
+            for (int bb = 0; bb < NB; ++bb) {
+                h2 dv01, dv23;
+                const uint32_t u01 = pair_dv(o, bb, 0), u23 = pair_dv(o, bb, 1);
+                __builtin_memcpy(&dv01, &u01, 4);
+                __builtin_memcpy(&dv23, &u23, 4);
+                cur.pb[bb] = cat_h4(p01 * dv01, p23 * dv23);
+            }
+        } else {
+#pragma unroll
+            for (int bb = 0; bb < NB; ++bb) {
+                h4 r;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t w = pair_dv(o, bb, i >> 1);
+                    r[i] = (_Float16)(p[i] * f16_to_f32((uint16_t)((i & 1) ? (w >> 16) : (w & 0xffffu))));
+                }
+                cur.pb[bb] = r;
+            }
         }
     };
 
@@ -739,6 +816,7 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, StreamSte
 #pragma unroll
         for (int u = 0; u < NSUB; ++u) smax = fmaxf(smax, fmaxf(fmaxf(sc[u][0], sc[u][1]), fmaxf(sc[u][2], sc[u][3])));
         rescale(smax);
+        vrange(ops);
 #pragma unroll
         for (int u = 0; u < NSUB; ++u) group_probs(ops[u], sc[u], cur[u]);
     };
@@ -785,7 +863,7 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, StreamSte
             *(float4*)(prow + 32 * bb + 8 * g) = make_float4(e[0], o[0], e[1], o[1]);
             *(float4*)(prow + 32 * bb + 8 * g + 4) = make_float4(e[2], o[2], e[3], o[3]);
         }
-        if (g == 0) { prow[D] = m; prow[D + 1] = l; }
+        if (g == 0) { prow[D] = m + (float)vexp; prow[D + 1] = l; }   // the record's base (-inf stays -inf)
     }
     __syncthreads();
 

@@ -134,6 +134,20 @@ char* kv_tensor(const vva_kv* kv, int layer, int seq, int which) {
     return kv->base + idx * kv->tensor_bytes;
 }
 
+// Bytes [data, data + span) a tensor's elements occupy (ne >= 1 everywhere).
+// For Q8_0, ne[0] counts elements and nb[0] is the 34-byte block.
+size_t tensor_span(const vva_tensor* t) {
+    const bool q8 = t->type == VVA_TYPE_Q8_0;
+    int64_t last = ((q8 ? t->ne[0] / kQK8 : t->ne[0]) - 1) * (int64_t)t->nb[0];
+    for (int i = 1; i < 4; ++i) last += (t->ne[i] - 1) * (int64_t)t->nb[i];
+    const int64_t eb = q8 ? kQ8Bytes : type_elem_bytes(t->type);
+    return (size_t)(last + (eb > 0 ? eb : 1));
+}
+bool overlaps(const vva_tensor* a, const vva_tensor* b) {
+    const uintptr_t a0 = (uintptr_t)a->data, b0 = (uintptr_t)b->data;
+    return a0 < b0 + tensor_span(b) && b0 < a0 + tensor_span(a);
+}
+
 vva_status check_tensor(vva_context* ctx, const vva_tensor* t, const char* name) {
     if (!t || !t->data) return fail(ctx, VVA_ERR_INVALID_ARG, "%s: null tensor", name);
     for (int i = 0; i < 4; ++i)
@@ -145,7 +159,10 @@ vva_status check_tensor(vva_context* ctx, const vva_tensor* t, const char* name)
 // allocates, which a stream under HIP graph capture must not do: such a call
 // fails with VVA_ERR_INVALID_ARG (run one call of the largest shape before
 // capturing).  The outgrown workspace is retired, not freed (see
-// vva_context::ws_retired).
+// vva_context::ws_retired).  The size at least doubles at every growth (a
+// power of two, 1 MiB at least), so the retired buffers together never
+// exceed the live one: a chunked prefill whose window grows by one chunk per
+// call retires O(log n) buffers, not one per chunk.
 vva_status ensure_ws(vva_context* ctx, size_t bytes) {
     if (bytes <= ctx->ws_bytes) return VVA_OK;
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
@@ -153,7 +170,8 @@ vva_status ensure_ws(vva_context* ctx, size_t bytes) {
         return fail(ctx, VVA_ERR_INVALID_ARG,
                     "split workspace must grow to %zu bytes during stream capture; run one call of this "
                     "shape before capturing", bytes);
-    size_t sz = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
+    size_t sz = (size_t)1 << 20;
+    while (sz < bytes) sz <<= 1;
     float* p = nullptr;
     hipError_t e = hipMalloc(&p, sz);
     if (e != hipSuccess) return hip_fail(ctx, e, "hipMalloc(split workspace)");
@@ -225,8 +243,10 @@ vva_status run_attention(vva_context* ctx, AttnArgs& a, bool fixed = false) {
     // Q8_0 windows, and F32 windows under flash-attention semantics (the
     // reference casts them to F16 before ggml_flash_attn_ext,
     // src/qwen2.cpp:328-331): converted to f16 on the device, then the MFMA
-    // prefill (Q through a Q8_0 round trip for Q8_0 K, ggml's dot type).
-    // Not on the no-allocation path, whose scratch cannot hold a window.
+    // prefill (Q through a Q8_0 round trip for Q8_0 K, ggml's dot type).  On
+    // the no-allocation path the converted window and the split partials
+    // share the static scratch; a call whose window does not fit there is
+    // refused rather than sent to a different kernel.
     const bool convert = a.k_type == a.v_type &&
                          (a.k_type == VVA_TYPE_Q8_0 || (a.k_type == VVA_TYPE_F32 && ctx->use_flash_attn));
     // prefill plan of call shape c, reused while the shape repeats
@@ -244,7 +264,7 @@ vva_status run_attention(vva_context* ctx, AttnArgs& a, bool fixed = false) {
         }
         return ctx->plan;
     };
-    if (ctx->attn_path != 1 && a.T > 1 && convert && !fixed && (a.d == 64 || a.d == 128)) {
+    if (ctx->attn_path != 1 && a.T > 1 && convert && (a.d == 64 || a.d == 128)) {
         AttnArgs c = a;
         const size_t wb = window_f16_bytes(a);
         c.k_type = c.v_type = VVA_TYPE_F16;
@@ -255,10 +275,24 @@ vva_status run_attention(vva_context* ctx, AttnArgs& a, bool fixed = false) {
         // with the final alignment for the support check
         for (int b = 0; b < a.B; ++b) c.k[b] = c.v[b] = (const char*)(uintptr_t)256;
         if (prefill_supported(c)) {
-            const PrefillPlan plan = plan_for(c, (size_t)1 << 34);
-            vva_status st = ensure_ws(ctx, wb + prefill_ws_bytes(c, plan));
-            if (st != VVA_OK) return st;
-            char* wbase = (char*)ctx->ws;
+            if (fixed && wb >= kScratchBytes)
+                return fail(ctx, VVA_ERR_NOT_IMPLEMENTED,
+                            "attn_noalloc: the f16 window of this %s cache (%zu bytes) does not fit the %zu-byte "
+                            "static scratch", a.k_type == VVA_TYPE_Q8_0 ? "Q8_0" : "F32", wb, kScratchBytes);
+            const PrefillPlan plan = plan_for(c, fixed ? kScratchBytes - wb : ((size_t)1 << 34));
+            const size_t need = wb + prefill_ws_bytes(c, plan);
+            char* wbase = nullptr;
+            if (fixed) {
+                if (need > kScratchBytes)
+                    return fail(ctx, VVA_ERR_NOT_IMPLEMENTED,
+                                "attn_noalloc: the f16 window and split partials of this call (%zu bytes) do not "
+                                "fit the %zu-byte static scratch", need, kScratchBytes);
+                wbase = (char*)ctx->scratch;
+            } else {
+                vva_status st = ensure_ws(ctx, need);
+                if (st != VVA_OK) return st;
+                wbase = (char*)ctx->ws;
+            }
             size_t off = 0;
             for (int b = 0; b < a.B; ++b) {
                 c.k[b] = wbase + off;
@@ -996,6 +1030,11 @@ extern "C" vva_status vva_out_proj_residual(vva_context* ctx, const vva_tensor* 
     if ((uintptr_t)x->data % 16 || x->nb[1] % 16 || x->nb[2] % 16 || (uintptr_t)h->data % 16 || h->nb[1] % 16 ||
         h->nb[2] % 16)
         return fail(ctx, VVA_ERR_INVALID_ARG, "out_proj_residual: x and h rows must be 16-byte aligned");
+    // h may alias x (the residual added in place), never o or the weights:
+    // the few-row kernel reads every row of o in each workgroup while others
+    // already write h
+    if (overlaps(h, o) || overlaps(h, w_o))
+        return fail(ctx, VVA_ERR_INVALID_ARG, "out_proj_residual: h overlaps o or w_o (only h == x may alias)");
     const int64_t N = T * B;
     if (N * K * 2 >= ((int64_t)1 << 31) || 128 * K * 2 >= ((int64_t)1 << 31))
         return fail(ctx, VVA_ERR_NOT_IMPLEMENTED, "out_proj_residual: %lld x %lld inputs exceed 2 GiB", (long long)N,
