@@ -170,7 +170,9 @@ VVA_API vva_status vva_rope_append(vva_context* ctx, vva_kv* kv, int layer,
  *         keys (the T new rows were appended by vva_rope_append);
  *   mask: NULL for implicit causal masking (key j visible to query row i
  *         iff j <= len(seq_b) + i), or F16 ne = [>=L_b, T, 1, 1 or B] with
- *         0 / -inf entries as built at src/vibevoice_asr.cpp:616-627;
+ *         0 / -inf entries as built at src/vibevoice_asr.cpp:616-627; F32
+ *         masks (ggml_soft_max_ext's type, the eager branch
+ *         src/qwen2.cpp:336-344) are read as F32;
  *   out:  F32 ne = [d, Hq, T, B], the FA output layout (src/qwen2.cpp:156-159).
  * Q is rounded to the dot type of K as ggml's CPU FA does (F16 -> f16,
  * BF16 -> bf16, Q8_0 -> Q8_0 blocks, F32 -> f32, or f16 under
@@ -222,7 +224,7 @@ VVA_API vva_status vva_attn_noalloc(vva_context* ctx, const vva_kv* kv, int laye
  *   q: ne = [d, T, Hq, B] (F32 / F16 / BF16)  — the permuted q_p of
  *      src/qwen2.cpp:320;
  *   k, v: ne = [d, L, Hkv, B] (F32 / F16 / BF16 / Q8_0), any strides;
- *   mask: NULL (no masking, as in ggml) or F16 ne = [>=L, T, 1, 1 or B];
+ *   mask: NULL (no masking, as in ggml) or F16 / F32 ne = [>=L, T, 1, 1 or B];
  *   dst: F32 ne = [d, Hq, T, B] (contiguous rows of d).
  * max_bias and logit_softcap must be 0 (the reference passes 0, 0 at
  * src/qwen2.cpp:332-333); anything else returns VVA_ERR_NOT_IMPLEMENTED. */

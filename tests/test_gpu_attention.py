@@ -264,3 +264,95 @@ def test_empty_calls_are_rejected(ctx, torch_gpu):
         assert err.value.status == vva.ERR_INVALID_ARG, err.value
     assert kv.get_len(0) == 0
     kv.free()
+
+
+MASK_PATHS = [
+    # d, Hq, Hkv, cache type, T, past, flash branch, q type — the kernel each reaches
+    (128, 12, 2, vva.F32, 9, 600, False, vva.F32),     # fp32 eager rows (the reference's F32-mask branch)
+    (128, 28, 4, vva.Q8_0, 1, 3000, True, vva.F32),    # streamed Q8_0 decode
+    (64, 14, 2, vva.F16, 1, 1500, True, vva.F32),      # register-streamed decode
+    (128, 28, 4, vva.F16, 64, 900, True, vva.F16),     # MFMA prefill
+]
+
+
+@pytest.mark.parametrize("d,Hq,Hkv,t,T,past,flash,qt", MASK_PATHS)
+def test_f32_mask_equals_f16_mask(ctx, torch_gpu, d, Hq, Hkv, t, T, past, flash, qt):
+    """An F32 mask (ggml_soft_max_ext's type, src/qwen2.hpp:34-37) holding
+    the values of an F16 mask (0, -inf holes, a fully masked row and finite
+    biases that f16 represents) gives the same output bit for bit on every
+    kernel path; it also matches the oracle run with the F16 mask."""
+    torch = torch_gpu
+    print(f"f32 mask d={d} type={t} T={T} past={past} flash={flash}", flush=True)
+    L = past + T
+    kv = vva.KVCache(ctx, 1, Hkv, d, L, 1, t)
+    fill_cache(kv, [L], seed=L + d)
+    kv.set_len(0, past)
+    rng = np.random.default_rng(L)
+    m = np.where(rng.random((1, T, L)) < 0.15, -np.inf, 0.0).astype(np.float32)
+    m += np.where(np.isfinite(m), np.round(rng.uniform(-2.0, 0.0, m.shape) * 64) / 64, 0.0).astype(np.float32)
+    if T > 1:
+        m[0, T - 1, :] = -np.inf                              # a row with nothing visible: output 0
+    mbits = vvo.f16_bits(m)
+    assert np.array_equal(mbits.view(np.float16).astype(np.float32), m)
+    q = to_gpu(torch, rng.standard_normal((1, T, Hq, d)), qt)
+    outs = []
+    ctx.set_flash_attn(flash)
+    try:
+        for mt in (torch.from_numpy(mbits.view(np.float16)).cuda(), torch.from_numpy(m).cuda()):
+            out = torch.full((1, T, Hq, d), float("nan"), dtype=torch.float32, device="cuda")
+            ctx.attn(kv, 0, q, out, d ** -0.5, mask=mt)
+            torch.cuda.synchronize()
+            outs.append(as_f32(torch, out))
+    finally:
+        ctx.set_flash_attn(True)
+    assert np.array_equal(outs[0], outs[1]), "F32 mask result differs from the F16 mask's"
+    ref = oracle_attn(as_f32(torch, q), kv, 0, [0], [L], T, d ** -0.5, mask=mbits)
+    mx, mn = assert_close(outs[1], ref, *TOL[t], what="F32 mask vs oracle")
+    print(f"  bit-equal to the F16 mask; vs oracle max {mx:.2e} mean {mn:.2e}")
+    kv.free()
+
+
+def test_f32_mask_beyond_f16_precision_eager_branch(ctx, torch_gpu):
+    """The eager branch reads F32 mask entries at full precision: biases
+    that f16 cannot hold (random fp32 in [-12, 0]) match an fp64 brute force
+    softmax(scale q k^T + mask) v on the downloaded F32 cache, 1e-4."""
+    torch = torch_gpu
+    d, Hq, Hkv, T, past = 64, 14, 2, 5, 200
+    L = past + T
+    kv = vva.KVCache(ctx, 1, Hkv, d, L, 1, vva.F32)
+    fill_cache(kv, [L], seed=9, scale=2.0)
+    kv.set_len(0, past)
+    rng = np.random.default_rng(10)
+    m = rng.uniform(-12.0, 0.0, (1, T, L)).astype(np.float32)
+    m[0, :, 17] = -np.inf
+    q = to_gpu(torch, rng.standard_normal((1, T, Hq, d)), vva.F32)
+    out = torch.full((1, T, Hq, d), float("nan"), dtype=torch.float32, device="cuda")
+    ctx.set_flash_attn(False)
+    try:
+        ctx.attn(kv, 0, q, out, d ** -0.5, mask=torch.from_numpy(m).cuda())
+        torch.cuda.synchronize()
+    finally:
+        ctx.set_flash_attn(True)
+    k, v = kv.download(0, 0, L)                              # raw bytes of the F32 rows
+    k = np.ascontiguousarray(k).view(np.float32).reshape(L, Hkv, d).astype(np.float64)
+    v = np.ascontiguousarray(v).view(np.float32).reshape(L, Hkv, d).astype(np.float64)
+    q64 = as_f32(torch, q).reshape(T, Hq, d).astype(np.float64)
+    ref = np.zeros((T, Hq, d))
+    g = Hq // Hkv
+    for h in range(Hq):
+        s = q64[:, h, :] @ k[:, h // g, :].T * d ** -0.5 + m[0].astype(np.float64)
+        p = np.exp(s - s.max(axis=1, keepdims=True))
+        ref[:, h, :] = (p / p.sum(axis=1, keepdims=True)) @ v[:, h // g, :]
+    got = as_f32(torch, out).reshape(T, Hq, d)
+    mx, mn = assert_close(got, ref, 1e-4, 1e-4, what="eager branch, fp32 mask")
+    # the f16-rounded mask moves the result by more than the tolerance: the
+    # test would catch a kernel that rounds F32 mask entries to f16
+    m16 = vvo.f16_bits(m).view(np.float16).astype(np.float64)
+    ref16 = np.zeros_like(ref)
+    for h in range(Hq):
+        s = q64[:, h, :] @ k[:, h // g, :].T * d ** -0.5 + m16[0]
+        p = np.exp(s - s.max(axis=1, keepdims=True))
+        ref16[:, h, :] = (p / p.sum(axis=1, keepdims=True)) @ v[:, h // g, :]
+    print(f"  vs fp64 max {mx:.2e}; the f16-rounded mask would be {np.abs(ref16 - ref).max():.2e} away")
+    assert np.abs(ref16 - ref).max() > 1e-4
+    kv.free()

@@ -90,7 +90,7 @@ __global__ void __launch_bounds__(256) attn_rows_kernel(AttnArgs a) {
             mv[u] = -INFINITY;
             if (j < jend) {
                 mv[u] = (a.mask_mode == kMaskExplicit)
-                            ? f16_to_f32(*(const uint16_t*)(mrow + 2 * (int64_t)j)) : 0.0f;
+                            ? mask_at(mrow, j, a.mask_f32) : 0.0f;
                 const char* kr = kbase + (int64_t)j * a.k_nb_tok;
 #pragma unroll
                 for (int r = 0; r < DPL; ++r) {
@@ -250,7 +250,7 @@ __global__ void __launch_bounds__(256) attn_rows_f32_kernel(AttnArgs a) {
         }
         float sc = -INFINITY;
         if (live) {
-            const float mv = (a.mask_mode == kMaskExplicit) ? f16_to_f32(*(const uint16_t*)(mrow + 2 * (int64_t)j)) : 0.0f;
+            const float mv = (a.mask_mode == kMaskExplicit) ? mask_at(mrow, j, a.mask_f32) : 0.0f;
             sc = mv == -INFINITY ? -INFINITY : (dot0 + dot1) * a.scale + mv;
         }
         const float mx = wave_max(sc);
@@ -405,7 +405,7 @@ __global__ void __launch_bounds__(64 * kGqaWaves) attn_gqa_f32_kernel(AttnArgs a
 #pragma unroll
             for (int r = 0; r < DPL; ++r)
                 vv[u][r] = lane + 64 * r < D ? *((const float*)(vr + (int64_t)min(u, nk - 1) * a.v_nb_tok) + lane + 64 * r) : 0.0f;
-        const float mv = live && a.mask_mode == kMaskExplicit ? f16_to_f32(*(const uint16_t*)(mrow + 2 * (int64_t)j)) : 0.0f;
+        const float mv = live && a.mask_mode == kMaskExplicit ? mask_at(mrow, j, a.mask_f32) : 0.0f;
         // every head slot in straight-line code (slots past G score -inf),
         // so that the heads' dot products and wave reductions interleave
         float sc[kGqaMaxG], p[kGqaMaxG], alpha[kGqaMaxG], mx[kGqaMaxG], ps[kGqaMaxG];

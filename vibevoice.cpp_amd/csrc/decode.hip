@@ -272,7 +272,7 @@ decode_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, int split_len) {
             const int j = i0 + st * TPS + tl;
             mv[st] = 0.0f;
             if (a.mask_mode == kMaskExplicit && j < j_end)
-                mv[st] = f16_to_f32(*(const uint16_t*)(mrow + 2 * (int64_t)j)) * kLog2e;
+                mv[st] = mask_at(mrow, j, a.mask_f32) * kLog2e;
             live[st] = j < j_end && mv[st] != -INFINITY;
             const uint32_t* kc = kbuf[st];
             if constexpr (Q8) {
@@ -622,7 +622,7 @@ bool decode_supported(const AttnArgs& a) {
     if (a.k_type != VVA_TYPE_F16 && a.k_type != VVA_TYPE_BF16 && a.k_type != VVA_TYPE_Q8_0) return false;
     if (a.Hq % a.Hkv != 0 || a.Hq / a.Hkv > 8) return false;
     if (kWaves % a.Hkv != 0) return false;
-    if (a.mask_mode == kMaskExplicit && (a.mask_nb_b % 2 != 0)) return false;
+    if (a.mask_mode == kMaskExplicit && (a.mask_nb_b % (a.mask_f32 ? 4 : 2) != 0)) return false;
     // vector-load alignment of cache rows, Q rows and output rows
     const int64_t need = a.k_type == VVA_TYPE_Q8_0 ? 4 : 16;
     if (a.k_nb_tok % need || a.k_nb_head % need || a.v_nb_tok % need || a.v_nb_head % need) return false;

@@ -670,7 +670,7 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, StreamSte
                 const int j = jt + kb + SK * sr + 4 * i + g;
                 bool live = j < jend;
                 if (mrow) {
-                    const float mv = live ? f16_to_f32(*(const uint16_t*)(mrow + 2 * (int64_t)j)) * kLog2e : 0.0f;
+                    const float mv = live ? mask_at(mrow, j, a.mask_f32) * kLog2e : 0.0f;
                     live = live && mv != -INFINITY;
                     sc[i] += mv;
                 }
@@ -970,7 +970,7 @@ bool decode_stream_supported(const AttnArgs& a) {
         // every buffer range and live offset stays below the padding offset
         if ((int64_t)(a.L[b] + 1) * a.k_nb_tok + 2 * kOpBytes >= kDead) return false;
     }
-    if (a.mask_mode == kMaskExplicit && (a.mask_nb_b % 2 != 0)) return false;
+    if (a.mask_mode == kMaskExplicit && (a.mask_nb_b % (a.mask_f32 ? 4 : 2) != 0)) return false;
     if (((uintptr_t)a.q % 16) || a.q_nb_h % 16 || a.q_nb_b % 16) return false;
     // Q rows contiguous and small enough for the raw-Q area, codes after them
     const int64_t qrow = (int64_t)a.d * type_elem_bytes(a.q_type);

@@ -357,7 +357,7 @@ __global__ void __launch_bounds__(kWaves * 64) prefill_kernel(AttnArgs a, float*
                 const int key = k0 + kt * 32 + 8 * (r / 4) + 4 * half + (r % 4);
                 float x = s[kt][r];
                 if constexpr (EXPL)
-                    x = fmaf(f16_to_f32(*(const uint16_t*)(mrow + 2 * min(key, L - 1))), inv_scale, x);
+                    x = fmaf(mask_at(mrow, min(key, L - 1), a.mask_f32), inv_scale, x);
                 s[kt][r] = key > lim ? -INFINITY : x;
             }
     };
@@ -776,7 +776,7 @@ bool prefill_supported(const AttnArgs& a) {
     }
     if (((uintptr_t)a.q % 16) || a.q_nb_t % 16 || a.q_nb_h % 16 || a.q_nb_b % 16) return false;
     if (((uintptr_t)a.out % 16) || a.o_nb_t % 16 || a.o_nb_h % 16 || a.o_nb_b % 16) return false;
-    if (a.mask_mode == kMaskExplicit && (a.mask_nb_row % 2 || a.mask_nb_b % 2)) return false;
+    if (a.mask_mode == kMaskExplicit && (a.mask_nb_row % (a.mask_f32 ? 4 : 2) || a.mask_nb_b % (a.mask_f32 ? 4 : 2))) return false;
     return true;
 }
 

@@ -327,8 +327,12 @@ vva_status fill_mask(vva_context* ctx, AttnArgs& a, const vva_tensor* mask, int 
     if (!mask) return VVA_OK;
     vva_status st = check_tensor(ctx, mask, "mask");
     if (st != VVA_OK) return st;
-    if (mask->type != VVA_TYPE_F16) return fail(ctx, VVA_ERR_INVALID_ARG, "mask must be F16");
-    if (mask->nb[0] != 2) return fail(ctx, VVA_ERR_INVALID_ARG, "mask rows must be contiguous");
+    // F16 (ggml_flash_attn_ext's mask type, the reference's callers) or F32
+    // (ggml_soft_max_ext's, the eager branch src/qwen2.cpp:336-344)
+    if (mask->type != VVA_TYPE_F16 && mask->type != VVA_TYPE_F32)
+        return fail(ctx, VVA_ERR_INVALID_ARG, "mask must be F16 or F32");
+    const size_t es = mask->type == VVA_TYPE_F32 ? 4 : 2;
+    if (mask->nb[0] != es) return fail(ctx, VVA_ERR_INVALID_ARG, "mask rows must be contiguous");
     if (mask->ne[0] < Lmax || mask->ne[1] < T)
         return fail(ctx, VVA_ERR_INVALID_ARG, "mask ne=[%lld,%lld] smaller than [L=%d,T=%d]",
                     (long long)mask->ne[0], (long long)mask->ne[1], Lmax, T);
@@ -339,6 +343,7 @@ vva_status fill_mask(vva_context* ctx, AttnArgs& a, const vva_tensor* mask, int 
     a.mask_nb_row = (int64_t)mask->nb[1];
     a.mask_nb_b = mask->ne[3] == 1 ? 0 : (int64_t)mask->nb[3];
     a.mask_mode = kMaskExplicit;
+    a.mask_f32 = mask->type == VVA_TYPE_F32;
     return VVA_OK;
 }
 

@@ -66,9 +66,10 @@ struct AttnArgs {
     int k_type, v_type;
     int L[kMaxBatch];
     int past[kMaxBatch];
-    const char* mask;                 // F16 rows (bytes strides)
+    const char* mask;                 // F16 or F32 rows (bytes strides)
     int64_t mask_nb_row, mask_nb_b;
     int mask_mode;                    // 0 none, 1 explicit, 2 causal
+    int mask_f32;                     // explicit mask rows are F32 (else F16)
     float scale;
     float* out;
     int64_t o_nb_t, o_nb_h, o_nb_b;   // in bytes
@@ -299,6 +300,10 @@ __device__ __forceinline__ float round_to_type(float f, int type) {
     if (type == VVA_TYPE_F16) return f16_to_f32(f32_to_f16(f));
     if (type == VVA_TYPE_BF16) return bf16_to_f32(f32_to_bf16(f));
     return f;
+}
+// element j of an explicit mask row (F32 or F16; -inf = masked)
+__device__ __forceinline__ float mask_at(const char* mrow, int64_t j, int f32) {
+    return f32 ? ((const float*)mrow)[j] : f16_to_f32(((const uint16_t*)mrow)[j]);
 }
 __device__ __forceinline__ float load_elem(const char* p, int type) {
     if (type == VVA_TYPE_F32) return *(const float*)p;

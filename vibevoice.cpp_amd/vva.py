@@ -290,11 +290,12 @@ def _ids(seq_ids):
 
 
 def _mask_view(mask) -> Tensor:
-    """mask: f16 torch [Bm, T, Lm] -> ggml ne=[Lm, T, 1, Bm]."""
+    """mask: f16 or f32 torch [Bm, T, Lm] -> ggml ne=[Lm, T, 1, Bm]."""
     Bm, T, Lm = mask.shape
     es = mask.element_size()
     return view(mask, ggml_ne=[Lm, T, 1, Bm],
-                ggml_nb=[es, mask.stride(1) * es, mask.stride(0) * es * T, mask.stride(0) * es], type_=F16)
+                ggml_nb=[es, mask.stride(1) * es, mask.stride(0) * es * T, mask.stride(0) * es],
+                type_=F32 if es == 4 else F16)
 
 
 class KVCache:
