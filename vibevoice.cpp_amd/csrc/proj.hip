@@ -1078,19 +1078,44 @@ __device__ __forceinline__ void x_from_raw(const ProjArgs& a, const u32x4 (&r)[E
     }
 }
 
-// What the output of lane (row m0 + r, token n = lane - r N) adds: its row's
-// bias (kProjQKV) or the residual (kProjResidual).  Loaded before the
-// weights, branch-free (lanes past the outputs and a missing bias read a
-// valid address and add 0), so that it is not a second round trip at the end.
+// The weight rows of a wave, as offsets from its slot's first row mrow0 (a
+// multiple of 4 within its matrix).  kProjQKVRope: the slot's 4 rows are two
+// NeoX rotation pairs of one head, dims 2w, 2w + 1, 2w + d/2 and 2w + d/2 + 1
+// for the slot's index w in the head, so the wave holds both members of each
+// pair; otherwise the slot's rows in order.
+template <int MODE>
+__device__ __forceinline__ void gemv_rofs(const ProjArgs& a, int mrow0, int (&ro)[kGvRows]) {
+    if constexpr (MODE == kProjQKVRope) {
+        const int P = a.d >> 1;
+        const int hr = mrow0 & (a.d - 1);                   // d is 64 or 128
+        const int w2 = 2 * (hr >> 2);
+        ro[0] = w2 - hr;
+        ro[1] = w2 + 1 - hr;
+        ro[2] = w2 + P - hr;
+        ro[3] = w2 + P + 1 - hr;
+    } else {
+#pragma unroll
+        for (int r = 0; r < kGvRows; ++r) ro[r] = r;
+    }
+}
+__device__ __forceinline__ int pick4(const int (&v)[kGvRows], int r) {
+    return r == 0 ? v[0] : r == 1 ? v[1] : r == 2 ? v[2] : v[3];
+}
+
+// What the output of lane (row r of the slot, token n = lane - r N) adds:
+// its row's bias (kProjQKV, kProjQKVRope) or the residual (kProjResidual).
+// Loaded before the weights, branch-free (lanes past the outputs and a
+// missing bias read a valid address and add 0), so that it is not a second
+// round trip at the end.
 template <int MODE>
 __device__ __forceinline__ float gemv_addend(const ProjArgs& a, int lane, int N, int m0, int mat, int mrow0,
-                                             const char* any) {
+                                             const char* any, const int (&ro)[kGvRows]) {
     const bool out = lane < kGvRows * N;
     const int l = out ? lane : 0;
     const int r = l / N, n = l - r * N;
-    if constexpr (MODE == kProjQKV) {
+    if constexpr (MODE != kProjResidual) {
         const float* bias = mat == 0 ? a.bias[0] : mat == 1 ? a.bias[1] : a.bias[2];
-        const float v = *(bias ? bias + mrow0 + r : (const float*)any);
+        const float v = *(bias ? bias + mrow0 + pick4(ro, r) : (const float*)any);
         return out && bias ? v : 0.0f;
     } else {
         const int b = n / a.T, t = n - b * a.T;
@@ -1109,6 +1134,39 @@ __device__ __forceinline__ void gemv_store(const ProjArgs& a, int lane, int N, i
             const int b = n / a.T, t = n - b * a.T;
             *(float*)(a.h + b * a.h_nb_b + t * a.h_nb_t + (int64_t)m * 4) = v;
         }
+    }
+}
+// kProjQKVRope epilogue: lane (r, n) holds projection + bias of dim 2w +
+// (r & 1) (+ d/2 for r >= 2) of its head for token n, and takes its
+// partner's value (row r ^ 2, same token) across the wave.  q and k rows are
+// rotated with the fp32 angle recurrence and the operation order of
+// rope_append.hip, so the stored values equal the GEMV + rope_append pair's;
+// q goes to q_out, k and v to the cache rows (F32 / F16 / BF16).
+__device__ __forceinline__ void gemv_rope_store(const ProjArgs& a, int lane, int N, int mat, int mrow0,
+                                                const int (&ro)[kGvRows], float v) {
+    const bool out = lane < kGvRows * N;
+    const int l = out ? lane : 0;
+    const int r = l / N, n = l - r * N;
+    const float vp = __shfl(v, (r ^ 2) * N + n);
+    if (!out) return;
+    const int P = a.d >> 1;
+    const int dim = (mrow0 & (a.d - 1)) + pick4(ro, r), head = mrow0 / a.d;
+    const int b = n / a.T, t = n - b * a.T;
+    float y = v;
+    if (mat < 2) {
+        const int i = dim & (P - 1);
+        const float th = rope_theta((float)a.pos[b * a.pos_stride_b + t], a.theta_scale, i, P);
+        const float c = cosf(th), sn = sinf(th);
+        const bool hi = r >= 2;
+        const float x0 = hi ? vp : v, x1 = hi ? v : vp;
+        y = hi ? fmaf(x0, sn, x1 * c) : fmaf(x0, c, -(x1 * sn));
+    }
+    if (mat == 0) {
+        store_elem(a.q_out + b * a.qo_nb_b + t * a.qo_nb_t + head * a.qo_nb_h + dim * type_elem_bytes(a.q_out_type),
+                   a.q_out_type, y);
+    } else {
+        char* row = (mat == 1 ? a.k_dst[b] : a.v_dst[b]) + t * a.cache_row_bytes + head * a.cache_head_bytes;
+        store_elem(row + dim * type_elem_bytes(a.cache_type), a.cache_type, y);
     }
 }
 
@@ -1141,7 +1199,9 @@ __global__ void __launch_bounds__(64 * kGvhWaves) proj_gemv_f16_kernel(ProjArgs 
     const int mrow0 = m0 - (mat == 0 ? 0 : mat == 1 ? a.m_end[0] : a.m_end[1]);
     const int64_t wnb = mat == 0 ? a.w_nb[0] : mat == 1 ? a.w_nb[1] : a.w_nb[2];
     const char* wb = (mat == 0 ? a.w[0] : mat == 1 ? a.w[1] : a.w[2]) + (int64_t)mrow0 * wnb;
-    const float addend = gemv_addend<MODE>(a, lane, N, m0, mat, mrow0, wb);
+    int ro[kGvRows];
+    gemv_rofs<MODE>(a, mrow0, ro);
+    const float addend = gemv_addend<MODE>(a, lane, N, m0, mat, mrow0, wb, ro);
     // token-row chunk t = (n, c): 16 bytes, and for F32 rows the next 16
     // (16-bit rows load the same 16 bytes twice: no branch, no read past the row)
     const bool f32 = a.x_type == VVA_TYPE_F32;
@@ -1164,7 +1224,7 @@ __global__ void __launch_bounds__(64 * kGvhWaves) proj_gemv_f16_kernel(ProjArgs 
         const int c = lane + 64 * it;
         const int cc = c < nch ? c : 0;
 #pragma unroll
-        for (int r = 0; r < kGvRows; ++r) wq[it][r] = *(const u32x4*)(wb + r * wnb + (int64_t)cc * 16);
+        for (int r = 0; r < kGvRows; ++r) wq[it][r] = *(const u32x4*)(wb + ro[r] * wnb + (int64_t)cc * 16);
     }
     const bool bf = a.x_type == VVA_TYPE_BF16;
 #pragma unroll
@@ -1221,7 +1281,8 @@ __global__ void __launch_bounds__(64 * kGvhWaves) proj_gemv_f16_kernel(ProjArgs 
             const float sum = wave_sum(acc[r][n]);
             if (n < N && lane == r * N + n) outv = sum;
         }
-    gemv_store<MODE>(a, lane, N, m0, outv + addend);
+    if constexpr (MODE == kProjQKVRope) gemv_rope_store(a, lane, N, mat, mrow0, ro, outv + addend);
+    else gemv_store<MODE>(a, lane, N, m0, outv + addend);
 }
 template <int MODE>
 hipError_t launch_gemv_f16(const ProjArgs& a, hipStream_t s) {
@@ -1260,7 +1321,9 @@ __global__ void __launch_bounds__(64 * kGv8Waves) proj_gemv_q8_kernel(ProjArgs a
     const int mrow0 = m0 - (mat == 0 ? 0 : mat == 1 ? a.m_end[0] : a.m_end[1]);
     const int64_t wnb = mat == 0 ? a.w_nb[0] : mat == 1 ? a.w_nb[1] : a.w_nb[2];
     const char* wb = (mat == 0 ? a.w[0] : mat == 1 ? a.w[1] : a.w[2]) + (int64_t)mrow0 * wnb;
-    const float addend = gemv_addend<MODE>(a, lane, N, m0, mat, mrow0, wb);
+    int ro[kGvRows];
+    gemv_rofs<MODE>(a, mrow0, ro);
+    const float addend = gemv_addend<MODE>(a, lane, N, m0, mat, mrow0, wb, ro);
     // this thread's first token-row block goes out ahead of the weights
     const int tasks = N * nbk;
     u32x4 xr0[8];
@@ -1290,7 +1353,7 @@ __global__ void __launch_bounds__(64 * kGv8Waves) proj_gemv_q8_kernel(ProjArgs a
         const int jj = j < nbk ? j : 0;
 #pragma unroll
         for (int r = 0; r < kGvRows; ++r) {
-            const uint32_t* p = (const uint32_t*)(wb + r * wnb + (((int64_t)jj * kQ8Bytes) & ~(int64_t)3));
+            const uint32_t* p = (const uint32_t*)(wb + ro[r] * wnb + (((int64_t)jj * kQ8Bytes) & ~(int64_t)3));
 #pragma unroll
             for (int i = 0; i < 9; ++i) qw[it][r][i] = p[i];
         }
@@ -1369,7 +1432,8 @@ __global__ void __launch_bounds__(64 * kGv8Waves) proj_gemv_q8_kernel(ProjArgs a
             const float sum = wave_sum(acc[r][n]);
             if (lane == r * N + n) outv = sum;
         }
-    gemv_store<MODE>(a, lane, N, m0, outv + addend);
+    if constexpr (MODE == kProjQKVRope) gemv_rope_store(a, lane, N, mat, mrow0, ro, outv + addend);
+    else gemv_store<MODE>(a, lane, N, m0, outv + addend);
 }
 
 }  // namespace
@@ -1378,17 +1442,41 @@ bool proj_gemv_supported(int N, int K, int M) {
     return N >= 1 && N <= kGvMaxN && K <= kGvMaxK && K % 64 == 0 && M % kGvRows == 0;
 }
 
+namespace {
+bool gemv_q8_ok(const ProjArgs& a) {
+    return a.w_type == VVA_TYPE_Q8_0 && a.M % kGv8Rows == 0 && a.m_end[0] % kGv8Rows == 0 &&
+           a.m_end[1] % kGv8Rows == 0;
+}
+bool gemv_f16_ok(const ProjArgs& a) {
+    return a.w_type == VVA_TYPE_F16 && a.N <= kGvhN && a.M % kGvhRows == 0 && a.m_end[0] % kGvhRows == 0 &&
+           a.m_end[1] % kGvhRows == 0;
+}
+}  // namespace
+
+bool proj_gemv_rope_ok(const ProjArgs& a) {
+    const bool float_cache = a.cache_type == VVA_TYPE_F32 || a.cache_type == VVA_TYPE_F16 ||
+                             a.cache_type == VVA_TYPE_BF16;
+    const bool float_q = a.q_out_type == VVA_TYPE_F32 || a.q_out_type == VVA_TYPE_F16 ||
+                         a.q_out_type == VVA_TYPE_BF16;
+    return a.mode == kProjQKV && float_cache && float_q && (a.d == 64 || a.d == 128) &&
+           a.m_end[0] % a.d == 0 && a.m_end[1] % a.d == 0 && (gemv_q8_ok(a) || gemv_f16_ok(a));
+}
+
 hipError_t launch_proj_gemv(ProjArgs& a, float* y_ws, hipStream_t s) {
     const bool q8 = a.w_type == VVA_TYPE_Q8_0;
     a.y = y_ws;
-    if (q8 && a.M % kGv8Rows == 0 && a.m_end[0] % kGv8Rows == 0 && a.m_end[1] % kGv8Rows == 0) {
+    if (gemv_q8_ok(a)) {
         const dim3 g8(a.M / kGv8Rows), b8(64 * kGv8Waves);
-        if (a.mode == kProjQKV) hipLaunchKernelGGL((proj_gemv_q8_kernel<kProjQKV>), g8, b8, 0, s, a);
-        else                    hipLaunchKernelGGL((proj_gemv_q8_kernel<kProjResidual>), g8, b8, 0, s, a);
+        if (a.mode == kProjQKVRope)  hipLaunchKernelGGL((proj_gemv_q8_kernel<kProjQKVRope>), g8, b8, 0, s, a);
+        else if (a.mode == kProjQKV) hipLaunchKernelGGL((proj_gemv_q8_kernel<kProjQKV>), g8, b8, 0, s, a);
+        else                         hipLaunchKernelGGL((proj_gemv_q8_kernel<kProjResidual>), g8, b8, 0, s, a);
         return hipGetLastError();
     }
-    if (!q8 && a.N <= kGvhN && a.M % kGvhRows == 0 && a.m_end[0] % kGvhRows == 0 && a.m_end[1] % kGvhRows == 0)
-        return a.mode == kProjQKV ? launch_gemv_f16<kProjQKV>(a, s) : launch_gemv_f16<kProjResidual>(a, s);
+    if (gemv_f16_ok(a))
+        return a.mode == kProjQKVRope ? launch_gemv_f16<kProjQKVRope>(a, s)
+               : a.mode == kProjQKV   ? launch_gemv_f16<kProjQKV>(a, s)
+                                      : launch_gemv_f16<kProjResidual>(a, s);
+    if (a.mode == kProjQKVRope) return hipErrorInvalidValue;
     const dim3 grid(a.M / kGvRows), block(64);
     if (a.mode == kProjQKV) {
         if (q8) hipLaunchKernelGGL((proj_gemv_kernel<true, kProjQKV>), grid, block, 0, s, a);

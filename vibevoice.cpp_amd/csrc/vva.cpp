@@ -990,10 +990,19 @@ extern "C" vva_status vva_qkv_rope_append(vva_context* ctx, vva_kv* kv, int laye
     p.theta_scale = powf(freq_base, -2.0f / (float)d);
     DeviceGuard g(ctx->device);
     if (proj_gemv_supported((int)N, (int)K, a.M) && rows16(x)) {
-        // a decode step: the weight-streaming GEMV writes the F32 projections,
-        // then the RoPE + append kernel rotates q and k and stores the rows
-        if ((st = ensure_ws(ctx, (size_t)N * a.M * sizeof(float))) != VVA_OK) return st;
+        // a decode step: the weight-streaming GEMV.  F32 / F16 / BF16 caches:
+        // it rotates q and k and stores q_out and the cache rows itself (each
+        // wave computes two whole rotation pairs), one launch.  Q8_0 caches
+        // (a block's scale needs 32 dims of a head): it writes the F32
+        // projections and the RoPE + append kernel quantizes and stores them.
         a.x = p.x; a.x_type = p.x_type; a.x_nb_t = p.x_nb_t; a.x_nb_b = p.x_nb_b;
+        a.pos = p.pos; a.pos_stride_b = p.pos_stride_b; a.theta_scale = p.theta_scale;
+        if (proj_gemv_rope_ok(a)) {
+            a.mode = kProjQKVRope;
+            hipError_t e = launch_proj_gemv(a, nullptr, ctx->stream);
+            return e == hipSuccess ? VVA_OK : hip_fail(ctx, e, "qkv_rope_append launch");
+        }
+        if ((st = ensure_ws(ctx, (size_t)N * a.M * sizeof(float))) != VVA_OK) return st;
         float* y = ctx->ws;
         hipError_t e = launch_proj_gemv(a, y, ctx->stream);
         if (e != hipSuccess) return hip_fail(ctx, e, "qkv_rope_append launch");

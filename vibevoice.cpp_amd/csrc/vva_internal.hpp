@@ -112,7 +112,9 @@ int decode_step_splits(const StepArgs& a);
 hipError_t launch_decode_step(const StepArgs& a, int n_splits, hipStream_t s);
 
 // Linear layers around the attention (proj.hip).  Token row n = b * T + t.
-enum { kProjQKV = 0, kProjResidual = 1 };
+// kProjQKVRope: the few-row GEMV of kProjQKV with the RoPE and the append in
+// its epilogue (F32 / F16 / BF16 caches)
+enum { kProjQKV = 0, kProjResidual = 1, kProjQKVRope = 2 };
 struct ProjPrepArgs {
     const char* x; int x_type; int64_t x_nb_t, x_nb_b;   // rows of K elements (F32 / F16 / BF16)
     int K, T, N;
@@ -153,6 +155,9 @@ struct ProjArgs {
     // kProjQKV: q_out and cache rows take 8-element vector stores (F32 / F16 /
     // BF16 destinations, 16-byte aligned rows); else one element per lane
     int vec_store;
+    // kProjQKVRope: the positions of the token rows and powf(base, -2 / d)
+    const int32_t* pos; int64_t pos_stride_b;
+    float theta_scale;
 };
 constexpr int kMaxProjTickets = 1024;
 // K split of the GEMM of a call (1: none; *tail0 > 0: only the last round's
@@ -228,6 +233,9 @@ hipError_t launch_proj(ProjPrepArgs& p, ProjArgs& a, void* ws, hipStream_t s);
 // at `ws`) for the caller's RoPE + append; kProjResidual writes h.
 bool proj_gemv_supported(int N, int K, int M);
 hipError_t launch_proj_gemv(ProjArgs& a, float* y_ws, hipStream_t s);
+// Whether launch_proj_gemv can run a kProjQKV call as kProjQKVRope (one
+// launch: projections, bias, RoPE and the append of F32 / F16 / BF16 rows).
+bool proj_gemv_rope_ok(const ProjArgs& a);
 
 }  // namespace vva
 
