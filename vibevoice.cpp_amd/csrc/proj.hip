@@ -1102,72 +1102,138 @@ __device__ __forceinline__ int pick4(const int (&v)[kGvRows], int r) {
     return r == 0 ? v[0] : r == 1 ? v[1] : r == 2 ? v[2] : v[3];
 }
 
+// Output lane l = r N + n of a slot: row r, token row n; token row n =
+// (sequence b, position t); MAXN = 2 (the decode step's one or two token
+// rows) takes shifts and compares instead of integer divisions.
+template <int MAXN>
+__device__ __forceinline__ void lane_rn(int l, int N, int& r, int& n) {
+    if constexpr (MAXN == 2) {
+        r = N == 2 ? l >> 1 : l;
+        n = N == 2 ? l & 1 : 0;
+    } else {
+        r = l / N;
+        n = l - r * N;
+    }
+}
+template <int MAXN>
+__device__ __forceinline__ void tok_bt(const ProjArgs& a, int n, int& b, int& t) {
+    if constexpr (MAXN == 2) {
+        b = n >= a.T ? 1 : 0;
+        t = n - b * a.T;
+    } else {
+        b = n / a.T;
+        t = n - b * a.T;
+    }
+}
+
 // What the output of lane (row r of the slot, token n = lane - r N) adds:
 // its row's bias (kProjQKV, kProjQKVRope) or the residual (kProjResidual).
 // Loaded before the weights, branch-free (lanes past the outputs and a
 // missing bias read a valid address and add 0), so that it is not a second
 // round trip at the end.
-template <int MODE>
+template <int MODE, int MAXN = kGvMaxN>
 __device__ __forceinline__ float gemv_addend(const ProjArgs& a, int lane, int N, int m0, int mat, int mrow0,
                                              const char* any, const int (&ro)[kGvRows]) {
     const bool out = lane < kGvRows * N;
     const int l = out ? lane : 0;
-    const int r = l / N, n = l - r * N;
+    int r, n;
+    lane_rn<MAXN>(l, N, r, n);
     if constexpr (MODE != kProjResidual) {
         const float* bias = mat == 0 ? a.bias[0] : mat == 1 ? a.bias[1] : a.bias[2];
         const float v = *(bias ? bias + mrow0 + pick4(ro, r) : (const float*)any);
         return out && bias ? v : 0.0f;
     } else {
-        const int b = n / a.T, t = n - b * a.T;
+        int b, t;
+        tok_bt<MAXN>(a, n, b, t);
         const float v = *(const float*)(a.res + b * a.res_nb_b + t * a.res_nb_t + (int64_t)(m0 + r) * 4);
         return out ? v : 0.0f;
     }
 }
-template <int MODE>
+template <int MODE, int MAXN = kGvMaxN>
 __device__ __forceinline__ void gemv_store(const ProjArgs& a, int lane, int N, int m0, float v) {
     if (lane < kGvRows * N) {
-        const int r = lane / N, n = lane - r * N;
+        int r, n;
+        lane_rn<MAXN>(lane, N, r, n);
         const int m = m0 + r;
         if constexpr (MODE == kProjQKV) {
             a.y[(int64_t)n * a.M + m] = v;
         } else {
-            const int b = n / a.T, t = n - b * a.T;
+            int b, t;
+            tok_bt<MAXN>(a, n, b, t);
             *(float*)(a.h + b * a.h_nb_b + t * a.h_nb_t + (int64_t)m * 4) = v;
         }
     }
 }
-// kProjQKVRope epilogue: lane (r, n) holds projection + bias of dim 2w +
-// (r & 1) (+ d/2 for r >= 2) of its head for token n, and takes its
-// partner's value (row r ^ 2, same token) across the wave.  q and k rows are
-// rotated with the fp32 angle recurrence and the operation order of
-// rope_append.hip, so the stored values equal the GEMV + rope_append pair's;
-// q goes to q_out, k and v to the cache rows (F32 / F16 / BF16).
-__device__ __forceinline__ void gemv_rope_store(const ProjArgs& a, int lane, int N, int mat, int mrow0,
-                                                const int (&ro)[kGvRows], float v) {
+// kProjQKVRope, lane (r, n) of a slot: its output is dim 2w + (r & 1) (+ d/2
+// for r >= 2) of the slot's head for token n.  Where it goes (q_out or the
+// cache row), the token's position and the dim's angle index, found before
+// the weight loads' wait so that none of it is a round trip at the end.
+struct RopeLane {
+    char* dst;
+    int pos;                                                // 0 for v rows and without POS
+    int i, r, n;                                            // angle index, slot row, token row
+};
+// arr[b] for b < NB, by selects of argument fields (no indexed load)
+template <int NB>
+__device__ __forceinline__ char* pick_ptr(char* const (&arr)[kMaxBatch], int b) {
+    static_assert(NB <= kMaxBatch, "batch index range");
+    char* p = arr[0];
+#pragma unroll
+    for (int i = 1; i < NB; ++i) p = b == i ? arr[i] : p;
+    return p;
+}
+template <bool POS, int MAXN = kGvMaxN>
+__device__ __forceinline__ RopeLane gemv_rope_lane(const ProjArgs& a, int lane, int N, int mat, int mrow0,
+                                                   const int (&ro)[kGvRows]) {
     const bool out = lane < kGvRows * N;
     const int l = out ? lane : 0;
-    const int r = l / N, n = l - r * N;
-    const float vp = __shfl(v, (r ^ 2) * N + n);
+    int r, n, b, t;
+    lane_rn<MAXN>(l, N, r, n);
+    tok_bt<MAXN>(a, n, b, t);
+    // d is 64 or 128; destinations are F32, F16 or BF16
+    const int dim = (mrow0 & (a.d - 1)) + pick4(ro, r), head = mrow0 >> (a.d == 128 ? 7 : 6);
+    const int qes = a.q_out_type == VVA_TYPE_F32 ? 4 : 2, ces = a.cache_type == VVA_TYPE_F32 ? 4 : 2;
+    RopeLane o;
+    o.pos = 0;
+    if constexpr (POS) o.pos = mat < 2 ? a.pos[b * a.pos_stride_b + t] : 0;
+    o.i = dim & ((a.d >> 1) - 1);
+    o.r = r;
+    o.n = n;
+    if (mat == 0)
+        o.dst = a.q_out + b * a.qo_nb_b + t * a.qo_nb_t + head * a.qo_nb_h + dim * qes;
+    else
+        o.dst = pick_ptr<MAXN>(mat == 1 ? a.k_dst : a.v_dst, b) + t * a.cache_row_bytes +
+                head * a.cache_head_bytes + dim * ces;
+    return o;
+}
+// kProjQKVRope epilogue: lane (r, n) holds projection + bias v and takes its
+// partner's value (row r ^ 2, same token) across the wave.  q and k rows are
+// rotated by the angle with cosine c and sine sn (the fp32 angle recurrence
+// and operation order of rope_append.hip), so the stored values equal the
+// GEMV + rope_append pair's; q goes to q_out, k and v to the cache rows
+// (F32 / F16 / BF16).
+__device__ __forceinline__ void gemv_rope_finish(const ProjArgs& a, int lane, int N, int mat, const RopeLane& rl,
+                                                 float c, float sn, float v) {
+    const bool out = lane < kGvRows * N;
+    const float vp = __shfl(v, (rl.r ^ 2) * N + rl.n);
     if (!out) return;
-    const int P = a.d >> 1;
-    const int dim = (mrow0 & (a.d - 1)) + pick4(ro, r), head = mrow0 / a.d;
-    const int b = n / a.T, t = n - b * a.T;
     float y = v;
     if (mat < 2) {
-        const int i = dim & (P - 1);
-        const float th = rope_theta((float)a.pos[b * a.pos_stride_b + t], a.theta_scale, i, P);
-        const float c = cosf(th), sn = sinf(th);
-        const bool hi = r >= 2;
+        const bool hi = rl.r >= 2;
         const float x0 = hi ? vp : v, x1 = hi ? v : vp;
         y = hi ? fmaf(x0, sn, x1 * c) : fmaf(x0, c, -(x1 * sn));
     }
-    if (mat == 0) {
-        store_elem(a.q_out + b * a.qo_nb_b + t * a.qo_nb_t + head * a.qo_nb_h + dim * type_elem_bytes(a.q_out_type),
-                   a.q_out_type, y);
-    } else {
-        char* row = (mat == 1 ? a.k_dst[b] : a.v_dst[b]) + t * a.cache_row_bytes + head * a.cache_head_bytes;
-        store_elem(row + dim * type_elem_bytes(a.cache_type), a.cache_type, y);
+    store_elem(rl.dst, mat == 0 ? a.q_out_type : a.cache_type, y);
+}
+__device__ __forceinline__ void gemv_rope_store(const ProjArgs& a, int lane, int N, int mat, const RopeLane& rl,
+                                                float v) {
+    float c = 1.0f, sn = 0.0f;
+    if (mat < 2) {
+        const float th = rope_theta((float)rl.pos, a.theta_scale, rl.i, a.d >> 1);
+        c = cosf(th);
+        sn = sinf(th);
     }
+    gemv_rope_finish(a, lane, N, mat, rl, c, sn, v);
 }
 
 // F16 weights, one or two token rows (the decode step), 8 weight rows per
@@ -1202,6 +1268,8 @@ __global__ void __launch_bounds__(64 * kGvhWaves) proj_gemv_f16_kernel(ProjArgs 
     int ro[kGvRows];
     gemv_rofs<MODE>(a, mrow0, ro);
     const float addend = gemv_addend<MODE>(a, lane, N, m0, mat, mrow0, wb, ro);
+    RopeLane rl{};
+    if constexpr (MODE == kProjQKVRope) rl = gemv_rope_lane<true>(a, lane, N, mat, mrow0, ro);
     // token-row chunk t = (n, c): 16 bytes, and for F32 rows the next 16
     // (16-bit rows load the same 16 bytes twice: no branch, no read past the row)
     const bool f32 = a.x_type == VVA_TYPE_F32;
@@ -1281,7 +1349,7 @@ __global__ void __launch_bounds__(64 * kGvhWaves) proj_gemv_f16_kernel(ProjArgs 
             const float sum = wave_sum(acc[r][n]);
             if (n < N && lane == r * N + n) outv = sum;
         }
-    if constexpr (MODE == kProjQKVRope) gemv_rope_store(a, lane, N, mat, mrow0, ro, outv + addend);
+    if constexpr (MODE == kProjQKVRope) gemv_rope_store(a, lane, N, mat, rl, outv + addend);
     else gemv_store<MODE>(a, lane, N, m0, outv + addend);
 }
 template <int MODE>
@@ -1324,6 +1392,8 @@ __global__ void __launch_bounds__(64 * kGv8Waves) proj_gemv_q8_kernel(ProjArgs a
     int ro[kGvRows];
     gemv_rofs<MODE>(a, mrow0, ro);
     const float addend = gemv_addend<MODE>(a, lane, N, m0, mat, mrow0, wb, ro);
+    RopeLane rl{};
+    if constexpr (MODE == kProjQKVRope) rl = gemv_rope_lane<true>(a, lane, N, mat, mrow0, ro);
     // this thread's first token-row block goes out ahead of the weights
     const int tasks = N * nbk;
     u32x4 xr0[8];
@@ -1432,7 +1502,7 @@ __global__ void __launch_bounds__(64 * kGv8Waves) proj_gemv_q8_kernel(ProjArgs a
             const float sum = wave_sum(acc[r][n]);
             if (lane == r * N + n) outv = sum;
         }
-    if constexpr (MODE == kProjQKVRope) gemv_rope_store(a, lane, N, mat, mrow0, ro, outv + addend);
+    if constexpr (MODE == kProjQKVRope) gemv_rope_store(a, lane, N, mat, rl, outv + addend);
     else gemv_store<MODE>(a, lane, N, m0, outv + addend);
 }
 
@@ -1440,6 +1510,396 @@ __global__ void __launch_bounds__(64 * kGv8Waves) proj_gemv_q8_kernel(ProjArgs a
 
 bool proj_gemv_supported(int N, int K, int M) {
     return N >= 1 && N <= kGvMaxN && K <= kGvMaxK && K % 64 == 0 && M % kGvRows == 0;
+}
+
+// Sums over the wave of 8 values per lane at once, value k ending in every
+// lane of 8 k .. 8 k + 7: halves exchanged by permlane32 swaps (values k
+// and k + 4 meet), rows of 16 by permlane16 swaps, groups of 8 by a row
+// rotation, then 3 DPP steps within each group; 18 exchanges and adds
+// instead of 8 full butterflies.
+__device__ __forceinline__ float sum8_rows(const float (&w)[4]) {
+    // w[i]: lanes 0..31 carry value i, lanes 32..63 value i + 4
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(w[0]), __float_as_uint(w[2]), false, false);
+    const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(w[1]), __float_as_uint(w[3]), false, false);
+    // rows of 16 (k = 0..3): x0 carries value 2 k, x1 value 2 k + 1
+    const float x0 = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    const float x1 = __uint_as_float(q[0]) + __uint_as_float(q[1]);
+    const bool upper8 = (threadIdx.x & 8) != 0;
+    const float keep = upper8 ? x1 : x0, send = upper8 ? x0 : x1;
+    float z = keep + dpp<0x128>(send);                      // row_ror:8, the partner lane l ^ 8
+    z += dpp<kDppXor1>(z);
+    z += dpp<kDppXor2>(z);
+    z += dpp<kDppHalfMirror>(z);
+    return z;
+}
+__device__ __forceinline__ float wave_sum8(const float (&v)[8]) {
+    float w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i + 4]), false, false);
+        w[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    return sum8_rows(w);
+}
+// The same where lanes 0..31 hold only values 0..3 and lanes 32..63 only
+// values 4..7, as v[0..3] (the halves' partial sums need no exchange)
+__device__ __forceinline__ float wave_sum8_halves(const float (&v)[8]) {
+    const float w[4] = {v[0], v[1], v[2], v[3]};
+    return sum8_rows(w);
+}
+
+// Few-row GEMV with the weights streamed into LDS (the decode step's
+// projections).  A workgroup holds up to kGlMaxSlots "slot" waves and
+// kGlXWaves staging waves.  Slot wave w owns the 4 weight rows of slot
+// blockIdx.x * SW + w (consecutive rows, or two NeoX rotation pairs under
+// kProjQKVRope).  The staging waves first issue the loads of the token rows
+// (and of the positions), and only then, after barrier 0, do the slot waves
+// issue every 1 KB chunk of their rows as buffer_load_dwordx4 ... nt lds into
+// their own LDS area, chunk-major (chunk c of rows 0..3, then chunk c + 1),
+// so the token rows are not queued behind the weights and each CU has all
+// of its rows' bytes in flight.  The staging waves convert the token rows
+// once for the workgroup, rounded to f16 (F16 weights) or quantized to Q8_0
+// blocks as ggml's quantize_row_q8_0 does (Q8_0 weights), and tabulate the
+// RoPE cosines and sines of the tokens' positions; barrier 1.  A slot wave
+// then takes each part of its rows as soon as the chunks under it have
+// landed (loads complete in order: a vmcnt wait per part), so its dot
+// products overlap the rest of the stream.  F16: part it is chunk it, lane l
+// takes 8-element chunk l + 64 it of each row; products and summation order
+// of proj_gemv_f16_kernel.  Q8_0: part it is blocks 32 it .. 32 it + 31, lane
+// pair (2 j', 2 j' + 1) takes the two 16-code halves of block 32 it + j', and
+// the pair's integer sums are added across the pair before the block's
+// single scaled fma (ggml's integer block dot).
+constexpr int kGlMaxSlots = 8;
+constexpr int kGlMaxXWaves = 4;
+__host__ __device__ constexpr int gl_xwaves(bool q8) { return q8 ? 4 : 2; }   // Q8_0 quantizes: more hands
+constexpr int kGlMaxTok = 2;                  // token rows
+constexpr int kGlMaxK = 4096;
+constexpr int kGlLdsMax = 160 * 1024;         // the whole of a CU's LDS (one workgroup per CU)
+constexpr int kGlDead = 0x40000000;           // DMA offset past every range: zeros, no memory access
+
+__device__ __forceinline__ void gldma16(i32x4 rsrc, uint32_t lds_addr, int voffset) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 4\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
+                 :
+                 : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voffset), "s"(rsrc)
+                 : "m0");
+}
+// s_waitcnt vmcnt(n) for a wave-uniform n in [0, 31]
+__device__ __forceinline__ void wait_vmcnt_le(int n) {
+    switch (n) {
+#define VVA_W(I) case I: asm volatile("s_waitcnt vmcnt(" #I ")" : : : "memory"); break;
+        VVA_W(0) VVA_W(1) VVA_W(2) VVA_W(3) VVA_W(4) VVA_W(5) VVA_W(6) VVA_W(7)
+        VVA_W(8) VVA_W(9) VVA_W(10) VVA_W(11) VVA_W(12) VVA_W(13) VVA_W(14) VVA_W(15)
+        VVA_W(16) VVA_W(17) VVA_W(18) VVA_W(19) VVA_W(20) VVA_W(21) VVA_W(22) VVA_W(23)
+        VVA_W(24) VVA_W(25) VVA_W(26) VVA_W(27) VVA_W(28) VVA_W(29) VVA_W(30) VVA_W(31)
+#undef VVA_W
+        default: asm volatile("s_waitcnt vmcnt(0)" : : : "memory"); break;
+    }
+}
+
+// LDS layout: [token rows: xbytes][RoPE table: kGlMaxTok x 64 (cos, sin)]
+// [dummy 1 KB for dead loads][slot w: 4 rows x rp]
+__host__ __device__ inline int gl_xbytes(bool q8, int K) {
+    return q8 ? kGlMaxTok * (K + K / 32 * 4) : kGlMaxTok * K * 2;
+}
+__host__ __device__ inline int gl_row_pitch(bool q8, int K) {
+    const int rb = q8 ? K / 32 * kQ8Bytes : K * 2;
+    return (rb + 1023) / 1024 * 1024;
+}
+__host__ __device__ inline int gl_slots_at(bool q8, int K) { return gl_xbytes(q8, K) + 2048; }
+
+// Staging of token-row tasks t = tid, tid + NT, ... (row n = t >= per, part
+// c): E elements of row type XT, as loaded (F32: E / 4 vectors; 16-bit: the
+// first E / 8), rounded to f16 (F16 weights) or quantized to a Q8_0 block
+// (Q8_0 weights: ggml's quantize_row_q8_0, d = amax / 127 rounded to fp16,
+// codes roundf(x / d) with the fp32 d) into LDS.
+template <bool Q8, int XT, int E, int XI, int NT>
+__device__ __forceinline__ void gl_stage(char* glds, const u32x4 (&raw)[XI][E / 4], int tid, int tasks, int per,
+                                         int K) {
+#pragma unroll
+    for (int i = 0; i < XI; ++i) {
+        const int t = tid + NT * i;
+        if (t >= tasks) break;
+        const int n = t >= per ? 1 : 0, c = t - n * per;
+        float x[E];
+        if constexpr (XT == VVA_TYPE_F32) {
+#pragma unroll
+            for (int e = 0; e < E; ++e) x[e] = __uint_as_float(raw[i][e / 4][e % 4]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                const uint32_t h = raw[i][e / 8][(e % 8) / 2];
+                const uint16_t v16 = (uint16_t)(e & 1 ? h >> 16 : h & 0xffffu);
+                x[e] = XT == VVA_TYPE_BF16 ? bf16_to_f32(v16) : f16_to_f32(v16);
+            }
+        }
+        if constexpr (!Q8) {
+            uint16_t* xh = (uint16_t*)glds;                 // [kGlMaxTok][K] f16
+            *(u32x4*)(xh + (int64_t)n * K + c * 8) =
+                u32x4{pack_f16(x[0], x[1]), pack_f16(x[2], x[3]), pack_f16(x[4], x[5]), pack_f16(x[6], x[7])};
+        } else {
+            uint32_t* xq = (uint32_t*)glds;                 // [kGlMaxTok][K / 32][8] codes
+            float* xd = (float*)(glds + kGlMaxTok * K);     // [kGlMaxTok][K / 32] fp16-rounded scales
+            float am = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 32; ++e) am = fmaxf(am, fabsf(x[e]));
+            const float d = am / 127.0f;
+            const float id = d != 0.0f ? 1.0f / d : 0.0f;
+            uint32_t cw[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                cw[q] = 0u;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) cw[q] |= ((uint32_t)(uint8_t)(int8_t)roundf(x[4 * q + e] * id)) << (8 * e);
+            }
+            *(u32x4*)(xq + ((int64_t)n * per + c) * 8) = u32x4{cw[0], cw[1], cw[2], cw[3]};
+            *(u32x4*)(xq + ((int64_t)n * per + c) * 8 + 4) = u32x4{cw[4], cw[5], cw[6], cw[7]};
+            xd[(int64_t)n * per + c] = f16_to_f32(f32_to_f16(d));
+        }
+    }
+}
+
+template <bool Q8, int MODE, int IPR>
+__global__ void __launch_bounds__(64 * (kGlMaxSlots + kGlMaxXWaves)) proj_gemv_lds_kernel(ProjArgs a, int sw) {
+    prefetch_kernargs<sizeof(ProjArgs) + 4>();
+    __shared__ __attribute__((aligned(16))) char glds[kGlLdsMax];
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int N = a.N, K = a.K;
+    const int xbytes = gl_xbytes(Q8, K);
+    float2* tab = (float2*)(glds + xbytes);                 // [kGlMaxTok][64]
+    if (w >= sw) {
+        // ---- staging waves: the token rows (and positions), once per workgroup
+        constexpr int NT = gl_xwaves(Q8) * 64;
+        constexpr int E = Q8 ? 32 : 8;                      // elements per task
+        constexpr int XI = kGlMaxTok * (kGlMaxK / E) / NT;  // tasks per thread at most
+        const int tid = threadIdx.x - sw * 64;
+        const int per = K / E, tasks = N * per;
+        // every load unconditional and back to back (no branch, no division:
+        // n < 2): task t = (row n, part c) reads its E elements, F32 rows in
+        // E / 4 vectors, 16-bit rows in E / 8 vectors read twice (no read past
+        // the row); tasks past the end re-read task 0
+        const bool f32 = a.x_type == VVA_TYPE_F32;
+        const int eb = E * (f32 ? 4 : 2);
+        const char* row0 = a.x;                             // token rows 0 and 1
+        const char* row1 = a.x + (a.T == 1 ? a.x_nb_b : a.x_nb_t);
+        u32x4 raw[XI][E / 4];
+#pragma unroll
+        for (int i = 0; i < XI; ++i) {
+            const int t0 = tid + NT * i, t = t0 < tasks ? t0 : 0;
+            const bool second = t >= per;
+            const char* src = (second ? row1 : row0) + (uint32_t)((t - (second ? per : 0)) * eb);
+#pragma unroll
+            for (int q = 0; q < E / 4; ++q) raw[i][q] = *(const u32x4*)(src + 16 * (f32 ? q : q % (E / 8)));
+        }
+        const int P = a.d >> 1;
+        int pv = 0;
+        if constexpr (MODE == kProjQKVRope) {
+            const int n = tid < N * P && tid >= P ? 1 : 0, b = n >= a.T ? 1 : 0, t = n - b * a.T;
+            pv = a.pos[b * a.pos_stride_b + t];
+        }
+        asm volatile("s_barrier" : : : "memory");          // 0: the token-row loads are out
+        // one code path per row type (a select between the types' decodes
+        // would run both)
+        if (f32) gl_stage<Q8, VVA_TYPE_F32, E, XI, NT>(glds, raw, tid, tasks, per, K);
+        else if (a.x_type == VVA_TYPE_BF16) gl_stage<Q8, VVA_TYPE_BF16, E, XI, NT>(glds, raw, tid, tasks, per, K);
+        else gl_stage<Q8, VVA_TYPE_F16, E, XI, NT>(glds, raw, tid, tasks, per, K);
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory");   // 1: token rows staged
+        if constexpr (MODE == kProjQKVRope) {
+            // the RoPE table, needed only by the slot waves' epilogues
+            if (tid < N * P) {
+                const int n = tid >= P ? 1 : 0, i = tid - n * P;
+                const float th = P == 64 ? rope_theta_n<64>((float)pv, a.theta_scale, i)
+                                         : rope_theta_n<32>((float)pv, a.theta_scale, i);
+                tab[n * 64 + i] = make_float2(cosf(th), sinf(th));
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory");   // 2: RoPE table
+        }
+        return;
+    }
+    // ---- slot waves
+    const int rb = Q8 ? K / 32 * kQ8Bytes : K * 2;          // weight row bytes
+    const int rp = IPR * 1024;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)glds;
+    const uint32_t dummy = lds0 + (uint32_t)xbytes + 1024;
+    const int S = a.M / kGvRows;
+    const int slot = blockIdx.x * sw + w;
+    const bool has = slot < S;                              // wave-uniform
+    const int m0 = (has ? slot : 0) * kGvRows;
+    const int mat = m0 < a.m_end[0] ? 0 : (m0 < a.m_end[1] ? 1 : 2);
+    const int mstart = mat == 0 ? 0 : mat == 1 ? a.m_end[0] : a.m_end[1];
+    const int mrow0 = m0 - mstart;
+    const int64_t wnb = mat == 0 ? a.w_nb[0] : mat == 1 ? a.w_nb[1] : a.w_nb[2];
+    const char* wmat = mat == 0 ? a.w[0] : mat == 1 ? a.w[1] : a.w[2];
+    int ro[kGvRows];
+    gemv_rofs<MODE>(a, mrow0, ro);
+    const float addend = gemv_addend<MODE, kGlMaxTok>(a, lane, N, m0, mat, mrow0, wmat, ro);
+    const int sofs = gl_slots_at(Q8, K) + w * kGvRows * rp;
+    asm volatile("s_barrier" : : : "memory");              // 0: the token-row loads are out
+    {
+        const i32x4 rs = make_rsrc_sgpr(wmat, (uint32_t)((a.m_end[mat] - mstart) * wnb));
+#pragma unroll
+        for (int c = 0; c < IPR; ++c)
+#pragma unroll
+            for (int r = 0; r < kGvRows; ++r) {
+                const int b = c * 1024 + lane * 16;
+                const bool live = has && c * 1024 < rb;     // wave-uniform
+                const int off = b < rb ? (int)((mrow0 + ro[r]) * wnb) + b : kGlDead;
+                gldma16(rs, live ? lds0 + (uint32_t)(sofs + r * rp + c * 1024) : dummy, live ? off : kGlDead);
+            }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory");   // 1: token rows staged
+    if (!has) {
+        asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+        if constexpr (MODE == kProjQKVRope) asm volatile("s_barrier" : : : "memory");   // 2
+        return;
+    }
+    // the epilogue's lane facts, while the first chunks are still in flight
+    RopeLane rl{};
+    if constexpr (MODE == kProjQKVRope) rl = gemv_rope_lane<false, kGlMaxTok>(a, lane, N, mat, mrow0, ro);
+    const char* srow = glds + sofs;
+    // v[r * 2 + n]: this lane's partial sum of (row r, token n)
+    float v[kGvRows * kGlMaxTok];
+#pragma unroll
+    for (int i = 0; i < kGvRows * kGlMaxTok; ++i) v[i] = 0.0f;
+    if constexpr (!Q8) {
+        const uint16_t* xh = (const uint16_t*)glds;
+        const int nch = K / 8;
+#pragma unroll
+        for (int it = 0; it < IPR; ++it) {
+            wait_vmcnt_le(kGvRows * (IPR - 1 - it));      // chunk it of the 4 rows landed
+            const int c = lane + 64 * it;
+            if (c < nch) {
+                u32x4 xv[kGlMaxTok];
+#pragma unroll
+                for (int n = 0; n < kGlMaxTok; ++n) xv[n] = *(const u32x4*)(xh + (int64_t)(n < N ? n : 0) * K + c * 8);
+#pragma unroll
+                for (int r = 0; r < kGvRows; ++r) {
+                    const u32x4 wq = *(const u32x4*)(srow + r * rp + c * 16);
+#pragma unroll
+                    for (int n = 0; n < kGlMaxTok; ++n) {
+                        float s2 = v[r * 2 + n];
+                        s2 = dot2_f16(wq.x, xv[n].x, s2);
+                        s2 = dot2_f16(wq.y, xv[n].y, s2);
+                        s2 = dot2_f16(wq.z, xv[n].z, s2);
+                        s2 = dot2_f16(wq.w, xv[n].w, s2);
+                        v[r * 2 + n] = s2;
+                    }
+                }
+            }
+        }
+    } else {
+        // lanes 0..31: rows 0 and 1, lanes 32..63: rows 2 and 3; lane l takes
+        // whole block 32 it + (l & 31) of both of its rows
+        const uint32_t* xq = (const uint32_t*)glds;
+        const float* xd = (const float*)(glds + kGlMaxTok * K);
+        const int nbk = K / 32;
+        const int hr = lane >> 5;
+        float acc[2][kGlMaxTok];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int n = 0; n < kGlMaxTok; ++n) acc[i][n] = 0.0f;
+        for (int it = 0; 32 * it < nbk; ++it) {
+            // the part's last byte read: 9 dwords from below block jl's codes
+            const int jl = min(32 * it + 31, nbk - 1);
+            const int last = ((jl * kQ8Bytes + 2) & ~3) + 35;
+            const int cl = min(last >> 10, IPR - 1);
+            wait_vmcnt_le(kGvRows * (IPR - 1 - cl));
+            const int j = 32 * it + (lane & 31);
+            const bool live = j < nbk;
+            const int jj = live ? j : 0;
+            const int ca = (jj * kQ8Bytes + 2) & ~3;         // codes from this dword boundary
+            const int sh = (jj * kQ8Bytes + 2) & 3;          // at this byte offset (0 or 2)
+            float dw[2];
+            uint32_t codes[2][8];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const char* row = srow + (2 * hr + i) * rp;
+                const uint32_t sc = *(const uint32_t*)(row + ((jj * kQ8Bytes) & ~3));
+                dw[i] = f16_to_f32((uint16_t)((jj & 1) ? sc >> 16 : sc & 0xffffu));
+                const uint32_t* q = (const uint32_t*)(row + ca);
+                uint32_t qv[9];
+#pragma unroll
+                for (int e = 0; e < 9; ++e) qv[e] = q[e];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) codes[i][e] = __builtin_amdgcn_alignbyte(qv[e + 1], qv[e], sh);
+            }
+#pragma unroll
+            for (int n = 0; n < kGlMaxTok; ++n) {
+                if (n >= N) break;                           // uniform
+                const u32x4 c0 = *(const u32x4*)(xq + ((int64_t)n * nbk + jj) * 8);
+                const u32x4 c1 = *(const u32x4*)(xq + ((int64_t)n * nbk + jj) * 8 + 4);
+                const uint32_t xc[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+                const float dx = xd[(int64_t)n * nbk + jj];
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    int sm = 0;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) sm = __builtin_amdgcn_sdot4((int)codes[i][e], (int)xc[e], sm, false);
+                    const float f = fmaf((float)sm, dw[i] * dx, acc[i][n]);
+                    acc[i][n] = live ? f : acc[i][n];
+                }
+            }
+        }
+        // as (row, token) sums: this lane's rows are 2 hr and 2 hr + 1
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int n = 0; n < kGlMaxTok; ++n) v[i * 2 + n] = acc[i][n];
+    }
+    // sums over the lanes: value (r, n) ends in lanes 8 (2 r + n) .. + 7,
+    // then lane r N + n takes its own
+    const float tot = Q8 ? wave_sum8_halves(v) : wave_sum8(v);
+    int orr, on;
+    lane_rn<kGlMaxTok>(lane < kGvRows * N ? lane : 0, N, orr, on);
+    const float outv = __shfl(tot, 8 * (orr * 2 + on));
+    if constexpr (MODE == kProjQKVRope) {
+        asm volatile("s_barrier" : : : "memory");          // 2: RoPE table
+        float c = 1.0f, sn = 0.0f;
+        if (mat < 2) {
+            const float2 cs = tab[rl.n * 64 + rl.i];
+            c = cs.x;
+            sn = cs.y;
+        }
+        gemv_rope_finish(a, lane, N, mat, rl, c, sn, outv + addend);
+    } else {
+        gemv_store<MODE, kGlMaxTok>(a, lane, N, m0, outv + addend);
+    }
+}
+
+// Slots per workgroup of proj_gemv_lds_kernel (0: the call does not fit it)
+int gemv_lds_slots(const ProjArgs& a, int n_cu) {
+    const bool q8 = a.w_type == VVA_TYPE_Q8_0;
+    if (a.N > kGlMaxTok || a.K > kGlMaxK || a.K % 64 || a.M % kGvRows) return 0;
+    if (a.mode == kProjQKVRope && a.d > 128) return 0;        // the RoPE table holds 64 angles
+    // Q8_0: the last block's reads (20 bytes from below its second half) stay in the row pitch
+    if (q8 && a.K / 32 * kQ8Bytes + 4 > gl_row_pitch(true, a.K)) return 0;
+    if (a.m_end[0] % kGvRows || a.m_end[1] % kGvRows) return 0;
+    for (int i = 0; i < 3; ++i) {                    // every row offset below the dead offset
+        const int64_t rows = a.m_end[i] - (i == 0 ? 0 : a.m_end[i - 1]);
+        if (rows > 0 && rows * a.w_nb[i] >= kGlDead) return 0;
+    }
+    const int rp = gl_row_pitch(q8, a.K);
+    const int fit = (kGlLdsMax - gl_slots_at(q8, a.K)) / (kGvRows * rp);
+    const int S = a.M / kGvRows;
+    int sw = (S + n_cu - 1) / n_cu;
+    if (sw > fit) sw = fit;
+    if (sw > kGlMaxSlots) sw = kGlMaxSlots;
+    return sw >= 1 ? sw : 0;
+}
+
+template <bool Q8, int MODE>
+hipError_t launch_gemv_lds(const ProjArgs& a, int sw, hipStream_t s) {
+    const int rp = gl_row_pitch(Q8, a.K);
+    const dim3 g((a.M / kGvRows + sw - 1) / sw), bl(64 * (sw + gl_xwaves(Q8)));
+    const int ipr = rp / 1024;
+#define VVA_GL(I) case I: hipLaunchKernelGGL((proj_gemv_lds_kernel<Q8, MODE, I>), g, bl, 0, s, a, sw); break;
+    switch (ipr) {
+        VVA_GL(1) VVA_GL(2) VVA_GL(3) VVA_GL(4) VVA_GL(5) VVA_GL(6) VVA_GL(7) VVA_GL(8)
+        default: return hipErrorInvalidValue;
+    }
+#undef VVA_GL
+    return hipGetLastError();
 }
 
 namespace {
@@ -1459,12 +1919,23 @@ bool proj_gemv_rope_ok(const ProjArgs& a) {
     const bool float_q = a.q_out_type == VVA_TYPE_F32 || a.q_out_type == VVA_TYPE_F16 ||
                          a.q_out_type == VVA_TYPE_BF16;
     return a.mode == kProjQKV && float_cache && float_q && (a.d == 64 || a.d == 128) &&
-           a.m_end[0] % a.d == 0 && a.m_end[1] % a.d == 0 && (gemv_q8_ok(a) || gemv_f16_ok(a));
+           a.m_end[0] % a.d == 0 && a.m_end[1] % a.d == 0 &&
+           (gemv_lds_slots(a, 1) > 0 || gemv_q8_ok(a) || gemv_f16_ok(a));
 }
 
-hipError_t launch_proj_gemv(ProjArgs& a, float* y_ws, hipStream_t s) {
+hipError_t launch_proj_gemv(ProjArgs& a, float* y_ws, int n_cu, hipStream_t s) {
     const bool q8 = a.w_type == VVA_TYPE_Q8_0;
     a.y = y_ws;
+    if (const int sw = gemv_lds_slots(a, n_cu)) {
+        if (q8) {
+            if (a.mode == kProjQKVRope) return launch_gemv_lds<true, kProjQKVRope>(a, sw, s);
+            if (a.mode == kProjQKV) return launch_gemv_lds<true, kProjQKV>(a, sw, s);
+            return launch_gemv_lds<true, kProjResidual>(a, sw, s);
+        }
+        if (a.mode == kProjQKVRope) return launch_gemv_lds<false, kProjQKVRope>(a, sw, s);
+        if (a.mode == kProjQKV) return launch_gemv_lds<false, kProjQKV>(a, sw, s);
+        return launch_gemv_lds<false, kProjResidual>(a, sw, s);
+    }
     if (gemv_q8_ok(a)) {
         const dim3 g8(a.M / kGv8Rows), b8(64 * kGv8Waves);
         if (a.mode == kProjQKVRope)  hipLaunchKernelGGL((proj_gemv_q8_kernel<kProjQKVRope>), g8, b8, 0, s, a);

@@ -999,12 +999,12 @@ extern "C" vva_status vva_qkv_rope_append(vva_context* ctx, vva_kv* kv, int laye
         a.pos = p.pos; a.pos_stride_b = p.pos_stride_b; a.theta_scale = p.theta_scale;
         if (proj_gemv_rope_ok(a)) {
             a.mode = kProjQKVRope;
-            hipError_t e = launch_proj_gemv(a, nullptr, ctx->stream);
+            hipError_t e = launch_proj_gemv(a, nullptr, ctx->n_cu, ctx->stream);
             return e == hipSuccess ? VVA_OK : hip_fail(ctx, e, "qkv_rope_append launch");
         }
         if ((st = ensure_ws(ctx, (size_t)N * a.M * sizeof(float))) != VVA_OK) return st;
         float* y = ctx->ws;
-        hipError_t e = launch_proj_gemv(a, y, ctx->stream);
+        hipError_t e = launch_proj_gemv(a, y, ctx->n_cu, ctx->stream);
         if (e != hipSuccess) return hip_fail(ctx, e, "qkv_rope_append launch");
         auto proj_view = [&](int64_t first_row, int64_t heads) {
             vva_tensor t{};
@@ -1073,7 +1073,7 @@ extern "C" vva_status vva_out_proj_residual(vva_context* ctx, const vva_tensor* 
     hipError_t e;
     if (proj_gemv_supported((int)N, (int)K, (int)M) && rows16(o)) {
         a.x = p.x; a.x_type = p.x_type; a.x_nb_t = p.x_nb_t; a.x_nb_b = p.x_nb_b;
-        e = launch_proj_gemv(a, nullptr, ctx->stream);
+        e = launch_proj_gemv(a, nullptr, ctx->n_cu, ctx->stream);
         return e == hipSuccess ? VVA_OK : hip_fail(ctx, e, "out_proj_residual launch");
     }
     return run_proj_gemm(ctx, p, a, (int)N, (int)K, 0);

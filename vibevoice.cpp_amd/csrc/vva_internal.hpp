@@ -232,7 +232,7 @@ hipError_t launch_proj(ProjPrepArgs& p, ProjArgs& a, void* ws, hipStream_t s);
 // converts the rows itself.  kProjQKV writes y = x w^T + bias (F32 [N][M],
 // at `ws`) for the caller's RoPE + append; kProjResidual writes h.
 bool proj_gemv_supported(int N, int K, int M);
-hipError_t launch_proj_gemv(ProjArgs& a, float* y_ws, hipStream_t s);
+hipError_t launch_proj_gemv(ProjArgs& a, float* y_ws, int n_cu, hipStream_t s);
 // Whether launch_proj_gemv can run a kProjQKV call as kProjQKVRope (one
 // launch: projections, bias, RoPE and the append of F32 / F16 / BF16 rows).
 bool proj_gemv_rope_ok(const ProjArgs& a);
@@ -273,6 +273,14 @@ __device__ __forceinline__ void prefetch_kernargs() {
 __device__ __forceinline__ float rope_theta(float p, float ts, int i, int n) {
     float th = p;
     for (int k = 0; k < n - 1; ++k) th = k < i ? th * ts : th;
+    return th;
+}
+// The same for a pair count NP known at compile time: straight-line code
+template <int NP>
+__device__ __forceinline__ float rope_theta_n(float p, float ts, int i) {
+    float th = p;
+#pragma unroll
+    for (int k = 0; k < NP - 1; ++k) th = k < i ? th * ts : th;
     return th;
 }
 
