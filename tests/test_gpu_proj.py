@@ -147,6 +147,49 @@ def test_qkv_rope_append_without_bias_equals_rope_append(ctx, torch_gpu):
     b.free()
 
 
+@pytest.mark.parametrize("d,Hq,Hkv,hidden,wt,ct,T,B", [
+    (128, 28, 4, 3584, vva.F16, vva.F16, 1, 2),      # 7B CFG decode step
+    (128, 28, 4, 3584, vva.Q8_0, vva.BF16, 1, 2),
+    (64, 14, 2, 896, vva.F16, vva.F32, 2, 1),        # two tokens of one sequence
+    (64, 14, 2, 896, vva.Q8_0, vva.F16, 1, 1),
+])
+def test_decode_step_fused_rope_equals_rope_append(ctx, torch_gpu, d, Hq, Hkv, hidden, wt, ct, T, B):
+    """The decode step's one- and two-row call (RoPE and the append in the
+    projection's epilogue, the angles tabulated once per workgroup) stores
+    the same bits as projecting with out_proj (zero residual, the same
+    kernel's dot products) and then running vva_rope_append, at positions
+    whose angles need the large-argument reduction of cos / sin."""
+    torch = torch_gpu
+    rng = np.random.default_rng(d + T + wt)
+    x = torch.from_numpy(rng.standard_normal((B, T, hidden)).astype(np.float32)).cuda()
+    ws = [_weight(torch, rng, n * d, hidden, wt) for n in (Hq, Hkv, Hkv)]
+    pos = torch.tensor([[30011 + 977 * b + t for t in range(T)] for b in range(B)], dtype=torch.int32, device="cuda")
+    past = 5
+    a = vva.KVCache(ctx, 1, Hkv, d, past + T + 4, B, ct)
+    c = vva.KVCache(ctx, 1, Hkv, d, past + T + 4, B, ct)
+    for kv in (a, c):
+        for b in range(B):
+            kv.set_len(b, past)
+    qa = torch.empty((B, T, Hq, d), dtype=torch.float32, device="cuda")
+    ctx.qkv_rope_append(a, 0, x, ws[0][1], ws[1][1], ws[2][1], pos, qa)
+    proj = []
+    for (_, w), n in zip(ws, (Hq, Hkv, Hkv)):
+        y = torch.zeros((B, T, n * d), dtype=torch.float32, device="cuda")
+        ctx.out_proj_residual(x, w, y, y)            # y = x w^T + 0
+        proj.append(y.reshape(B, T, n, d))
+    qc = torch.empty_like(qa)
+    ctx.rope_append(c, 0, proj[0], proj[1], proj[2], pos, qc)
+    torch.cuda.synchronize()
+    assert torch.equal(qa, qc), f"q differs: max {float((qa - qc).abs().max()):.3e}"
+    for b in range(B):
+        ka, va = a.download(0, b, past + T)
+        kc, vc = c.download(0, b, past + T)
+        np.testing.assert_array_equal(ka, kc)
+        np.testing.assert_array_equal(va, vc)
+    a.free()
+    c.free()
+
+
 O_CASES = [
     # in (Hq * d), hidden, weights, T, B, o type
     (896, 896, vva.F16, 256, 1, vva.F32),       # 0.5B layer of the TTS prefill

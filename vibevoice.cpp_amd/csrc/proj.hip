@@ -1512,64 +1512,55 @@ bool proj_gemv_supported(int N, int K, int M) {
     return N >= 1 && N <= kGvMaxN && K <= kGvMaxK && K % 64 == 0 && M % kGvRows == 0;
 }
 
-// Sums over the wave of 8 values per lane at once, value k ending in every
-// lane of 8 k .. 8 k + 7: halves exchanged by permlane32 swaps (values k
-// and k + 4 meet), rows of 16 by permlane16 swaps, groups of 8 by a row
-// rotation, then 3 DPP steps within each group; 18 exchanges and adds
-// instead of 8 full butterflies.
-__device__ __forceinline__ float sum8_rows(const float (&w)[4]) {
-    // w[i]: lanes 0..31 carry value i, lanes 32..63 value i + 4
-    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(w[0]), __float_as_uint(w[2]), false, false);
-    const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(w[1]), __float_as_uint(w[3]), false, false);
-    // rows of 16 (k = 0..3): x0 carries value 2 k, x1 value 2 k + 1
-    const float x0 = __uint_as_float(p[0]) + __uint_as_float(p[1]);
-    const float x1 = __uint_as_float(q[0]) + __uint_as_float(q[1]);
-    const bool upper8 = (threadIdx.x & 8) != 0;
-    const float keep = upper8 ? x1 : x0, send = upper8 ? x0 : x1;
-    float z = keep + dpp<0x128>(send);                      // row_ror:8, the partner lane l ^ 8
+// Sums over the wave of 4 values per lane at once, value k ending in every
+// lane of 16 k .. 16 k + 15: lane halves exchanged by permlane32 swaps
+// (values k and k + 2 meet), rows of 16 by a permlane16 swap, then a row
+// rotation by 8 and 3 DPP steps within each row of 16; 10 exchanges and
+// adds instead of 4 full butterflies.
+__device__ __forceinline__ float sum4_rows(float w0, float w1) {
+    // w0: lanes 0..31 carry value 0, lanes 32..63 value 2; w1: values 1, 3
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(w0), __float_as_uint(w1), false, false);
+    float z = __uint_as_float(p[0]) + __uint_as_float(p[1]);   // row k of 16 carries value k
+    z += dpp<0x128>(z);                                     // row_ror:8: lanes l and l ^ 8
     z += dpp<kDppXor1>(z);
     z += dpp<kDppXor2>(z);
     z += dpp<kDppHalfMirror>(z);
     return z;
 }
-__device__ __forceinline__ float wave_sum8(const float (&v)[8]) {
-    float w[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i + 4]), false, false);
-        w[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-    }
-    return sum8_rows(w);
+__device__ __forceinline__ float wave_sum4(const float (&v)[4]) {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[0]), __float_as_uint(v[2]), false, false);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[1]), __float_as_uint(v[3]), false, false);
+    return sum4_rows(__uint_as_float(a[0]) + __uint_as_float(a[1]), __uint_as_float(b[0]) + __uint_as_float(b[1]));
 }
-// The same where lanes 0..31 hold only values 0..3 and lanes 32..63 only
-// values 4..7, as v[0..3] (the halves' partial sums need no exchange)
-__device__ __forceinline__ float wave_sum8_halves(const float (&v)[8]) {
-    const float w[4] = {v[0], v[1], v[2], v[3]};
-    return sum8_rows(w);
-}
+// The same where lanes 0..31 hold only values 0, 1 and lanes 32..63 only
+// values 2, 3, as h[0], h[1] (the halves' partial sums need no exchange)
+__device__ __forceinline__ float wave_sum4_halves(const float (&h)[2]) { return sum4_rows(h[0], h[1]); }
 
 // Few-row GEMV with the weights streamed into LDS (the decode step's
-// projections).  A workgroup holds up to kGlMaxSlots "slot" waves and
-// kGlXWaves staging waves.  Slot wave w owns the 4 weight rows of slot
-// blockIdx.x * SW + w (consecutive rows, or two NeoX rotation pairs under
-// kProjQKVRope).  The staging waves first issue the loads of the token rows
-// (and of the positions), and only then, after barrier 0, do the slot waves
+// projections, one or two token rows).  A workgroup holds 2 (F16 weights)
+// or 4 (Q8_0) staging waves, launched first, and up to kGlMaxSlots "slot"
+// waves; slot wave w owns the 2 weight rows of slot blockIdx.x * SW + w: two
+// consecutive rows, or under kProjQKVRope one NeoX rotation pair (dims i
+// and i + d/2 of a head), so the wave holds both members of its pair.  Two
+// rows per slot deal a 7B layer's rows to 256 workgroups evenly (q/k/v: 9
+// slots each, o: 7).  The staging waves first issue the loads of the token
+// rows (and positions), and only then, after barrier 0, do the slot waves
 // issue every 1 KB chunk of their rows as buffer_load_dwordx4 ... nt lds into
-// their own LDS area, chunk-major (chunk c of rows 0..3, then chunk c + 1),
-// so the token rows are not queued behind the weights and each CU has all
-// of its rows' bytes in flight.  The staging waves convert the token rows
-// once for the workgroup, rounded to f16 (F16 weights) or quantized to Q8_0
-// blocks as ggml's quantize_row_q8_0 does (Q8_0 weights), and tabulate the
-// RoPE cosines and sines of the tokens' positions; barrier 1.  A slot wave
-// then takes each part of its rows as soon as the chunks under it have
+// their own LDS area, chunk-major, so the token rows are not queued behind
+// the weights and each CU has all of its rows' bytes in flight.  The staging
+// waves convert the token rows once for the workgroup, rounded to f16 (F16
+// weights) or quantized to Q8_0 blocks as ggml's quantize_row_q8_0 does
+// (Q8_0 weights), and tabulate the RoPE cosines and sines of the tokens'
+// positions, while the slot waves are still issuing; barrier 1.  A slot
+// wave then takes each part of its rows as soon as the chunks under it have
 // landed (loads complete in order: a vmcnt wait per part), so its dot
-// products overlap the rest of the stream.  F16: part it is chunk it, lane l
-// takes 8-element chunk l + 64 it of each row; products and summation order
-// of proj_gemv_f16_kernel.  Q8_0: part it is blocks 32 it .. 32 it + 31, lane
-// pair (2 j', 2 j' + 1) takes the two 16-code halves of block 32 it + j', and
-// the pair's integer sums are added across the pair before the block's
-// single scaled fma (ggml's integer block dot).
-constexpr int kGlMaxSlots = 8;
+// products overlap the rest of the stream.  F16: part it is chunk it, lane l takes 8-element
+// chunk l + 64 it of both rows, with the products of proj_gemv_f16_kernel.
+// Q8_0: part it is blocks 32 it .. 32 it + 31, lanes 0..31 take row 0's
+// blocks and lanes 32..63 row 1's, one whole block each (ggml's integer
+// block dot, then one scaled fma).
+constexpr int kGlRows = 2;                    // weight rows per slot (one wave)
+constexpr int kGlMaxSlots = 12;
 constexpr int kGlMaxXWaves = 4;
 __host__ __device__ constexpr int gl_xwaves(bool q8) { return q8 ? 4 : 2; }   // Q8_0 quantizes: more hands
 constexpr int kGlMaxTok = 2;                  // token rows
@@ -1597,7 +1588,7 @@ __device__ __forceinline__ void wait_vmcnt_le(int n) {
 }
 
 // LDS layout: [token rows: xbytes][RoPE table: kGlMaxTok x 64 (cos, sin)]
-// [dummy 1 KB for dead loads][slot w: 4 rows x rp]
+// [dummy 1 KB for dead loads][slot w: 2 rows x rp]
 __host__ __device__ inline int gl_xbytes(bool q8, int K) {
     return q8 ? kGlMaxTok * (K + K / 32 * 4) : kGlMaxTok * K * 2;
 }
@@ -1606,6 +1597,53 @@ __host__ __device__ inline int gl_row_pitch(bool q8, int K) {
     return (rb + 1023) / 1024 * 1024;
 }
 __host__ __device__ inline int gl_slots_at(bool q8, int K) { return gl_xbytes(q8, K) + 2048; }
+
+// Output lane l = r N + n (N <= 2) of a slot: row r, token row n = (sequence
+// b, position t), by compares (T is 1 with two sequences, or 2 with one).
+struct GlLane {
+    int r, n, b, t;
+    bool out;
+};
+__device__ __forceinline__ GlLane gl_lane(const ProjArgs& a, int lane, int N) {
+    GlLane o;
+    o.out = lane < kGlRows * N;
+    const int l = o.out ? lane : 0;
+    o.r = N == 2 ? l >> 1 : l;
+    o.n = N == 2 ? l & 1 : 0;
+    o.b = o.n >= a.T ? 1 : 0;
+    o.t = o.n - o.b * a.T;
+    return o;
+}
+// The slot's rows as offsets from its first row mrow0: under kProjQKVRope
+// dims i and i + d/2 of the head for the slot's index i in it, else the two
+// rows in order.
+template <int MODE>
+__device__ __forceinline__ void gl_rofs(const ProjArgs& a, int mrow0, int (&ro)[kGlRows]) {
+    if constexpr (MODE == kProjQKVRope) {
+        const int hr = mrow0 & (a.d - 1);                   // d is 64 or 128; hr = 2 i
+        ro[0] = (hr >> 1) - hr;
+        ro[1] = (hr >> 1) + (a.d >> 1) - hr;
+    } else {
+        ro[0] = 0;
+        ro[1] = 1;
+    }
+}
+// What the output of lane L adds: its row's bias (kProjQKV, kProjQKVRope)
+// or the residual (kProjResidual).  Loaded before the weights, branch-free
+// (lanes past the outputs and a missing bias read a valid address and add 0).
+template <int MODE>
+__device__ __forceinline__ float gl_addend(const ProjArgs& a, const GlLane& L, int m0, int mat, int mrow0,
+                                           const char* any, const int (&ro)[kGlRows]) {
+    const int rr = L.r == 0 ? ro[0] : ro[1];
+    if constexpr (MODE != kProjResidual) {
+        const float* bias = mat == 0 ? a.bias[0] : mat == 1 ? a.bias[1] : a.bias[2];
+        const float v = *(bias ? bias + mrow0 + rr : (const float*)any);
+        return L.out && bias ? v : 0.0f;
+    } else {
+        const float v = *(const float*)(a.res + L.b * a.res_nb_b + L.t * a.res_nb_t + (int64_t)(m0 + L.r) * 4);
+        return L.out ? v : 0.0f;
+    }
+}
 
 // Staging of token-row tasks t = tid, tid + NT, ... (row n = t >= per, part
 // c): E elements of row type XT, as loaded (F32: E / 4 vectors; 16-bit: the
@@ -1663,16 +1701,20 @@ __global__ void __launch_bounds__(64 * (kGlMaxSlots + kGlMaxXWaves)) proj_gemv_l
     prefetch_kernargs<sizeof(ProjArgs) + 4>();
     __shared__ __attribute__((aligned(16))) char glds[kGlLdsMax];
     const int lane = threadIdx.x & 63;
-    const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    // waves 0 .. XW - 1 stage the token rows (launched first, their loads go
+    // out first); wave XW + w is slot wave w
+    constexpr int XW = gl_xwaves(Q8);
+    const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int w = wv - XW;
     const int N = a.N, K = a.K;
     const int xbytes = gl_xbytes(Q8, K);
     float2* tab = (float2*)(glds + xbytes);                 // [kGlMaxTok][64]
-    if (w >= sw) {
+    if (wv < XW) {
         // ---- staging waves: the token rows (and positions), once per workgroup
-        constexpr int NT = gl_xwaves(Q8) * 64;
+        constexpr int NT = XW * 64;
         constexpr int E = Q8 ? 32 : 8;                      // elements per task
         constexpr int XI = kGlMaxTok * (kGlMaxK / E) / NT;  // tasks per thread at most
-        const int tid = threadIdx.x - sw * 64;
+        const int tid = threadIdx.x;
         const int per = K / E, tasks = N * per;
         // every load unconditional and back to back (no branch, no division:
         // n < 2): task t = (row n, part c) reads its E elements, F32 rows in
@@ -1703,17 +1745,17 @@ __global__ void __launch_bounds__(64 * (kGlMaxSlots + kGlMaxXWaves)) proj_gemv_l
         if (f32) gl_stage<Q8, VVA_TYPE_F32, E, XI, NT>(glds, raw, tid, tasks, per, K);
         else if (a.x_type == VVA_TYPE_BF16) gl_stage<Q8, VVA_TYPE_BF16, E, XI, NT>(glds, raw, tid, tasks, per, K);
         else gl_stage<Q8, VVA_TYPE_F16, E, XI, NT>(glds, raw, tid, tasks, per, K);
-        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory");   // 1: token rows staged
+        // the RoPE table (cos, sin of the tokens' angles), while the slot
+        // waves are still issuing their loads
         if constexpr (MODE == kProjQKVRope) {
-            // the RoPE table, needed only by the slot waves' epilogues
             if (tid < N * P) {
                 const int n = tid >= P ? 1 : 0, i = tid - n * P;
                 const float th = P == 64 ? rope_theta_n<64>((float)pv, a.theta_scale, i)
                                          : rope_theta_n<32>((float)pv, a.theta_scale, i);
                 tab[n * 64 + i] = make_float2(cosf(th), sinf(th));
             }
-            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory");   // 2: RoPE table
         }
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory");   // 1: token rows and table staged
         return;
     }
     // ---- slot waves
@@ -1721,26 +1763,27 @@ __global__ void __launch_bounds__(64 * (kGlMaxSlots + kGlMaxXWaves)) proj_gemv_l
     const int rp = IPR * 1024;
     const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)glds;
     const uint32_t dummy = lds0 + (uint32_t)xbytes + 1024;
-    const int S = a.M / kGvRows;
+    const int S = a.M / kGlRows;
     const int slot = blockIdx.x * sw + w;
     const bool has = slot < S;                              // wave-uniform
-    const int m0 = (has ? slot : 0) * kGvRows;
+    const int m0 = (has ? slot : 0) * kGlRows;
     const int mat = m0 < a.m_end[0] ? 0 : (m0 < a.m_end[1] ? 1 : 2);
     const int mstart = mat == 0 ? 0 : mat == 1 ? a.m_end[0] : a.m_end[1];
     const int mrow0 = m0 - mstart;
     const int64_t wnb = mat == 0 ? a.w_nb[0] : mat == 1 ? a.w_nb[1] : a.w_nb[2];
     const char* wmat = mat == 0 ? a.w[0] : mat == 1 ? a.w[1] : a.w[2];
-    int ro[kGvRows];
-    gemv_rofs<MODE>(a, mrow0, ro);
-    const float addend = gemv_addend<MODE, kGlMaxTok>(a, lane, N, m0, mat, mrow0, wmat, ro);
-    const int sofs = gl_slots_at(Q8, K) + w * kGvRows * rp;
+    int ro[kGlRows];
+    gl_rofs<MODE>(a, mrow0, ro);
+    const GlLane L = gl_lane(a, lane, N);
+    const float addend = gl_addend<MODE>(a, L, m0, mat, mrow0, wmat, ro);
+    const int sofs = gl_slots_at(Q8, K) + w * kGlRows * rp;
     asm volatile("s_barrier" : : : "memory");              // 0: the token-row loads are out
     {
         const i32x4 rs = make_rsrc_sgpr(wmat, (uint32_t)((a.m_end[mat] - mstart) * wnb));
 #pragma unroll
         for (int c = 0; c < IPR; ++c)
 #pragma unroll
-            for (int r = 0; r < kGvRows; ++r) {
+            for (int r = 0; r < kGlRows; ++r) {
                 const int b = c * 1024 + lane * 16;
                 const bool live = has && c * 1024 < rb;     // wave-uniform
                 const int off = b < rb ? (int)((mrow0 + ro[r]) * wnb) + b : kGlDead;
@@ -1750,30 +1793,27 @@ __global__ void __launch_bounds__(64 * (kGlMaxSlots + kGlMaxXWaves)) proj_gemv_l
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory");   // 1: token rows staged
     if (!has) {
         asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
-        if constexpr (MODE == kProjQKVRope) asm volatile("s_barrier" : : : "memory");   // 2
         return;
     }
-    // the epilogue's lane facts, while the first chunks are still in flight
-    RopeLane rl{};
-    if constexpr (MODE == kProjQKVRope) rl = gemv_rope_lane<false, kGlMaxTok>(a, lane, N, mat, mrow0, ro);
     const char* srow = glds + sofs;
-    // v[r * 2 + n]: this lane's partial sum of (row r, token n)
-    float v[kGvRows * kGlMaxTok];
-#pragma unroll
-    for (int i = 0; i < kGvRows * kGlMaxTok; ++i) v[i] = 0.0f;
+    float tot;
     if constexpr (!Q8) {
+        // v[r * 2 + n]: this lane's partial sum of (row r, token n)
+        float v[kGlRows * kGlMaxTok];
+#pragma unroll
+        for (int i = 0; i < kGlRows * kGlMaxTok; ++i) v[i] = 0.0f;
         const uint16_t* xh = (const uint16_t*)glds;
         const int nch = K / 8;
 #pragma unroll
         for (int it = 0; it < IPR; ++it) {
-            wait_vmcnt_le(kGvRows * (IPR - 1 - it));      // chunk it of the 4 rows landed
+            wait_vmcnt_le(kGlRows * (IPR - 1 - it));      // chunk it of both rows landed
             const int c = lane + 64 * it;
             if (c < nch) {
                 u32x4 xv[kGlMaxTok];
 #pragma unroll
                 for (int n = 0; n < kGlMaxTok; ++n) xv[n] = *(const u32x4*)(xh + (int64_t)(n < N ? n : 0) * K + c * 8);
 #pragma unroll
-                for (int r = 0; r < kGvRows; ++r) {
+                for (int r = 0; r < kGlRows; ++r) {
                     const u32x4 wq = *(const u32x4*)(srow + r * rp + c * 16);
 #pragma unroll
                     for (int n = 0; n < kGlMaxTok; ++n) {
@@ -1787,43 +1827,36 @@ __global__ void __launch_bounds__(64 * (kGlMaxSlots + kGlMaxXWaves)) proj_gemv_l
                 }
             }
         }
+        tot = wave_sum4(v);
     } else {
-        // lanes 0..31: rows 0 and 1, lanes 32..63: rows 2 and 3; lane l takes
-        // whole block 32 it + (l & 31) of both of its rows
+        // lanes 0..31: row 0, lanes 32..63: row 1; lane l takes whole block
+        // 32 it + (l & 31) of its row
         const uint32_t* xq = (const uint32_t*)glds;
         const float* xd = (const float*)(glds + kGlMaxTok * K);
         const int nbk = K / 32;
-        const int hr = lane >> 5;
-        float acc[2][kGlMaxTok];
+        const char* row = srow + (lane >> 5) * rp;
+        float acc[kGlMaxTok];
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int n = 0; n < kGlMaxTok; ++n) acc[i][n] = 0.0f;
+        for (int n = 0; n < kGlMaxTok; ++n) acc[n] = 0.0f;
         for (int it = 0; 32 * it < nbk; ++it) {
             // the part's last byte read: 9 dwords from below block jl's codes
             const int jl = min(32 * it + 31, nbk - 1);
             const int last = ((jl * kQ8Bytes + 2) & ~3) + 35;
             const int cl = min(last >> 10, IPR - 1);
-            wait_vmcnt_le(kGvRows * (IPR - 1 - cl));
+            wait_vmcnt_le(kGlRows * (IPR - 1 - cl));
             const int j = 32 * it + (lane & 31);
             const bool live = j < nbk;
             const int jj = live ? j : 0;
             const int ca = (jj * kQ8Bytes + 2) & ~3;         // codes from this dword boundary
             const int sh = (jj * kQ8Bytes + 2) & 3;          // at this byte offset (0 or 2)
-            float dw[2];
-            uint32_t codes[2][8];
+            const uint32_t sc = *(const uint32_t*)(row + ((jj * kQ8Bytes) & ~3));
+            const float dw = f16_to_f32((uint16_t)((jj & 1) ? sc >> 16 : sc & 0xffffu));
+            const uint32_t* q = (const uint32_t*)(row + ca);
+            uint32_t qv[9], codes[8];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const char* row = srow + (2 * hr + i) * rp;
-                const uint32_t sc = *(const uint32_t*)(row + ((jj * kQ8Bytes) & ~3));
-                dw[i] = f16_to_f32((uint16_t)((jj & 1) ? sc >> 16 : sc & 0xffffu));
-                const uint32_t* q = (const uint32_t*)(row + ca);
-                uint32_t qv[9];
+            for (int e = 0; e < 9; ++e) qv[e] = q[e];
 #pragma unroll
-                for (int e = 0; e < 9; ++e) qv[e] = q[e];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) codes[i][e] = __builtin_amdgcn_alignbyte(qv[e + 1], qv[e], sh);
-            }
+            for (int e = 0; e < 8; ++e) codes[e] = __builtin_amdgcn_alignbyte(qv[e + 1], qv[e], sh);
 #pragma unroll
             for (int n = 0; n < kGlMaxTok; ++n) {
                 if (n >= N) break;                           // uniform
@@ -1831,57 +1864,72 @@ __global__ void __launch_bounds__(64 * (kGlMaxSlots + kGlMaxXWaves)) proj_gemv_l
                 const u32x4 c1 = *(const u32x4*)(xq + ((int64_t)n * nbk + jj) * 8 + 4);
                 const uint32_t xc[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
                 const float dx = xd[(int64_t)n * nbk + jj];
+                int sm = 0;
 #pragma unroll
-                for (int i = 0; i < 2; ++i) {
-                    int sm = 0;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) sm = __builtin_amdgcn_sdot4((int)codes[i][e], (int)xc[e], sm, false);
-                    const float f = fmaf((float)sm, dw[i] * dx, acc[i][n]);
-                    acc[i][n] = live ? f : acc[i][n];
-                }
+                for (int e = 0; e < 8; ++e) sm = __builtin_amdgcn_sdot4((int)codes[e], (int)xc[e], sm, false);
+                const float f = fmaf((float)sm, dw * dx, acc[n]);
+                acc[n] = live ? f : acc[n];
             }
         }
-        // as (row, token) sums: this lane's rows are 2 hr and 2 hr + 1
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int n = 0; n < kGlMaxTok; ++n) v[i * 2 + n] = acc[i][n];
+        tot = wave_sum4_halves(acc);
     }
-    // sums over the lanes: value (r, n) ends in lanes 8 (2 r + n) .. + 7,
-    // then lane r N + n takes its own
-    const float tot = Q8 ? wave_sum8_halves(v) : wave_sum8(v);
-    int orr, on;
-    lane_rn<kGlMaxTok>(lane < kGvRows * N ? lane : 0, N, orr, on);
-    const float outv = __shfl(tot, 8 * (orr * 2 + on));
+    // (row r, token n) sums end in lanes 16 (2 r + n) .. + 15; lane r N + n takes its own
+    const float outv = __shfl(tot, 16 * (L.r * 2 + L.n)) + addend;
     if constexpr (MODE == kProjQKVRope) {
-        asm volatile("s_barrier" : : : "memory");          // 2: RoPE table
+        // the rotation partner (row r ^ 1, same token) across the wave
+        const float vp = __shfl(outv, (L.r ^ 1) * N + L.n);
+        const int dim = (mrow0 & (a.d - 1)) + (L.r == 0 ? ro[0] : ro[1]);
+        const int head = mrow0 >> (a.d == 128 ? 7 : 6);
         float c = 1.0f, sn = 0.0f;
         if (mat < 2) {
-            const float2 cs = tab[rl.n * 64 + rl.i];
+            const float2 cs = tab[L.n * 64 + (dim & ((a.d >> 1) - 1))];
             c = cs.x;
             sn = cs.y;
         }
-        gemv_rope_finish(a, lane, N, mat, rl, c, sn, outv + addend);
+        if (!L.out) return;
+        float y = outv;
+        if (mat < 2) {
+            const bool hi = L.r == 1;
+            const float x0 = hi ? vp : outv, x1 = hi ? outv : vp;
+            y = hi ? fmaf(x0, sn, x1 * c) : fmaf(x0, c, -(x1 * sn));
+        }
+        // destinations are F32, F16 or BF16
+        char* dst;
+        if (mat == 0) {
+            dst = a.q_out + L.b * a.qo_nb_b + L.t * a.qo_nb_t + head * a.qo_nb_h +
+                  dim * (a.q_out_type == VVA_TYPE_F32 ? 4 : 2);
+        } else {
+            char* base = mat == 1 ? (L.b ? a.k_dst[1] : a.k_dst[0]) : (L.b ? a.v_dst[1] : a.v_dst[0]);
+            dst = base + L.t * a.cache_row_bytes + head * a.cache_head_bytes +
+                  dim * (a.cache_type == VVA_TYPE_F32 ? 4 : 2);
+        }
+        store_elem(dst, mat == 0 ? a.q_out_type : a.cache_type, y);
     } else {
-        gemv_store<MODE, kGlMaxTok>(a, lane, N, m0, outv + addend);
+        if (!L.out) return;
+        const int m = m0 + L.r;
+        if constexpr (MODE == kProjQKV) {
+            a.y[(int64_t)L.n * a.M + m] = outv;
+        } else {
+            *(float*)(a.h + L.b * a.h_nb_b + L.t * a.h_nb_t + (int64_t)m * 4) = outv;
+        }
     }
 }
 
 // Slots per workgroup of proj_gemv_lds_kernel (0: the call does not fit it)
 int gemv_lds_slots(const ProjArgs& a, int n_cu) {
     const bool q8 = a.w_type == VVA_TYPE_Q8_0;
-    if (a.N > kGlMaxTok || a.K > kGlMaxK || a.K % 64 || a.M % kGvRows) return 0;
+    if (a.N > kGlMaxTok || a.K > kGlMaxK || a.K % 64 || a.M % kGlRows) return 0;
     if (a.mode == kProjQKVRope && a.d > 128) return 0;        // the RoPE table holds 64 angles
-    // Q8_0: the last block's reads (20 bytes from below its second half) stay in the row pitch
+    // Q8_0: the last block's reads (9 dwords from below its codes) stay in the row pitch
     if (q8 && a.K / 32 * kQ8Bytes + 4 > gl_row_pitch(true, a.K)) return 0;
-    if (a.m_end[0] % kGvRows || a.m_end[1] % kGvRows) return 0;
+    if (a.m_end[0] % kGlRows || a.m_end[1] % kGlRows) return 0;
     for (int i = 0; i < 3; ++i) {                    // every row offset below the dead offset
         const int64_t rows = a.m_end[i] - (i == 0 ? 0 : a.m_end[i - 1]);
         if (rows > 0 && rows * a.w_nb[i] >= kGlDead) return 0;
     }
     const int rp = gl_row_pitch(q8, a.K);
-    const int fit = (kGlLdsMax - gl_slots_at(q8, a.K)) / (kGvRows * rp);
-    const int S = a.M / kGvRows;
+    const int fit = (kGlLdsMax - gl_slots_at(q8, a.K)) / (kGlRows * rp);
+    const int S = a.M / kGlRows;
     int sw = (S + n_cu - 1) / n_cu;
     if (sw > fit) sw = fit;
     if (sw > kGlMaxSlots) sw = kGlMaxSlots;
@@ -1891,7 +1939,7 @@ int gemv_lds_slots(const ProjArgs& a, int n_cu) {
 template <bool Q8, int MODE>
 hipError_t launch_gemv_lds(const ProjArgs& a, int sw, hipStream_t s) {
     const int rp = gl_row_pitch(Q8, a.K);
-    const dim3 g((a.M / kGvRows + sw - 1) / sw), bl(64 * (sw + gl_xwaves(Q8)));
+    const dim3 g((a.M / kGlRows + sw - 1) / sw), bl(64 * (sw + gl_xwaves(Q8)));
     const int ipr = rp / 1024;
 #define VVA_GL(I) case I: hipLaunchKernelGGL((proj_gemv_lds_kernel<Q8, MODE, I>), g, bl, 0, s, a, sw); break;
     switch (ipr) {
