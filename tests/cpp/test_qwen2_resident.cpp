@@ -30,6 +30,16 @@
 //              q, the appended rows, o and h against the oracle (ggml-order
 //              linear layers, RoPE recurrence, attention on the device's own
 //              operands).
+//   step       the cfg and q8 decodes with a q work buffer, so each layer's
+//              step runs as one vva_decode_step, in lockstep with the two-call
+//              path on a twin cache: rotated q and cache rows bit-identical,
+//              outputs bit-identical on Q8_0 caches and within 2e-3 / 1e-3 on
+//              F16, and against the oracle.
+//   timing     a 28-layer 7B CFG decode step (B = 2, Q8_0 cache, 32k and 2k
+//              keys) four ways: the two calls or the fused step, with a
+//              stream synchronization after every layer (as the ggml adapter
+//              does between its graphs) or once per step.  Prints the time per
+//              step; asserts only that every call succeeds.
 //   errors     past_len + T > max_seq, a bad layer and a bad sequence id come
 //              back as VVA_ERR_INVALID_ARG (the reference's GGML_ASSERTs,
 //              src/qwen2.cpp:269-270).
@@ -43,6 +53,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <chrono>
 #include <functional>
 #include <string>
 #include <vector>
@@ -356,39 +367,88 @@ int test_stack(vva_context* ctx) {
 }
 
 // Decode steps of B = 2 sequences after voice prompts of lengths `prompt`.
+// fused: every step also runs through the q work buffer (one
+// vva_decode_step per layer) on a twin cache holding the same rows, checked
+// against the two-call path and the oracle.
 int decode_steps(vva_context* ctx, int d, int Hq, int Hkv, int type, const int prompt[2], int steps,
-                 uint64_t seed, int code) {
+                 uint64_t seed, int code, bool fused = false) {
     const int layers = 2;
-    vva::ResidentKV kvs;
+    vva::ResidentKV kvs, kvf;
     if (!kvs.init(ctx, layers, d, Hkv, prompt[0] + prompt[1] + steps, 2, type)) return code;
+    if (fused && !kvf.init(ctx, layers, d, Hkv, prompt[0] + prompt[1] + steps, 2, type)) return code;
     Rng r(seed);
     for (int l = 0; l < layers; ++l)
         for (int s = 0; s < 2; ++s) {
             const std::vector<float> k = r.normal((size_t)prompt[s] * Hkv * d), v = r.normal(k.size());
             if (!status_ok("upload", kvs.upload(l, s, prompt[s], k.data(), v.data()), kvs)) return code + 1;
+            if (fused && !status_ok("upload", kvf.upload(l, s, prompt[s], k.data(), v.data()), kvf)) return code + 1;
         }
     kvs.past_len = {prompt[0], prompt[1]};
+    kvf.past_len = kvs.past_len;
     const vva::Qwen2Hparams hp = {Hq * d, Hq, Hkv, d, 1.0e6f, true};
     const int32_t seq_ids[2] = {0, 1};
-    Dev dq((size_t)2 * Hq * d * 4), dk((size_t)2 * Hkv * d * 4), dv((size_t)2 * Hkv * d * 4),
-        dout((size_t)2 * Hq * d * 4), dpos(8);
-    double worst = 0.0;
+    const size_t nq = (size_t)2 * Hq * d;
+    Dev dq(nq * 4), dk((size_t)2 * Hkv * d * 4), dv((size_t)2 * Hkv * d * 4), dout(nq * 4), dpos(8), dqf(nq * 4),
+        dqw(nq * 4), doutf(nq * 4);
+    double worst = 0.0, worst_pair = 0.0;
     for (int step = 0; step < steps; ++step) {
         const int32_t pos[2] = {kvs.past_len[0], kvs.past_len[1]};
         (void)hipMemcpy(dpos.p, pos, 8, hipMemcpyHostToDevice);
         for (int l = 0; l < layers; ++l) {
-            upload_as(dq, r.normal((size_t)2 * Hq * d), VVA_TYPE_F32);
+            const std::vector<float> q0 = r.normal(nq);
+            upload_as(dq, q0, VVA_TYPE_F32);
             upload_as(dk, r.normal((size_t)2 * Hkv * d), VVA_TYPE_F32);
             upload_as(dv, r.normal((size_t)2 * Hkv * d), VVA_TYPE_F32);
             vva_tensor tp = view4(dpos.p, VVA_TYPE_I32, 1, 2, 1, 1);     // pos ne=[T=1, B=2]
             const vva_tensor tq = view4(dq.p, VVA_TYPE_F32, d, Hq, 1, 2), tk = view4(dk.p, VVA_TYPE_F32, d, Hkv, 1, 2),
                              tv = view4(dv.p, VVA_TYPE_F32, d, Hkv, 1, 2),
                              to = view4(dout.p, VVA_TYPE_F32, d, Hq, 1, 2);
+            if (fused) {
+                upload_as(dqf, q0, VVA_TYPE_F32);
+                const vva_tensor tqf = view4(dqf.p, VVA_TYPE_F32, d, Hq, 1, 2),
+                                 tqw = view4(dqw.p, VVA_TYPE_F32, d, Hq, 1, 2),
+                                 tof = view4(doutf.p, VVA_TYPE_F32, d, Hq, 1, 2);
+                if (!status_ok("fused decode step",
+                               vva::qwen2_attention_resident(kvf, l, tqf, tk, tv, tp, nullptr, hp, tof, seq_ids, &tqw),
+                               kvf))
+                    return code + 4;
+            }
             if (!status_ok("decode step", vva::qwen2_attention_resident(kvs, l, tq, tk, tv, tp, nullptr, hp, to, seq_ids),
                            kvs))
                 return code + 2;
-            const std::vector<float> got = download_f32(dout.p, (size_t)2 * Hq * d, VVA_TYPE_F32);
-            const std::vector<float> q = download_f32(dq.p, (size_t)2 * Hq * d, VVA_TYPE_F32);
+            const std::vector<float> got = download_f32(dout.p, nq, VVA_TYPE_F32);
+            const std::vector<float> q = download_f32(dq.p, nq, VVA_TYPE_F32);
+            if (fused) {
+                const std::vector<float> gotf = download_f32(doutf.p, nq, VVA_TYPE_F32);
+                const std::vector<float> qw = download_f32(dqw.p, nq, VVA_TYPE_F32);
+                const std::vector<float> qf = download_f32(dqf.p, nq, VVA_TYPE_F32);
+                if (qw != q || qf != q0) {
+                    printf("  step %d layer %d: the work buffer's q differs from the in-place rotation, or q changed\n",
+                           step, l);
+                    return code + 5;
+                }
+                for (int s = 0; s < 2; ++s) {
+                    const int rows = kvs.past_len[s] + 1;
+                    if (cache_bytes(kvs.k(l, s), rows) != cache_bytes(kvf.k(l, s), rows) ||
+                        cache_bytes(kvs.v(l, s), rows) != cache_bytes(kvf.v(l, s), rows)) {
+                        printf("  step %d layer %d seq %d: cache rows differ between the paths\n", step, l, s);
+                        return code + 6;
+                    }
+                }
+                const Stats p = compare(gotf, got);
+                worst_pair = p.max_abs > worst_pair ? p.max_abs : worst_pair;
+                if (type == VVA_TYPE_Q8_0 ? gotf != got : !(p.finite && p.max_abs <= kMaxTol && p.mean_abs <= kMeanTol)) {
+                    within("fused step vs the two calls", p, 0.0, 0.0);
+                    return code + 7;
+                }
+                const std::vector<float> reff =
+                    oracle_out(qw, kvf, l, {0, 1}, {kvf.past_len[0] + 1, kvf.past_len[1] + 1}, 1, Hq, Hkv, d, type);
+                const Stats sf = compare(gotf, reff);
+                if (!sf.finite || sf.max_abs > kMaxTol || sf.mean_abs > kMeanTol) {
+                    within("fused step vs oracle", sf, kMaxTol, kMeanTol);
+                    return code + 8;
+                }
+            }
             const std::vector<float> ref =
                 oracle_out(q, kvs, l, {0, 1}, {kvs.past_len[0] + 1, kvs.past_len[1] + 1}, 1, Hq, Hkv, d, type);
             const Stats s = compare(got, ref);
@@ -401,9 +461,13 @@ int decode_steps(vva_context* ctx, int d, int Hq, int Hkv, int type, const int p
         }
         kvs.past_len[0] += 1;
         kvs.past_len[1] += 1;
+        kvf.past_len = kvs.past_len;
     }
     printf("  %d steps x %d layers, lengths %d / %d -> %d / %d: worst max-abs %.3e (tol %.0e)\n", steps, layers,
            prompt[0], prompt[1], kvs.past_len[0], kvs.past_len[1], worst, kMaxTol);
+    if (fused)
+        printf("  fused step (q work buffer) vs the two calls: q and cache rows bit-identical, output worst %.3e%s\n",
+               worst_pair, type == VVA_TYPE_Q8_0 ? " (bit-identical)" : "");
     return 0;
 }
 
@@ -415,6 +479,61 @@ int test_cfg(vva_context* ctx) {
 int test_q8(vva_context* ctx) {
     const int prompt[2] = {3000, 2311};
     return decode_steps(ctx, 128, 28, 4, VVA_TYPE_Q8_0, prompt, 3, 41, 40);
+}
+
+int test_step(vva_context* ctx) {
+    const int p05[2] = {1024, 957}, p7[2] = {3000, 2311};
+    const int rc = decode_steps(ctx, 64, 14, 2, VVA_TYPE_F16, p05, 4, 131, 90, true);
+    return rc ? rc : decode_steps(ctx, 128, 28, 4, VVA_TYPE_Q8_0, p7, 3, 141, 100, true);
+}
+
+// A 28-layer 7B CFG decode step (B = 2) on a Q8_0 cache, timed four ways.
+// The cache holds zeros (the time does not depend on the values); pos and
+// the lengths stay fixed, so every step appends at the same row.
+int test_timing(vva_context* ctx) {
+    const int d = 128, Hq = 28, Hkv = 4, layers = 28, B = 2, steps = 20;
+    const vva::Qwen2Hparams hp = {Hq * d, Hq, Hkv, d, 1.0e6f, true};
+    const int32_t seq_ids[2] = {0, 1};
+    for (const int past : {32768, 2048}) {
+        vva::ResidentKV kvs;
+        if (!kvs.init(ctx, layers, d, Hkv, past + 1, B, VVA_TYPE_Q8_0)) return 110;
+        kvs.past_len = {past, past};
+        const size_t nq = (size_t)B * Hq * d, nk = (size_t)B * Hkv * d;
+        Dev dq(nq * 4), dqw(nq * 4), dk(nk * 4), dv(nk * 4), dout(nq * 4), dpos(8);
+        Rng r(7);
+        upload_as(dq, r.normal(nq), VVA_TYPE_F32);
+        upload_as(dk, r.normal(nk), VVA_TYPE_F32);
+        upload_as(dv, r.normal(nk), VVA_TYPE_F32);
+        const int32_t pos[2] = {past, past};
+        (void)hipMemcpy(dpos.p, pos, 8, hipMemcpyHostToDevice);
+        const vva_tensor tq = view4(dq.p, VVA_TYPE_F32, d, Hq, 1, B), tqw = view4(dqw.p, VVA_TYPE_F32, d, Hq, 1, B),
+                         tk = view4(dk.p, VVA_TYPE_F32, d, Hkv, 1, B), tv = view4(dv.p, VVA_TYPE_F32, d, Hkv, 1, B),
+                         to = view4(dout.p, VVA_TYPE_F32, d, Hq, 1, B), tp = view4(dpos.p, VVA_TYPE_I32, 1, B, 1, 1);
+        double us[2][2];
+        for (int fused = 0; fused < 2; ++fused)
+            for (int per_layer = 0; per_layer < 2; ++per_layer) {
+                auto step = [&]() {
+                    for (int l = 0; l < layers; ++l) {
+                        const int st = vva::qwen2_attention_resident(kvs, l, tq, tk, tv, tp, nullptr, hp, to, seq_ids,
+                                                                     fused ? &tqw : nullptr);
+                        if (st != VVA_OK) return st;
+                        if (per_layer && hipStreamSynchronize(nullptr) != hipSuccess) return (int)VVA_ERR_DEVICE;
+                    }
+                    return hipStreamSynchronize(nullptr) == hipSuccess ? (int)VVA_OK : (int)VVA_ERR_DEVICE;
+                };
+                for (int w = 0; w < 3; ++w)
+                    if (!status_ok("timing warm-up", step(), kvs)) return 111;
+                const auto t0 = std::chrono::steady_clock::now();
+                for (int i = 0; i < steps; ++i)
+                    if (!status_ok("timing", step(), kvs)) return 112;
+                const auto t1 = std::chrono::steady_clock::now();
+                us[fused][per_layer] = std::chrono::duration<double, std::micro>(t1 - t0).count() / steps;
+            }
+        printf("  %d keys x 2 sequences, 28 layers, us per step:\n", past);
+        printf("    two calls,  sync per layer %8.1f   sync per step %8.1f\n", us[0][1], us[0][0]);
+        printf("    fused step, sync per layer %8.1f   sync per step %8.1f\n", us[1][1], us[1][0]);
+    }
+    return 0;
 }
 
 // ------------------------------------------------------------ the attention block
@@ -629,9 +748,10 @@ struct Case {
 }  // namespace
 
 int main(int argc, char** argv) {
-    const std::vector<Case> cases = {{"chunks", test_chunks}, {"stack", test_stack}, {"cfg", test_cfg},
-                                     {"q8", test_q8},         {"block", test_block},   {"errors", test_errors},
-                                     {"supports", test_supports}, {"order", test_order}};
+    const std::vector<Case> cases = {{"chunks", test_chunks},     {"stack", test_stack},   {"cfg", test_cfg},
+                                     {"q8", test_q8},             {"step", test_step},     {"timing", test_timing},
+                                     {"block", test_block},       {"errors", test_errors}, {"supports", test_supports},
+                                     {"order", test_order}};
     std::vector<std::string> want;
     for (int i = 1; i < argc; ++i) {
         if (!strcmp(argv[i], "--list")) {

@@ -13,7 +13,7 @@ import pytest
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 BIN = os.path.join(REPO, "tests", "cpp", "bin", "test_qwen2_resident")
 HOSTLIB = os.path.join(REPO, "vibevoice.cpp_amd", "lib", "libvva_qwen2.a")
-CASES = ["chunks", "stack", "cfg", "q8", "block", "errors", "supports", "order"]
+CASES = ["chunks", "stack", "cfg", "q8", "step", "timing", "block", "errors", "supports", "order"]
 
 
 def _need_built():

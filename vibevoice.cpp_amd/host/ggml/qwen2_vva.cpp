@@ -1,5 +1,6 @@
-// qwen2_vva.cpp — ggml side of the drop-in (see qwen2_vva.hpp).  Not
-// compiled in this repository: it needs the reference's headers and ggml's.
+// qwen2_vva.cpp — ggml side of the drop-in (see qwen2_vva.hpp).  Not built
+// in this repository: it needs the reference's headers and ggml's (its
+// syntax is checked against stand-in declarations, tests/ggml_standin/).
 #include "qwen2_vva.hpp"
 
 #include "rms_norm.hpp"           // vv::rms_norm (src/rms_norm.hpp)
@@ -43,6 +44,17 @@ bool run_graph(F build) {
 }
 
 bool sync(const VvaAttn& a) { return hipStreamSynchronize(a.stream) == hipSuccess; }
+
+// the first n0 * n1 * n2 * n3 elements of an F32 work tensor as a contiguous
+// library view of ne = [n0, n1, n2, n3]
+vva_tensor work_rows(const struct ggml_tensor* w, int64_t n0, int64_t n1, int64_t n2, int64_t n3) {
+    vva_tensor v = {};
+    v.data = w->data;
+    v.type = VVA_TYPE_F32;
+    v.ne[0] = n0; v.ne[1] = n1; v.ne[2] = n2; v.ne[3] = n3;
+    v.nb[0] = 4; v.nb[1] = 4 * n0; v.nb[2] = 4 * n0 * n1; v.nb[3] = 4 * n0 * n1 * n2;
+    return v;
+}
 
 }  // namespace
 
@@ -94,10 +106,16 @@ bool qwen2_attention_vva(VvaAttn& a, int layer_idx, struct ggml_tensor* q, struc
     const vva_tensor tq = view_of(q), tk = view_of(k), tv = view_of(v), tp = view_of(pos), to = view_of(o);
     vva_tensor tm = {};
     if (mask) tm = view_of(mask);
+    // a decode step (one token per stream, causal) rotates q into the work
+    // tensor a.q and runs as one fused vva_decode_step
+    const int64_t T = q->ne[2], B = q->ne[3] > 0 ? q->ne[3] : 1;
+    vva_tensor tw = {};
+    const bool step = T == 1 && !mask && B <= a.max_tokens;
+    if (step) tw = work_rows(a.q, q->ne[0], q->ne[1], T, B);
     // the graph that produced q / k / v has completed (ggml_backend_graph_compute
     // returns after synchronizing); the library works on its own stream
     const int st = vva::qwen2_attention_resident(a.kv, layer_idx, tq, tk, tv, tp, mask ? &tm : nullptr, a.hp, to,
-                                                 seq_ids);
+                                                 seq_ids, step ? &tw : nullptr);
     return st == VVA_OK && sync(a);
 }
 

@@ -1,7 +1,9 @@
 // qwen2_vva.hpp — ggml side of the drop-in, for the reference's src/ tree.
 //
-// Not compiled in this repository: it includes the reference's qwen2.hpp /
-// backend.hpp and ggml's headers, which are not here.  A maintainer adds
+// Not built in this repository: it includes the reference's qwen2.hpp /
+// backend.hpp and ggml's headers, and ggml is not here.  A CPU test checks
+// its syntax against stand-in declarations of ggml's API
+// (tests/ggml_standin/).  A maintainer adds
 // qwen2_vva.cpp to the reference's library target with the include
 // directories <repo>/include and <repo>/vibevoice.cpp_amd/host and links
 // <repo>/vibevoice.cpp_amd/lib/libvva_qwen2.a, libvva.so and amdhip64.
@@ -61,7 +63,9 @@ vva_tensor as_vva(const struct ggml_tensor* t);
 
 // The attention section of qwen2_layer_forward_resident (src/qwen2.cpp:282-335)
 // on tensors a ggml graph has already computed (device memory):
-//   q ne=[hd, n_h, T, B], rotated in place; k, v ne=[hd, n_kv_h, T, B];
+//   q ne=[hd, n_h, T, B], rotated in place, except for a decode step (T = 1,
+//   no mask), which rotates it into a.q and runs as one vva_decode_step;
+//   k, v ne=[hd, n_kv_h, T, B];
 //   pos I32 ne=[T] or [T, B]; mask NULL (causal) or the F16 mask;
 //   o F32 ne=[hd, n_h, T, B] (the cont_2d'd FA output).
 // Returns when the result is in o.  past_len is not advanced.

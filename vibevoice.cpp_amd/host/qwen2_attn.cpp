@@ -80,18 +80,29 @@ int prepare(ResidentKV& kvs, int layer_idx, int64_t n_tokens, int64_t n_batch, c
 
 int qwen2_attention_resident(ResidentKV& kvs, int layer_idx, const vva_tensor& q, const vva_tensor& k,
                              const vva_tensor& v, const vva_tensor& pos, const vva_tensor* mask,
-                             const Qwen2Hparams& hp, const vva_tensor& o, const int32_t* seq_ids) {
+                             const Qwen2Hparams& hp, const vva_tensor& o, const int32_t* seq_ids,
+                             const vva_tensor* q_ws) {
     const int hd = hp.head_dim;
     if (q.ne[0] != hd || q.ne[1] != hp.n_heads || k.ne[1] != hp.n_kv_heads || v.ne[1] != hp.n_kv_heads)
         return VVA_ERR_INVALID_ARG;
+    if (q_ws && (q_ws->ne[0] != q.ne[0] || q_ws->ne[1] != q.ne[1] || q_ws->ne[2] != q.ne[2] ||
+                 q_ws->ne[3] != q.ne[3]))
+        return VVA_ERR_INVALID_ARG;
     int fa = prepare(kvs, layer_idx, q.ne[2], q.ne[3] > 0 ? q.ne[3] : 1, hp, seq_ids);
     if (fa != VVA_OK) return fa;
+    const float scale = 1.0f / sqrtf((float)hd);
+    const vva_tensor& qr = q_ws ? *q_ws : q;                 // where RoPE(q) goes
+    if (q_ws && q.ne[2] == 1 && !mask) {
+        // one new token per sequence under the causal mask: RoPE, append and
+        // attention as one fused step (src/qwen2.cpp:282-335 for T = 1)
+        return vva_decode_step(kvs.ctx, kvs.kv, layer_idx, &q, &k, &v, &pos, seq_ids, hp.rope_theta, scale, &qr,
+                               &o);
+    }
     // rope(q), rope(k), cpy(k -> window at past_len), cpy(v -> ...)  src/qwen2.cpp:282-306
-    int st = vva_rope_append(kvs.ctx, kvs.kv, layer_idx, &q, &k, &v, &pos, seq_ids, hp.rope_theta, &q);
+    int st = vva_rope_append(kvs.ctx, kvs.kv, layer_idx, &q, &k, &v, &pos, seq_ids, hp.rope_theta, &qr);
     if (st != VVA_OK) return st;
     // views of the window + flash_attn_ext(scale 1/sqrt(hd)), prec F32  src/qwen2.cpp:312-335
-    const float scale = 1.0f / sqrtf((float)hd);
-    return vva_attn(kvs.ctx, kvs.kv, layer_idx, &q, seq_ids, mask, scale, &o);
+    return vva_attn(kvs.ctx, kvs.kv, layer_idx, &qr, seq_ids, mask, scale, &o);
 }
 
 int qwen2_attention_block_resident(ResidentKV& kvs, int layer_idx, const vva_tensor& xn, const vva_tensor& x,

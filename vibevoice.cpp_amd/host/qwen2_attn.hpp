@@ -87,20 +87,25 @@ struct ResidentKV {
 // written into the resident window at each sequence's past_len
 // (src/qwen2.cpp:293-306), then attention of q over the window
 // [0, past_len + T) with scale 1/sqrt(hd) (src/qwen2.cpp:312-335).
-//   q:       F32/F16/BF16 ne=[hd, n_heads, T, B], rotated in place;
+//   q:       F32/F16/BF16 ne=[hd, n_heads, T, B], rotated in place (unless q_ws);
 //   k, v:    F32/F16/BF16 ne=[hd, n_kv_heads, T, B];
 //   pos:     I32 ne=[T] (shared) or [T, B] (per sequence): absolute positions;
 //   mask:    nullptr = causal (key j visible to row t iff j <= past_len + t),
 //            or F16 ne=[>= past_len + T, T, 1, 1 or B] with 0 / -inf entries;
 //   o:       F32 ne=[hd, n_heads, T, B];
 //   seq_ids: host [B], the cache sequence of batch b (nullptr: b).
+//   q_ws:    nullptr, or a work tensor of q's shape that receives RoPE(q)
+//            instead of q: then a decode step (T = 1, mask nullptr) runs as
+//            one vva_decode_step (RoPE, append and attention fused; q left
+//            as it was), with the two calls' results.
 // All device tensors are read and written in stream order on the context's
 // stream.  past_len is not advanced: the caller does that once the whole
 // stack ran for these T tokens (ResidentKV::past_len += T).  Returns a
 // vva_status.
 int qwen2_attention_resident(ResidentKV& kvs, int layer_idx, const vva_tensor& q, const vva_tensor& k,
                              const vva_tensor& v, const vva_tensor& pos, const vva_tensor* mask,
-                             const Qwen2Hparams& hp, const vva_tensor& o, const int32_t* seq_ids = nullptr);
+                             const Qwen2Hparams& hp, const vva_tensor& o, const int32_t* seq_ids = nullptr,
+                             const vva_tensor* q_ws = nullptr);
 
 // Device views of the attention weights of a layer (the attn_q / attn_k /
 // attn_v / attn_o fields of vv::Qwen2LayerWeights, src/qwen2.hpp:41-54):
