@@ -18,7 +18,8 @@ THETA_RECURRENCE, THETA_POW = 0, 1
 MAX_B = 16
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "lib", "libvvo.so")
+# VVO_LIB names another build of the oracle (the sanitized lib/san/libvvo.so)
+LIB_PATH = os.environ.get("VVO_LIB") or os.path.join(_HERE, "lib", "libvvo.so")
 
 
 class AttnArgs(ctypes.Structure):
