@@ -499,16 +499,19 @@ def run_proj(torch, vva, vvo, reps: int = 10):
                       f"{reps} times (us_per_call), and the same calls launched eagerly", **out}
 
 
-def run_small_prefills(torch, vva, reps: int = 20):
+def run_small_prefills(torch, vva, reps: int = 20, vvo=None):
     """The two short prefill configurations, attention launch only (after the
-    RoPE + append), HIP events around `reps` launches per layer of a 28- (or
-    24-) layer stack:
+    RoPE + append), HIP events around `reps` passes over the launches of a
+    28- (or 24-) layer stack:
       C1  0.5B heads (14 q / 2 kv, d = 64), 256 tokens, F32 Q/K/V and F32
           cache: the fp32 eager branch (src/qwen2.cpp:336-344; the 1e-4
           tolerance), and beside it the flash branch, which casts the F32
           window to F16 (src/qwen2.cpp:328-331) and runs the MFMA prefill;
       C3  1.5B heads (12 q / 2 kv, d = 128), 4096 tokens, bf16 Q/K/V, F16
-          cache: the MFMA flash prefill."""
+          cache: the MFMA flash prefill.
+    With vvo, C1's eager line and C3 carry a cpu_baseline: the oracle on
+    layer 0's cache and rotated Q (C1: every row, fp32 accumulation; C3: 512
+    rows spread over the 4096, ggml order), repeated for about 2 s."""
     ctx = vva.Context(0)
     res = {}
     for name, (d, hq, hkv, T, layers, qt, ct, fa) in {
@@ -526,26 +529,51 @@ def run_small_prefills(torch, vva, reps: int = 20):
         kv.set_len(0, 0)
         for layer in range(layers):
             ctx.rope_append(kv, layer, q, k, v, pos, qr, freq_base=THETA)
-        ev = []
-        for rep in range(reps + 2):
+        for rep in range(2):
             for layer in range(layers):
-                e = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                e[0].record()
                 ctx.attn(kv, layer, qr, out, d ** -0.5)
-                e[1].record()
-                if rep >= 2:
-                    ev.append(e)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for rep in range(reps):
+            for layer in range(layers):
+                ctx.attn(kv, layer, qr, out, d ** -0.5)
+        e1.record()
         torch.cuda.synchronize()
-        ms = float(np.mean([a.elapsed_time(b) for a, b in ev]))
+        ms = e0.elapsed_time(e1) / (reps * layers)
         flops = 4.0 * hq * d * T * (T + 1) / 2
         peak = 157.3 if not fa else PEAK_F16_TFLOPS
         res[name] = {"attn_ms_per_layer": round(ms, 4), "tflops": round(flops / ms / 1e9, 2),
                      "peak_tflops": peak, "frac": round(flops / ms / 1e9 / peak, 4), "layers": layers,
                      "flop_per_layer": flops}
+        if vvo is not None and name != "c1_0p5b_f32cache_flash_T256":
+            res[name]["cpu_baseline"] = cpu_baseline_small(vvo, kv, qr, d, hq, hkv, T, ct)
         kv.free()
     ctx.close()
-    res["timing"] = "HIP events around each attention launch, mean over layers x reps"
+    res["timing"] = "HIP events around reps x layers back-to-back attention launches (the stack's order), per launch"
     return res
+
+
+def cpu_baseline_small(vvo, kv, qr, d, hq, hkv, T, ct):
+    """Oracle on layer 0 of a short prefill (all host cores), repeated for about 2 s: F32 caches
+    every query row in fp32 accumulation, F16 caches 512 rows spread over [0, T) in ggml order."""
+    kraw, vraw = kv.download(0, 0, T)
+    q32 = qr.float().cpu().numpy()
+    if ct == vvo.F32:
+        rows, mode, what = np.arange(T, dtype=np.int32), vvo.GGML_F32ACC, "every row, fp32 accumulation, F32 K/V"
+    else:
+        rows, mode, what = np.linspace(0, T - 1, 512).astype(np.int32), vvo.GGML, "512 rows spread, ggml order, F16 K/V"
+    calls = 0
+    t0 = time.perf_counter()
+    while True:
+        vvo.attn(q32, [kraw.reshape(-1)], [vraw.reshape(-1)], ct, ct, [T], n_kv_heads=hkv, scale=d ** -0.5,
+                 mode=mode, rows=rows)
+        calls += 1
+        dt = time.perf_counter() - t0
+        if dt >= 2.0:
+            break
+    flops = calls * float(sum(4.0 * hq * d * (int(r) + 1) for r in rows))
+    return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": vvo.n_cores(), "kind": "port",
+            "sample": f"1 layer, {len(rows)} query rows x {hq} heads ({what}), {calls} calls, {dt:.1f} s"}
 
 
 def cpu_baseline_prefill(torch, vva, vvo, kv, qr):
@@ -630,7 +658,7 @@ def main() -> int:
         elif args.only == "proj":
             r = run_proj(torch, vva, vvo)
         else:
-            r = run_small_prefills(torch, vva)
+            r = run_small_prefills(torch, vva, vvo=None if args.no_cpu else vvo)
             c = vva.Context(0)
             r["c2_decode_small"] = run_decode_small(torch, vva, c, steps=200)
             c.close()
@@ -703,7 +731,7 @@ def main() -> int:
         line["prefill_chunked_q8_0"] = run_prefill_chunked(torch, vva, ctx, layers=2, cache_type=vva.Q8_0)
         torch.cuda.empty_cache()
         line["decode_small"] = run_decode_small(torch, vva, ctx, steps=200, vvo=None if args.no_cpu else vvo)
-        line["prefill_small"] = run_small_prefills(torch, vva)
+        line["prefill_small"] = run_small_prefills(torch, vva, vvo=None if args.no_cpu else vvo)
         torch.cuda.empty_cache()
         line["proj"] = run_proj(torch, vva, vvo)
     ctx.close()

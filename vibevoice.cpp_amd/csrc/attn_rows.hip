@@ -503,6 +503,183 @@ __global__ void __launch_bounds__(64 * kGqaWaves) attn_gqa_f32_kernel(AttnArgs a
     }
 }
 
+// F32 K and V on fp32 MFMA (v_mfma_f32_16x16x4f32): the eager branch's two
+// mul_mats (src/qwen2.cpp:337-343) as matrix products.  A workgroup takes 16
+// consecutive query rows i = t G + h of one (sequence, kv head), so the kv
+// head's K and V rows are read once for its whole query-head group, and
+// kMfWaves waves; wave w takes the 16-key blocks w, w + W, ... of the keys
+// visible to any of the rows, the next block's K and V loads in flight while
+// it computes one.  Per block, with lane l = 16 g + c (c = l % 16, g = l / 16)
+// owning query row c:
+//   S^T = K Q^T (keys x rows): the contraction over d in D / 4 steps, lane
+//     group g supplying d = g D/4 + s at step s (K row key0 + c and Q row c
+//     read as contiguous chunks); lane l receives S^T[key 4 g + j][row c];
+//   the online softmax of row c over the block: scale, mask, max and sum over
+//     the lane's 4 keys and across the 4 lane groups (permlane swaps);
+//   O^T += V^T P^T (d x rows) in D / 16 tiles of 16 d: at step s lane group g
+//     supplies key 4 g + s (its own p[s] as the B operand, V[key][D/16 c + ct]
+//     of tile ct as the A operand), so lane l accumulates O[row c][d] for the
+//     D / 4 consecutive d = g D/4 .. g D/4 + D/4 - 1.
+// Products and sums in fp32 (MFMA accumulation order instead of ggml's
+// sequential one); the waves' (max, sum, O) per row are combined through
+// LDS by log-sum-exp.  Same semantics as attn_gqa_f32_kernel.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+constexpr int kMfWaves = 8;
+template <int D>
+__global__ void __launch_bounds__(64 * kMfWaves) attn_gqa_f32_mfma_kernel(AttnArgs a) {
+    prefetch_kernargs<sizeof(AttnArgs)>();
+    constexpr int DQ = D / 4;                                // d per lane group (S^T steps)
+    constexpr int CT = D / 16;                               // O^T tiles
+    __shared__ float msh[kMfWaves][16], lsh[kMfWaves][16];
+    __shared__ __attribute__((aligned(16))) float osh[kMfWaves][16][D + 4];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int c = lane & 15, g = lane >> 4;
+    const int G = a.Hq / a.Hkv;
+    const int rows = a.T * G;
+    const int ntile = (rows + 15) / 16;
+    const int tile = blockIdx.x % ntile;
+    const int kvh = (blockIdx.x / ntile) % a.Hkv;
+    const int b = blockIdx.x / (ntile * a.Hkv);
+    const int i = tile * 16 + c;                             // this lane's query row
+    const bool rlive = i < rows;
+    const int ii = rlive ? i : rows - 1;
+    const int t = ii / G, h = ii - t * G;
+    const int L = a.L[b];
+    const int t_last = min(tile * 16 + 15, rows - 1) / G;
+    const bool causal = a.mask_mode == kMaskCausal;
+    const int jend = causal ? min(L, a.past[b] + t_last + 1) : L;   // keys any row of the tile may see
+    const int jrow = !rlive ? 0 : causal ? min(L, a.past[b] + t + 1) : L;
+    const char* mrow = a.mask_mode == kMaskExplicit ? a.mask + b * a.mask_nb_b + t * a.mask_nb_row : nullptr;
+
+    // Q[row c][g DQ .. g DQ + DQ): one code path per type, so the DQ loads
+    // go out together (a per-element type switch would wait on each)
+    float q[DQ];
+    {
+        const char* qr = a.q + b * a.q_nb_b + t * a.q_nb_t + (int64_t)(kvh * G + h) * a.q_nb_h;
+        if (a.q_type == VVA_TYPE_F32) {
+#pragma unroll
+            for (int s = 0; s < DQ; ++s) q[s] = *(const float*)(qr + (int64_t)(g * DQ + s) * 4);
+        } else {
+            uint16_t q16[DQ];
+#pragma unroll
+            for (int s = 0; s < DQ; ++s) q16[s] = *(const uint16_t*)(qr + (int64_t)(g * DQ + s) * 2);
+            if (a.q_type == VVA_TYPE_BF16) {
+#pragma unroll
+                for (int s = 0; s < DQ; ++s) q[s] = bf16_to_f32(q16[s]);
+            } else {
+#pragma unroll
+                for (int s = 0; s < DQ; ++s) q[s] = f16_to_f32(q16[s]);
+            }
+        }
+    }
+    const char* kbase = a.k[b] + kvh * a.k_nb_head;
+    const char* vbase = a.v[b] + kvh * a.v_nb_head;
+    float m = -INFINITY, l = 0.0f;
+    f32x4 o[CT];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) o[ct] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    // K row key0 + c as DQ / 4 vectors; V rows key0 + 4 g + s, d = CT c ..
+    // CT c + CT - 1 as CT / 4 vectors each (rows past the window repeat the
+    // last one: their scores are masked)
+    float4 kr4[DQ / 4], vv4[4][CT / 4];
+    auto load_block = [&](int key0, float4 (&kq)[DQ / 4], float4 (&vq)[4][CT / 4]) {
+        const float4* kp = (const float4*)(kbase + (int64_t)min(key0 + c, L - 1) * a.k_nb_tok) + g * (DQ / 4);
+#pragma unroll
+        for (int s4 = 0; s4 < DQ / 4; ++s4) kq[s4] = kp[s4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const float4* vp = (const float4*)(vbase + (int64_t)min(key0 + 4 * g + s, L - 1) * a.v_nb_tok) + c * (CT / 4);
+#pragma unroll
+            for (int c4 = 0; c4 < CT / 4; ++c4) vq[s][c4] = vp[c4];
+        }
+    };
+    load_block(16 * wv, kr4, vv4);
+    for (int kb = wv; kb * 16 < jend; kb += kMfWaves) {
+        const int key0 = kb * 16;
+        float4 krn[DQ / 4], vvn[4][CT / 4];
+        load_block(key0 + 16 * kMfWaves, krn, vvn);          // the next block's rows, in flight meanwhile
+        float kr[DQ], vv[4][CT];
+#pragma unroll
+        for (int s4 = 0; s4 < DQ / 4; ++s4) {
+            kr[4 * s4] = kr4[s4].x; kr[4 * s4 + 1] = kr4[s4].y; kr[4 * s4 + 2] = kr4[s4].z; kr[4 * s4 + 3] = kr4[s4].w;
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int c4 = 0; c4 < CT / 4; ++c4) {
+                vv[s][4 * c4] = vv4[s][c4].x; vv[s][4 * c4 + 1] = vv4[s][c4].y;
+                vv[s][4 * c4 + 2] = vv4[s][c4].z; vv[s][4 * c4 + 3] = vv4[s][c4].w;
+            }
+        f32x4 st = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < DQ; ++s) st = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[s], q[s], st, 0, 0, 0);
+        // scores of row c for keys key0 + 4 g + j
+        float sc[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int key = key0 + 4 * g + j;
+            const float mv = mrow && key < L ? mask_at(mrow, key, a.mask_f32) : 0.0f;
+            sc[j] = key >= jrow || mv == -INFINITY ? -INFINITY : st[j] * a.scale + mv;
+        }
+        float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+        mx = max_swap32(max_swap16(mx));
+        const float mn = fmaxf(m, mx);
+        const float alpha = mn == -INFINITY ? 1.0f : __expf(m - mn);   // 0 while m = -inf
+        float p[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) p[j] = sc[j] == -INFINITY ? 0.0f : __expf(sc[j] - mn);
+        const float ps = add_swap32(add_swap16((p[0] + p[1]) + (p[2] + p[3])));
+        l = fmaf(l, alpha, ps);
+        m = mn;
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) o[ct] *= alpha;
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) o[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[s][ct], p[s], o[ct], 0, 0, 0);
+#pragma unroll
+        for (int s4 = 0; s4 < DQ / 4; ++s4) kr4[s4] = krn[s4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int c4 = 0; c4 < CT / 4; ++c4) vv4[s][c4] = vvn[s][c4];
+    }
+    // combine the waves per row: log-sum-exp of (m, l, O)
+    if (g == 0) {
+        msh[wv][c] = m;
+        lsh[wv][c] = l;
+    }
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) osh[wv][c][g * DQ + CT * j + ct] = o[ct][j];
+    __syncthreads();
+    // thread -> (row r, EPT consecutive d): the waves' weights once per thread
+    constexpr int EPT = 16 * D / (64 * kMfWaves);
+    const int r = threadIdx.x / (D / EPT), e0 = (threadIdx.x - r * (D / EPT)) * EPT;
+    const int ir = tile * 16 + r;
+    if (ir >= rows) return;
+    float Mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kMfWaves; ++w) Mx = fmaxf(Mx, msh[w][r]);
+    float num[EPT], den = 0.0f;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) num[e] = 0.0f;
+    if (Mx != -INFINITY) {
+#pragma unroll
+        for (int w = 0; w < kMfWaves; ++w) {
+            const float f = __expf(msh[w][r] - Mx);          // 0 for a wave that saw nothing
+            den = fmaf(lsh[w][r], f, den);
+#pragma unroll
+            for (int e = 0; e < EPT; ++e) num[e] = fmaf(osh[w][r][e0 + e], f, num[e]);
+        }
+    }
+    const int tr = ir / G, hr = ir - tr * G;
+    float* orow = (float*)((char*)a.out + b * a.o_nb_b + tr * a.o_nb_t + (int64_t)(kvh * G + hr) * a.o_nb_h) + e0;
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) orow[e] = den == 0.0f ? 0.0f : num[e] / den;
+}
+
 // F32 K and V with 16-byte aligned rows take attn_rows_f32_kernel.
 bool rows_f32_ok(const AttnArgs& a) {
     if (a.k_type != VVA_TYPE_F32 || a.v_type != VVA_TYPE_F32) return false;
@@ -513,6 +690,14 @@ bool rows_f32_ok(const AttnArgs& a) {
     return true;
 }
 
+// V rows 16-byte aligned (the MFMA kernel reads them as float4)
+bool v_rows_aligned(const AttnArgs& a) {
+    if (a.v_nb_tok % 16 || a.v_nb_head % 16) return false;
+    for (int b = 0; b < a.B; ++b)
+        if ((uintptr_t)a.v[b] % 16) return false;
+    return true;
+}
+
 }  // namespace
 
 hipError_t launch_attn_rows(const AttnArgs& a, hipStream_t s) {
@@ -520,6 +705,14 @@ hipError_t launch_attn_rows(const AttnArgs& a, hipStream_t s) {
     if (rows == 0) return hipSuccess;
     dim3 grid((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock));
     const int dpl = (a.d + 63) / 64;
+    if (rows_f32_ok(a) && (a.d == 64 || a.d == 128) && a.T >= 4 && v_rows_aligned(a)) {
+        // several tokens: the fp32 MFMA kernel, 16 query rows of a kv head per workgroup
+        const int G = a.Hq / a.Hkv;
+        const dim3 g((unsigned)((int64_t)a.B * a.Hkv * ((a.T * G + 15) / 16)));
+        if (a.d == 64) hipLaunchKernelGGL((attn_gqa_f32_mfma_kernel<64>), g, dim3(64 * kMfWaves), 0, s, a);
+        else           hipLaunchKernelGGL((attn_gqa_f32_mfma_kernel<128>), g, dim3(64 * kMfWaves), 0, s, a);
+        return hipGetLastError();
+    }
     if (rows_f32_ok(a) && (a.d == 64 || a.d == 128) && a.Hq / a.Hkv <= kGqaMaxG) {
         const dim3 g((unsigned)((int64_t)a.B * a.T * a.Hkv));
         if (a.d == 64) hipLaunchKernelGGL((attn_gqa_f32_kernel<64>), g, dim3(64 * kGqaWaves), 0, s, a);
