@@ -1,4 +1,7 @@
-// attn_rows.hip — VALU attention, one wavefront per query row.
+// attn_rows.hip — attention for the shapes the MFMA prefill and split-K
+// decode kernels do not take: VALU kernels (one wavefront per query row, or
+// per token and kv head), and the fp32 MFMA kernel of the eager branch for
+// several tokens over F32 caches (attn_gqa_f32_mfma_kernel).
 //
 // Covers every combination the MFMA prefill and split-K decode kernels do
 // not: F32 caches (the eager mul_mat -> soft_max_ext -> mul_mat branch,
