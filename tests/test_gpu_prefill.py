@@ -431,3 +431,46 @@ def test_prefill_v_at_the_f16_range_edge(ctx, torch_gpu, t):
         kv.free()
     assert np.isfinite(outs[1]).all()
     np.testing.assert_array_equal(outs[1], outs[0] * 2.0 ** 14)
+
+
+@pytest.mark.parametrize("which", ["v", "k"])
+def test_prefill_q8_0_window_beyond_the_f16_range(ctx, torch_gpu, which):
+    """A Q8_0 prefill converts the window to f16 for the MFMA kernel; a block
+    with |d q| > 65504 has no f16 value.  ggml dequantizes Q8_0 to fp32
+    (src/qwen2.cpp:332-335), so the result must stay finite and match the
+    oracle: the conversion flags the call and a gated fp32 kernel recomputes
+    it from the Q8_0 cache.  "v": V * 2^16 (values to ~2.6e5; the output
+    scales by exactly 2^16); "k": K * 2^16 with Q * 2^-16 (the scores keep
+    their size), against the oracle on those inputs.  A 256-token chunk over
+    a 300-token past at the 7B head shape."""
+    torch = torch_gpu
+    d, Hq, Hkv, T, past = 128, 28, 4, 256, 300
+    L = past + T
+    rng = np.random.default_rng(57)
+    k = rng.standard_normal((L, Hkv, d)).astype(np.float32)
+    v = rng.standard_normal((L, Hkv, d)).astype(np.float32)
+    q = rng.standard_normal((1, T, Hq, d)).astype(np.float32)
+    big = 2.0 ** 16
+    if which == "v":
+        v = v * big
+    else:
+        k, q = k * big, q / big
+    kv = vva.KVCache(ctx, 1, Hkv, d, L, 1, vva.Q8_0)
+    kv.upload(0, 0, 0, k, v)
+    kv.set_len(0, past)
+    qg = to_gpu(torch, q, vva.F32)
+    out = torch.full((1, T, Hq, d), float("nan"), dtype=torch.float32, device="cuda")
+    ctx.attn(kv, 0, qg, out, d ** -0.5)
+    torch.cuda.synchronize()
+    got = as_f32(torch, out)
+    raw = kv.download(0, 0, L)[0 if which == "k" else 1].reshape(-1)
+    vmax = np.abs(vvo.to_f32(raw, vva.Q8_0, L * Hkv * d)).max()
+    assert vmax > 65504.0, vmax
+    assert np.isfinite(got).all(), "non-finite output beyond the f16 range"
+    ref = oracle_attn(as_f32(torch, qg), kv, 0, [0], [L], T, d ** -0.5)
+    if which == "v":
+        mx, mn = assert_close(got / big, ref / big, *TOL, what="V * 2^16, rescaled")
+    else:
+        mx, mn = assert_close(got, ref, *TOL, what="K * 2^16, Q * 2^-16")
+    print(f"  {which} up to {vmax:.3g}: max {mx:.2e} mean {mn:.2e}")
+    kv.free()

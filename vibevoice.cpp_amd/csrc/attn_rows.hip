@@ -30,6 +30,7 @@ constexpr int kRowsPerBlock = 4;   // one row per wave
 template <int DPL>
 __global__ void __launch_bounds__(256) attn_rows_kernel(AttnArgs a) {
     prefetch_kernargs<sizeof(AttnArgs)>();
+    if (a.gate && *a.gate != a.gate_epoch) return;     // a gated fallback that is not needed
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
     if (row >= a.B * a.T * a.Hq) return;        // whole wave leaves together
@@ -176,6 +177,7 @@ constexpr int kVBatch = 16;
 template <int DPL, int D>
 __global__ void __launch_bounds__(256) attn_rows_f32_kernel(AttnArgs a) {
     prefetch_kernargs<sizeof(AttnArgs)>();
+    if (a.gate && *a.gate != a.gate_epoch) return;     // a gated fallback that is not needed
     __shared__ __attribute__((aligned(16))) float qsh[kRowsPerBlock][256];
     __shared__ __attribute__((aligned(16))) float psh[kRowsPerBlock][64];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -355,6 +357,7 @@ constexpr int kGqaMaxG = 8;
 template <int D>
 __global__ void __launch_bounds__(64 * kGqaWaves) attn_gqa_f32_kernel(AttnArgs a) {
     prefetch_kernargs<sizeof(AttnArgs)>();
+    if (a.gate && *a.gate != a.gate_epoch) return;     // a gated fallback that is not needed
     constexpr int DPL = (D + 63) / 64;
     constexpr int VB = D == 64 ? 64 : 16;                    // V keys loaded together
     __shared__ __attribute__((aligned(16))) float qsh[kGqaMaxG][D];
@@ -531,6 +534,7 @@ constexpr int kMfWaves = 8;
 template <int D>
 __global__ void __launch_bounds__(64 * kMfWaves) attn_gqa_f32_mfma_kernel(AttnArgs a) {
     prefetch_kernargs<sizeof(AttnArgs)>();
+    if (a.gate && *a.gate != a.gate_epoch) return;     // a gated fallback that is not needed
     constexpr int DQ = D / 4;                                // d per lane group (S^T steps)
     constexpr int CT = D / 16;                               // O^T tiles
     __shared__ float msh[kMfWaves][16], lsh[kMfWaves][16];

@@ -710,7 +710,8 @@ hipError_t launch_pf(const AttnArgs& a, float* ws, unsigned* tickets, const Pref
 
 // One thread per 32-element block of a K or V head row of one sequence:
 // grid (blocks of the longest window / 256, 2 B: K and V of each sequence).
-__global__ void __launch_bounds__(256) window_to_f16_kernel(AttnArgs a, uint16_t* __restrict__ dst) {
+__global__ void __launch_bounds__(256) window_to_f16_kernel(AttnArgs a, uint16_t* __restrict__ dst,
+                                                            unsigned long long* ovf, unsigned long long epoch) {
     prefetch_kernargs<sizeof(AttnArgs)>();
     const int b = blockIdx.y >> 1, which = blockIdx.y & 1;
     const int nblk = a.d / 32;
@@ -733,6 +734,12 @@ __global__ void __launch_bounds__(256) window_to_f16_kernel(AttnArgs a, uint16_t
         for (int e = 0; e < 16; ++e)
             w[e] = (uint32_t)f32_to_f16(d * (float)(int8_t)blk[2 + 2 * e]) |
                    ((uint32_t)f32_to_f16(d * (float)(int8_t)blk[3 + 2 * e]) << 16);
+        // a value beyond the f16 range (ggml dequantizes Q8_0 to fp32: it
+        // stays finite there): flag the call for the fp32 fallback
+        bool inf = false;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) inf |= (w[e] & 0x7c00u) == 0x7c00u || (w[e] & 0x7c000000u) == 0x7c000000u;
+        if (inf && ovf) *ovf = epoch;
     } else {
         const float* f = (const float*)src + bk * 32;
 #pragma unroll
@@ -750,12 +757,13 @@ size_t window_f16_bytes(const AttnArgs& a) {
     return (n + 255) / 256 * 256;
 }
 
-hipError_t launch_window_to_f16(const AttnArgs& a, void* dst, hipStream_t s) {
+hipError_t launch_window_to_f16(const AttnArgs& a, void* dst, unsigned long long* ovf, unsigned long long epoch,
+                                hipStream_t s) {
     int Lmax = 1;
     for (int b = 0; b < a.B; ++b) Lmax = max(Lmax, a.L[b]);
     const int64_t n = (int64_t)Lmax * a.Hkv * (a.d / 32);
     hipLaunchKernelGGL(window_to_f16_kernel, dim3((unsigned)((n + 255) / 256), 2 * a.B), dim3(256), 0, s, a,
-                       (uint16_t*)dst);
+                       (uint16_t*)dst, ovf, epoch);
     return hipGetLastError();
 }
 

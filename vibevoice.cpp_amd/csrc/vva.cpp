@@ -42,6 +42,10 @@ struct vva_context {
     // prefill's in-launch merge [kMaxPrefillTickets], then the projection
     // GEMM's split along K [kMaxProjTickets]
     unsigned* tickets = nullptr;
+    // the f16 window of a Q8_0 prefill flags an out-of-range value here
+    // with the call's epoch; the call's gated fp32 fallback then runs
+    unsigned long long* ovf = nullptr;
+    unsigned long long ovf_epoch = 0;
     std::set<vva_kv*> caches;            // released by vva_destroy if still alive
     // the last prefill plan and the call shape it was made for: a layer stack
     // repeats one shape layer after layer
@@ -299,9 +303,21 @@ vva_status run_attention(vva_context* ctx, AttnArgs& a, bool fixed = false) {
                 c.v[b] = wbase + off + (size_t)a.L[b] * a.Hkv * a.d * 2;
                 off += (size_t)2 * a.L[b] * a.Hkv * a.d * 2;
             }
-            e = launch_window_to_f16(a, wbase, ctx->stream);
+            // Q8_0: a value beyond the f16 range flags the call, and the fp32
+            // row kernel, launched gated behind the prefill, recomputes it
+            // from the Q8_0 cache (ggml dequantizes Q8_0 to fp32: finite);
+            // F32 windows overflow in the reference's own F16 cast too
+            const bool q8 = a.k_type == VVA_TYPE_Q8_0;
+            const unsigned long long epoch = q8 ? ++ctx->ovf_epoch : 0;
+            e = launch_window_to_f16(a, wbase, q8 ? ctx->ovf : nullptr, epoch, ctx->stream);
             if (e == hipSuccess)
                 e = launch_prefill(c, (float*)(wbase + wb), ctx->tickets + kMaxStepTickets, plan, ctx->stream);
+            if (e == hipSuccess && q8) {
+                AttnArgs g = a;
+                g.gate = ctx->ovf;
+                g.gate_epoch = epoch;
+                e = launch_attn_rows(g, ctx->stream);
+            }
             if (e != hipSuccess) return hip_fail(ctx, e, "prefill launch");
             ctx->last_splits = plan.max_ks;
             return VVA_OK;
@@ -385,8 +401,11 @@ extern "C" vva_status vva_create(int device, void* stream, vva_context** out) {
     constexpr size_t ticket_bytes = sizeof(unsigned) * (kMaxStepTickets + kMaxPrefillTickets + kMaxProjTickets);
     e = hipMalloc(&ctx->tickets, ticket_bytes);
     if (e == hipSuccess) e = hipMemset(ctx->tickets, 0, ticket_bytes);
+    if (e == hipSuccess) e = hipMalloc(&ctx->ovf, 256);
+    if (e == hipSuccess) e = hipMemset(ctx->ovf, 0, 256);
     if (e != hipSuccess) {
         if (ctx->tickets) (void)hipFree(ctx->tickets);
+        if (ctx->ovf) (void)hipFree(ctx->ovf);
         delete ctx;
         *out = nullptr;
         return fail(nullptr, VVA_ERR_DEVICE, "vva_create: ticket buffer: %s", hipGetErrorString(e));
@@ -411,6 +430,7 @@ extern "C" void vva_destroy(vva_context* ctx) {
     if (ctx->ws) (void)hipFree(ctx->ws);
     for (float* p : ctx->ws_retired) (void)hipFree(p);
     if (ctx->tickets) (void)hipFree(ctx->tickets);
+    if (ctx->ovf) (void)hipFree(ctx->ovf);
     delete ctx;
 }
 

@@ -75,6 +75,10 @@ struct AttnArgs {
     int64_t o_nb_t, o_nb_h, o_nb_b;   // in bytes
     int d, Hq, Hkv, T, B;
     int q_round_q8;                   // prefill: Q through a Q8_0 round trip first (window of Q8_0 K)
+    // attn_rows kernels: when gate is set, run only if *gate == gate_epoch
+    // (the device-side fallback of a Q8_0 window that overflowed f16)
+    const unsigned long long* gate;
+    unsigned long long gate_epoch;
 };
 
 enum { kMaskNone = 0, kMaskExplicit = 1, kMaskCausal = 2 };
@@ -84,7 +88,10 @@ enum { kMaskNone = 0, kMaskExplicit = 1, kMaskCausal = 2 };
 // to F16 before flash attention, src/qwen2.cpp:328-331).  dst holds, per
 // sequence, K then V as [L_b][Hkv][d] f16; window_f16_bytes sizes it.
 size_t window_f16_bytes(const AttnArgs& a);
-hipError_t launch_window_to_f16(const AttnArgs& a, void* dst, hipStream_t s);
+// ovf (may be null): set to epoch when a Q8_0 value exceeds the f16 range
+// (its f16 is infinite), for the gated fallback through launch_attn_rows.
+hipError_t launch_window_to_f16(const AttnArgs& a, void* dst, unsigned long long* ovf, unsigned long long epoch,
+                                hipStream_t s);
 
 // Single-token decode step in one launch (decode_step.hip): RoPE + append +
 // split attention + in-kernel merge.  F16 / BF16 caches, len + 1 <=
