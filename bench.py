@@ -60,7 +60,7 @@ S_D, S_HQ, S_HKV, S_LAYERS, S_L = 64, 14, 2, 24, 1024
 # WRITE_SIZE 1 GiB (x 1.0).  Counters and commands: profiles/prefill_kernel_7b_32k.md,
 # profiles/decode_stream_q8_0_7b_32k.md.
 TRAFFIC_PREFILL = (605956.9 * 2.0 + 459122.8 * 1.0) * 1024          # prefill_kernel<128,F16>
-TRAFFIC_DECODE = ((35116.1 + 937.5) * 2.0 + (1904.0 + 28.0) * 1.0) * 1024    # stream + merge
+TRAFFIC_DECODE = ((35170.0 + 938.0) * 2.0 + (1904.0 + 28.0) * 1.0) * 1024    # stream + merge
 
 
 def prefill_flops_per_layer(T: int, past: int = 0) -> float:
