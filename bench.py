@@ -136,12 +136,13 @@ def run_decode(torch, vva, ctx, steps: int, warmup: int):
     chunk = 8192
     for layer in range(LAYERS):
         for c0 in range(0, L_DECODE, chunk):
+            n = min(chunk, L_DECODE - c0)
             for s in range(B_DECODE):
                 kv.set_len(s, c0)
-            kk = torch.randn((B_DECODE, chunk, HKV, D), generator=rng, device="cuda")
-            vv = torch.randn((B_DECODE, chunk, HKV, D), generator=rng, device="cuda")
-            qq = torch.empty((B_DECODE, chunk, 1 * HKV, D), device="cuda")
-            pos = torch.arange(c0, c0 + chunk, dtype=torch.int32, device="cuda")
+            kk = torch.randn((B_DECODE, n, HKV, D), generator=rng, device="cuda")
+            vv = torch.randn((B_DECODE, n, HKV, D), generator=rng, device="cuda")
+            qq = torch.empty((B_DECODE, n, 1 * HKV, D), device="cuda")
+            pos = torch.arange(c0, c0 + n, dtype=torch.int32, device="cuda")
             ctx.rope_append(kv, layer, qq, kk, vv, pos, qq, freq_base=THETA)
     torch.cuda.synchronize()
     for s in range(B_DECODE):

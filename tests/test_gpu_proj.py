@@ -68,6 +68,10 @@ QKV_CASES = [
     (3584, 28, 4, 128, vva.F16, vva.Q8_0, 200, 2, vva.F32),    # F16 weights into a Q8_0 cache, two sequences
     (3584, 28, 4, 128, vva.F16, vva.F16, 1, 2, vva.F32),       # 7B CFG decode step, F16 weights (GEMV)
     (896, 14, 2, 64, vva.F16, vva.Q8_0, 3, 2, vva.F32),        # 6 token rows, F16 weights (GEMV)
+    # >= 1024 token rows, F16 weights: the 256 x 256 tile GEMM
+    (3584, 28, 4, 128, vva.F16, vva.Q8_0, 1030, 1, vva.F32),   # ragged last token tile, Q8_0 cache (pair epilogue)
+    (896, 14, 2, 64, vva.F16, vva.F16, 640, 2, vva.BF16),      # two sequences, a half-filled last feature tile
+    (1536, 12, 2, 128, vva.F16, vva.BF16, 1500, 1, vva.F16),   # 1.5B long chunk
 ]
 
 
@@ -199,6 +203,8 @@ O_CASES = [
     (3584, 3584, vva.F16, 2, 2, vva.F16),
     (1536, 1536, vva.F16, 4, 2, vva.BF16),      # 8 token rows: more row chunks than the staged batch
     (3584, 3584, vva.F16, 1, 2, vva.F32),       # 7B CFG decode step
+    (3584, 3584, vva.F16, 1024, 2, vva.F32),    # 2048 token rows: the 256 x 256 tile GEMM
+    (1536, 1536, vva.F16, 1100, 1, vva.BF16),   # ragged last token tile
 ]
 
 

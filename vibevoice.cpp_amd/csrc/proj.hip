@@ -862,6 +862,381 @@ __global__ void __launch_bounds__((kWCompute + kWProd) * 64) proj_gemm_wide_kern
     }
 }
 
+// ------------------------------------------------------------ big GEMM (F16 weights, long calls)
+
+// 256 output features x 256 token rows per workgroup, k in steps of 64, eight
+// waves (two per SIMD), each a 128 x 64 block of 4 x 2
+// v_mfma_f32_32x32x16_f16 blocks whose 128 accumulators live in AGPRs: per
+// k16 step a wave reads 6 fragments (6 KB of LDS) for 8 MFMAs, 3/4 of the LDS
+// reads per MFMA of the wide kernel's 64 x 64 quadrants, whose fragment
+// reads and DMA writes kept LDS saturated.  The waves DMA the tiles into a
+// 2-stage LDS ring themselves (buffer_load_dwordx4 ... lds, 8 loads per wave
+// and stage): eight issuing waves, since one wave's LDS loads stream at
+// ~20 GB/s.  Rows are 128 bytes (64 f16 of k) in LDS, laid out as the
+// wide kernel's: a DMA instruction fills 8 rows, lane l writing 16-byte slot
+// l % 8 of row l / 8 with the row's k chunk (l % 8) ^ ((row / 2) % 8), so a
+// fragment read (16 lanes, rows r .. r + 15 at one k chunk) touches every
+// bank once.  Step kt: the MFMAs of each k16 quarter run while the next
+// quarter's fragments are read; after the third quarter, the barrier that
+// publishes stage kt + 1 (every wave has read all of stage kt by then, so
+// stage kt takes the loads of kt + 2), the first fragments of kt + 1, and
+// the fourth quarter's MFMAs.  (A 5-stage ring of 32-wide k steps, four
+// stages in flight, measured slower: the loads' latency is not what the
+// loop waits for.)  The epilogue runs in two halves of 128 tokens
+// (the [token][feature] tile of 256 tokens would not fit LDS).
+constexpr int kBM = 256, kBN = 256, kBK = 64;
+constexpr int kBStages = 2;
+constexpr int kBA = kBM * kBK * 2;             // 32 KB of weights per stage
+constexpr int kBB = kBN * kBK * 2;             // 32 KB of token rows per stage
+constexpr int kBStage = kBA + kBB;
+constexpr int kBWaves = 8;
+constexpr int kBLoadsA = kBA / 1024 / kBWaves;  // DMA loads per wave, operand and stage
+constexpr int kBLoadsB = kBB / 1024 / kBWaves;
+constexpr int kBLoads = kBLoadsA + kBLoadsB;
+constexpr int kBHalf = kBN / 2;                 // tokens per epilogue half
+constexpr int kBCPitch = kBM + 4;               // floats per token row of the epilogue tile
+constexpr int kBRing = kBStages * kBStage;
+constexpr int kBCBytes = kBHalf * kBCPitch * 4;
+constexpr int kBLds = kBRing > kBCBytes ? kBRing : kBCBytes;
+constexpr int kBPiece = kBWaves * 8 * 4096;     // bytes of one K piece's accumulators (256 x 256 f32)
+constexpr int kBMaxSplit = 4;
+static_assert(kBStages == 2 && kBStages * kBLoads <= 63, "two stages of a wave's loads fit its 6-bit vmcnt");
+static_assert(kBLds <= 160 * 1024, "LDS");
+
+// q/k/v epilogue, one element pair per thread (Q8_0 caches, unaligned rows):
+// NTH threads over the tile's TM / 2 rotation pairs of each token
+template <int TN, int NTH>
+__device__ __forceinline__ void qkv_epilogue_pair(const ProjArgs& a, const float* C, int cpitch, int m0, int n0, int tid) {
+    constexpr int PAIRS = kBM / 2;                     // pairs per token of the tile
+    constexpr int PS = NTH / PAIRS;                    // tokens per pass
+    const int d = a.d, P = d >> 1;
+    const int pi = tid % PAIRS, hl = pi / P, i = pi - hl * P;
+    const int f0 = m0 + hl * d;                        // first feature of the head
+    if (f0 >= a.M) return;                             // past the last matrix
+    const int mat = f0 < a.m_end[0] ? 0 : (f0 < a.m_end[1] ? 1 : 2);
+    const int mrow = f0 - (mat ? a.m_end[mat - 1] : 0);
+    const int head = mrow / d;
+    const float* bias = a.bias[mat];
+    const float b0 = bias ? bias[mrow + i] : 0.0f;
+    const float b1 = bias ? bias[mrow + i + P] : 0.0f;
+    for (int nb = tid / PAIRS; nb < TN; nb += PS * kEpiQkv) {
+        float2 csb[kEpiQkv];
+#pragma unroll
+        for (int e = 0; e < kEpiQkv; ++e)
+            csb[e] = a.rope[(int64_t)min(n0 + nb + PS * e, a.N - 1) * P + i];      // used for q and k only
+#pragma unroll
+        for (int e = 0; e < kEpiQkv; ++e) {
+            const int nl = nb + PS * e, n = n0 + nl;
+            if (nl >= TN || n >= a.N) break;
+            float y0 = C[nl * cpitch + hl * d + i] + b0;
+            float y1 = C[nl * cpitch + hl * d + i + P] + b1;
+            if (mat < 2) {
+                const float2 cs = csb[e];
+                const float r0 = fmaf(y0, cs.x, -(y1 * cs.y));
+                const float r1 = fmaf(y0, cs.y, y1 * cs.x);
+                y0 = r0;
+                y1 = r1;
+            }
+            const int b = a.N == a.T ? 0 : n / a.T, t = n - b * a.T;
+            if (mat == 0) {
+                const int64_t eo = type_elem_bytes(a.q_out_type);
+                char* dst = a.q_out + b * a.qo_nb_b + t * a.qo_nb_t + head * a.qo_nb_h;
+                store_elem(dst + i * eo, a.q_out_type, y0);
+                store_elem(dst + (i + P) * eo, a.q_out_type, y1);
+            } else {
+                char* const kd = a.N == a.T ? a.k_dst[0] : a.k_dst[b];
+                char* const vd = a.N == a.T ? a.v_dst[0] : a.v_dst[b];
+                char* row = (mat == 1 ? kd : vd) + t * a.cache_row_bytes + head * a.cache_head_bytes;
+                if (a.cache_type == VVA_TYPE_Q8_0) {
+                    store_q8_pair(row, i, P, y0, y1);
+                } else {
+                    const int64_t ec = type_elem_bytes(a.cache_type);
+                    store_elem(row + i * ec, a.cache_type, y0);
+                    store_elem(row + (i + P) * ec, a.cache_type, y1);
+                }
+            }
+        }
+    }
+}
+
+// h = y + x over a tile's TN tokens: 4 features per thread, NTH / 64 tokens per pass
+template <int TN, int NTH>
+__device__ __forceinline__ void residual_epilogue(const ProjArgs& a, const float* C, int cpitch, int m0, int n0, int tid) {
+    constexpr int PS = NTH / (kBM / 4);
+    const int c4 = (tid % (kBM / 4)) * 4;
+    if (m0 + c4 >= a.M) return;
+    for (int nb = tid / (kBM / 4); nb < TN; nb += PS * kEpiRes) {
+        float4 xrb[kEpiRes];
+#pragma unroll
+        for (int e = 0; e < kEpiRes; ++e) {
+            const int n = min(n0 + nb + PS * e, a.N - 1);
+            const int b = a.N == a.T ? 0 : n / a.T, t = n - b * a.T;
+            xrb[e] = *(const float4*)(a.res + b * a.res_nb_b + t * a.res_nb_t + (int64_t)(m0 + c4) * 4);
+        }
+#pragma unroll
+        for (int e = 0; e < kEpiRes; ++e) {
+            const int nl = nb + PS * e, n = n0 + nl;
+            if (nl >= TN || n >= a.N) break;
+            const int b = a.N == a.T ? 0 : n / a.T, t = n - b * a.T;
+            const float4 xr = xrb[e];
+            const float* cr = C + nl * cpitch + c4;
+            *(float4*)(a.h + b * a.h_nb_b + t * a.h_nb_t + (int64_t)(m0 + c4) * 4) =
+                make_float4(cr[0] + xr.x, cr[1] + xr.y, cr[2] + xr.z, cr[3] + xr.w);
+        }
+    }
+}
+
+// Tile order of the big GEMM: XCD x (workgroup i runs on XCD i % 8) takes a
+// contiguous run of an order that walks groups of 4 token tiles, the 4 token
+// tiles of every weight tile in turn.  Returns (weight tile, token tile) of
+// place wo.
+__device__ __forceinline__ int2 big_order(int wo, int n_mt, int n_nt) {
+    const int grp = wo / (n_mt * 4), gn = min(4, n_nt - grp * 4), j = wo - grp * n_mt * 4;
+    return make_int2(j / gn, grp * 4 + j % gn);
+}
+
+// A K piece's accumulators as [wave][block][4-register group][lane] (1 KB of
+// whole lines per store instruction); a later launch sums them
+__device__ __forceinline__ void big_split_store(const f32x16 (&acc)[4][2], char* piece, int w, int lane) {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(piece, (short)0, kBPiece, 0x00020000);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const u32x4 v = {__float_as_uint(acc[i][j][4 * g]), __float_as_uint(acc[i][j][4 * g + 1]),
+                                 __float_as_uint(acc[i][j][4 * g + 2]), __float_as_uint(acc[i][j][4 * g + 3])};
+                __builtin_amdgcn_raw_buffer_store_b128(v, rs, (w * 32 + (i * 2 + j) * 4 + g) * 1024 + lane * 16, 0, 0);
+            }
+}
+
+template <int MODE>
+__global__ void __launch_bounds__(kBWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+proj_gemm_big_kernel(ProjArgs a) {
+    prefetch_kernargs<sizeof(ProjArgs)>();
+    __shared__ __attribute__((aligned(16))) char lds[kBLds];
+    const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5, l32 = lane & 31;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+    // Tile order as in the wide kernel: XCD x (workgroup i runs on XCD i % 8)
+    // takes a contiguous run of an order that walks groups of 4 token tiles,
+    // the 4 token tiles of every weight tile in turn.
+    const int n_mt = (a.M + kBM - 1) / kBM, n_nt = (a.N + kBN - 1) / kBN;
+    const int ksplit = a.ksplit, tail0 = a.tail0;
+    int ks = 0, tile = 0;
+    int2 mn;
+    if (ksplit > 1 && (int)blockIdx.x >= tail0) {
+        // the last round's tiles, split along K (after the unsplit ones)
+        const int qq = (int)blockIdx.x - tail0;
+        mn = big_order(tail0 + qq / ksplit, n_mt, n_nt);
+        ks = qq % ksplit;
+        tile = qq / ksplit;
+    } else {
+        const int hp = ksplit > 1 ? tail0 : (int)gridDim.x;
+        const int q = hp / 8, r = hp % 8, x = blockIdx.x % 8;
+        mn = big_order(x * q + min(x, r) + (int)blockIdx.x / 8, n_mt, n_nt);
+    }
+    const int mt = mn.x, nt = mn.y;
+    const bool split = ksplit > 1 && (int)blockIdx.x >= tail0;
+    const int m0 = mt * kBM, n0 = nt * kBN;
+    const int nk_all = a.K / kBK;
+    const int nsp = split ? ksplit : 1;
+    const int k_lo = ks * nk_all / nsp;
+    const int nk = (ks + 1) * nk_all / nsp - k_lo;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
+
+    // ---- the wave's DMA loads: instructions w, w + 8, ... of each operand
+    // (8 rows each); lane l takes row l / 8, LDS slot l % 8
+    const int sub = lane >> 3, slot = lane & 7;
+    // the k chunk that slot holds in row r of the tile
+    auto chunk = [&](int r) { return (slot ^ ((r >> 1) & 7)) << 4; };
+    int aoff[kBLoadsA], boff[kBLoadsB];
+    i32x4 ars[kBLoadsA];
+#pragma unroll
+    for (int i = 0; i < kBLoadsA; ++i) {
+        const int ins = w + kBWaves * i;
+        const int g = m0 + ins * 8;                              // its 8-row group (one matrix)
+        const int mat = g < a.m_end[0] ? 0 : (g < a.m_end[1] ? 1 : (g < a.m_end[2] ? 2 : 3));
+        const int mbeg = mat == 0 ? 0 : a.m_end[mat - 1];
+        const int mrows = mat < 3 ? a.m_end[mat] - mbeg : 0;
+        ars[i] = make_rsrc_sgpr(mat < 3 ? a.w[mat] : a.w[0], (uint32_t)(mrows * a.w_nb[mat < 3 ? mat : 0]));
+        aoff[i] = (g + sub - mbeg) * (int)a.w_nb[mat < 3 ? mat : 0] + chunk(ins * 8 + sub);
+    }
+    const int nrows = max(0, min(a.N - n0, kBN));
+    const i32x4 brs = make_rsrc_sgpr((const char*)(a.xh + (int64_t)n0 * a.K), (uint32_t)(nrows * a.K * 2));
+#pragma unroll
+    for (int i = 0; i < kBLoadsB; ++i) {
+        const int r = (w + kBWaves * i) * 8 + sub;
+        boff[i] = r * a.K * 2 + chunk(r);
+    }
+    // a stage past the last loads zeros (offsets past every range)
+    auto issue = [&](int kt, int stage) {
+        const uint32_t st = lds0 + (uint32_t)stage * kBStage;
+        const bool live = kt < nk;
+        const int ko = (k_lo + kt) * kBK * 2;
+#pragma unroll
+        for (int i = 0; i < kBLoadsA; ++i)
+            wdma16(ars[i], st + (w + kBWaves * i) * 1024, live ? aoff[i] + ko : 0x40000000);
+#pragma unroll
+        for (int i = 0; i < kBLoadsB; ++i)
+            wdma16(brs, st + kBA + (w + kBWaves * i) * 1024, live ? boff[i] + ko : 0x40000000);
+    };
+
+    // ---- block (wm, wn): 128 features x 64 tokens
+    const int wm = w & 1, wn = w >> 1;
+    const int sw = (l32 >> 1) & 7;
+    const int a_rd = (wm * 128 + l32) * 128;
+    const int b_rd = kBA + (wn * 64 + l32) * 128;
+    auto frags = [&](const char* st, int k16, h8 (&af)[4], h8 (&bf)[2]) {
+        const int ch = ((2 * k16 + half) ^ sw) << 4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const u32x4 ua = *(const u32x4*)(st + a_rd + i * 32 * 128 + ch);
+            __builtin_memcpy(&af[i], &ua, 16);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const u32x4 ub = *(const u32x4*)(st + b_rd + j * 32 * 128 + ch);
+            __builtin_memcpy(&bf[j], &ub, 16);
+        }
+    };
+    f32x16 acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+    auto mma = [&](const h8 (&af)[4], const h8 (&bf)[2]) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    };
+    issue(0, 0);
+    issue(1, 1);
+    wwait_barrier<kBLoads>();                              // stage 0 landed
+    // (scheduling fences keep this order: the compiler would otherwise read
+    // each fragment just before its first MFMA and expose the LDS latency)
+    h8 a0[4], b0[2], a1[4], b1[2];
+    frags(lds, 0, a0, b0);
+    for (int kt = 0; kt < nk; ++kt) {
+        const char* st = lds + (kt & 1) * kBStage;
+        frags(st, 1, a1, b1);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(a0, b0);
+        __builtin_amdgcn_sched_barrier(0);
+        frags(st, 2, a0, b0);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(a1, b1);
+        __builtin_amdgcn_sched_barrier(0);
+        frags(st, 3, a1, b1);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(a0, b0);
+        __builtin_amdgcn_sched_barrier(0);
+        wwait_barrier<0>();                                // stage kt + 1 landed; stage kt read by all
+        issue(kt + 2, kt & 1);                             // into stage kt's place
+        frags(lds + ((kt + 1) & 1) * kBStage, 0, a0, b0);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(a1, b1);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" : : : "memory");     // the padding stages' zeros have landed
+    __syncthreads();
+
+    if (split) {                                           // proj_big_merge_kernel finishes the tile
+        big_split_store(acc, a.part + ((int64_t)tile * ksplit + ks) * kBPiece, w, lane);
+        return;
+    }
+    float* C = (float*)lds;
+#pragma unroll 1
+    for (int hh = 0; hh < 2; ++hh) {
+        // ---- accumulators to LDS as C[token][feature] for tokens 128 hh ..:
+        // lane (half, l32) of block (i, j) holds features 8 (r / 4) + 4 half +
+        // r % 4 of token l32
+        if ((wn >> 1) == hh) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    float* crow = C + ((wn & 1) * 64 + 32 * j + l32) * kBCPitch + wm * 128 + 32 * i + 4 * half;
+#pragma unroll
+                    for (int g = 0; g < 4; ++g)
+                        *(float4*)(crow + 8 * g) = make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1],
+                                                               acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
+                }
+        }
+        __syncthreads();
+        const int nh = n0 + kBHalf * hh;
+        if constexpr (MODE == kProjQKV) {
+            if (a.vec_store) qkv_epilogue_vec<kBM, kBHalf, kBWaves * 64>(a, C, kBCPitch, m0, nh, tid);
+            else             qkv_epilogue_pair<kBHalf, kBWaves * 64>(a, C, kBCPitch, m0, nh, tid);
+        } else {
+            residual_epilogue<kBHalf, kBWaves * 64>(a, C, kBCPitch, m0, nh, tid);
+        }
+        __syncthreads();
+    }
+}
+
+// The split tail of the big GEMM: one workgroup per (split tile, 32-token
+// slab) sums the tile's K pieces for its slab, in split order, into a
+// [token][feature] LDS tile and runs the epilogue on it.  A piece's slab s
+// is the blocks j = s % 2 of waves wn = s / 2 (both wm), 32 KB.
+constexpr int kBSlab = 32;
+template <int MODE>
+__global__ void __launch_bounds__(256) proj_big_merge_kernel(ProjArgs a) {
+    prefetch_kernargs<sizeof(ProjArgs)>();
+    __shared__ __attribute__((aligned(16))) float C[kBSlab * kBCPitch];
+    const int n_mt = (a.M + kBM - 1) / kBM, n_nt = (a.N + kBN - 1) / kBN;
+    constexpr int NS = kBN / kBSlab;
+    const int tile = blockIdx.x / NS, slab = blockIdx.x % NS;
+    const int2 mn = big_order(a.tail0 + tile, n_mt, n_nt);
+    const int m0 = mn.x * kBM, n0 = mn.y * kBN + slab * kBSlab;
+    if (n0 >= a.N) return;                                 // a slab past the tokens (uniform)
+    const int tid = threadIdx.x;
+    const int wn = slab >> 1, j = slab & 1;
+    const char* piece0 = a.part + (int64_t)tile * a.ksplit * kBPiece;
+    // float4 f of the slab: wm = f / 1024, i = (f / 256) % 4, g = (f / 64) % 4, lane = f % 64
+    constexpr int NF = 2 * 4 * 4 * 64 / 256;               // float4s per thread
+    u32x4 v[NF][kBMaxSplit];
+#pragma unroll
+    for (int e = 0; e < NF; ++e) {
+        const int f = tid + 256 * e;
+        const int wm = f >> 10, i = (f >> 8) & 3, g = (f >> 6) & 3, lane = f & 63;
+        const int off = ((2 * wn + wm) * 32 + (i * 2 + j) * 4 + g) * 1024 + lane * 16;
+#pragma unroll
+        for (int k = 0; k < kBMaxSplit; ++k) {
+            if (k >= a.ksplit) break;                      // uniform
+            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<char*>(piece0) + (int64_t)k * kBPiece, (short)0, kBPiece, 0x00020000);
+            v[e][k] = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < NF; ++e) {
+        const int f = tid + 256 * e;
+        const int wm = f >> 10, i = (f >> 8) & 3, g = (f >> 6) & 3, lane = f & 63;
+        const int l32 = lane & 31, half = lane >> 5;
+        float4 s = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+        for (int k = 0; k < kBMaxSplit; ++k) {
+            if (k >= a.ksplit) break;
+            s.x += __uint_as_float(v[e][k].x);
+            s.y += __uint_as_float(v[e][k].y);
+            s.z += __uint_as_float(v[e][k].z);
+            s.w += __uint_as_float(v[e][k].w);
+        }
+        *(float4*)(C + l32 * kBCPitch + wm * 128 + 32 * i + 4 * half + 8 * g) = s;
+    }
+    __syncthreads();
+    if constexpr (MODE == kProjQKV) {
+        if (a.vec_store) qkv_epilogue_vec<kBM, kBSlab, 256>(a, C, kBCPitch, m0, n0, tid);
+        else             qkv_epilogue_pair<kBSlab, 256>(a, C, kBCPitch, m0, n0, tid);
+    } else {
+        residual_epilogue<kBSlab, 256>(a, C, kBCPitch, m0, n0, tid);
+    }
+}
+
 // ------------------------------------------------------------ GEMV
 
 constexpr int kGvRows = 4;                       // output rows per workgroup (one wave)
@@ -2011,8 +2386,25 @@ hipError_t launch_proj_gemv(ProjArgs& a, float* y_ws, int n_cu, hipStream_t s) {
 // workgroup per CU, two of the 128 x 128 kernel): a call whose tiles fill
 // at most half of them (short chunks, e.g. 512 tokens) is split along K, at
 // least 4 k steps per piece, up to 4 pieces, one round.
+namespace {
+// F16 weights over at least 1024 token rows take the big kernel (256 x 256
+// tiles); shorter calls the wide one (256 x 128), whose split pieces are half
+// the size
+bool proj_big(const ProjArgs& a) { return a.w_type != VVA_TYPE_Q8_0 && a.N >= 1024; }
+}  // namespace
+
 int proj_ksplit(const ProjArgs& a, int n_cu, int* tail0) {
     const bool q8 = a.w_type == VVA_TYPE_Q8_0;
+    if (proj_big(a)) {
+        // the last round's tiles, when they fill at most a quarter of the CUs,
+        // split along K (at most kBMaxSplit pieces of at least 8 k steps)
+        const int tiles = ((a.M + kBM - 1) / kBM) * ((a.N + kBN - 1) / kBN);
+        const int nk = a.K / kBK, r = tiles % n_cu;
+        *tail0 = 0;
+        if (r == 0 || 4 * r > n_cu || r > kMaxProjTickets || nk < 16) return 1;
+        *tail0 = tiles - r;
+        return max(1, min(min(kBMaxSplit, n_cu / r), nk / 8));
+    }
     const int tiles = q8 ? (a.M / kTM) * ((a.N + kTN - 1) / kTN) : ((a.M + kWM - 1) / kWM) * ((a.N + kWN - 1) / kWN);
     const int slots = q8 ? 2 * n_cu : n_cu;
     const int nk = a.K / (q8 ? kTK : kWK);
@@ -2030,6 +2422,10 @@ int proj_ksplit(const ProjArgs& a, int n_cu, int* tail0) {
 }
 size_t proj_part_bytes(const ProjArgs& a) {
     if (a.ksplit <= 1) return 0;
+    if (proj_big(a)) {
+        const size_t tiles = (size_t)((a.M + kBM - 1) / kBM) * ((a.N + kBN - 1) / kBN);
+        return (tiles - a.tail0) * a.ksplit * kBPiece;
+    }
     const bool q8 = a.w_type == VVA_TYPE_Q8_0;
     const size_t tiles = q8 ? (size_t)(a.M / kTM) * ((a.N + kTN - 1) / kTN)
                             : (size_t)((a.M + kWM - 1) / kWM) * ((a.N + kWN - 1) / kWN);
@@ -2057,6 +2453,17 @@ hipError_t launch_proj(ProjPrepArgs& p, ProjArgs& a, void* ws, hipStream_t s) {
     }
     // every tile's pieces, or the unsplit tiles then the split tail's pieces
     auto grid = [&](int tiles) { return a.tail0 > 0 ? a.tail0 + (tiles - a.tail0) * a.ksplit : tiles * a.ksplit; };
+    if (proj_big(a)) {
+        const int tiles = ((a.M + kBM - 1) / kBM) * ((a.N + kBN - 1) / kBN);
+        const dim3 g(grid(tiles)), b(kBWaves * 64);
+        if (a.mode == kProjQKV) hipLaunchKernelGGL((proj_gemm_big_kernel<kProjQKV>), g, b, 0, s, a);
+        else                    hipLaunchKernelGGL((proj_gemm_big_kernel<kProjResidual>), g, b, 0, s, a);
+        if ((e = hipGetLastError()) != hipSuccess || a.ksplit <= 1) return e;
+        const dim3 gm((tiles - a.tail0) * (kBN / kBSlab));
+        if (a.mode == kProjQKV) hipLaunchKernelGGL((proj_big_merge_kernel<kProjQKV>), gm, dim3(256), 0, s, a);
+        else                    hipLaunchKernelGGL((proj_big_merge_kernel<kProjResidual>), gm, dim3(256), 0, s, a);
+        return hipGetLastError();
+    }
     if (!q8) {
         const int wtiles = grid(((a.M + kWM - 1) / kWM) * ((a.N + kWN - 1) / kWN));
         const dim3 block((kWCompute + kWProd) * 64);
