@@ -72,6 +72,7 @@ QKV_CASES = [
     (3584, 28, 4, 128, vva.F16, vva.Q8_0, 1030, 1, vva.F32),   # ragged last token tile, Q8_0 cache (pair epilogue)
     (896, 14, 2, 64, vva.F16, vva.F16, 640, 2, vva.BF16),      # two sequences, a half-filled last feature tile
     (1536, 12, 2, 128, vva.F16, vva.BF16, 1500, 1, vva.F16),   # 1.5B long chunk
+    (1536, 12, 2, 128, vva.Q8_0, vva.F16, 1100, 1, vva.F32),   # Q8_0 weights dequantized for the long-call GEMM
 ]
 
 
@@ -205,6 +206,7 @@ O_CASES = [
     (3584, 3584, vva.F16, 1, 2, vva.F32),       # 7B CFG decode step
     (3584, 3584, vva.F16, 1024, 2, vva.F32),    # 2048 token rows: the 256 x 256 tile GEMM
     (1536, 1536, vva.F16, 1100, 1, vva.BF16),   # ragged last token tile
+    (3584, 3584, vva.Q8_0, 640, 2, vva.F32),    # Q8_0 weights dequantized for the long-call GEMM
 ]
 
 

@@ -2433,6 +2433,53 @@ size_t proj_part_bytes(const ProjArgs& a) {
     return split * a.ksplit * (q8 ? 4 : kWCompute) * 4096 * sizeof(float);
 }
 
+// Q8_0 weight rows dequantized to f16 rows of d * q: the products the Q8_0
+// GEMM forms while staging its tiles (code and fp16 scale multiplied in
+// f16, the exact product rounded once), so that long calls run the F16 GEMM
+// on them.  One thread per 32-element block; a block's 34 bytes are read as
+// 9 dwords from the 4-byte boundary at or below it (the buffer range ends at
+// the matrix's last row, so a dword past it reads as zero).
+__global__ void __launch_bounds__(256) proj_dequant_q8_kernel(ProjArgs a, uint16_t* dst) {
+    const int nb = a.K / 32;
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= (int64_t)a.M * nb) return;
+    const int row = (int)(t / nb), blk = (int)(t - (int64_t)row * nb);
+    const int mat = row < a.m_end[0] ? 0 : (row < a.m_end[1] ? 1 : 2);
+    const int mbeg = mat == 0 ? 0 : a.m_end[mat - 1];
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char*>(a.w[mat]), (short)0, (int)((a.m_end[mat] - mbeg) * a.w_nb[mat]), 0x00020000);
+    const uint32_t off = (uint32_t)((row - mbeg) * a.w_nb[mat]) + (uint32_t)blk * kQ8Bytes;
+    uint32_t q[9];
+#pragma unroll
+    for (int i = 0; i < 9; ++i) q[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, (off & ~3u) + 4 * i, 0, 0);
+    const bool odd = off & 2;                           // the block starts 2 bytes into dword 0
+    const uint16_t d16 = (uint16_t)(odd ? (q[0] >> 16) : (q[0] & 0xffffu));
+    _Float16 dh;
+    __builtin_memcpy(&dh, &d16, 2);
+    const h2 dd = {dh, dh};
+    uint32_t outw[16];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t c = odd ? q[i + 1] : __builtin_amdgcn_alignbyte(q[i + 1], q[i], 2);
+        const h2 lo = {(_Float16)(int8_t)(c & 0xff), (_Float16)(int8_t)((c >> 8) & 0xff)};
+        const h2 hi = {(_Float16)(int8_t)((c >> 16) & 0xff), (_Float16)(int8_t)(c >> 24)};
+        const h2 plo = lo * dd, phi = hi * dd;
+        __builtin_memcpy(&outw[2 * i], &plo, 4);
+        __builtin_memcpy(&outw[2 * i + 1], &phi, 4);
+    }
+    u32x4* o = (u32x4*)(dst + (int64_t)row * a.K + blk * 32);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = u32x4{outw[4 * i], outw[4 * i + 1], outw[4 * i + 2], outw[4 * i + 3]};
+}
+
+bool proj_dequant_q8(const ProjArgs& a) { return a.w_type == VVA_TYPE_Q8_0 && a.N >= 1024; }
+
+hipError_t launch_proj_dequant_q8(const ProjArgs& a, uint16_t* dst, hipStream_t s) {
+    const int64_t n = (int64_t)a.M * (a.K / 32);
+    hipLaunchKernelGGL(proj_dequant_q8_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a, dst);
+    return hipGetLastError();
+}
+
 size_t proj_ws_bytes(int N, int K, int P) {
     const size_t xh = ((size_t)N * K * 2 + 255) / 256 * 256;
     return xh + (size_t)N * P * sizeof(float2);

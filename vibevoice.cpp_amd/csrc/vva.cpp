@@ -901,17 +901,31 @@ bool rows16(const vva_tensor* x) {
 }  // namespace
 
 // The prep + GEMM launches of a projection with their workspace: the
-// converted token rows (and RoPE table), then, when the GEMM is split along
-// K, the pieces' partials; the split tickets follow the decode step's and the
-// prefill's in the context's ticket buffer.
+// converted token rows (and RoPE table), then, for Q8_0 weights over a long
+// call, the weights dequantized to f16 (the GEMM then runs on those), then,
+// when the GEMM is split along K, the pieces' partials; the split tickets
+// follow the decode step's and the prefill's in the context's ticket buffer.
 static vva_status run_proj_gemm(vva_context* ctx, ProjPrepArgs& p, ProjArgs& a, int N, int K, int P) {
-    a.ksplit = proj_ksplit(a, ctx->n_cu, &a.tail0);
-    a.tickets = ctx->tickets + kMaxStepTickets + kMaxPrefillTickets;
+    const bool dq = proj_dequant_q8(a);
+    ProjArgs g = a;                                    // the GEMM's view of the weights
+    if (dq) g.w_type = VVA_TYPE_F16;
+    g.ksplit = proj_ksplit(g, ctx->n_cu, &g.tail0);
+    g.tickets = ctx->tickets + kMaxStepTickets + kMaxPrefillTickets;
     const size_t base = (proj_ws_bytes(N, K, P) + 255) / 256 * 256;
-    vva_status st = ensure_ws(ctx, base + proj_part_bytes(a));
+    const size_t wbytes = dq ? ((size_t)a.M * K * 2 + 255) / 256 * 256 : 0;
+    vva_status st = ensure_ws(ctx, base + wbytes + proj_part_bytes(g));
     if (st != VVA_OK) return st;
-    a.part = a.ksplit > 1 ? (char*)ctx->ws + base : nullptr;
-    const hipError_t e = launch_proj(p, a, ctx->ws, ctx->stream);
+    if (dq) {
+        uint16_t* wd = (uint16_t*)((char*)ctx->ws + base);
+        const hipError_t e = launch_proj_dequant_q8(a, wd, ctx->stream);
+        if (e != hipSuccess) return hip_fail(ctx, e, "projection weight dequantization");
+        for (int i = 0; i < 3; ++i) {
+            g.w[i] = (const char*)(wd + (int64_t)(i == 0 ? 0 : a.m_end[i - 1]) * K);
+            g.w_nb[i] = (int64_t)K * 2;
+        }
+    }
+    g.part = g.ksplit > 1 ? (char*)ctx->ws + base + wbytes : nullptr;
+    const hipError_t e = launch_proj(p, g, ctx->ws, ctx->stream);
     return e == hipSuccess ? VVA_OK : hip_fail(ctx, e, "projection launch");
 }
 

@@ -234,6 +234,10 @@ PrefillPlan prefill_plan(const AttnArgs& a, int n_cu, int forced, size_t ws_cap,
 size_t prefill_ws_bytes(const AttnArgs& a, const PrefillPlan& p);
 // Prep + GEMM of a linear layer; ws holds proj_ws_bytes(N, K, P) bytes.
 size_t proj_ws_bytes(int N, int K, int P);
+// Q8_0 weights over a long call (>= 1024 token rows): the rows are
+// dequantized to f16 d * q (M x K) for the F16 GEMM
+bool proj_dequant_q8(const ProjArgs& a);
+hipError_t launch_proj_dequant_q8(const ProjArgs& a, uint16_t* dst, hipStream_t s);
 hipError_t launch_proj(ProjPrepArgs& p, ProjArgs& a, void* ws, hipStream_t s);
 // Few token rows (decode steps): one weight-streaming GEMV launch that
 // converts the rows itself.  kProjQKV writes y = x w^T + bias (F32 [N][M],
