@@ -26,14 +26,12 @@ namespace {
 #include "wave_ops.hpp"
 
 constexpr int kRowsPerBlock = 4;   // one row per wave
+constexpr unsigned kGatedGrid = 512; // workgroups of a gated attn_rows_kernel launch
 
+// One query row (b, t, head) on one wave.
 template <int DPL>
-__global__ void __launch_bounds__(256) attn_rows_kernel(AttnArgs a) {
-    prefetch_kernargs<sizeof(AttnArgs)>();
-    if (a.gate && *a.gate != a.gate_epoch) return;     // a gated fallback that is not needed
+__device__ __forceinline__ void attn_row(const AttnArgs& a, int row) {
     const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
-    if (row >= a.B * a.T * a.Hq) return;        // whole wave leaves together
     const int h = row % a.Hq;
     const int bt = row / a.Hq;
     const int t = bt % a.T;
@@ -150,6 +148,17 @@ __global__ void __launch_bounds__(256) attn_rows_kernel(AttnArgs a) {
         const int i = lane + 64 * r;
         if (i < d) orow[i] = acc[r] * inv;
     }
+}
+
+// Rows on waves, grid-stride (a gated launch takes a small grid: when its
+// gate is closed every workgroup leaves after one load).
+template <int DPL>
+__global__ void __launch_bounds__(256) attn_rows_kernel(AttnArgs a) {
+    prefetch_kernargs<sizeof(AttnArgs)>();
+    if (a.gate && *a.gate != a.gate_epoch) return;     // a gated fallback that is not needed
+    const int rows = a.B * a.T * a.Hq;
+    for (int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6); row < rows; row += gridDim.x * kRowsPerBlock)
+        attn_row<DPL>(a, row);                         // (row is uniform per wave)
 }
 
 // Max over all 64 lanes (every lane gets it).
@@ -744,6 +753,7 @@ hipError_t launch_attn_rows(const AttnArgs& a, hipStream_t s) {
         }
         return hipGetLastError();
     }
+    if (a.gate && grid.x > kGatedGrid) grid.x = kGatedGrid;
     switch (dpl) {
         case 1: hipLaunchKernelGGL(attn_rows_kernel<1>, grid, dim3(256), 0, s, a); break;
         case 2: hipLaunchKernelGGL(attn_rows_kernel<2>, grid, dim3(256), 0, s, a); break;
