@@ -79,6 +79,23 @@ def decode_append_bytes(B: int) -> float:
     return B * ((HQ + 2 * HKV) * D * 4 + HQ * D * 4 + 2 * HKV * (D // 32) * 34)
 
 
+def synth_weight(torch, vva, rng, m: int, k: int, wt: int):
+    """Random weight bytes of m rows of k inputs as ggml stores them: F16
+    values ~ N(0, 1/k), or GGUF Q8_0 blocks (fp16 scale of the same spread /
+    127, int8 codes uniform in [-127, 127]) -- synthetic data, nothing is
+    quantized."""
+    if wt == vva.F16:
+        raw = (rng.standard_normal((m, k)) * k ** -0.5).astype(np.float16).view(np.uint8).reshape(-1)
+    else:
+        nb = k // 32
+        blk = np.empty((m, nb, 34), dtype=np.uint8)
+        d = (rng.uniform(0.5, 1.5, (m, nb)) * 1.7 * k ** -0.5 / 127.0).astype(np.float16)
+        blk[:, :, 0:2] = d.view(np.uint8).reshape(m, nb, 2)
+        blk[:, :, 2:] = rng.integers(-127, 128, (m, nb, 32), dtype=np.int8).view(np.uint8)
+        raw = blk.reshape(-1)
+    return vva.Weight(torch.from_numpy(raw).cuda(), wt, k, m)
+
+
 def run_prefill(torch, vva, ctx, steps: int, warmup: int, heavy: bool = False):
     rng = torch.Generator(device="cuda").manual_seed(1234)
     q = torch.randn((1, T_PREFILL, HQ, D), generator=rng, device="cuda").to(torch.bfloat16)
@@ -131,7 +148,9 @@ def run_prefill(torch, vva, ctx, steps: int, warmup: int, heavy: bool = False):
 def run_decode(torch, vva, ctx, steps: int, warmup: int):
     rng = torch.Generator(device="cuda").manual_seed(4321)
     n_layer_steps = 32                  # per form, in the decode-step comparison below
-    kv = vva.KVCache(ctx, LAYERS, HKV, D, L_DECODE + steps + warmup + 2 * n_layer_steps + 16, B_DECODE, vva.Q8_0)
+    n_block_steps = 16                  # per form, in the attention-block comparison below
+    kv = vva.KVCache(ctx, LAYERS, HKV, D, L_DECODE + steps + warmup + 2 * (n_layer_steps + n_block_steps) + 16,
+                     B_DECODE, vva.Q8_0)
     # fill every layer's caches by appending L_DECODE random rows (RoPE'd K, raw V)
     chunk = 8192
     for layer in range(LAYERS):
@@ -224,6 +243,60 @@ def run_decode(torch, vva, ctx, steps: int, warmup: int):
     torch.cuda.synchronize()
     step_fused_us = float(np.mean([a.elapsed_time(b) for a, b in ev_f])) * 1e3 / LAYERS
     step_pair_us = float(np.mean([a.elapsed_time(b) for a, b in ev_u])) * 1e3 / LAYERS
+
+    # The attention half of a decode layer (normed input to residual sum,
+    # src/qwen2.cpp:273-350) with Q8_0 weights, 28 layers' weights in
+    # rotation: the bare projections and the fused step (vva_qkv_proj +
+    # vva_decode_step, which rotates and quantizes the new rows itself) against
+    # vva_qkv_rope_append (projection, then RoPE and the Q8_0 append as a
+    # second launch) + vva_attn; both end with vva_out_proj_residual.
+    wrng = np.random.default_rng(23)
+    hidden, m_qkv = HQ * D, (HQ + 2 * HKV) * D
+    wshape = {"q": (HQ * D, hidden), "k": (HKV * D, hidden), "v": (HKV * D, hidden), "o": (hidden, HQ * D)}
+    w0 = {key: synth_weight(torch, vva, wrng, m, k, vva.Q8_0) for key, (m, k) in wshape.items()}
+    wsets = [w0] + [{key: vva.Weight(w.raw.clone(), w.w_type, w.K, w.M) for key, w in w0.items()}
+                    for _ in range(LAYERS - 1)]
+    wrefs = [tuple(byref(ws[key].t) for key in "qkvo") for ws in wsets]
+    xb = torch.randn((B_DECODE, 1, hidden), generator=rng, device="cuda")
+    hb = torch.empty_like(xb)
+    yb = torch.empty((B_DECODE, 1, m_qkv), device="cuda")
+    qy = yb[:, :, :HQ * D].view(B_DECODE, 1, HQ, D)
+    ky = yb[:, :, HQ * D:(HQ + HKV) * D].view(B_DECODE, 1, HKV, D)
+    vy = yb[:, :, (HQ + HKV) * D:].view(B_DECODE, 1, HKV, D)
+    orows = out.view(B_DECODE, 1, HQ * D)
+    bt = [vva.view(t) for t in (xb, hb, yb, qy, ky, vy, orows)]
+    xr, hr, yr, qyr, kyr, vyr, orr = (byref(t) for t in bt)
+
+    def block_step(fused, events):
+        cur = kv.get_len(0)
+        pos.fill_(cur)
+        events[0].record()
+        for layer in range(LAYERS):
+            w = wrefs[layer]
+            if fused:
+                ctx.check(lib.vva_qkv_proj(h, xr, w[0], w[1], w[2], None, None, None, yr))
+                ctx.check(lib.vva_decode_step(h, kvh, layer, qyr, kyr, vyr, pv_r, None, THETA, scale, qrv_r, ov_r))
+            else:
+                ctx.check(lib.vva_qkv_rope_append(h, kvh, layer, xr, w[0], w[1], w[2], None, None, None, pv_r, None,
+                                                  THETA, qrv_r))
+                ctx.check(lib.vva_attn(h, kvh, layer, qrv_r, None, None, scale, ov_r))
+            ctx.check(lib.vva_out_proj_residual(h, orr, w[3], xr, hr))
+        events[1].record()
+        for s in range(B_DECODE):
+            kv.set_len(s, cur + 1)
+
+    block_step(True, ev[0])
+    block_step(False, ev[0])
+    torch.cuda.synchronize()
+    ev_bf = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n_block_steps)]
+    ev_bu = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n_block_steps)]
+    for i in range(n_block_steps):
+        block_step(True, ev_bf[i])
+        block_step(False, ev_bu[i])
+    torch.cuda.synchronize()
+    block_fused_us = float(np.mean([a.elapsed_time(b) for a, b in ev_bf])) * 1e3 / LAYERS
+    block_pair_us = float(np.mean([a.elapsed_time(b) for a, b in ev_bu])) * 1e3 / LAYERS
+    del wsets, wrefs
     bytes_total = sum(decode_attn_bytes([L] * B_DECODE) + decode_append_bytes(B_DECODE)
                       for L in lens_timed) * LAYERS
     mean_L = float(np.mean(lens_timed))
@@ -241,6 +314,8 @@ def run_decode(torch, vva, ctx, steps: int, warmup: int):
         "step_fused_us": step_fused_us,
         "step_pair_us": step_pair_us,
         "step_bytes": decode_attn_bytes([float(np.mean(lens_fused))] * B_DECODE) + decode_append_bytes(B_DECODE),
+        "block_fused_us": block_fused_us,
+        "block_pair_us": block_pair_us,
     }
     return res, kv
 
@@ -398,7 +473,7 @@ def run_decode_small(torch, vva, ctx, steps: int, vvo=None):
             "timing": "HIP events around `steps` back-to-back steps; graph: one captured step replayed"}
 
 
-def run_proj(torch, vva, vvo, reps: int = 10):
+def run_proj(torch, vva, reps: int = 10):
     """The fused projections at 7B shapes (hidden 3584, 28 q / 4 kv heads,
     d = 128), F16 and Q8_0 weights: vva_qkv_rope_append (q/k/v GEMM + bias +
     RoPE + F16 cache append) and vva_out_proj_residual.
@@ -420,12 +495,10 @@ def run_proj(torch, vva, vvo, reps: int = 10):
         for layer in range(n_layers):
             ws = {}
             for key, (m, k) in shapes.items():
-                w = (rng.standard_normal((m, k)) * k ** -0.5).astype(np.float32) if layer == 0 else None
                 if layer == 0:
-                    raw = torch.from_numpy(vvo.from_f32(w, wt)).cuda()
+                    ws[key] = synth_weight(torch, vva, rng, m, k, wt)
                 else:                                       # same bytes, another buffer
-                    raw = sets[0][key].raw.clone()
-                ws[key] = vva.Weight(raw, wt, k, m)
+                    ws[key] = vva.Weight(sets[0][key].raw.clone(), wt, k, m)
             sets.append(ws)
         wbytes_qkv = sum(sets[0][k_].raw.numel() for k_ in "qkv")
         wbytes_o = sets[0]["o"].raw.numel()
@@ -657,7 +730,7 @@ def main() -> int:
             r = run_prefill_chunked(torch, vva, c, layers=2)
             c.close()
         elif args.only == "proj":
-            r = run_proj(torch, vva, vvo)
+            r = run_proj(torch, vva)
         else:
             r = run_small_prefills(torch, vva, vvo=None if args.no_cpu else vvo)
             c = vva.Context(0)
@@ -717,6 +790,13 @@ def main() -> int:
                      "fused_gbs": round(dec["step_bytes"] / (dec["step_fused_us"] * 1e-6) / 1e9, 1),
                      "fused_frac_of_hbm_peak": round(dec["step_bytes"] / (dec["step_fused_us"] * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
                      "timing": "HIP events around each step's 28 layers, 32 steps per form, alternating"},
+            "block": {"workload": "the attention half of a decode layer, normed input to residual sum, Q8_0 "
+                                  "weights (28 layers' in rotation): vva_qkv_proj + vva_decode_step against "
+                                  "vva_qkv_rope_append + vva_attn, each followed by vva_out_proj_residual",
+                      "fused_us_per_layer": round(dec["block_fused_us"], 3),
+                      "unfused_us_per_layer": round(dec["block_pair_us"], 3),
+                      "kernels_per_layer": {"fused": 4, "unfused": 5},
+                      "timing": "HIP events around each step's 28 layers, 16 steps per form, alternating"},
         }
         if not args.no_cpu:
             line["decode"]["cpu_baseline"] = cpu_baseline_decode(torch, vva, vvo, kvd)
@@ -734,7 +814,7 @@ def main() -> int:
         line["decode_small"] = run_decode_small(torch, vva, ctx, steps=200, vvo=None if args.no_cpu else vvo)
         line["prefill_small"] = run_small_prefills(torch, vva, vvo=None if args.no_cpu else vvo)
         torch.cuda.empty_cache()
-        line["proj"] = run_proj(torch, vva, vvo)
+        line["proj"] = run_proj(torch, vva)
     ctx.close()
     print(json.dumps(line), flush=True)
     return 0

@@ -255,6 +255,22 @@ VVA_API vva_status vva_qkv_rope_append(vva_context* ctx, vva_kv* kv, int layer, 
                                        const vva_tensor* pos, const int32_t* seq_ids, float freq_base,
                                        const vva_tensor* q_out);
 
+/* Q/K/V projections with bias and nothing else, for a decode step: the three
+ * linear() calls (ggml_mul_mat + ggml_add of the bias, src/qwen2.cpp:19-25,
+ * :273-275) at most 8 token rows at a time, whose outputs a following
+ * vva_decode_step rotates and appends itself (into a Q8_0 cache the append
+ * needs whole 32-dim blocks, which the fused projection of
+ * vva_qkv_rope_append cannot form in its epilogue):
+ *   x, wq, wk, wv, bq, bk, bv: as vva_qkv_rope_append (Mq, Mk, Mv = the
+ *       weights' output rows, multiples of 64);
+ *   y: F32 ne = [Mq + Mk + Mv, T, B], contiguous: token row (b, t) holds
+ *      [x wq^T + bq | x wk^T + bk | x wv^T + bv].
+ * Same numerics as vva_qkv_rope_append.  T * B > 8 (a prefill chunk: use
+ * vva_qkv_rope_append) returns VVA_ERR_NOT_IMPLEMENTED. */
+VVA_API vva_status vva_qkv_proj(vva_context* ctx, const vva_tensor* x, const vva_tensor* wq, const vva_tensor* wk,
+                                const vva_tensor* wv, const vva_tensor* bq, const vva_tensor* bk,
+                                const vva_tensor* bv, const vva_tensor* y);
+
 /* Output projection + residual: h = o w_o^T + x, the ggml_mul_mat(attn_o)
  * and ggml_add(x, o) of src/qwen2.cpp:348-349:
  *   o:   ne = [Hq*d, T, B] (F32 / F16 / BF16), e.g. vva_attn's output viewed

@@ -680,10 +680,94 @@ int block_case(vva_context* ctx, int wt) {
     return 0;
 }
 
+// A decode step into a Q8_0 cache through the attention block: given a y
+// work tensor the block runs vva_qkv_proj + vva_decode_step, without it
+// vva_qkv_rope_append + vva_attn.  Twin caches with the same history take
+// three consecutive steps (B = 2) each way; h, the rotated q, the attention
+// output and every cache row must agree bit for bit.
+int block_step_case(vva_context* ctx, int wt) {
+    const int hidden = 896, Hq = 14, Hkv = 2, d = 64, qd = Hq * d, kd = Hkv * d, M = qd + 2 * kd, B = 2;
+    Rng r(950 + (uint64_t)wt);
+    const std::vector<uint8_t> wq = make_weight(r, qd, hidden, wt), wk = make_weight(r, kd, hidden, wt),
+                               wv = make_weight(r, kd, hidden, wt), wo = make_weight(r, hidden, qd, wt);
+    std::vector<float> bq = r.normal(qd), bk = r.normal(kd), bv = r.normal(kd);
+    Dev dwq(wq.size()), dwk(wk.size()), dwv(wv.size()), dwo(wo.size()), dbq(4 * (size_t)qd), dbk(4 * (size_t)kd),
+        dbv(4 * (size_t)kd);
+    (void)hipMemcpy(dwq.p, wq.data(), wq.size(), hipMemcpyHostToDevice);
+    (void)hipMemcpy(dwk.p, wk.data(), wk.size(), hipMemcpyHostToDevice);
+    (void)hipMemcpy(dwv.p, wv.data(), wv.size(), hipMemcpyHostToDevice);
+    (void)hipMemcpy(dwo.p, wo.data(), wo.size(), hipMemcpyHostToDevice);
+    (void)hipMemcpy(dbq.p, bq.data(), 4 * (size_t)qd, hipMemcpyHostToDevice);
+    (void)hipMemcpy(dbk.p, bk.data(), 4 * (size_t)kd, hipMemcpyHostToDevice);
+    (void)hipMemcpy(dbv.p, bv.data(), 4 * (size_t)kd, hipMemcpyHostToDevice);
+    vva::Qwen2AttnWeights W;
+    W.q = weight_view(dwq.p, wt, hidden, qd);
+    W.k = weight_view(dwk.p, wt, hidden, kd);
+    W.v = weight_view(dwv.p, wt, hidden, kd);
+    W.o = weight_view(dwo.p, wt, qd, hidden);
+    W.q_bias = view4(dbq.p, VVA_TYPE_F32, qd, 1, 1, 1);
+    W.k_bias = view4(dbk.p, VVA_TYPE_F32, kd, 1, 1, 1);
+    W.v_bias = view4(dbv.p, VVA_TYPE_F32, kd, 1, 1, 1);
+    vva::ResidentKV ka, kb;                                   // with / without y_ws
+    if (!ka.init(ctx, 1, d, Hkv, 256, B, VVA_TYPE_Q8_0) || !kb.init(ctx, 1, d, Hkv, 256, B, VVA_TYPE_Q8_0)) return 90;
+    const int pasts[2] = {70, 33};
+    for (int s = 0; s < B; ++s) {
+        const std::vector<float> k = r.normal((size_t)pasts[s] * kd), v = r.normal((size_t)pasts[s] * kd);
+        if (!status_ok("upload", ka.upload(0, s, pasts[s], k.data(), v.data()), ka)) return 91;
+        if (!status_ok("upload", kb.upload(0, s, pasts[s], k.data(), v.data()), kb)) return 91;
+        ka.past_len[s] = kb.past_len[s] = pasts[s];
+    }
+    const vva::Qwen2Hparams hp = {hidden, Hq, Hkv, d, 1.0e6f, true};
+    for (int step = 0; step < 3; ++step) {
+        const std::vector<float> x = r.normal((size_t)B * hidden), xn = r.normal((size_t)B * hidden);
+        const std::vector<int32_t> pos = {ka.past_len[0], ka.past_len[1]};
+        Dev dx(4 * (size_t)B * hidden), dxn(4 * (size_t)B * hidden), dpos(4 * (size_t)B), dy(4 * (size_t)B * M);
+        Dev dh[2] = {Dev(4 * (size_t)B * hidden), Dev(4 * (size_t)B * hidden)};
+        Dev dq[2] = {Dev(4 * (size_t)B * qd), Dev(4 * (size_t)B * qd)};
+        Dev dout[2] = {Dev(4 * (size_t)B * qd), Dev(4 * (size_t)B * qd)};
+        (void)hipMemcpy(dx.p, x.data(), 4 * x.size(), hipMemcpyHostToDevice);
+        (void)hipMemcpy(dxn.p, xn.data(), 4 * xn.size(), hipMemcpyHostToDevice);
+        (void)hipMemcpy(dpos.p, pos.data(), 4 * pos.size(), hipMemcpyHostToDevice);
+        const vva_tensor tx = view4(dx.p, VVA_TYPE_F32, hidden, 1, B, 1), txn = view4(dxn.p, VVA_TYPE_F32, hidden, 1, B, 1),
+                         tp = view4(dpos.p, VVA_TYPE_I32, 1, B, 1, 1), ty = view4(dy.p, VVA_TYPE_F32, M, 1, B, 1);
+        for (int way = 0; way < 2; ++way) {
+            vva::ResidentKV& kv = way == 0 ? ka : kb;
+            const vva_tensor th = view4(dh[way].p, VVA_TYPE_F32, hidden, 1, B, 1),
+                             tq = view4(dq[way].p, VVA_TYPE_F32, d, Hq, 1, B),
+                             to = view4(dout[way].p, VVA_TYPE_F32, d, Hq, 1, B);
+            if (!status_ok("qwen2_attention_block_resident",
+                           vva::qwen2_attention_block_resident(kv, 0, txn, tx, W, tp, nullptr, hp, tq, to, th, nullptr,
+                                                               way == 0 ? &ty : nullptr),
+                           kv))
+                return 92;
+        }
+        (void)hipDeviceSynchronize();
+        auto same = [](const Dev& a, const Dev& b, size_t n) {
+            std::vector<uint8_t> ha(n), hb(n);
+            (void)hipMemcpy(ha.data(), a.p, n, hipMemcpyDeviceToHost);
+            (void)hipMemcpy(hb.data(), b.p, n, hipMemcpyDeviceToHost);
+            return ha == hb;
+        };
+        if (!same(dq[0], dq[1], 4 * (size_t)B * qd)) return 93;
+        if (!same(dout[0], dout[1], 4 * (size_t)B * qd)) return 94;
+        if (!same(dh[0], dh[1], 4 * (size_t)B * hidden)) return 95;
+        for (int s = 0; s < B; ++s) {
+            const int L = ka.past_len[s] + 1;
+            if (cache_bytes(ka.k(0, s), L) != cache_bytes(kb.k(0, s), L)) return 96;
+            if (cache_bytes(ka.v(0, s), L) != cache_bytes(kb.v(0, s), L)) return 97;
+        }
+        for (int s = 0; s < B; ++s) ka.past_len[s] = ++kb.past_len[s];
+    }
+    printf("  %s weights, Q8_0 cache, 3 steps B = 2: vva_qkv_proj + vva_decode_step equal vva_qkv_rope_append + "
+           "vva_attn bit for bit (q, o, h, cache rows)\n", wt == VVA_TYPE_F16 ? "F16" : "Q8_0");
+    return 0;
+}
+
 int test_block(vva_context* ctx) {
     for (const int wt : {VVA_TYPE_F16, VVA_TYPE_Q8_0}) {
-        const int rc = block_case(ctx, wt);
+        int rc = block_case(ctx, wt);
         if (rc) return rc;
+        if ((rc = block_step_case(ctx, wt))) return rc;
     }
     return 0;
 }

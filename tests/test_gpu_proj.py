@@ -195,6 +195,42 @@ def test_decode_step_fused_rope_equals_rope_append(ctx, torch_gpu, d, Hq, Hkv, h
     c.free()
 
 
+@pytest.mark.parametrize("hidden,Hq,Hkv,d,wt,T,B", [
+    (3584, 28, 4, 128, vva.Q8_0, 1, 2),    # 7B CFG decode step, Q8_0 weights
+    (3584, 28, 4, 128, vva.F16, 1, 2),
+    (896, 14, 2, 64, vva.F16, 3, 2),       # 6 token rows
+    (1536, 12, 2, 128, vva.Q8_0, 1, 1),
+])
+def test_qkv_proj_matches_oracle(ctx, torch_gpu, hidden, Hq, Hkv, d, wt, T, B):
+    """vva_qkv_proj: the bare q/k/v projections with bias of a decode step,
+    one [q | k | v] row per token, against the oracle's linear()."""
+    torch = torch_gpu
+    print(f"qkv_proj hidden={hidden} Hq={Hq} Hkv={Hkv} d={d} w={wt} T={T} B={B}", flush=True)
+    rng = np.random.default_rng(5 * hidden + T + wt)
+    x = rng.standard_normal((B, T, hidden)).astype(np.float32)
+    wq_raw, wq = _weight(torch, rng, Hq * d, hidden, wt)
+    wk_raw, wk = _weight(torch, rng, Hkv * d, hidden, wt)
+    wv_raw, wv = _weight(torch, rng, Hkv * d, hidden, wt)
+    bq, bk, bv = [(rng.standard_normal(n) * 0.5).astype(np.float32) for n in (Hq * d, Hkv * d, Hkv * d)]
+    M = (Hq + 2 * Hkv) * d
+    y = torch.full((B, T, M), float("nan"), dtype=torch.float32, device="cuda")
+    ctx.qkv_proj(torch.from_numpy(x).cuda(), wq, wk, wv, y, bq=torch.from_numpy(bq).cuda(),
+                 bk=torch.from_numpy(bk).cuda(), bv=torch.from_numpy(bv).cuda())
+    torch.cuda.synchronize()
+    got = as_f32(torch, y)
+    for b in range(B):
+        ref = np.concatenate([vvo.linear(x[b], wq_raw, wt, Hq * d, bq), vvo.linear(x[b], wk_raw, wt, Hkv * d, bk),
+                              vvo.linear(x[b], wv_raw, wt, Hkv * d, bv)], axis=-1)
+        m = _check(got[b], ref, vva.F32, f"y (b={b})")
+        print(f"  b={b}: max {m[0]:.2e} mean {m[1]:.2e}")
+    # a prefill chunk is vva_qkv_rope_append's
+    x16 = torch.zeros((1, 16, hidden), dtype=torch.float32, device="cuda")
+    y16 = torch.zeros((1, 16, M), dtype=torch.float32, device="cuda")
+    with pytest.raises(vva.VvaError) as e:
+        ctx.qkv_proj(x16, wq, wk, wv, y16)
+    assert e.value.status == vva.ERR_NOT_IMPLEMENTED
+
+
 O_CASES = [
     # in (Hq * d), hidden, weights, T, B, o type
     (896, 896, vva.F16, 256, 1, vva.F32),       # 0.5B layer of the TTS prefill

@@ -1055,6 +1055,62 @@ extern "C" vva_status vva_qkv_rope_append(vva_context* ctx, vva_kv* kv, int laye
     return VVA_OK;
 }
 
+extern "C" vva_status vva_qkv_proj(vva_context* ctx, const vva_tensor* x, const vva_tensor* wq, const vva_tensor* wk,
+                                   const vva_tensor* wv, const vva_tensor* bq, const vva_tensor* bk,
+                                   const vva_tensor* bv, const vva_tensor* y) {
+    if (!ctx) return VVA_ERR_INVALID_ARG;
+    vva_status st;
+    if ((st = check_tensor(ctx, x, "x")) != VVA_OK) return st;
+    if ((st = check_tensor(ctx, y, "y")) != VVA_OK) return st;
+    if ((st = check_tensor(ctx, wq, "wq")) != VVA_OK) return st;
+    if ((st = check_tensor(ctx, wk, "wk")) != VVA_OK) return st;
+    if ((st = check_tensor(ctx, wv, "wv")) != VVA_OK) return st;
+    const int64_t K = x->ne[0], T = x->ne[1], B = x->ne[2];
+    const int64_t Mq = wq->ne[1], Mk = wk->ne[1], Mv = wv->ne[1], M = Mq + Mk + Mv;
+    const int wt = wq->type;
+    if (wt != VVA_TYPE_F16 && wt != VVA_TYPE_Q8_0)
+        return fail(ctx, VVA_ERR_NOT_IMPLEMENTED, "qkv_proj: weights must be F16 or Q8_0");
+    if (B < 1 || B > VVA_MAX_BATCH) return fail(ctx, VVA_ERR_INVALID_ARG, "qkv_proj: B must be 1..%d", VVA_MAX_BATCH);
+    if (K % 64 || Mq % 64 || Mk % 64 || Mv % 64 || Mq < 64 || Mk < 64 || Mv < 64)
+        return fail(ctx, VVA_ERR_NOT_IMPLEMENTED, "qkv_proj: needs hidden and the weights' output rows multiples of 64");
+    if ((st = check_act(ctx, x, "x", K, T, B)) != VVA_OK) return st;
+    if ((st = check_weight(ctx, wq, "wq", K, Mq, wt)) != VVA_OK) return st;
+    if ((st = check_weight(ctx, wk, "wk", K, Mk, wt)) != VVA_OK) return st;
+    if ((st = check_weight(ctx, wv, "wv", K, Mv, wt)) != VVA_OK) return st;
+    if ((st = check_bias(ctx, bq, "bq", Mq)) != VVA_OK) return st;
+    if ((st = check_bias(ctx, bk, "bk", Mk)) != VVA_OK) return st;
+    if ((st = check_bias(ctx, bv, "bv", Mv)) != VVA_OK) return st;
+    if (y->type != VVA_TYPE_F32 || y->ne[0] != M || y->ne[1] != T || y->ne[2] != B || y->ne[3] != 1 ||
+        y->nb[0] != 4 || (int64_t)y->nb[1] != 4 * M || (int64_t)y->nb[2] != 4 * M * T)
+        return fail(ctx, VVA_ERR_INVALID_ARG, "qkv_proj: y must be F32 ne=[%lld,%lld,%lld,1], contiguous", (long long)M,
+                    (long long)T, (long long)B);
+    const int64_t N = T * B;
+    if (!proj_gemv_supported((int)N, (int)K, (int)M) || !rows16(x))
+        return fail(ctx, VVA_ERR_NOT_IMPLEMENTED,
+                    "qkv_proj: decode-sized calls only (at most 8 token rows of 16-byte aligned x; hidden <= 4096); "
+                    "prefill chunks take vva_qkv_rope_append");
+    ProjArgs a{};
+    const vva_tensor* ws_[3] = {wq, wk, wv};
+    const vva_tensor* bs_[3] = {bq, bk, bv};
+    const int64_t rows[3] = {Mq, Mk, Mv};
+    int64_t m_end = 0;
+    for (int i = 0; i < 3; ++i) {
+        a.w[i] = (const char*)ws_[i]->data;
+        a.w_nb[i] = (int64_t)ws_[i]->nb[1];
+        m_end += rows[i];
+        a.m_end[i] = (int)m_end;
+        a.bias[i] = bs_[i] ? (const float*)bs_[i]->data : nullptr;
+    }
+    a.w_type = wt;
+    a.N = (int)N; a.K = (int)K; a.M = (int)M; a.T = (int)T;
+    a.mode = kProjQKV;
+    a.x = (const char*)x->data; a.x_type = x->type;
+    a.x_nb_t = (int64_t)x->nb[1]; a.x_nb_b = (int64_t)x->nb[2];
+    DeviceGuard g(ctx->device);
+    const hipError_t e = launch_proj_gemv(a, (float*)y->data, ctx->n_cu, ctx->stream);
+    return e == hipSuccess ? VVA_OK : hip_fail(ctx, e, "qkv_proj launch");
+}
+
 extern "C" vva_status vva_out_proj_residual(vva_context* ctx, const vva_tensor* o, const vva_tensor* w_o,
                                             const vva_tensor* x, const vva_tensor* h) {
     if (!ctx) return VVA_ERR_INVALID_ARG;

@@ -84,6 +84,7 @@ bool VvaAttn::init(const Qwen2Hparams& p, int n_layers, int max_seq, int n_seq, 
     h  = ggml_new_tensor_2d(wctx, GGML_TYPE_F32, p.hidden_size, max_tok);
     q  = ggml_new_tensor_3d(wctx, GGML_TYPE_F32, p.head_dim, p.n_heads, max_tok);
     o  = ggml_new_tensor_3d(wctx, GGML_TYPE_F32, p.head_dim, p.n_heads, max_tok);
+    qkv = ggml_new_tensor_2d(wctx, GGML_TYPE_F32, (p.n_heads + 2 * p.n_kv_heads) * p.head_dim, max_tok);
     wbuf = allocate_ctx_tensors(wctx);
     return wbuf != nullptr;
 }
@@ -96,7 +97,7 @@ void VvaAttn::free() {
     wbuf = nullptr;
     if (wctx) ggml_free(wctx);
     wctx = nullptr;
-    xn = h = q = o = nullptr;
+    xn = h = q = o = qkv = nullptr;
     max_tokens = 0;
 }
 
@@ -151,9 +152,11 @@ bool qwen2_layer_forward_vva(VvaAttn& a, struct ggml_tensor* x, struct ggml_tens
     W.v_bias = w.attn_v_bias ? view_of(w.attn_v_bias) : vva_tensor{};
     vva_tensor tm = {};
     if (mask) tm = view_of(mask);
+    // (a decode step into a Q8_0 cache projects into qkv, then one fused step)
+    const vva_tensor ty = work_rows(a.qkv, (int64_t)(hp.n_heads + 2 * hp.n_kv_heads) * hp.head_dim, T, B, 1);
     const int st = vva::qwen2_attention_block_resident(a.kv, layer_idx, view_of(xv), view_of(x), W, view_of(pos),
                                                        mask ? &tm : nullptr, a.hp, view_of(qv), view_of(ov),
-                                                       view_of(hv), seq_ids);
+                                                       view_of(hv), seq_ids, &ty);
     ggml_free(vc);
     if (st != VVA_OK || !sync(a)) return false;
     // graph 2: y = h + ffn(rms_norm(h) * ffn_norm)  (src/qwen2.cpp:351-355)

@@ -48,6 +48,8 @@ struct VvaAttn {
     struct ggml_tensor*   h  = nullptr;       // F32 [hidden, max_tokens]: x + attention
     struct ggml_tensor*   q  = nullptr;       // F32 [head_dim, n_heads, max_tokens]: rotated q
     struct ggml_tensor*   o  = nullptr;       // F32 [head_dim, n_heads, max_tokens]: attention output
+    struct ggml_tensor*   qkv = nullptr;      // F32 [(n_heads + 2 n_kv_heads) head_dim, max_tokens]: a decode
+                                              // step's bare q/k/v projections (Q8_0 caches)
     int                   max_tokens = 0;     // T * B of one call at most
 
     // hp: the layer stack's hyperparameters; cache_type VVA_TYPE_F16 /

@@ -21,6 +21,7 @@ bool ResidentKV::init(vva_context* c, int n_layers_in, int hd, int n_kv, int max
     n_layers = n_layers_in;
     max_seq = max_seq_in;
     n_seq = n_seq_in;
+    this->type = type;
     past_len.assign(n_seq_in, 0);
     return true;
 }
@@ -108,7 +109,7 @@ int qwen2_attention_resident(ResidentKV& kvs, int layer_idx, const vva_tensor& q
 int qwen2_attention_block_resident(ResidentKV& kvs, int layer_idx, const vva_tensor& xn, const vva_tensor& x,
                                    const Qwen2AttnWeights& w, const vva_tensor& pos, const vva_tensor* mask,
                                    const Qwen2Hparams& hp, const vva_tensor& q_ws, const vva_tensor& o_ws,
-                                   const vva_tensor& h, const int32_t* seq_ids) {
+                                   const vva_tensor& h, const int32_t* seq_ids, const vva_tensor* y_ws) {
     const int hd = hp.head_dim;
     const int64_t n_tokens = xn.ne[1], n_batch = xn.ne[2] > 0 ? xn.ne[2] : 1;
     if (xn.ne[0] != hp.hidden_size || q_ws.ne[0] != hd || q_ws.ne[1] != hp.n_heads || q_ws.ne[2] != n_tokens ||
@@ -122,12 +123,33 @@ int qwen2_attention_block_resident(ResidentKV& kvs, int layer_idx, const vva_ten
     const vva_tensor* bq = w.q_bias.data ? &w.q_bias : nullptr;
     const vva_tensor* bk = w.k_bias.data ? &w.k_bias : nullptr;
     const vva_tensor* bv = w.v_bias.data ? &w.v_bias : nullptr;
-    st = vva_qkv_rope_append(kvs.ctx, kvs.kv, layer_idx, &xn, &w.q, &w.k, &w.v, bq, bk, bv, &pos, seq_ids,
-                             hp.rope_theta, &q_ws);
-    if (st != VVA_OK) return st;
-    // flash_attn_ext over the window  src/qwen2.cpp:312-335
-    st = vva_attn(kvs.ctx, kvs.kv, layer_idx, &q_ws, seq_ids, mask, 1.0f / sqrtf((float)hd), &o_ws);
-    if (st != VVA_OK) return st;
+    const float scale = 1.0f / sqrtf((float)hd);
+    if (y_ws && !mask && n_tokens * n_batch <= 8 && kvs.type == VVA_TYPE_Q8_0) {
+        // a decode step into a Q8_0 cache: the bare projections, then RoPE,
+        // the append and attention as one fused step (src/qwen2.cpp:273-335)
+        const int64_t mq = (int64_t)hp.n_heads * hd, mkv = (int64_t)hp.n_kv_heads * hd;
+        if (y_ws->ne[0] != mq + 2 * mkv) return VVA_ERR_INVALID_ARG;
+        st = vva_qkv_proj(kvs.ctx, &xn, &w.q, &w.k, &w.v, bq, bk, bv, y_ws);
+        if (st != VVA_OK) return st;
+        auto part = [&](int64_t first, int64_t heads) {     // q, k or v of every token row
+            vva_tensor t = *y_ws;
+            t.data = (char*)y_ws->data + first * 4;
+            t.ne[0] = hd; t.ne[1] = heads; t.ne[2] = n_tokens; t.ne[3] = n_batch;
+            t.nb[0] = 4; t.nb[1] = (size_t)4 * hd; t.nb[2] = y_ws->nb[1]; t.nb[3] = y_ws->nb[2];
+            return t;
+        };
+        const vva_tensor q = part(0, hp.n_heads), k = part(mq, hp.n_kv_heads), v = part(mq + mkv, hp.n_kv_heads);
+        st = vva_decode_step(kvs.ctx, kvs.kv, layer_idx, &q, &k, &v, &pos, seq_ids, hp.rope_theta, scale, &q_ws,
+                             &o_ws);
+        if (st != VVA_OK) return st;
+    } else {
+        st = vva_qkv_rope_append(kvs.ctx, kvs.kv, layer_idx, &xn, &w.q, &w.k, &w.v, bq, bk, bv, &pos, seq_ids,
+                                 hp.rope_theta, &q_ws);
+        if (st != VVA_OK) return st;
+        // flash_attn_ext over the window  src/qwen2.cpp:312-335
+        st = vva_attn(kvs.ctx, kvs.kv, layer_idx, &q_ws, seq_ids, mask, scale, &o_ws);
+        if (st != VVA_OK) return st;
+    }
     // h = x + attn_o(o)  src/qwen2.cpp:349-350
     vva_tensor rows = o_ws;
     rows.ne[0] = (int64_t)hp.n_heads * hd; rows.ne[1] = n_tokens; rows.ne[2] = n_batch; rows.ne[3] = 1;

@@ -54,6 +54,7 @@ struct ResidentKV {
     int              n_layers = 0;
     int              max_seq  = 0;
     int              n_seq    = 0;
+    int              type     = VVA_TYPE_F16;   // cache type (ggml type number)
     std::vector<int> past_len;               // valid rows per sequence
 
     ResidentKV() = default;
@@ -126,12 +127,20 @@ struct Qwen2AttnWeights {
 //   q_ws:  F32 ne=[hd, n_heads, T, B], contiguous: receives the rotated q;
 //   o_ws:  F32 ne=[hd, n_heads, T, B], contiguous: the attention output;
 //   h:     F32 ne=[hidden, T, B], x + attn_o(o) (src/qwen2.cpp:349-350),
-//          may alias x.
+//          may alias x;
+//   y_ws:  nullptr, or F32 ne=[(n_heads + 2 n_kv_heads) hd, T, B],
+//          contiguous: then a decode step (T * B <= 8, mask nullptr) on a
+//          Q8_0 cache runs as the bare projections (vva_qkv_proj into y_ws)
+//          and one vva_decode_step, which rotates q and k and quantizes the
+//          new rows itself, instead of vva_qkv_rope_append (projection, then
+//          RoPE and the Q8_0 append as a second launch) and vva_attn; same
+//          results.
 // pos, mask, seq_ids, hp and the past_len contract are as for
 // qwen2_attention_resident.  Returns a vva_status.
 int qwen2_attention_block_resident(ResidentKV& kvs, int layer_idx, const vva_tensor& xn, const vva_tensor& x,
                                    const Qwen2AttnWeights& w, const vva_tensor& pos, const vva_tensor* mask,
                                    const Qwen2Hparams& hp, const vva_tensor& q_ws, const vva_tensor& o_ws,
-                                   const vva_tensor& h, const int32_t* seq_ids = nullptr);
+                                   const vva_tensor& h, const int32_t* seq_ids = nullptr,
+                                   const vva_tensor* y_ws = nullptr);
 
 }  // namespace vva

@@ -32,7 +32,7 @@ EXPORTS = [
     "vva_kv_view", "vva_kv_upload", "vva_rope_ext", "vva_rope_append", "vva_attn",
     "vva_flash_attn_ext", "vva_supports", "vva_set_attn_path", "vva_last_decode_splits",
     "vva_set_schedule", "vva_attn_noalloc", "vva_qkv_rope_append", "vva_out_proj_residual",
-    "vva_set_flash_attn", "vva_decode_step",
+    "vva_set_flash_attn", "vva_decode_step", "vva_qkv_proj",
 ]
 
 
@@ -99,6 +99,7 @@ def load_library(path: str = LIB_PATH):
         "vva_attn_noalloc": (I, [P, P, I, TP, P, TP, F, TP]),
         "vva_qkv_rope_append": (I, [P, P, I, TP, TP, TP, TP, TP, TP, TP, TP, P, F, TP]),
         "vva_out_proj_residual": (I, [P, TP, TP, TP, TP]),
+        "vva_qkv_proj": (I, [P, TP, TP, TP, TP, TP, TP, TP, TP]),
         "vva_flash_attn_ext": (I, [P, TP, TP, TP, TP, F, F, F, TP]),
         "vva_supports": (I, [P, I, I, I, I, I]),
         "vva_set_attn_path": (I, [P, I]),
@@ -264,6 +265,12 @@ class Context:
         self.check(self.lib.vva_qkv_rope_append(self.h, kv.h, layer, ctypes.byref(view(x)), ctypes.byref(wq.t),
                                                 ctypes.byref(wk.t), ctypes.byref(wv.t), bref[0], bref[1], bref[2],
                                                 ctypes.byref(view(pos)), ids, freq_base, ctypes.byref(view(q_out))))
+
+    def qkv_proj(self, x, wq: "Weight", wk: "Weight", wv: "Weight", y, bq=None, bk=None, bv=None):
+        """x: [B, T, hidden]; weights: Weight; biases f32 [rows] or None; y f32 [B, T, Mq + Mk + Mv]."""
+        bref = [ctypes.byref(view(t)) if t is not None else None for t in (bq, bk, bv)]
+        self.check(self.lib.vva_qkv_proj(self.h, ctypes.byref(view(x)), ctypes.byref(wq.t), ctypes.byref(wk.t),
+                                         ctypes.byref(wv.t), bref[0], bref[1], bref[2], ctypes.byref(view(y))))
 
     def out_proj_residual(self, o, w_o: "Weight", x, h):
         """o: [B, T, Hq*d] (or [B, T, Hq, d], viewed as rows); x, h: f32 [B, T, hidden]."""
