@@ -899,7 +899,8 @@ constexpr int kBRing = kBStages * kBStage;
 constexpr int kBCBytes = kBHalf * kBCPitch * 4;
 constexpr int kBLds = kBRing > kBCBytes ? kBRing : kBCBytes;
 constexpr int kBPiece = kBWaves * 8 * 4096;     // bytes of one K piece's accumulators (256 x 256 f32)
-constexpr int kBMaxSplit = 4;
+constexpr int kBMaxSplit = 8;
+constexpr int kBigMinRows = 1024;             // token rows from which the big GEMM runs (shorter: the wide one measured faster)
 static_assert(kBStages == 2 && kBStages * kBLoads <= 63, "two stages of a wave's loads fit its 6-bit vmcnt");
 static_assert(kBLds <= 160 * 1024, "LDS");
 
@@ -1196,20 +1197,40 @@ __global__ void __launch_bounds__(256) proj_big_merge_kernel(ProjArgs a) {
     const int tid = threadIdx.x;
     const int wn = slab >> 1, j = slab & 1;
     const char* piece0 = a.part + (int64_t)tile * a.ksplit * kBPiece;
-    // float4 f of the slab: wm = f / 1024, i = (f / 256) % 4, g = (f / 64) % 4, lane = f % 64
+    // float4 f of the slab: wm = f / 1024, i = (f / 256) % 4, g = (f / 64) % 4, lane = f % 64;
+    // pieces summed in split order, four at a time with their loads in flight
     constexpr int NF = 2 * 4 * 4 * 64 / 256;               // float4s per thread
-    u32x4 v[NF][kBMaxSplit];
+    constexpr int KB = 4;
+    int off[NF];
+    float4 s[NF];
 #pragma unroll
     for (int e = 0; e < NF; ++e) {
         const int f = tid + 256 * e;
         const int wm = f >> 10, i = (f >> 8) & 3, g = (f >> 6) & 3, lane = f & 63;
-        const int off = ((2 * wn + wm) * 32 + (i * 2 + j) * 4 + g) * 1024 + lane * 16;
+        off[e] = ((2 * wn + wm) * 32 + (i * 2 + j) * 4 + g) * 1024 + lane * 16;
+        s[e] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+#pragma unroll 1
+    for (int k0 = 0; k0 < a.ksplit; k0 += KB) {
+        u32x4 v[NF][KB];
 #pragma unroll
-        for (int k = 0; k < kBMaxSplit; ++k) {
-            if (k >= a.ksplit) break;                      // uniform
+        for (int k = 0; k < KB; ++k) {
+            if (k0 + k >= a.ksplit) break;                 // uniform
             const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-                const_cast<char*>(piece0) + (int64_t)k * kBPiece, (short)0, kBPiece, 0x00020000);
-            v[e][k] = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+                const_cast<char*>(piece0) + (int64_t)(k0 + k) * kBPiece, (short)0, kBPiece, 0x00020000);
+#pragma unroll
+            for (int e = 0; e < NF; ++e) v[e][k] = __builtin_amdgcn_raw_buffer_load_b128(rs, off[e], 0, 0);
+        }
+#pragma unroll
+        for (int k = 0; k < KB; ++k) {
+            if (k0 + k >= a.ksplit) break;
+#pragma unroll
+            for (int e = 0; e < NF; ++e) {
+                s[e].x += __uint_as_float(v[e][k].x);
+                s[e].y += __uint_as_float(v[e][k].y);
+                s[e].z += __uint_as_float(v[e][k].z);
+                s[e].w += __uint_as_float(v[e][k].w);
+            }
         }
     }
 #pragma unroll
@@ -1217,16 +1238,7 @@ __global__ void __launch_bounds__(256) proj_big_merge_kernel(ProjArgs a) {
         const int f = tid + 256 * e;
         const int wm = f >> 10, i = (f >> 8) & 3, g = (f >> 6) & 3, lane = f & 63;
         const int l32 = lane & 31, half = lane >> 5;
-        float4 s = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-#pragma unroll
-        for (int k = 0; k < kBMaxSplit; ++k) {
-            if (k >= a.ksplit) break;
-            s.x += __uint_as_float(v[e][k].x);
-            s.y += __uint_as_float(v[e][k].y);
-            s.z += __uint_as_float(v[e][k].z);
-            s.w += __uint_as_float(v[e][k].w);
-        }
-        *(float4*)(C + l32 * kBCPitch + wm * 128 + 32 * i + 4 * half + 8 * g) = s;
+        *(float4*)(C + l32 * kBCPitch + wm * 128 + 32 * i + 4 * half + 8 * g) = s[e];
     }
     __syncthreads();
     if constexpr (MODE == kProjQKV) {
@@ -2387,10 +2399,10 @@ hipError_t launch_proj_gemv(ProjArgs& a, float* y_ws, int n_cu, hipStream_t s) {
 // at most half of them (short chunks, e.g. 512 tokens) is split along K, at
 // least 4 k steps per piece, up to 4 pieces, one round.
 namespace {
-// F16 weights over at least 1024 token rows take the big kernel (256 x 256
+// F16 weights over at least kBigMinRows token rows take the big kernel (256 x 256
 // tiles); shorter calls the wide one (256 x 128), whose split pieces are half
 // the size
-bool proj_big(const ProjArgs& a) { return a.w_type != VVA_TYPE_Q8_0 && a.N >= 1024; }
+bool proj_big(const ProjArgs& a) { return a.w_type != VVA_TYPE_Q8_0 && a.N >= kBigMinRows; }
 }  // namespace
 
 int proj_ksplit(const ProjArgs& a, int n_cu, int* tail0) {
@@ -2472,7 +2484,7 @@ __global__ void __launch_bounds__(256) proj_dequant_q8_kernel(ProjArgs a, uint16
     for (int i = 0; i < 4; ++i) o[i] = u32x4{outw[4 * i], outw[4 * i + 1], outw[4 * i + 2], outw[4 * i + 3]};
 }
 
-bool proj_dequant_q8(const ProjArgs& a) { return a.w_type == VVA_TYPE_Q8_0 && a.N >= 1024; }
+bool proj_dequant_q8(const ProjArgs& a) { return a.w_type == VVA_TYPE_Q8_0 && a.N >= kBigMinRows; }
 
 hipError_t launch_proj_dequant_q8(const ProjArgs& a, uint16_t* dst, hipStream_t s) {
     const int64_t n = (int64_t)a.M * (a.K / 32);
