@@ -2448,47 +2448,58 @@ size_t proj_part_bytes(const ProjArgs& a) {
 // Q8_0 weight rows dequantized to f16 rows of d * q: the products the Q8_0
 // GEMM forms while staging its tiles (code and fp16 scale multiplied in
 // f16, the exact product rounded once), so that long calls run the F16 GEMM
-// on them.  One thread per 32-element block; a block's 34 bytes are read as
-// 9 dwords from the 4-byte boundary at or below it (the buffer range ends at
-// the matrix's last row, so a dword past it reads as zero).
-__global__ void __launch_bounds__(256) proj_dequant_q8_kernel(ProjArgs a, uint16_t* dst) {
-    const int nb = a.K / 32;
-    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (t >= (int64_t)a.M * nb) return;
-    const int row = (int)(t / nb), blk = (int)(t - (int64_t)row * nb);
+// on them.  One workgroup per row: the row's blocks are read as consecutive
+// dwords into LDS (coalesced; the buffer range ends at the matrix's last
+// row, so a dword past it reads as zero), then thread t converts the 8
+// codes t % 4 of block t / 4 and stores their 16 bytes, so that every store
+// instruction writes 1 KB of the row contiguously.
+constexpr int kDqMaxK = 8192;
+constexpr int kDqThreads = 256;
+__global__ void __launch_bounds__(kDqThreads) proj_dequant_q8_kernel(ProjArgs a, uint16_t* dst) {
+    __shared__ uint32_t rowbuf[kDqMaxK / 32 * kQ8Bytes / 4 + 4];
+    const int row = blockIdx.x, nb = a.K / 32;
     const int mat = row < a.m_end[0] ? 0 : (row < a.m_end[1] ? 1 : 2);
     const int mbeg = mat == 0 ? 0 : a.m_end[mat - 1];
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<char*>(a.w[mat]), (short)0, (int)((a.m_end[mat] - mbeg) * a.w_nb[mat]), 0x00020000);
-    const uint32_t off = (uint32_t)((row - mbeg) * a.w_nb[mat]) + (uint32_t)blk * kQ8Bytes;
-    uint32_t q[9];
+    const uint32_t base = (uint32_t)((row - mbeg) * a.w_nb[mat]);
+    const int nd = (nb * kQ8Bytes + 3) / 4;
+    for (int i = threadIdx.x; i < nd; i += kDqThreads) rowbuf[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, base + 4 * i, 0, 0);
+    __syncthreads();
+    const char* rb = (const char*)rowbuf;
+    u32x4* orow = (u32x4*)(dst + (int64_t)row * a.K);
+    for (int t = threadIdx.x; t < 4 * nb; t += kDqThreads) {
+        const int blk = t >> 2, qd = t & 3;
+        const int off = blk * kQ8Bytes;                    // even
+        const uint16_t d16 = *(const uint16_t*)(rb + off);
+        _Float16 dh;
+        __builtin_memcpy(&dh, &d16, 2);
+        const h2 dd = {dh, dh};
+        // codes 8 qd .. 8 qd + 7: bytes off + 2 + 8 qd .., from the dword at or below
+        const int cb = off + 2 + 8 * qd;
+        const uint32_t* w = (const uint32_t*)(rb + (cb & ~3));
+        const uint32_t w0 = w[0], w1 = w[1], w2 = w[2];
+        const bool mis = cb & 2;
+        const uint32_t c0 = mis ? __builtin_amdgcn_alignbyte(w1, w0, 2) : w0;
+        const uint32_t c1 = mis ? __builtin_amdgcn_alignbyte(w2, w1, 2) : w1;
+        uint32_t outw[4];
 #pragma unroll
-    for (int i = 0; i < 9; ++i) q[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, (off & ~3u) + 4 * i, 0, 0);
-    const bool odd = off & 2;                           // the block starts 2 bytes into dword 0
-    const uint16_t d16 = (uint16_t)(odd ? (q[0] >> 16) : (q[0] & 0xffffu));
-    _Float16 dh;
-    __builtin_memcpy(&dh, &d16, 2);
-    const h2 dd = {dh, dh};
-    uint32_t outw[16];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const uint32_t c = odd ? q[i + 1] : __builtin_amdgcn_alignbyte(q[i + 1], q[i], 2);
-        const h2 lo = {(_Float16)(int8_t)(c & 0xff), (_Float16)(int8_t)((c >> 8) & 0xff)};
-        const h2 hi = {(_Float16)(int8_t)((c >> 16) & 0xff), (_Float16)(int8_t)(c >> 24)};
-        const h2 plo = lo * dd, phi = hi * dd;
-        __builtin_memcpy(&outw[2 * i], &plo, 4);
-        __builtin_memcpy(&outw[2 * i + 1], &phi, 4);
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t c = i ? c1 : c0;
+            const h2 lo = {(_Float16)(int8_t)(c & 0xff), (_Float16)(int8_t)((c >> 8) & 0xff)};
+            const h2 hi = {(_Float16)(int8_t)((c >> 16) & 0xff), (_Float16)(int8_t)(c >> 24)};
+            const h2 plo = lo * dd, phi = hi * dd;
+            __builtin_memcpy(&outw[2 * i], &plo, 4);
+            __builtin_memcpy(&outw[2 * i + 1], &phi, 4);
+        }
+        orow[t] = u32x4{outw[0], outw[1], outw[2], outw[3]};
     }
-    u32x4* o = (u32x4*)(dst + (int64_t)row * a.K + blk * 32);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) o[i] = u32x4{outw[4 * i], outw[4 * i + 1], outw[4 * i + 2], outw[4 * i + 3]};
 }
 
-bool proj_dequant_q8(const ProjArgs& a) { return a.w_type == VVA_TYPE_Q8_0 && a.N >= kBigMinRows; }
+bool proj_dequant_q8(const ProjArgs& a) { return a.w_type == VVA_TYPE_Q8_0 && a.N >= kBigMinRows && a.K <= kDqMaxK; }
 
 hipError_t launch_proj_dequant_q8(const ProjArgs& a, uint16_t* dst, hipStream_t s) {
-    const int64_t n = (int64_t)a.M * (a.K / 32);
-    hipLaunchKernelGGL(proj_dequant_q8_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a, dst);
+    hipLaunchKernelGGL(proj_dequant_q8_kernel, dim3((unsigned)a.M), dim3(kDqThreads), 0, s, a, dst);
     return hipGetLastError();
 }
 
