@@ -727,7 +727,8 @@ def main() -> int:
     if args.only in ("proj", "small", "chunked"):
         if args.only == "chunked":
             c = vva.Context(0)
-            r = run_prefill_chunked(torch, vva, c, layers=2)
+            r = {"f16": run_prefill_chunked(torch, vva, c, layers=2),
+                 "q8_0": run_prefill_chunked(torch, vva, c, layers=2, cache_type=vva.Q8_0)}
             c.close()
         elif args.only == "proj":
             r = run_proj(torch, vva)

@@ -708,16 +708,21 @@ hipError_t launch_pf(const AttnArgs& a, float* ws, unsigned* tickets, const Pref
     return hipGetLastError();
 }
 
-// One thread per 32-element block of a K or V head row of one sequence:
-// grid (blocks of the longest window / 256, 2 B: K and V of each sequence).
+// One thread per 8 consecutive elements (quarter q of 32-element block k of
+// a K or V head row of one sequence), so that consecutive threads store
+// consecutive 16 bytes: grid (quarters of the longest window / 256, 2 B: K
+// and V of each sequence).  Q8_0: d * q in fp32 (exact: an 11-bit scale
+// times a 7-bit code) rounded once to f16; F32: rounded to f16.
 __global__ void __launch_bounds__(256) window_to_f16_kernel(AttnArgs a, uint16_t* __restrict__ dst,
                                                             unsigned long long* ovf, unsigned long long epoch) {
     prefetch_kernargs<sizeof(AttnArgs)>();
     const int b = blockIdx.y >> 1, which = blockIdx.y & 1;
     const int nblk = a.d / 32;
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;       // (row, head, block)
+    const int64_t i4 = (int64_t)blockIdx.x * 256 + threadIdx.x;      // (row, head, block, quarter)
     const int L = a.L[b];
-    if (i >= (int64_t)L * a.Hkv * nblk) return;
+    if (i4 >= (int64_t)L * a.Hkv * nblk * 4) return;
+    const int q = (int)(i4 & 3);
+    const int64_t i = i4 >> 2;
     const int bk = (int)(i % nblk), h = (int)((i / nblk) % a.Hkv);
     const int64_t row = i / ((int64_t)nblk * a.Hkv);
     const int type = which ? a.v_type : a.k_type;
@@ -725,28 +730,39 @@ __global__ void __launch_bounds__(256) window_to_f16_kernel(AttnArgs a, uint16_t
                       h * (which ? a.v_nb_head : a.k_nb_head);
     size_t off = 0;                                                   // this sequence's K, then V
     for (int b2 = 0; b2 < b; ++b2) off += (size_t)2 * a.L[b2] * a.Hkv * a.d;
-    uint16_t* o = dst + off + (size_t)which * L * a.Hkv * a.d + ((size_t)row * a.Hkv + h) * a.d + bk * 32;
-    uint32_t w[16];
+    uint16_t* o = dst + off + (size_t)which * L * a.Hkv * a.d + ((size_t)row * a.Hkv + h) * a.d + bk * 32 + q * 8;
+    uint32_t w[4];
     if (type == VVA_TYPE_Q8_0) {
+        // the block's scale and codes 8 q .. 8 q + 7 (2-byte aligned): dwords
+        // from the 4-byte boundary at or below them (a dword holding a byte
+        // of the block lies in the block's page)
         const char* blk = src + bk * kQ8Bytes;
-        const float d = f16_to_f32(*(const uint16_t*)blk);
+        const uintptr_t sa = (uintptr_t)blk, ca = sa + 2 + 8 * q;
+        const uint32_t sw = *(const uint32_t*)(sa & ~(uintptr_t)3);
+        const float d = f16_to_f32((uint16_t)((sa & 2) ? (sw >> 16) : (sw & 0xffffu)));
+        const uint32_t* cw = (const uint32_t*)(ca & ~(uintptr_t)3);
+        const uint32_t w0 = cw[0], w1 = cw[1];
+        const uint32_t w2 = (ca & 2) ? cw[2] : 0u;
+        const uint32_t c0 = (ca & 2) ? __builtin_amdgcn_alignbyte(w1, w0, 2) : w0;
+        const uint32_t c1 = (ca & 2) ? __builtin_amdgcn_alignbyte(w2, w1, 2) : w1;
 #pragma unroll
-        for (int e = 0; e < 16; ++e)
-            w[e] = (uint32_t)f32_to_f16(d * (float)(int8_t)blk[2 + 2 * e]) |
-                   ((uint32_t)f32_to_f16(d * (float)(int8_t)blk[3 + 2 * e]) << 16);
+        for (int e = 0; e < 4; ++e) {
+            const uint32_t c = e < 2 ? c0 : c1, sh = 16 * (e & 1);
+            w[e] = (uint32_t)f32_to_f16(d * (float)(int8_t)(c >> sh)) |
+                   ((uint32_t)f32_to_f16(d * (float)(int8_t)(c >> (sh + 8))) << 16);
+        }
         // a value beyond the f16 range (ggml dequantizes Q8_0 to fp32: it
         // stays finite there): flag the call for the fp32 fallback
         bool inf = false;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) inf |= (w[e] & 0x7c00u) == 0x7c00u || (w[e] & 0x7c000000u) == 0x7c000000u;
+        for (int e = 0; e < 4; ++e) inf |= (w[e] & 0x7c00u) == 0x7c00u || (w[e] & 0x7c000000u) == 0x7c000000u;
         if (inf && ovf) *ovf = epoch;
     } else {
-        const float* f = (const float*)src + bk * 32;
+        const float* f = (const float*)src + bk * 32 + q * 8;       // (4-byte aligned views)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) w[e] = (uint32_t)f32_to_f16(f[2 * e]) | ((uint32_t)f32_to_f16(f[2 * e + 1]) << 16);
+        for (int e = 0; e < 4; ++e) w[e] = (uint32_t)f32_to_f16(f[2 * e]) | ((uint32_t)f32_to_f16(f[2 * e + 1]) << 16);
     }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) ((uint4*)o)[e] = make_uint4(w[4 * e], w[4 * e + 1], w[4 * e + 2], w[4 * e + 3]);
+    *(uint4*)o = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
 }  // namespace
@@ -761,7 +777,7 @@ hipError_t launch_window_to_f16(const AttnArgs& a, void* dst, unsigned long long
                                 hipStream_t s) {
     int Lmax = 1;
     for (int b = 0; b < a.B; ++b) Lmax = max(Lmax, a.L[b]);
-    const int64_t n = (int64_t)Lmax * a.Hkv * (a.d / 32);
+    const int64_t n = (int64_t)Lmax * a.Hkv * (a.d / 32) * 4;
     hipLaunchKernelGGL(window_to_f16_kernel, dim3((unsigned)((n + 255) / 256), 2 * a.B), dim3(256), 0, s, a,
                        (uint16_t*)dst, ovf, epoch);
     return hipGetLastError();
