@@ -96,6 +96,26 @@ VVA_API const char* vva_last_error(const vva_context* ctx);
 /* Library version string. */
 VVA_API const char* vva_version(void);
 
+/* Log levels: numbering follows vv_log_level (include/vibevoice.h:36-41). */
+typedef enum {
+    VVA_LOG_ERROR = 0,
+    VVA_LOG_WARN  = 1,
+    VVA_LOG_INFO  = 2,
+    VVA_LOG_DEBUG = 3
+} vva_log_level;
+
+typedef void (*vva_log_cb)(vva_log_level lvl, const char* msg, void* user_data);
+
+/* Route the library's messages to cb (NULL: none are delivered; every
+ * error message stays readable through vva_last_error either way).
+ * Delivered: each failed call's message (ERROR), the device a context is
+ * created on (INFO), and the plans calls settle on: decode key splits,
+ * prefill key splits (DEBUG).  Messages above max_lvl are dropped before
+ * formatting.  cb may be called from any thread that calls the library,
+ * one call at a time (a process-wide lock).  Replaces vv_set_log_callback
+ * (src/common.cpp:79-84), with the level filter made explicit. */
+VVA_API void        vva_set_log_callback(vva_log_cb cb, void* user_data, vva_log_level max_lvl);
+
 /* ------------------------------------------------------------- KV cache */
 
 /* Resident KV cache: one K and one V tensor per (layer, sequence), each

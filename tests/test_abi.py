@@ -66,3 +66,24 @@ def test_null_arguments_are_rejected_without_a_device():
     assert lib.vva_synchronize(None) == vva.ERR_INVALID_ARG
     assert lib.vva_supports(None, 128, 28, 4, vva.F16, vva.Q8_0) == 0
     assert lib.vva_attn(None, None, 0, None, None, None, 0.0, None) == vva.ERR_INVALID_ARG
+
+
+def test_log_callback_receives_failed_calls():
+    torch = pytest.importorskip("torch")
+    if torch.cuda.device_count() > 0:
+        pytest.skip("a GPU is visible")
+    import vva
+    got = []
+    vva.set_log_callback(lambda lvl, msg: got.append((lvl, msg)), vva.LOG_DEBUG)
+    lib = vva.load_library()
+    h = ctypes.c_void_p()
+    try:
+        assert lib.vva_create(0, None, ctypes.byref(h)) < 0
+        assert lib.vva_create(-1, None, ctypes.byref(h)) < 0
+    finally:
+        vva.set_log_callback(None)
+    assert [lvl for lvl, _ in got] == [vva.LOG_ERROR, vva.LOG_ERROR], got
+    assert got[1][1] == lib.vva_last_error(None).decode()
+    # removed: nothing more is delivered
+    assert lib.vva_create(0, None, ctypes.byref(h)) < 0
+    assert len(got) == 2

@@ -29,6 +29,7 @@ struct vva_context {
     int attn_path = 0;
     int use_flash_attn = 1;              // F32 caches: 1 = F16 cast + MFMA prefill, 0 = fp32 throughout
     int last_splits = 0;
+    int logged_splits = -1;              // the decode split count last logged
     // scheduling overrides (vva_set_schedule); 0 = automatic
     int sched_decode_wgs = 0, sched_decode_splits = 0, sched_prefill_splits = 0;
     float* ws = nullptr;                 // split partials (decode and key-split prefill)
@@ -77,6 +78,31 @@ namespace {
 
 thread_local std::string g_create_err;
 
+// The vva_set_log_callback sink: process-wide, one delivery at a time.
+struct LogSink {
+    std::mutex mu;
+    vva_log_cb cb = nullptr;
+    void* user = nullptr;
+    int max_lvl = -1;                        // nothing delivered until a callback is set
+};
+LogSink& log_sink() {
+    static LogSink s;
+    return s;
+}
+
+// Formats into a stack buffer (no allocation: vva_attn_noalloc logs too).
+void log_msg(vva_log_level lvl, const char* fmt, ...) {
+    LogSink& s = log_sink();
+    std::lock_guard<std::mutex> lk(s.mu);
+    if (!s.cb || (int)lvl > s.max_lvl) return;
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    s.cb(lvl, buf, s.user);
+}
+
 // Device address of `scratch` per device, resolved once per device by
 // vva_create with that device current.
 constexpr int kMaxDevices = 64;
@@ -114,6 +140,7 @@ vva_status fail(vva_context* ctx, vva_status st, const char* fmt, ...) {
     va_end(ap);
     if (ctx) ctx->err = buf;
     else g_create_err = buf;
+    log_msg(VVA_LOG_ERROR, "%s", buf);
     return st;
 }
 
@@ -218,7 +245,10 @@ vva_status run_attention(vva_context* ctx, AttnArgs& a, bool fixed = false) {
         }
         e = launch_decode_stream(a, ws, n_splits, ctx->stream);
         if (e != hipSuccess) return hip_fail(ctx, e, "decode launch");
-        ctx->last_splits = n_splits;
+        if (n_splits != ctx->logged_splits)
+            log_msg(VVA_LOG_DEBUG, "decode: streamed Q8_0 kernel, %d key splits per sequence (B=%d, L[0]=%d)",
+                    n_splits, a.B, a.L[0]);
+        ctx->last_splits = ctx->logged_splits = n_splits;
         return VVA_OK;
     }
     if (ctx->attn_path != 1 && a.T == 1 && decode_supported(a)) {
@@ -241,7 +271,10 @@ vva_status run_attention(vva_context* ctx, AttnArgs& a, bool fixed = false) {
         }
         e = launch_decode(a, ws, n_splits, split_len, ctx->stream);
         if (e != hipSuccess) return hip_fail(ctx, e, "decode launch");
-        ctx->last_splits = n_splits;
+        if (n_splits != ctx->logged_splits)
+            log_msg(VVA_LOG_DEBUG, "decode: register-streamed kernel, %d key splits of %d keys (B=%d, L[0]=%d)",
+                    n_splits, split_len, a.B, a.L[0]);
+        ctx->last_splits = ctx->logged_splits = n_splits;
         return VVA_OK;
     }
     // Q8_0 windows, and F32 windows under flash-attention semantics (the
@@ -265,6 +298,8 @@ vva_status run_attention(vva_context* ctx, AttnArgs& a, bool fixed = false) {
         if (key != ctx->plan_key) {
             ctx->plan = prefill_plan(c, ctx->n_cu, ctx->sched_prefill_splits, cap, !fixed);
             ctx->plan_key = std::move(key);
+            log_msg(VVA_LOG_DEBUG, "prefill plan: T=%d B=%d L[0]=%d: row tiles from %d split %d ways%s", c.T, c.B,
+                    c.L[0], ctx->plan.R, ctx->plan.max_ks, ctx->plan.in_launch ? ", merged in the launch" : "");
         }
         return ctx->plan;
     };
@@ -410,6 +445,7 @@ extern "C" vva_status vva_create(int device, void* stream, vva_context** out) {
         *out = nullptr;
         return fail(nullptr, VVA_ERR_DEVICE, "vva_create: ticket buffer: %s", hipGetErrorString(e));
     }
+    log_msg(VVA_LOG_INFO, "context on device %d (%s, %s, %d CUs)", device, prop.name, prop.gcnArchName, ctx->n_cu);
     *out = ctx;
     return VVA_OK;
 }
@@ -456,6 +492,14 @@ extern "C" const char* vva_last_error(const vva_context* ctx) {
 }
 
 extern "C" const char* vva_version(void) { return "vva 0.1.0 (gfx950)"; }
+
+extern "C" void vva_set_log_callback(vva_log_cb cb, void* user_data, vva_log_level max_lvl) {
+    LogSink& s = log_sink();
+    std::lock_guard<std::mutex> lk(s.mu);
+    s.cb = cb;
+    s.user = user_data;
+    s.max_lvl = cb ? (int)max_lvl : -1;
+}
 
 extern "C" vva_status vva_set_attn_path(vva_context* ctx, int path) {
     if (!ctx || path < 0 || path > 2) return VVA_ERR_INVALID_ARG;

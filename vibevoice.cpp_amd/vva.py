@@ -32,8 +32,12 @@ EXPORTS = [
     "vva_kv_view", "vva_kv_upload", "vva_rope_ext", "vva_rope_append", "vva_attn",
     "vva_flash_attn_ext", "vva_supports", "vva_set_attn_path", "vva_last_decode_splits",
     "vva_set_schedule", "vva_attn_noalloc", "vva_qkv_rope_append", "vva_out_proj_residual",
-    "vva_set_flash_attn", "vva_decode_step", "vva_qkv_proj",
+    "vva_set_flash_attn", "vva_decode_step", "vva_qkv_proj", "vva_set_log_callback",
 ]
+
+LOG_ERROR, LOG_WARN, LOG_INFO, LOG_DEBUG = 0, 1, 2, 3
+# void (*)(vva_log_level lvl, const char* msg, void* user_data)
+LOG_CB = ctypes.CFUNCTYPE(None, ctypes.c_int, ctypes.c_char_p, ctypes.c_void_p)
 
 
 class VvaError(RuntimeError):
@@ -107,6 +111,7 @@ def load_library(path: str = LIB_PATH):
         "vva_set_schedule": (I, [P, I, I, I]),
         "vva_set_flash_attn": (I, [P, I]),
         "vva_decode_step": (I, [P, P, I, TP, TP, TP, TP, P, F, F, TP, TP]),
+        "vva_set_log_callback": (None, [LOG_CB, P, I]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -114,6 +119,23 @@ def load_library(path: str = LIB_PATH):
         fn.argtypes = args
     _lib = L
     return L
+
+
+_log_cb_ref = None      # the installed ctypes callback (kept alive while set)
+
+
+def set_log_callback(fn, max_level: int = LOG_INFO):
+    """Deliver the library's messages to fn(level, message) up to max_level
+    (fn None: none).  Mirrors vv_set_log_callback."""
+    global _log_cb_ref
+    lib = load_library()
+    if fn is None:
+        lib.vva_set_log_callback(LOG_CB(), None, LOG_ERROR)
+        _log_cb_ref = None
+        return
+    cb = LOG_CB(lambda lvl, msg, _user: fn(int(lvl), msg.decode(errors="replace")))
+    lib.vva_set_log_callback(cb, None, max_level)
+    _log_cb_ref = cb
 
 
 def _torch():
