@@ -473,7 +473,7 @@ def run_decode_small(torch, vva, ctx, steps: int, vvo=None):
             "timing": "HIP events around `steps` back-to-back steps; graph: one captured step replayed"}
 
 
-def run_proj(torch, vva, reps: int = 10):
+def run_proj(torch, vva, reps: int = 10, token_shapes=((4096, 1), (512, 1), (1, 2)), weight_types=None):
     """The fused projections at 7B shapes (hidden 3584, 28 q / 4 kv heads,
     d = 128), F16 and Q8_0 weights: vva_qkv_rope_append (q/k/v GEMM + bias +
     RoPE + F16 cache append) and vva_out_proj_residual.
@@ -490,7 +490,7 @@ def run_proj(torch, vva, reps: int = 10):
     shapes = {"q": (HQ * D, hidden), "k": (HKV * D, hidden), "v": (HKV * D, hidden), "o": (hidden, HQ * D)}
     out = {}
     n_layers = 28
-    for wt, name in ((vva.F16, "f16"), (vva.Q8_0, "q8_0")):
+    for wt, name in weight_types or ((vva.F16, "f16"), (vva.Q8_0, "q8_0")):
         sets = []
         for layer in range(n_layers):
             ws = {}
@@ -502,7 +502,7 @@ def run_proj(torch, vva, reps: int = 10):
             sets.append(ws)
         wbytes_qkv = sum(sets[0][k_].raw.numel() for k_ in "qkv")
         wbytes_o = sets[0]["o"].raw.numel()
-        for T, B in ((4096, 1), (512, 1), (1, 2)):
+        for T, B in token_shapes:
             kv = vva.KVCache(ctx, 1, HKV, D, T + 8, B, vva.F16)
             x = torch.randn((B, T, hidden), device="cuda")
             q_out = torch.empty((B, T, HQ, D), dtype=torch.float16, device="cuda")
@@ -518,7 +518,16 @@ def run_proj(torch, vva, reps: int = 10):
                 M = M_qkv if op == "qkv" else hidden
                 flops = 2.0 * B * T * hidden * M
                 if T > 1:
+                    # untimed calls for >= 3 ms of GPU time: after the heavier shape
+                    # before it the GPU's clock recovers over ~1 ms (kernel trace:
+                    # the first 512-token calls after 4096-token ones run 8-10 % slow)
+                    e0.record()
                     for _ in range(3):
+                        fn(sets[0])
+                    e1.record()
+                    torch.cuda.synchronize()
+                    n_more = int(3000.0 / max(e0.elapsed_time(e1) * 1e3 / 3, 1.0)) + 1
+                    for _ in range(n_more):
                         fn(sets[0])
                     torch.cuda.synchronize()
                     e0.record()
