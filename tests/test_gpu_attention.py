@@ -235,6 +235,50 @@ def test_flash_attn_ext_strided_head_major_kv(ctx, torch_gpu):
     assert_close(as_f32(torch, out), ref, *TOL[vva.F16], what="flash_attn_ext strided")
 
 
+@pytest.mark.parametrize("t", [vva.Q8_0, vva.F32])
+def test_flash_attn_ext_converted_strided_window(ctx, torch_gpu, t):
+    """A multi-token call on K/V laid out [B][Hkv][L][d] (head-major, not the
+    cache layout) of a type the MFMA prefill reads through the f16 window:
+    Q8_0 rows in 34-byte blocks, and F32 rows starting 4 bytes past a 16-byte
+    boundary (the conversion's 4-byte load path).  No mask (every key)."""
+    torch = torch_gpu
+    rng = np.random.default_rng(41)
+    B, Hq, Hkv, L, T, d = 2, 28, 4, 700, 64, 128
+    print(f"converted strided window type={t} B={B} L={L} T={T}", flush=True)
+    q = to_gpu(torch, rng.standard_normal((B, Hq, T, d)), vva.F32)
+    kf = rng.standard_normal((B, Hkv, L, d)).astype(np.float32)
+    vf = rng.standard_normal((B, Hkv, L, d)).astype(np.float32)
+    if t == vva.Q8_0:
+        rb = d // 32 * vva.Q8_BLOCK_BYTES
+        kb = vvo.from_f32(kf.reshape(-1), vvo.Q8_0).reshape(B, Hkv, L, rb)
+        vb = vvo.from_f32(vf.reshape(-1), vvo.Q8_0).reshape(B, Hkv, L, rb)
+        kg, vg = torch.from_numpy(kb).cuda(), torch.from_numpy(vb).cuda()
+        ne, nb = [d, L, Hkv, B], [vva.Q8_BLOCK_BYTES, rb, L * rb, Hkv * L * rb]
+        kt, vt = vva.view(kg, ne, nb, vva.Q8_0), vva.view(vg, ne, nb, vva.Q8_0)
+        kc = [np.ascontiguousarray(kb[b].transpose(1, 0, 2)).reshape(-1) for b in range(B)]
+        vc = [np.ascontiguousarray(vb[b].transpose(1, 0, 2)).reshape(-1) for b in range(B)]
+        ct = vvo.Q8_0
+    else:
+        n = B * Hkv * L * d
+        kflat = torch.from_numpy(np.concatenate([[0.0], kf.reshape(-1)]).astype(np.float32)).cuda()
+        vflat = torch.from_numpy(np.concatenate([[0.0], vf.reshape(-1)]).astype(np.float32)).cuda()
+        kg, vg = kflat[1:1 + n].view(B, Hkv, L, d), vflat[1:1 + n].view(B, Hkv, L, d)
+        assert kg.data_ptr() % 16 == 4
+        kt, vt = vva.view(kg), vva.view(vg)
+        # the flash branch casts the window to F16, as the reference does
+        kc = [vvo.from_f32(kf[b].transpose(1, 0, 2).reshape(-1), vvo.F16) for b in range(B)]
+        vc = [vvo.from_f32(vf[b].transpose(1, 0, 2).reshape(-1), vvo.F16) for b in range(B)]
+        ct = vvo.F16
+    out = torch.full((B, T, Hq, d), float("nan"), dtype=torch.float32, device="cuda")
+    ctx.flash_attn_ext(q, None, None, out, d ** -0.5, k_view=kt, v_view=vt)
+    torch.cuda.synchronize()
+    q32 = as_f32(torch, q).transpose(0, 2, 1, 3)                  # [B, T, Hq, d]
+    ref = vvo.attn(q32, kc, vc, ct, ct, [L] * B, n_kv_heads=Hkv, scale=d ** -0.5, mask_mode=vvo.MASK_NONE)
+    mx, mn = assert_close(as_f32(torch, out), ref, *TOL[vva.Q8_0 if t == vva.Q8_0 else vva.F16],
+                          what="converted strided window")
+    print(f"  max {mx:.2e} mean {mn:.2e}")
+
+
 def test_unsupported_options_are_rejected(ctx, torch_gpu):
     torch = torch_gpu
     q = torch.zeros((1, 4, 1, 64), device="cuda")
