@@ -29,6 +29,11 @@ CASES = [
     (64, 14, 2, vva.F16, 256, 0, vva.F32, 1),       # 0.5B
     (64, 14, 2, vva.F16, 5, 1030, vva.F32, 2),      # TTS text window on both CFG streams
     (128, 28, 4, vva.F16, 2, 0, vva.F32, 1),
+    # Q8_0 caches: the window converted to f16 (contiguous rows: the flat
+    # conversion), ragged sequences of one call included
+    (128, 28, 4, vva.Q8_0, 512, 1536, vva.F32, 1),
+    (128, 28, 4, vva.Q8_0, 33, 700, vva.BF16, 2),
+    (64, 14, 2, vva.Q8_0, 40, 1030, vva.F32, 2),
 ]
 
 
