@@ -78,9 +78,11 @@ namespace {
 
 thread_local std::string g_create_err;
 
-// The vva_set_log_callback sink: process-wide, one delivery at a time.
+// The vva_set_log_callback sink: process-wide, one delivery at a time (a
+// recursive lock: a callback that calls a failing entry point logs again on
+// the same thread rather than deadlocking).
 struct LogSink {
-    std::mutex mu;
+    std::recursive_mutex mu;
     vva_log_cb cb = nullptr;
     void* user = nullptr;
     int max_lvl = -1;                        // nothing delivered until a callback is set
@@ -93,7 +95,7 @@ LogSink& log_sink() {
 // Formats into a stack buffer (no allocation: vva_attn_noalloc logs too).
 void log_msg(vva_log_level lvl, const char* fmt, ...) {
     LogSink& s = log_sink();
-    std::lock_guard<std::mutex> lk(s.mu);
+    std::lock_guard<std::recursive_mutex> lk(s.mu);
     if (!s.cb || (int)lvl > s.max_lvl) return;
     char buf[512];
     va_list ap;
@@ -495,7 +497,7 @@ extern "C" const char* vva_version(void) { return "vva 0.1.0 (gfx950)"; }
 
 extern "C" void vva_set_log_callback(vva_log_cb cb, void* user_data, vva_log_level max_lvl) {
     LogSink& s = log_sink();
-    std::lock_guard<std::mutex> lk(s.mu);
+    std::lock_guard<std::recursive_mutex> lk(s.mu);
     s.cb = cb;
     s.user = user_data;
     s.max_lvl = cb ? (int)max_lvl : -1;
