@@ -660,8 +660,8 @@ def cpu_baseline_small(vvo, kv, qr, d, hq, hkv, T, ct):
 
 
 def cpu_baseline_prefill(torch, vva, vvo, kv, qr):
-    """Oracle (ggml-order mode, all host cores) on layer 0: 1024 query rows spread over [0, 32k)."""
-    rows = np.linspace(0, T_PREFILL - 1, 1024).astype(np.int32)
+    """Oracle (ggml-order mode, all host cores) on layer 0: 4096 query rows spread over [0, 32k)."""
+    rows = np.linspace(0, T_PREFILL - 1, 4096).astype(np.int32)
     kraw, vraw = kv.download(0, 0, T_PREFILL)
     q32 = qr.float().cpu().numpy()
     t0 = time.perf_counter()

@@ -24,6 +24,18 @@
 #include <stdlib.h>
 #include <string.h>
 
+#if defined(__F16C__) && defined(__AVX2__) && defined(__FMA__)
+#include <immintrin.h>
+#define VVO_F16C 1
+#endif
+
+/* The ggml-order attention's F16 rows may be converted 8 at a time with the
+ * F16C instructions (vcvtph2ps, and vcvtps2ph with round-to-nearest-even: the
+ * same values as the scalar conversions below for every finite input).
+ * vvo_set_simd(0) selects the scalar loops, so the tests can compare the two. */
+static int g_simd = 1;
+void vvo_set_simd(int on) { g_simd = on; }
+
 /* ------------------------------------------------------------ conversions */
 
 static inline uint32_t f_bits(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
@@ -331,6 +343,12 @@ static void attn_ggml_one(const vvo_attn_args* a, int b, int t, int h,
                 s += (float)sumi * (h2f(dk) * h2f(dq));
             }
         } else {
+#ifdef VVO_F16C
+            if (g_simd && a->k_type == VVO_F16 && d % 8 == 0) {
+                for (int i = 0; i < d; i += 8)
+                    _mm256_storeu_ps(krow + i, _mm256_cvtph_ps(_mm_loadu_si128((const __m128i*)(kp + 2 * i))));
+            } else
+#endif
             vvo_to_f32(kp, a->k_type, krow, d);
             s = dot32(qr, krow, d);
         }
@@ -339,15 +357,40 @@ static void attn_ggml_one(const vvo_attn_args* a, int b, int t, int h,
         const float Mold = M;
         float ms = 1.0f, vs = 1.0f;
         const uint8_t* vp = (const uint8_t*)a->v[b] + (int64_t)j * rv + (int64_t)kvh * hv;
+#ifdef VVO_F16C
+        const int vec16 = v16 && g_simd && d % 8 == 0;
+#else
+        const int vec16 = 0;
+#endif
         if (s > M) {
             M = s;
             ms = expf(Mold - M);
-            if (v16) for (int i = 0; i < d; ++i) vkq16[i] = vvo_f32_to_f16(h2f(vkq16[i]) * ms);
-            else     for (int i = 0; i < d; ++i) vkq[i] *= ms;
+            if (vec16) {
+#ifdef VVO_F16C
+                const __m256 f = _mm256_set1_ps(ms);
+                for (int i = 0; i < d; i += 8) {
+                    const __m256 x = _mm256_cvtph_ps(_mm_loadu_si128((const __m128i*)(vkq16 + i)));
+                    _mm_storeu_si128((__m128i*)(vkq16 + i), _mm256_cvtps_ph(_mm256_mul_ps(x, f), _MM_FROUND_TO_NEAREST_INT));
+                }
+#endif
+            } else if (v16) {
+                for (int i = 0; i < d; ++i) vkq16[i] = vvo_f32_to_f16(h2f(vkq16[i]) * ms);
+            } else {
+                for (int i = 0; i < d; ++i) vkq[i] *= ms;
+            }
         } else {
             vs = expf(s - M);
         }
-        if (v16) {
+        if (vec16) {
+#ifdef VVO_F16C
+            const __m256 f = _mm256_set1_ps(vs);
+            for (int i = 0; i < d; i += 8) {
+                const __m256 v = _mm256_cvtph_ps(_mm_loadu_si128((const __m128i*)(vp + 2 * i)));
+                const __m256 x = _mm256_cvtph_ps(_mm_loadu_si128((const __m128i*)(vkq16 + i)));
+                _mm_storeu_si128((__m128i*)(vkq16 + i), _mm256_cvtps_ph(_mm256_fmadd_ps(v, f, x), _MM_FROUND_TO_NEAREST_INT));
+            }
+#endif
+        } else if (v16) {
             const uint16_t* vv = (const uint16_t*)vp;
             for (int i = 0; i < d; ++i) vkq16[i] = vvo_f32_to_f16(fmaf(h2f(vv[i]), vs, h2f(vkq16[i])));
         } else {

@@ -90,6 +90,9 @@ typedef struct {
 
 int      vvo_attn(const vvo_attn_args* a);
 int      vvo_n_cores(void);
+/* 1 (default): F16 rows of the ggml-order attention converted 8 at a time
+ * with F16C (same values); 0: the scalar conversions */
+void     vvo_set_simd(int on);
 
 /* Linear layer y = x W^T (+ bias): ggml_mul_mat(W, x) followed by ggml_add
  * of the bias (linear(), src/qwen2.cpp:19-25), as used for the q/k/v

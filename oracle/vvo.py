@@ -69,6 +69,8 @@ def lib():
         L.vvo_attn.restype = ctypes.c_int
         L.vvo_attn.argtypes = [ctypes.POINTER(AttnArgs)]
         L.vvo_n_cores.restype = ctypes.c_int
+        L.vvo_set_simd.restype = None
+        L.vvo_set_simd.argtypes = [ctypes.c_int]
         L.vvo_linear.restype = ctypes.c_int
         L.vvo_linear.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p,
                                  ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int,
@@ -164,6 +166,11 @@ def attn(q: np.ndarray, k_caches, v_caches, k_type: int, v_type: int, L, *, n_kv
 
 def n_cores() -> int:
     return int(lib().vvo_n_cores())
+
+
+def set_simd(on: bool) -> None:
+    """F16C conversions in the ggml-order attention (default) or the scalar loops."""
+    lib().vvo_set_simd(1 if on else 0)
 
 
 def linear(x: np.ndarray, w_raw: np.ndarray, w_type: int, M: int, bias: np.ndarray | None = None,

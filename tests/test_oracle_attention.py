@@ -230,3 +230,27 @@ def test_planted_mistake_is_caught_by_brute_force(vvo):
                      past=[past + 1])[0]
     ref = brute(q[0], k, v, past, 0.3, 2)
     assert np.abs(wrong[:-1] - ref[:-1]).max() > 1e-2
+
+
+@pytest.mark.parametrize("mode_name", ["GGML", "GGML_F32ACC"])
+def test_ggml_order_f16c_path_equals_scalar_path(vvo, mode_name):
+    """The F16C conversions of F16 K rows and of the F16 running V sum give
+    the scalar loops' values bit for bit (vcvtps2ph rounds to nearest even, as
+    vvo_f32_to_f16 does).  Heavy-tailed scores force running-max rescales."""
+    rng = np.random.default_rng(23)
+    Hq, Hkv, d, T, past = 12, 2, 128, 9, 700
+    L = past + T
+    q = rng.standard_normal((1, T, Hq, d)).astype(np.float32)
+    k = rng.standard_normal((L, Hkv, d)).astype(np.float32)
+    k *= (1.0 + 3.0 * (np.arange(L) // 64))[:, None, None].astype(np.float32)
+    kraw, _ = make_cache(vvo, k, TYPES["f16"])
+    vraw, _ = make_cache(vvo, rng.standard_normal((L, Hkv, d)).astype(np.float32) * 40.0, TYPES["f16"])
+    mode = getattr(vvo, mode_name)
+    args = dict(n_kv_heads=Hkv, scale=d ** -0.5, mode=mode)
+    fast = vvo.attn(q, [kraw], [vraw], 1, 1, [L], **args)
+    vvo.set_simd(False)
+    try:
+        slow = vvo.attn(q, [kraw], [vraw], 1, 1, [L], **args)
+    finally:
+        vvo.set_simd(True)
+    assert np.array_equal(fast.view(np.uint32), slow.view(np.uint32))
