@@ -338,9 +338,14 @@ def run_prefill_chunked(torch, vva, ctx, layers: int, cache_type: int = None):
           for _ in range(layers * n_chunks)]
     scale = D ** -0.5
     pos_all = torch.arange(T_PREFILL, dtype=torch.int32, device="cuda")
-    for layer in range(layers + 1):                  # layer 0: untimed warm-up (sizes the workspace)
-        for c in range(n_chunks):
-            kv.set_len(0, c * CHUNK)
+    # chunk by chunk, the layer stack inside each chunk, as the reference's ASR
+    # loop builds one graph per chunk (src/vibevoice_asr.cpp:554-652); layer 0
+    # is untimed (it sizes the workspace).  The host settles a chunk's split
+    # plan at its first call and the chunk's other layers reuse it (the
+    # layer-major order measured the same: the host runs ahead of the GPU)
+    for c in range(n_chunks):
+        kv.set_len(0, c * CHUNK)
+        for layer in range(layers + 1):
             ctx.rope_append(kv, layer, q, k, v, pos_all[c * CHUNK:(c + 1) * CHUNK], qr, freq_base=THETA)
             if layer > 0:
                 ev[(layer - 1) * n_chunks + c][0].record()
