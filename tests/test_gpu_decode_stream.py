@@ -56,6 +56,7 @@ CASES = [
     (64, 16, 8, [1500], vva.BF16, 9),              # d = 64, eight kv heads
     (128, 28, 4, [700, 700], vva.F32, 1),          # one split: output written directly
     (128, 28, 4, [32769, 32769], vva.F32, None),   # the 7B CFG decode at full size: 32768 past + 1
+    (128, 28, 4, [131073, 98305], vva.F32, None),  # the longest window the benchmark sweeps (128k past)
 ]
 
 
