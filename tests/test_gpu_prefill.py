@@ -155,6 +155,36 @@ def test_decode_after_prefill_equals_last_prefill_row(ctx, torch_gpu):
     assert np.abs(step[0, N - 1] - full[0, N - 1]).max() < 1e-3
 
 
+@pytest.mark.parametrize("t", [vva.F16, vva.Q8_0])
+def test_chunk_over_a_128k_past(ctx, torch_gpu, t):
+    """The last 512-token ASR chunk of a 128k-token window (7B heads): key
+    splits merged in the launch (F16), and the converted f16 window of
+    67 MB per operand plus the gated fallback (Q8_0).  Rows: the chunk's first
+    and last 16 and 16 spread between."""
+    torch = torch_gpu
+    d, Hq, Hkv, T = 128, 28, 4, 512
+    L = 131072
+    past = L - T
+    print(f"chunk over a 128k past type={t}", flush=True)
+    kv = vva.KVCache(ctx, 1, Hkv, d, L, 1, t)
+    fill_cache(kv, [L], seed=1280 + t)
+    kv.set_len(0, past)
+    rng = np.random.default_rng(1281)
+    q = to_gpu(torch, rng.standard_normal((1, T, Hq, d)), vva.BF16)
+    out = torch.full((1, T, Hq, d), float("nan"), dtype=torch.float32, device="cuda")
+    ctx.attn(kv, 0, q, out, d ** -0.5)
+    torch.cuda.synchronize()
+    o = as_f32(torch, out)
+    assert np.isfinite(o).all()
+    rows = np.unique(np.concatenate([np.arange(16), np.arange(T - 16, T),
+                                     np.linspace(16, T - 17, 16).astype(np.int64)])).astype(np.int32)
+    q32 = as_f32(torch, q)
+    ref = oracle_attn(q32, kv, 0, [0], [L], T, d ** -0.5, rows=rows)
+    mx, mn = assert_close(o[0, rows], ref[0, rows], *TOL, what="128k-past chunk vs exact")
+    print(f"  splits {ctx.last_decode_splits()}: vs exact max {mx:.2e} mean {mn:.2e}")
+    kv.free()
+
+
 def test_full_size_7b_prefill_row_subset(ctx, torch_gpu):
     """32768-token causal prefill, 28q/4kv, d=128, F16 cache (bf16 inputs)."""
     torch = torch_gpu
