@@ -113,10 +113,18 @@ __device__ __forceinline__ void qkv_epilogue_vec(const ProjArgs& a, const float*
             const int nl = nb + TPP * e, n = n0 + nl;
             if (nl >= TN || n >= a.N) break;
             const float* cr = C + nl * cpitch + hl * d;
+            // the chunk and its partners' chunk as 16-byte reads (the row
+            // pitch, d and i0 keep them 16-byte aligned): 8 scalar reads at a
+            // 32-byte lane stride would meet on the same banks
+            float yv[8], qv[8];
+            *(float4*)&yv[0] = *(const float4*)(cr + i0);
+            *(float4*)&yv[4] = *(const float4*)(cr + i0 + 4);
+            *(float4*)&qv[0] = *(const float4*)(cr + ip);
+            *(float4*)&qv[4] = *(const float4*)(cr + ip + 4);
             float out[8];
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
-                const float y = cr[i0 + k] + bs[k], yq = cr[ip + k] + bp[k];
+                const float y = yv[k] + bs[k], yq = qv[k] + bp[k];
                 const float cs = (k & 1) ? csr[e][k >> 1].z : csr[e][k >> 1].x;
                 const float sn = (k & 1) ? csr[e][k >> 1].w : csr[e][k >> 1].y;
                 // pair (y0, y1) = (dim j, dim j + P): lo threads hold y0
