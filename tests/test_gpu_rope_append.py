@@ -113,6 +113,35 @@ def test_errors_are_reported_not_raised_in_native_code(ctx, torch_gpu):
     kv.free()
 
 
+def test_a_sequence_written_twice_in_one_call_is_refused(ctx, torch_gpu):
+    """Two rows of one call naming the same sequence would write the same
+    cache rows from two places: every writer (vva_rope_append,
+    vva_decode_step) refuses the call before anything is enqueued."""
+    torch = torch_gpu
+    d, Hq, Hkv = 64, 14, 2
+    kv = vva.KVCache(ctx, 1, Hkv, d, 32, 2, vva.F16)
+    kv.set_len(0, 4)
+    kv.set_len(1, 4)
+    before = kv.download(0, 0, 8)
+    q = torch.ones((2, 1, Hq, d), device="cuda")
+    k = torch.ones((2, 1, Hkv, d), device="cuda")
+    q_out = torch.full((2, 1, Hq, d), 7.0, device="cuda")
+    out = torch.full((2, 1, Hq, d), 7.0, device="cuda")
+    pos = torch.tensor([[4], [4]], dtype=torch.int32, device="cuda")
+    with pytest.raises(vva.VvaError) as e:
+        ctx.rope_append(kv, 0, q, k, k, pos, q_out, seq_ids=[0, 0])
+    assert e.value.status == vva.ERR_INVALID_ARG and "twice" in str(e.value)
+    with pytest.raises(vva.VvaError) as e:
+        ctx.decode_step(kv, 0, q, k, k, pos, q_out, out, d ** -0.5, seq_ids=[1, 1])
+    assert e.value.status == vva.ERR_INVALID_ARG and "twice" in str(e.value)
+    torch.cuda.synchronize()
+    after = kv.download(0, 0, 8)
+    assert all(np.array_equal(x, y) for x, y in zip(before, after)), "a refused call wrote the cache"
+    assert bool((q_out == 7.0).all()) and bool((out == 7.0).all())
+    assert kv.get_len(0) == 4 and kv.get_len(1) == 4
+    kv.free()
+
+
 @pytest.mark.parametrize("in_t,cache_t", [(vva.BF16, vva.F16), (vva.F32, vva.BF16), (vva.F16, vva.F32)])
 def test_vector_and_scalar_paths_agree_bit_for_bit(ctx, torch_gpu, in_t, cache_t):
     """Rows on 16-byte boundaries take the vector path (8 pairs per lane), a
