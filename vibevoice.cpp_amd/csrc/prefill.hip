@@ -951,24 +951,24 @@ PrefillPlan prefill_plan(const AttnArgs& a, int n_cu, int forced, size_t ws_cap,
     const double bytes_per_unit = 5.0e6 * unit_us;   // 5 TB/s
     const double merge_launch = 5.0 / unit_us;
     const double prologue = 3.0;                 // ~6 us per workgroup, measured at the 7B shape
-    std::vector<int> nt((size_t)a.B * n_rt);
-    for (int b = 0; b < a.B; ++b)
-        for (int rt = 0; rt < n_rt; ++rt) nt[(size_t)b * n_rt + rt] = rt_key_tiles(a, b, rt, causal);
     // cost of piece x of sequence b under plan p (key tiles + prologue)
     auto piece_cost = [&](const PrefillPlan& p, int b, int x) {
         const int nh = p.forced > 0 ? p.forced : p.n, R = p.forced > 0 ? 0 : p.R;
         const int heavy = (n_rt - R) * nh;
         const int rt = x < heavy ? n_rt - 1 - x / nh : R - 1 - (x - heavy);
         const int ks = x < heavy ? x % nh : 0, n_ks = x < heavy ? nh : 1;
-        const int n_all = nt[(size_t)b * n_rt + rt];
+        const int n_all = rt_key_tiles(a, b, rt, causal);
         return (double)((int64_t)(ks + 1) * n_all / n_ks - (int64_t)ks * n_all / n_ks) + prologue;
     };
     // finish time of plan p: the kv heads of one piece index cost the same,
     // so the CUs are taken in groups of Hkv; pieces go out in the kernel's
     // order (sequence-major, heaviest row tile first) to the group that frees
     // first.  One round (every piece has a group): the largest piece.
-    const int groups = max(1, n_cu / a.Hkv);
-    std::vector<double> cu;
+    // (fixed storage: the planner allocates nothing, for vva_attn_noalloc too;
+    // beyond kPlanMaxGroups groups the replay models that many)
+    constexpr int kPlanMaxGroups = 1024;
+    const int groups = min(max(1, n_cu / a.Hkv), kPlanMaxGroups);
+    double cu[kPlanMaxGroups];
     auto makespan = [&](const PrefillPlan& p) {
         const int pieces = plan_pieces(p, n_rt);
         double m = 0.0;
@@ -977,14 +977,14 @@ PrefillPlan prefill_plan(const AttnArgs& a, int n_cu, int forced, size_t ws_cap,
                 for (int x = 0; x < pieces; ++x) m = max(m, piece_cost(p, b, x));
             return m;
         }
-        cu.assign((size_t)groups, 0.0);
+        std::fill(cu, cu + groups, 0.0);
         for (int b = 0; b < a.B; ++b)
             for (int x = 0; x < pieces; ++x) {
-                std::pop_heap(cu.begin(), cu.end(), std::greater<double>());
-                cu.back() += piece_cost(p, b, x);
-                std::push_heap(cu.begin(), cu.end(), std::greater<double>());
+                std::pop_heap(cu, cu + groups, std::greater<double>());
+                cu[groups - 1] += piece_cost(p, b, x);
+                std::push_heap(cu, cu + groups, std::greater<double>());
             }
-        for (double c : cu) m = max(m, c);
+        for (int i = 0; i < groups; ++i) m = max(m, cu[i]);
         return m;
     };
     PrefillPlan best = none;

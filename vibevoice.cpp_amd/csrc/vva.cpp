@@ -7,6 +7,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <array>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -50,7 +51,9 @@ struct vva_context {
     std::set<vva_kv*> caches;            // released by vva_destroy if still alive
     // the last prefill plan and the call shape it was made for: a layer stack
     // repeats one shape layer after layer
-    std::vector<int64_t> plan_key;
+    // (a fixed array: the key is built on every prefill call, vva_attn_noalloc's included)
+    std::array<int64_t, 10 + 2 * VVA_MAX_BATCH> plan_key{};
+    int plan_key_n = 0;
     PrefillPlan plan{1, 0, 0, 1};
 };
 
@@ -291,15 +294,17 @@ vva_status run_attention(vva_context* ctx, AttnArgs& a, bool fixed = false) {
     // prefill plan of call shape c, reused while the shape repeats
     // (the merge in the launch needs the context's tickets: not vva_attn_noalloc)
     auto plan_for = [&](const AttnArgs& c, size_t cap) {
-        std::vector<int64_t> key = {c.d, c.Hq, c.Hkv, c.T, c.B, c.mask_mode, ctx->n_cu, ctx->sched_prefill_splits,
-                                    (int64_t)cap, (int64_t)fixed};
+        std::array<int64_t, 10 + 2 * VVA_MAX_BATCH> key{c.d, c.Hq, c.Hkv, c.T, c.B, c.mask_mode, ctx->n_cu,
+                                                       ctx->sched_prefill_splits, (int64_t)cap, (int64_t)fixed};
+        int n = 10;
         for (int b = 0; b < c.B; ++b) {
-            key.push_back(c.L[b]);
-            key.push_back(c.past[b]);
+            key[n++] = c.L[b];
+            key[n++] = c.past[b];
         }
-        if (key != ctx->plan_key) {
+        if (n != ctx->plan_key_n || !std::equal(key.begin(), key.begin() + n, ctx->plan_key.begin())) {
             ctx->plan = prefill_plan(c, ctx->n_cu, ctx->sched_prefill_splits, cap, !fixed);
-            ctx->plan_key = std::move(key);
+            ctx->plan_key = key;
+            ctx->plan_key_n = n;
             log_msg(VVA_LOG_DEBUG, "prefill plan: T=%d B=%d L[0]=%d: row tiles from %d split %d ways%s", c.T, c.B,
                     c.L[0], ctx->plan.R, ctx->plan.max_ks, ctx->plan.in_launch ? ", merged in the launch" : "");
         }
