@@ -139,3 +139,55 @@ def test_graph_replay_after_workspace_growth(torch_gpu):
             if kv is not None:
                 kv.free()
         c.close()
+
+
+@pytest.mark.parametrize("kt", [vva.F16, vva.Q8_0])
+def test_prefill_chunk_graph_replays(ctx, torch_gpu, kt):
+    """An ASR chunk step (per layer: RoPE + append of 512 tokens, then the
+    chunk's attention over a 2048-token past) captured and replayed three
+    times with eager work between the replays.  The captured work holds the
+    key-split prefill whose last split merges in the launch (its tickets
+    must return to zero) and, on the Q8_0 cache, the window conversion to f16
+    and the gated fp32 fallback (its gate closed: no value leaves the f16
+    range).  Every replay's outputs equal the eager step's, bit for bit."""
+    torch = torch_gpu
+    d, Hq, Hkv, T, past, layers = 128, 28, 4, 512, 2048, 2
+    print(f"graph chunk type={kt} T={T} past={past}", flush=True)
+    kv = vva.KVCache(ctx, layers, Hkv, d, past + T, 1, kt)
+    fill_cache(kv, [past], seed=4242 + kt)
+    rng = np.random.default_rng(43)
+    q = to_gpu(torch, rng.standard_normal((1, T, Hq, d)), vva.BF16)
+    k = to_gpu(torch, rng.standard_normal((1, T, Hkv, d)), vva.BF16)
+    v = to_gpu(torch, rng.standard_normal((1, T, Hkv, d)), vva.BF16)
+    pos = torch.arange(past, past + T, dtype=torch.int32, device="cuda")
+    qr = [torch.empty((1, T, Hq, d), dtype=torch.float16, device="cuda") for _ in range(layers)]
+    out = [torch.empty((1, T, Hq, d), dtype=torch.float32, device="cuda") for _ in range(layers)]
+
+    def step():
+        for layer in range(layers):
+            ctx.rope_append(kv, layer, q, k, v, pos, qr[layer])
+            ctx.attn(kv, layer, qr[layer], out[layer], d ** -0.5)
+
+    step()                                        # eager; sizes the workspace and settles the plan
+    torch.cuda.synchronize()
+    splits = ctx.last_decode_splits()
+    ref_out = [o.cpu().numpy().copy() for o in out]
+    g = torch.cuda.CUDAGraph()
+    default = torch.cuda.current_stream()
+    try:
+        with torch.cuda.graph(g):
+            ctx.set_stream(torch.cuda.current_stream())
+            step()
+    finally:
+        ctx.set_stream(default)
+    for r in range(3):
+        for o in out:
+            o.fill_(float("nan"))                 # eager work between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for layer in range(layers):
+            assert np.array_equal(out[layer].cpu().numpy(), ref_out[layer]), f"replay {r} layer {layer}"
+        print(f"  replay {r} ({splits} key splits): outputs equal the eager step", flush=True)
+    del g
+    kv.free()
