@@ -2549,14 +2549,11 @@ hipError_t launch_proj(ProjPrepArgs& p, ProjArgs& a, void* ws, hipStream_t s) {
         else                    hipLaunchKernelGGL((proj_gemm_wide_kernel<kProjResidual>), dim3(wtiles), block, 0, s, a);
         return hipGetLastError();
     }
+    // Q8_0 weights below the big-kernel threshold (F16 ones took the wide
+    // kernel above; the 128 x 128 kernel on F16 weights measured no faster)
     const int tiles = grid((a.M / kTM) * ((a.N + kTN - 1) / kTN));
-    if (a.mode == kProjQKV) {
-        if (q8) hipLaunchKernelGGL((proj_gemm_kernel<true, kProjQKV>), dim3(tiles), dim3(256), 0, s, a);
-        else    hipLaunchKernelGGL((proj_gemm_kernel<false, kProjQKV>), dim3(tiles), dim3(256), 0, s, a);
-    } else {
-        if (q8) hipLaunchKernelGGL((proj_gemm_kernel<true, kProjResidual>), dim3(tiles), dim3(256), 0, s, a);
-        else    hipLaunchKernelGGL((proj_gemm_kernel<false, kProjResidual>), dim3(tiles), dim3(256), 0, s, a);
-    }
+    if (a.mode == kProjQKV) hipLaunchKernelGGL((proj_gemm_kernel<true, kProjQKV>), dim3(tiles), dim3(256), 0, s, a);
+    else                    hipLaunchKernelGGL((proj_gemm_kernel<true, kProjResidual>), dim3(tiles), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
