@@ -361,53 +361,6 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, StreamSte
     // quarter block.
     lds_barrier();                                   // A
 
-    // ---- step mode, the split holding key L - 1: the new K row (waves 0,
-    // 1: RoPE'd) and V row (waves 2, 3) of the group's kv heads, one
-    // rotation pair (i, i + D / 2) per lane, quantized per 32-dim block
-    // (block max over a half-wave) like rope_append.hip's Q8_0 append; to the
-    // cache row and to new_rows
-    if constexpr (STEP) {
-        const int kind = w >> 1, hh = w & 1, i = lane;
-        if (owns_new && hh < HKV) {                  // wave-uniform
-            constexpr int P = D / 2;
-            const int head = hgrp * HKV + hh;
-            const int ii = i < P ? i : 0;
-            const float x0 = nx0, x1 = nx1;
-            float y0 = x0, y1 = x1;
-            if (kind == 0) {
-                const float c = rope_cs[ii], sn = rope_sn[ii];
-                y0 = fmaf(x0, c, -(x1 * sn));
-                y1 = fmaf(x0, sn, x1 * c);
-            }
-            float a0 = fabsf(y0), a1 = fabsf(y1);
-#pragma unroll
-            for (int m = 16; m >= 1; m >>= 1) {
-                a0 = fmaxf(a0, __shfl_xor(a0, m, 32));
-                a1 = fmaxf(a1, __shfl_xor(a1, m, 32));
-            }
-            const float d0 = a0 / 127.0f, d1 = a1 / 127.0f;
-            const float id0 = d0 != 0.0f ? 1.0f / d0 : 0.0f;
-            const float id1 = d1 != 0.0f ? 1.0f / d1 : 0.0f;
-            if (i < P) {
-                char* crow = (char*)(kind ? a.v[b] : a.k[b]) + (int64_t)(L - 1) * RBM + (int64_t)head * HB;
-                char* lrow = new_rows + kind * RB + hh * HB;
-                const int j0 = i, j1 = i + P;
-                const char c0 = (char)(int8_t)roundf(y0 * id0), c1 = (char)(int8_t)roundf(y1 * id1);
-                if ((j0 & 31) == 0) {
-                    const uint16_t h0 = f32_to_f16(d0), h1 = f32_to_f16(d1);
-                    *(uint16_t*)(crow + (j0 / 32) * kQ8Bytes) = h0;
-                    *(uint16_t*)(crow + (j1 / 32) * kQ8Bytes) = h1;
-                    *(uint16_t*)(lrow + (j0 / 32) * kQ8Bytes) = h0;
-                    *(uint16_t*)(lrow + (j1 / 32) * kQ8Bytes) = h1;
-                }
-                crow[(j0 / 32) * kQ8Bytes + 2 + (j0 & 31)] = c0;
-                crow[(j1 / 32) * kQ8Bytes + 2 + (j1 & 31)] = c1;
-                lrow[(j0 / 32) * kQ8Bytes + 2 + (j0 & 31)] = c0;
-                lrow[(j1 / 32) * kQ8Bytes + 2 + (j1 & 31)] = c1;
-            }
-        }
-    }
-
     const char* qraw = lds + (kStages - 1) * kStage;
     uint32_t* qlds = (uint32_t*)(lds + (kStages - 1) * kStage + kQRawBytes);
     constexpr int QI = 1024 / (kW * 64);              // quarters per thread (Hq * NB <= 256)
@@ -514,6 +467,55 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, StreamSte
         }
     }
     lds_barrier();                                   // B
+
+    // ---- step mode, the split holding key L - 1 (after Q is quantized: its
+    // raw k/v rows land late, ~3 us into the launch, and the row is needed
+    // only from tile new_t on): the new K row (waves 0,
+    // 1: RoPE'd) and V row (waves 2, 3) of the group's kv heads, one
+    // rotation pair (i, i + D / 2) per lane, quantized per 32-dim block
+    // (block max over a half-wave) like rope_append.hip's Q8_0 append; to the
+    // cache row and to new_rows
+    if constexpr (STEP) {
+        const int kind = w >> 1, hh = w & 1, i = lane;
+        if (owns_new && hh < HKV) {                  // wave-uniform
+            constexpr int P = D / 2;
+            const int head = hgrp * HKV + hh;
+            const int ii = i < P ? i : 0;
+            const float x0 = nx0, x1 = nx1;
+            float y0 = x0, y1 = x1;
+            if (kind == 0) {
+                const float c = rope_cs[ii], sn = rope_sn[ii];
+                y0 = fmaf(x0, c, -(x1 * sn));
+                y1 = fmaf(x0, sn, x1 * c);
+            }
+            float a0 = fabsf(y0), a1 = fabsf(y1);
+#pragma unroll
+            for (int m = 16; m >= 1; m >>= 1) {
+                a0 = fmaxf(a0, __shfl_xor(a0, m, 32));
+                a1 = fmaxf(a1, __shfl_xor(a1, m, 32));
+            }
+            const float d0 = a0 / 127.0f, d1 = a1 / 127.0f;
+            const float id0 = d0 != 0.0f ? 1.0f / d0 : 0.0f;
+            const float id1 = d1 != 0.0f ? 1.0f / d1 : 0.0f;
+            if (i < P) {
+                char* crow = (char*)(kind ? a.v[b] : a.k[b]) + (int64_t)(L - 1) * RBM + (int64_t)head * HB;
+                char* lrow = new_rows + kind * RB + hh * HB;
+                const int j0 = i, j1 = i + P;
+                const char c0 = (char)(int8_t)roundf(y0 * id0), c1 = (char)(int8_t)roundf(y1 * id1);
+                if ((j0 & 31) == 0) {
+                    const uint16_t h0 = f32_to_f16(d0), h1 = f32_to_f16(d1);
+                    *(uint16_t*)(crow + (j0 / 32) * kQ8Bytes) = h0;
+                    *(uint16_t*)(crow + (j1 / 32) * kQ8Bytes) = h1;
+                    *(uint16_t*)(lrow + (j0 / 32) * kQ8Bytes) = h0;
+                    *(uint16_t*)(lrow + (j1 / 32) * kQ8Bytes) = h1;
+                }
+                crow[(j0 / 32) * kQ8Bytes + 2 + (j0 & 31)] = c0;
+                crow[(j1 / 32) * kQ8Bytes + 2 + (j1 & 31)] = c1;
+                lrow[(j0 / 32) * kQ8Bytes + 2 + (j0 & 31)] = c0;
+                lrow[(j1 / 32) * kQ8Bytes + 2 + (j1 & 31)] = c1;
+            }
+        }
+    }
 
     // B operands of the score MFMAs, block-diagonal over k: per block and
     // 16-dim half j, lane (g, n) holds codes 16 j + 8 (g & 1) .. + 7 of row
