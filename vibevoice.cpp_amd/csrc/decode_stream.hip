@@ -488,12 +488,13 @@ decode_stream_kernel(AttnArgs a, float* __restrict__ ws, int n_splits, StreamSte
                 y0 = fmaf(x0, c, -(x1 * sn));
                 y1 = fmaf(x0, sn, x1 * c);
             }
+            // block max over the half-wave: DPP within rows, then the row pair
             float a0 = fabsf(y0), a1 = fabsf(y1);
-#pragma unroll
-            for (int m = 16; m >= 1; m >>= 1) {
-                a0 = fmaxf(a0, __shfl_xor(a0, m, 32));
-                a1 = fmaxf(a1, __shfl_xor(a1, m, 32));
-            }
+            a0 = fmaxf(a0, dpp<kDppXor1>(a0)); a1 = fmaxf(a1, dpp<kDppXor1>(a1));
+            a0 = fmaxf(a0, dpp<kDppXor2>(a0)); a1 = fmaxf(a1, dpp<kDppXor2>(a1));
+            a0 = fmaxf(a0, dpp<kDppHalfMirror>(a0)); a1 = fmaxf(a1, dpp<kDppHalfMirror>(a1));
+            a0 = fmaxf(a0, dpp<kDppMirror>(a0)); a1 = fmaxf(a1, dpp<kDppMirror>(a1));
+            a0 = max_swap16(a0); a1 = max_swap16(a1);
             const float d0 = a0 / 127.0f, d1 = a1 / 127.0f;
             const float id0 = d0 != 0.0f ? 1.0f / d0 : 0.0f;
             const float id1 = d1 != 0.0f ? 1.0f / d1 : 0.0f;
