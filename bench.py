@@ -720,7 +720,7 @@ def main() -> int:
                     help="copy: a plain 1 GiB device-to-device copy, the reference for FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: the attention path has no multi-GPU mode in this build "
+        print("bench.py measures one GPU: the attention library has no multi-GPU mode "
               "(heads or CFG streams would shard with no exchange); run with --gpus 1", file=sys.stderr)
         return 2
 
